@@ -1,0 +1,383 @@
+/*
+ * sv_verify.h — C ABI of the MI355X speculative-decoding verify path.
+ *
+ * This is the drop-in boundary for the kernel-dispatch surface of the reference engine
+ * (Belluxx/silicon-violetto): the Metal pipelines that `Engine::encode_*` binds and
+ * dispatches (engine/src/gpu.rs:158-194, engine/src/engine/encode.rs:99-573) become plain
+ * `extern "C"` calls on a HIP stream, and `Engine::{new_seq, step, sample_logits,
+ * bench_fill, settle}` (engine/src/engine.rs:267-379, engine/src/engine/hooks.rs:31-55)
+ * become the sv_engine_* calls.
+ *
+ * Conventions (mirroring the reference's, engine/src/gpu.rs:158-167):
+ *   - every call returns an sv_status; SV_OK is 0. On failure sv_last_error() returns a
+ *     thread-local message (the reference's Result<_, String>);
+ *   - pointers named d_* are device pointers (HBM); everything else is host memory;
+ *   - kernels never allocate. Callers own buffers and keep them alive while work that uses
+ *     them is in flight on the stream; calls on one stream run in order;
+ *   - a `workspace` is caller-owned device memory of at least the size the matching
+ *     *_workspace_bytes call returns, ZERO-FILLED ONCE before first use. The kernels keep
+ *     its counters at zero between calls, so one workspace serves any number of calls that
+ *     run in stream order (two calls that overlap in time must not share one).
+ *
+ * The #[repr(C)] argument structs of engine/src/engine/kernels.rs:36-136 are mirrored
+ * field for field (sv_mat_args, sv_kv_args, sv_attn_args, sv_sample_row, sv_run_in,
+ * sv_gen_state, sv_replay_args).
+ */
+#ifndef SV_VERIFY_H
+#define SV_VERIFY_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ constants */
+#define SV_FEED_ROW 0xffff0000u /* input token FEED_ROW + i is feed[slot][i] (kernels.rs:17) */
+#define SV_FEED_W 16u           /* GPU-fed tokens per slot (kernels.rs:19) */
+#define SV_NO_TOK 0xffffffffu   /* SampleRow.tok: not a token of the step (kernels.rs:28) */
+#define SV_NO_PARENT 0xffu      /* tree node without a parent (kernels.metal:66) */
+#define SV_MAX_STOP 8u          /* stop ids per slot (kernels.rs:32) */
+/* Tokens per run the fused verify attention takes. The reference stops at VERIFY_T = 8
+ * (kernels.rs:30) and sends longer runs to attn_mma, whose tree mask only holds within
+ * tiles of 8 (kernels.metal:1240-1241); here a run of up to FEED_W rows keeps one full
+ * 16-bit ancestry mask. */
+#define SV_MAX_RUN 16u
+#define SV_SAMPLE_THREADS 1024u /* the sampler's fixed summation order (kernels.rs:13) */
+#define SV_SAMPLE_ROUNDS 8u     /* top-p rejection rounds (kernels.metal:1413) */
+#define SV_RMS_EPS 1.1920928955078125e-07f /* 2^-23 (kernels.metal:13) */
+#define SV_ROPE_PAIRS 32u       /* RoPE pairs per head: dims 0..63 (kernels.metal:727-736) */
+
+/* Matmul epilogues and flags (kernels.metal:151-152, kernels.rs:4-10). */
+enum {
+  SV_EPI_NORM = 1,   /* y = scale * acc / rms(x)                                   */
+  SV_EPI_RESID = 2,  /* y = ra * base + rb * scale * acc                           */
+  SV_EPI_SWIGLU = 3, /* y[row/2] = silu(g) * u over interleaved (gate, up) rows, norm folded */
+  SV_EPI_HEAD = 4,   /* y = 23 sigmoid((acc + 5) / 7.5), -inf at rows >= vocab_real */
+  SV_EPI_RAW = 5     /* y = acc                                                     */
+};
+enum {
+  SV_FLAG_WRITE_INV = 1, /* aux[t] = 1 / rms(x[t]) (EPI_NORM)                   */
+  SV_FLAG_WRITE_RAW = 2, /* aux = scale * acc (EPI_RESID)                      */
+  /* Extension: acc *= 1/rms(x) for EPI_HEAD/EPI_RAW/EPI_RESID, i.e. the reference's
+   * rmsnorm_rows (kernels.metal:117-131) folded into the matmul that follows it. */
+  SV_FLAG_NORM_IN = 4
+};
+enum { SV_FMT_BF16 = 0, SV_FMT_I8 = 1 };
+
+typedef enum sv_status {
+  SV_OK = 0,
+  SV_ERR_ARG = 1,         /* a bad argument (shape, size, null pointer)          */
+  SV_ERR_HIP = 2,         /* a HIP runtime call failed                           */
+  SV_ERR_CAPACITY = 3,    /* a capacity of the engine would be exceeded          */
+  SV_ERR_UNSUPPORTED = 4, /* valid in the reference, not built here              */
+  SV_ERR_STATE = 5        /* call out of order (unknown sequence, no weights...) */
+} sv_status;
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* sv_last_error(void);
+
+/* ------------------------------------------------------------- model shapes */
+/* The reference hard-codes these (engine/src/model.rs:6-18); here they are runtime values.
+ * Supported: head_dim 64 or 128, hidden and ffn multiples of 256, n_heads a multiple of
+ * n_kv_heads, n_heads / n_kv_heads <= 8. */
+typedef struct sv_shape {
+  uint32_t hidden;     /* H                                    */
+  uint32_t n_heads;    /* NQ                                   */
+  uint32_t n_kv_heads; /* NKV                                  */
+  uint32_t head_dim;   /* D                                    */
+  uint32_t ffn;        /* F (gate_up has 2F interleaved rows)  */
+  uint32_t vocab;      /* embedding rows                       */
+  uint32_t vocab_real; /* ids from here on are masked padding  */
+  uint32_t n_layers;   /* L                                    */
+} sv_shape;
+
+/* A weight matrix [m][k] row-major (model.rs:22-47): bf16, or int8 with one bf16 scale per
+ * group of 2^gshift consecutive k in scales [m][k >> gshift]. int8 groups of 256 or more are
+ * built; gshift >= log2(k) (e.g. 31) means one scale per output row, scales [m][1]. */
+typedef struct sv_matrix {
+  const void* d_w;
+  const uint16_t* d_scales; /* NULL for bf16 */
+  uint32_t m, k;
+  uint32_t format; /* SV_FMT_* */
+  uint32_t gshift;
+} sv_matrix;
+
+/* MatArgs (kernels.rs:36-50, kernels.metal:157-165). ksplit/kchunk are ignored: the split
+ * of k is the implementation's. */
+typedef struct sv_mat_args {
+  uint32_t n, k, m;
+  uint32_t epi, flags;
+  uint32_t vocab_real;
+  float scale;
+  float ra, rb;
+  uint32_t ksplit, kchunk;
+  uint32_t gshift;
+} sv_mat_args;
+
+/* KvArgs (kernels.rs:53-63, kernels.metal:692-700). Only paged ("global") layers are built:
+ * is_global must be 1; ring and window are unused. Cache layout per tensor (K and V):
+ * bf16 [layers][n_pages][NKV][page][D], page = 1 << page_shift. */
+typedef struct sv_kv_args {
+  uint32_t is_global, kv_layer;
+  uint32_t ring, max_seqs;
+  uint32_t page_shift, n_pages, max_pages;
+  uint32_t window;
+} sv_kv_args;
+
+/* AttnArgs (kernels.rs:72-83, kernels.metal:813-823). Used here: split (cached keys per
+ * split, a multiple of 32), max_splits (grid size, at least the most splits any run needs,
+ * counting the split of its new keys), scale_log2 (softmax scale * log2 e), rope. ve,
+ * capture, fixed_splits, col_sets and one_round are ignored. */
+typedef struct sv_attn_args {
+  uint32_t split, max_splits;
+  float scale_log2;
+  uint32_t rope, ve, capture;
+  uint32_t fixed_splits, col_sets, one_round;
+} sv_attn_args;
+
+/* SampleRow (kernels.rs:86-99, kernels.metal:1454-1461). */
+typedef struct sv_sample_row {
+  uint32_t seed_lo, seed_hi;
+  uint32_t pos; /* position of the drawn token if tok == SV_NO_TOK */
+  float temperature;
+  float top_p;
+  uint32_t tok; /* the step's token whose head row this is: draw at its position + 1 */
+} sv_sample_row;
+
+/* RunIn (kernels.rs:103-111, kernels.metal:1591-1595). */
+typedef struct sv_run_in {
+  uint32_t slot, first, count;
+  uint32_t head0, nhead;
+  uint32_t verify;
+} sv_run_in;
+
+/* GenState (kernels.rs:115-127, kernels.metal:1597-1603). */
+typedef struct sv_gen_state {
+  uint32_t remaining;
+  uint32_t done;
+  uint32_t nstop;
+  uint32_t pad;
+  uint32_t stop[SV_MAX_STOP];
+} sv_gen_state;
+
+/* ReplayArgs (kernels.rs:129-136, kernels.metal:1698-1703). */
+typedef struct sv_replay_args {
+  uint32_t stride, seed;
+  float rate;
+  uint32_t vocab;
+} sv_replay_args;
+
+/* ======================================================= kernel-level calls
+ * One call per Metal pipeline group the forward pass dispatches. */
+
+/* embed (kernels.metal:82-114, encode.rs:128-140): resolves GPU-fed tokens in place,
+ * meta[t] = (slot, lens[slot] + depth), vis from the draft tree, and
+ * d_out[t] = rms_norm(embedding row). d_tin and d_meta are uint2 per token. */
+sv_status sv_embed(void* stream, const sv_shape* shape, const uint16_t* d_table, uint32_t* d_tokens,
+                   float* d_out, const uint32_t* d_tin, uint32_t* d_meta, const uint32_t* d_lens,
+                   const uint32_t* d_feed, const uint32_t* d_tree, uint32_t* d_vis, uint32_t n);
+
+/* rmsnorm_rows (kernels.metal:117-131): d_out[r] = rms_norm(d_in[d_rows[r]]). */
+sv_status sv_rmsnorm_rows(void* stream, const float* d_in, const uint32_t* d_rows, float* d_out, uint32_t n,
+                          uint32_t hidden);
+
+/* The matmul group (encode.rs:488-572 Engine::matmul_in; kernels.metal:151-690 gemv_*,
+ * gemms_*, gemm_*, gemm_splitk_reduce): d_y[t][row] = epilogue(W[row] . x[t]) for
+ * t < a->n, with x[t] = d_x[d_x_rows ? d_x_rows[t] : t] (rows of k floats). d_base is
+ * [n][m] for EPI_RESID; d_aux is [n] (WRITE_INV) or [n][m] (WRITE_RAW). The kernel variant
+ * is chosen from n (the reference's Matmul::for_tokens, encode.rs:33-44). */
+size_t sv_matmul_workspace_bytes(uint32_t n, uint32_t m, uint32_t k);
+sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_x, const uint32_t* d_x_rows, float* d_y,
+                    const float* d_base, float* d_aux, const sv_mat_args* a, void* d_workspace,
+                    size_t workspace_bytes);
+
+/* Fused verify attention (kernels.metal:1008-1148 attn_verify + 1316-1362 attn_dec_reduce;
+ * encode.rs:233-297): for each run (d_runs: uint2 (first token, count <= SV_MAX_RUN)),
+ * q/k rms-norm + RoPE, the run's new K/V written bf16 to the paged cache at p0 + row,
+ * attention over the cached keys [0, p0) and the new keys in each token's vis mask, with
+ * split-KV partials merged by plain sums. d_qkv is [n][(NQ + 2 NKV) D] fp32; d_out is
+ * [n][NQ D] fp32. XSA and the attention gate are not built (xsa = 0, gate = 1). */
+size_t sv_attn_workspace_bytes(const sv_shape* shape, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
+sv_status sv_attn_verify(void* stream, const sv_shape* shape, const float* d_qkv, const uint32_t* d_meta,
+                         uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
+                         const float* d_rope, const sv_kv_args* kv, const sv_attn_args* args,
+                         const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
+                         float* d_out, void* d_workspace, size_t workspace_bytes);
+
+/* sample (kernels.metal:1503-1576, with argmax_partial 1430-1451 folded in): one token
+ * per row of d_logits [rows][vocab]: the argmax at temperature 0 (ties to the lowest id),
+ * else the Philox-keyed inverse-CDF draw with top-p rounds. Bit-exact with the oracle. */
+sv_status sv_sample(void* stream, const float* d_logits, const sv_sample_row* d_rows, uint32_t* d_out,
+                    const uint32_t* d_meta, uint32_t n_rows, uint32_t vocab);
+
+/* accept (kernels.metal:1578-1657). d_path is [nruns][SV_FEED_W]. */
+sv_status sv_accept(void* stream, const sv_run_in* d_runs, const uint32_t* d_tokens, uint32_t* d_out,
+                    uint32_t* d_lens, uint32_t* d_feed, sv_gen_state* d_gen, uint32_t* d_emitted, uint32_t nruns,
+                    const uint32_t* d_tree, uint32_t* d_path, uint32_t* d_path_len, uint32_t* d_on_path);
+
+/* kv_compact (kernels.metal:1659-1693): each verify run's accepted path's K/V rows to
+ * p0 + j on every layer 0..n_layers-1. */
+sv_status sv_kv_compact(void* stream, const sv_shape* shape, const sv_run_in* d_runs, uint32_t nruns,
+                        const uint32_t* d_path, const uint32_t* d_path_len, const uint32_t* d_lens,
+                        uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
+                        const sv_kv_args* kv);
+
+/* replay_draft (kernels.metal:1705-1724): the test drafter. */
+sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,
+                          uint32_t* d_feed, const uint32_t* d_trace, const uint32_t* d_trace_len,
+                          const sv_replay_args* ra, uint32_t* d_tree);
+
+/* ========================================================= engine-level calls
+ * The reference's Engine (engine/src/engine.rs): owns the KV cache, its page pool and
+ * page table (kv.rs), the GPU-resident sequence state (buffers.rs:41-52), the scratch and
+ * the RoPE table; the caller owns the weights (device pointers). */
+typedef struct sv_engine sv_engine;
+
+/* EngineConfig (engine.rs:32-57) plus the model's shape and constants. */
+typedef struct sv_engine_config {
+  sv_shape shape;
+  uint32_t max_seqs;        /* sequence slots                                   */
+  uint32_t max_step_tokens; /* tokens per step over all runs                    */
+  uint32_t max_seq_len;     /* positions per sequence                           */
+  uint32_t max_head_rows;   /* rows that go through the head in one step        */
+  uint32_t kv_tokens;       /* page pool capacity, tokens, shared by all slots  */
+  uint32_t page_shift;      /* log2 tokens per page (reference: 7; configs: 4)  */
+  float attn_scale;         /* softmax scale (reference ATTN_SCALE, model.rs:19) */
+  uint32_t split_keys;      /* cached keys per attention split, multiple of 32; 0: auto */
+} sv_engine_config;
+
+/* One decoder layer (model.rs:49-67): matrices and scalars. rope: whether the layer's
+ * q/k get RoPE (the reference ropes its local layers only, encode.rs:237). */
+typedef struct sv_layer {
+  sv_matrix qkv, o, gate_up, down;
+  float qkv_scale, o_scale;
+  float resid_attn, post_attn;
+  float resid_mlp, post_mlp;
+  uint32_t rope;
+  uint32_t pad;
+} sv_layer;
+
+/* rope_freq: host [SV_ROPE_PAIRS] frequencies (model.rs:81, tools/convert.py:59-61). */
+sv_status sv_engine_create(const sv_engine_config* cfg, const float* rope_freq, sv_engine** out);
+void sv_engine_destroy(sv_engine* e);
+/* Tied bf16 embedding / head [vocab][hidden] (device), and the layers. */
+sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed);
+sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_layer* l);
+/* The HIP stream the engine runs on (a hipStream_t), created by the engine. */
+void* sv_engine_stream(sv_engine* e);
+
+/* Device buffers the engine owns, for tests and benchmarks to fill or read. */
+typedef struct sv_engine_buffers {
+  uint16_t* d_k_cache;      /* [L][n_pages][NKV][page][D] bf16      */
+  uint16_t* d_v_cache;
+  uint32_t* d_page_table;   /* [max_seqs][max_pages]                */
+  uint32_t* d_lens;         /* [max_seqs]                           */
+  uint32_t* d_feed;         /* [max_seqs][SV_FEED_W]                */
+  uint32_t* d_tree;         /* [max_seqs][SV_FEED_W]                */
+  sv_gen_state* d_gen;      /* [max_seqs]                           */
+  uint32_t* d_trace;        /* [max_seqs][max_seq_len]  replay drafter */
+  uint32_t* d_trace_len;    /* [max_seqs]                           */
+  float* d_logits;          /* [max_head_rows][vocab]               */
+  float* d_rope;            /* [max_seq_len + SV_FEED_W][32][2]     */
+  uint32_t* d_out_ids;      /* [max_head_rows]                      */
+  uint32_t* d_emitted;      /* [max_seqs]                           */
+  uint32_t* d_path;         /* [max_seqs][SV_FEED_W]                */
+  uint32_t* d_path_len;     /* [max_seqs]                           */
+  uint32_t n_pages, max_pages;
+  size_t kv_bytes;          /* bytes of each of K and V             */
+} sv_engine_buffers;
+sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* out);
+
+/* Sequences (engine.rs:267-306). */
+sv_status sv_new_seq(sv_engine* e, uint32_t* slot);
+sv_status sv_free_seq(sv_engine* e, uint32_t slot);
+sv_status sv_seq_len(sv_engine* e, uint32_t slot, uint32_t* len);
+/* The slot's pages in order (its page-table row); *n is set to the count. */
+sv_status sv_seq_pages(sv_engine* e, uint32_t slot, uint32_t* pages, uint32_t cap, uint32_t* n);
+/* Sampling (engine.rs:104-138): temperature 0 (greedy) or normal positive, 0 < top_p <= 1. */
+sv_status sv_set_sampling(sv_engine* e, uint32_t slot, float temperature, float top_p, uint64_t seed);
+/* GenState of a slot (stop ids, budget) for accept; the default never stops. */
+sv_status sv_set_gen(sv_engine* e, uint32_t slot, const sv_gen_state* g);
+/* hooks.rs:31-37 bench_fill: advance a sequence by len positions without computing them
+ * (reserving their pages); the caller fills the KV. */
+sv_status sv_bench_fill(sv_engine* e, uint32_t slot, uint32_t len);
+/* engine.rs:281-285 settle: give back `unused` positions of a speculative step. */
+sv_status sv_settle(sv_engine* e, uint32_t slot, uint32_t unused);
+/* Set a slot's device sequence position and GPU-fed input (the next input token). */
+sv_status sv_set_feed(sv_engine* e, uint32_t slot, uint32_t len, uint32_t token);
+
+/* One run of a step (plan.rs:8-18 PlanRun): tokens are ids or SV_FEED_ROW + i. */
+typedef struct sv_run {
+  uint32_t slot;
+  uint32_t count;
+  const uint32_t* tokens; /* host [count]                                 */
+  uint32_t verify;        /* head on every row, rows 1.. are drafts       */
+  uint32_t head;          /* non-verify runs: 0 no head row, 1 last row    */
+} sv_run;
+
+/* What a plan produced (plan.rs:20-36). */
+typedef struct sv_plan_info {
+  uint32_t n_tokens, n_head, n_runs;
+  uint32_t branches;   /* some verify run has > 2 rows: kv_compact runs */
+  uint32_t max_run;
+  uint32_t split, max_splits;
+} sv_plan_info;
+
+enum {
+  SV_STEP_REPLAY = 1,   /* after accept, the replay drafter writes the next drafts */
+  SV_STEP_COMPACT = 2,  /* run kv_compact even if no run branches               */
+  SV_STEP_NO_COMPACT = 4
+};
+
+/* Engine::plan (plan.rs:47-151): lays out a step, reserves pages, advances the host-side
+ * sequence lengths optimistically; `extra_keys` widens the attention grid for replays of
+ * this plan at later positions (graph replays). */
+sv_status sv_plan(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t extra_keys, sv_plan_info* info);
+/* Encode the planned step (encode_forward + tail, encode.rs:99-126,383-412) on the
+ * engine's stream: asynchronous, capturable. */
+sv_status sv_encode(sv_engine* e, uint32_t flags);
+/* Capture sv_encode(flags) of the current plan into a HIP graph; replay it `count` times. */
+sv_status sv_graph_capture(sv_engine* e, uint32_t flags);
+sv_status sv_graph_replay(sv_engine* e, uint32_t count);
+sv_status sv_sync(sv_engine* e);
+/* Replay-drafter settings (generate.rs:421-430). */
+sv_status sv_set_replay(sv_engine* e, uint32_t seed, float rate);
+
+/* A synchronous step (Engine::step, engine.rs:310-314): plan, encode, wait; read the head
+ * rows' ids (ids[n_head]) and, if logits is non-null, their logits [n_head][vocab], and
+ * per run the tokens emitted. */
+sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
+                  float* logits, uint32_t* emitted, sv_plan_info* info);
+
+/* Per-kernel timing of one encoded step (the reference's profile/bench_matmul hooks,
+ * hooks.rs:60-112, cli/src/profile.rs): encodes the planned step `reps` times on the engine's
+ * stream with a hipEvent pair around every kernel, waits, and adds each kernel's elapsed
+ * milliseconds and launch count into ms[kind] / launches[kind] (arrays of SV_KIND_COUNT).
+ * The steps really run (sequence state advances). */
+enum {
+  SV_KIND_EMBED = 0,
+  SV_KIND_QKV = 1,
+  SV_KIND_ATTN = 2,
+  SV_KIND_O = 3,
+  SV_KIND_GATE_UP = 4,
+  SV_KIND_DOWN = 5,
+  SV_KIND_HEAD = 6,
+  SV_KIND_SAMPLE = 7,
+  SV_KIND_ACCEPT = 8,
+  SV_KIND_COMPACT = 9,
+  SV_KIND_REPLAY = 10,
+  SV_KIND_COUNT = 11
+};
+sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
+
+/* hooks.rs:41-55 sample_logits: the sampler on caller logits (host [rows][vocab]) with
+ * per-row (temperature, top_p, seed, position). */
+sv_status sv_sample_logits(sv_engine* e, const float* logits, uint32_t rows, const float* temperature,
+                           const float* top_p, const uint64_t* seed, const uint32_t* pos, uint32_t* ids);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SV_VERIFY_H */

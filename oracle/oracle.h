@@ -1,0 +1,119 @@
+/*
+ * oracle.h — CPU restatement of the reference's verify path, for TESTS ONLY.
+ *
+ * This is test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it, and only as the checker (or the timed CPU baseline).
+ * The product path (libsv_verify.so) never calls it.
+ *
+ * Each function cites the reference file:line whose semantics it restates. Matmuls and
+ * attention accumulate in double (the reference's exact-arithmetic result; its own fp32
+ * order differs between its GEMV, streaming-GEMM and GEMM variants, kernels.metal:211-690),
+ * the sampler and every integer routine mirror the reference's operation order exactly.
+ *
+ * Pinning (what checks each function independently of its own formula) is listed in the
+ * header comment of oracle.c.
+ */
+#ifndef SV_ORACLE_H
+#define SV_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../include/sv_verify.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* scalars */
+float orc_bf(uint16_t u);
+uint16_t orc_to_bf(float f);
+float orc_round_bf16(float x);
+void orc_philox(uint32_t ctr[4], const uint32_t key[2]);
+float orc_uniform01(uint32_t seed_lo, uint32_t seed_hi, uint32_t pos, uint32_t round);
+float orc_exp2(float x);
+void orc_to_bf_array(const float* x, uint16_t* out, size_t n);
+void orc_exp2_array(const float* x, float* out, size_t n);
+
+/* data formats */
+void orc_quantize(const float* w, uint32_t m, uint32_t k, uint32_t group, int8_t* q, uint16_t* s);
+void orc_rope_table(const float* freq, uint32_t n_pos, float* tab);
+
+/* kernels */
+void orc_embed(const sv_shape* sh, const uint16_t* table, uint32_t* tokens, float* out, const uint32_t* tin,
+               uint32_t* meta, const uint32_t* lens, const uint32_t* feed, const uint32_t* tree, uint32_t* vis,
+               uint32_t n);
+void orc_rmsnorm_rows(const float* in, const uint32_t* rows, float* out, uint32_t n, uint32_t hidden);
+void orc_matmul(const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y, const float* base, float* aux,
+                const sv_mat_args* a);
+void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
+                     uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
+                     const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
+                     float* out);
+void orc_sample(const float* logits, const sv_sample_row* rows, uint32_t* out, const uint32_t* meta,
+                uint32_t n_rows, uint32_t vocab);
+void orc_accept(const sv_run_in* runs, const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed,
+                sv_gen_state* gen, uint32_t* emitted, uint32_t nruns, const uint32_t* tree, uint32_t* path,
+                uint32_t* path_len, uint32_t* on_path);
+void orc_kv_compact(const sv_shape* sh, const sv_run_in* runs, uint32_t nruns, const uint32_t* path,
+                    const uint32_t* path_len, const uint32_t* lens, uint16_t* k_cache, uint16_t* v_cache,
+                    const uint32_t* page_table, const sv_kv_args* kv);
+void orc_replay_draft(const sv_run_in* runs, uint32_t nruns, const uint32_t* lens, uint32_t* feed,
+                      const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra, uint32_t* tree);
+
+/* page pool (kv.rs:40-60): LIFO free list initialised (0..n).rev() */
+typedef struct orc_pool {
+  uint32_t* free_list; /* [n_pages] */
+  uint32_t n_free, n_pages, max_pages, page_shift;
+  uint32_t* page_table; /* [max_seqs][max_pages] */
+  uint32_t* seq_pages;  /* [max_seqs] pages held  */
+} orc_pool;
+void orc_pool_init(orc_pool* p, uint32_t n_pages, uint32_t max_seqs, uint32_t max_pages, uint32_t page_shift,
+                   uint32_t* free_list, uint32_t* page_table, uint32_t* seq_pages);
+int orc_pool_reserve(orc_pool* p, uint32_t slot, uint32_t len); /* 0 ok, -1 exhausted */
+void orc_pool_release(orc_pool* p, uint32_t slot);
+
+/* A step plan (plan.rs:47-151, without the split sizing). in_runs: (slot, count, verify,
+ * head) per run, in_tokens: the runs' tokens back to back. Outputs sized by the caller:
+ * tokens[n], tin[2n], vis[n], head_rows[n], samples[n], run_in[n_runs]. seq_len[] is the
+ * host-side length per slot, advanced by each run (optimistically, as the reference).
+ * Returns n_head, or -1 on a rejected plan. */
+int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens, uint32_t* seq_len,
+             const sv_sample_row* sampling_per_slot, uint32_t* tokens, uint32_t* tin, uint32_t* vis,
+             uint32_t* head_rows, sv_sample_row* samples, sv_run_in* run_in);
+
+/* The whole verify step on host memory (encode.rs:99-126 encode_forward + encode_tail
+ * 383-412). Weights in `layers` and `embed` are host pointers. */
+typedef struct orc_step_io {
+  /* plan */
+  uint32_t n, n_head, n_runs;
+  uint32_t* tokens;          /* [n], resolved in place          */
+  const uint32_t* tin;       /* [n][2]                           */
+  uint32_t* vis;             /* [n]                              */
+  const uint32_t* head_rows; /* [n_head]                         */
+  const sv_sample_row* samples;
+  const sv_run_in* runs;
+  const uint32_t* attn_runs; /* [n_runs][2] (first, count)      */
+  uint32_t compact;          /* run kv_compact                   */
+  /* device-resident state in the reference */
+  uint32_t* lens, *feed, *tree;
+  sv_gen_state* gen;
+  uint16_t* k_cache, *v_cache;
+  const uint32_t* page_table;
+  sv_kv_args kv;
+  const float* rope;
+  /* outputs */
+  uint32_t* meta;  /* [n][2]          */
+  float* logits;   /* [n_head][vocab] */
+  uint32_t* out;   /* [n_head]        */
+  uint32_t* emitted, *path, *path_len, *on_path;
+  float* hidden;   /* [n][H] final residual, may be NULL */
+} orc_step_io;
+
+int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,
+             orc_step_io* io);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,371 @@
+"""ctypes binding of the CPU oracle (liboracle.so). TEST INFRASTRUCTURE ONLY: imported by
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, never by the product."""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+u32 = C.c_uint32
+f32 = C.c_float
+vp = C.c_void_p
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = C.CDLL(str(LIB_PATH))
+        L.orc_bf.restype = f32
+        L.orc_bf.argtypes = [C.c_uint16]
+        L.orc_to_bf.restype = C.c_uint16
+        L.orc_to_bf.argtypes = [f32]
+        L.orc_round_bf16.restype = f32
+        L.orc_round_bf16.argtypes = [f32]
+        L.orc_uniform01.restype = f32
+        L.orc_uniform01.argtypes = [u32, u32, u32, u32]
+        L.orc_exp2.restype = f32
+        L.orc_exp2.argtypes = [f32]
+        L.orc_pool_reserve.restype = C.c_int
+        L.orc_plan.restype = C.c_int
+        L.orc_step.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def ptr(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(vp)
+
+
+def struct_ptr(s):
+    return C.byref(s) if s is not None else None
+
+
+# -- scalars / formats ------------------------------------------------------------------------
+def philox(ctr, key) -> list[int]:
+    c = (u32 * 4)(*ctr)
+    k = (u32 * 2)(*key)
+    lib().orc_philox(c, k)
+    return list(c)
+
+
+def exp2(x: float) -> float:
+    return lib().orc_exp2(x)
+
+
+def uniform01(seed_lo: int, seed_hi: int, pos: int, rnd: int) -> float:
+    return lib().orc_uniform01(seed_lo, seed_hi, pos, rnd)
+
+
+def quantize(w: np.ndarray, group: int) -> tuple[np.ndarray, np.ndarray]:
+    w = np.ascontiguousarray(w, np.float32)
+    m, k = w.shape
+    q = np.zeros((m, k), np.int8)
+    s = np.zeros((m, k // group), np.uint16)
+    lib().orc_quantize(ptr(w), m, k, group, ptr(q), ptr(s))
+    return q, s
+
+
+def rope_table(freq: np.ndarray, n_pos: int) -> np.ndarray:
+    f = np.ascontiguousarray(freq, np.float32)
+    tab = np.zeros((n_pos, 32, 2), np.float32)
+    lib().orc_rope_table(ptr(f), n_pos, ptr(tab))
+    return tab
+
+
+def bf16_to_f32(u: np.ndarray) -> np.ndarray:
+    return (np.asarray(u, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+# -- kernels ----------------------------------------------------------------------------------
+def matmul(L, mat_w: np.ndarray, scales: np.ndarray | None, gshift: int, x: np.ndarray, a, *,
+           base: np.ndarray | None = None, x_rows: np.ndarray | None = None, aux: np.ndarray | None = None
+           ) -> np.ndarray:
+    """y = epilogue(W x) as the reference's matmul group. L is violetto._lib (struct types)."""
+    m, k = mat_w.shape
+    fmt = 1 if mat_w.dtype == np.int8 else 0
+    w = np.ascontiguousarray(mat_w)
+    sc = np.ascontiguousarray(scales) if scales is not None else None
+    mat = L.Matrix(w.ctypes.data, sc.ctypes.data if sc is not None else None, m, k, fmt, gshift)
+    out_m = m // 2 if a.epi == 3 else m
+    y = np.zeros((a.n, out_m), np.float32)
+    lib().orc_matmul(C.byref(mat), ptr(np.ascontiguousarray(x, np.float32)),
+                     ptr(x_rows), ptr(y), ptr(base), ptr(aux), C.byref(a))
+    return y
+
+
+def attn_verify(L, shape, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, vis) -> np.ndarray:
+    sh = shape.c()
+    n = qkv.shape[0]
+    out = np.zeros((n, shape.n_heads * shape.head_dim), np.float32)
+    lib().orc_attn_verify(C.byref(sh), ptr(qkv), ptr(meta), ptr(k_cache), ptr(v_cache), ptr(page_table), ptr(rope),
+                          C.byref(kv), C.byref(args), ptr(runs), u32(len(runs) // 2), ptr(vis), ptr(out))
+    return out
+
+
+def sample(L, logits: np.ndarray, rows, meta: np.ndarray | None = None) -> np.ndarray:
+    logits = np.ascontiguousarray(logits, np.float32)
+    n, vocab = logits.shape
+    arr = (L.SampleRow * n)(*rows)
+    out = np.zeros(n, np.uint32)
+    lib().orc_sample(ptr(logits), arr, ptr(out), ptr(meta), u32(n), u32(vocab))
+    return out
+
+
+def accept(L, runs, tokens, out, lens, feed, gen, tree, n_tokens: int):
+    """Returns (out, lens, feed, gen, emitted, path, path_len, on_path) after accept."""
+    nr = len(runs)
+    runs_a = (L.RunIn * nr)(*runs)
+    gen_a = (L.GenState * len(gen))(*gen)
+    out = np.array(out, np.uint32)
+    lens = np.array(lens, np.uint32)
+    feed = np.array(feed, np.uint32)
+    emitted = np.zeros(nr, np.uint32)
+    path = np.zeros(nr * 16, np.uint32)
+    path_len = np.zeros(nr, np.uint32)
+    on_path = np.zeros(max(1, n_tokens), np.uint32)
+    lib().orc_accept(runs_a, ptr(np.ascontiguousarray(tokens, np.uint32)), ptr(out), ptr(lens), ptr(feed), gen_a,
+                     ptr(emitted), u32(nr), ptr(np.ascontiguousarray(tree, np.uint32)), ptr(path), ptr(path_len),
+                     ptr(on_path))
+    return out, lens, feed, list(gen_a), emitted, path, path_len, on_path
+
+
+def kv_compact(L, shape, runs, path, path_len, lens, k_cache, v_cache, page_table, kv):
+    sh = shape.c()
+    runs_a = (L.RunIn * len(runs))(*runs)
+    lib().orc_kv_compact(C.byref(sh), runs_a, u32(len(runs)), ptr(path), ptr(path_len), ptr(lens), ptr(k_cache),
+                         ptr(v_cache), ptr(page_table), C.byref(kv))
+
+
+def replay_draft(L, runs, lens, feed, trace, trace_len, ra, tree):
+    runs_a = (L.RunIn * len(runs))(*runs)
+    lib().orc_replay_draft(runs_a, u32(len(runs)), ptr(lens), ptr(feed), ptr(trace), ptr(trace_len), C.byref(ra),
+                           ptr(tree))
+
+
+def embed(L, shape, table, tokens, tin, lens, feed, tree, vis):
+    sh = shape.c()
+    n = len(tokens)
+    tokens = np.array(tokens, np.uint32)
+    out = np.zeros((n, shape.hidden), np.float32)
+    meta = np.zeros((n, 2), np.uint32)
+    vis = np.array(vis, np.uint32)
+    lib().orc_embed(C.byref(sh), ptr(table), ptr(tokens), ptr(out), ptr(np.ascontiguousarray(tin, np.uint32)),
+                    ptr(meta), ptr(np.ascontiguousarray(lens, np.uint32)), ptr(np.ascontiguousarray(feed, np.uint32)),
+                    ptr(np.ascontiguousarray(tree, np.uint32)), ptr(vis), u32(n))
+    return tokens, out, meta, vis
+
+
+class Pool:
+    """kv.rs page pool (LIFO free list)."""
+
+    class _S(C.Structure):
+        _fields_ = [("free_list", vp), ("n_free", u32), ("n_pages", u32), ("max_pages", u32), ("page_shift", u32),
+                    ("page_table", vp), ("seq_pages", vp)]
+
+    def __init__(self, n_pages: int, max_seqs: int, max_pages: int, page_shift: int):
+        self.free = np.zeros(n_pages, np.uint32)
+        self.table = np.zeros((max_seqs, max_pages), np.uint32)
+        self.held = np.zeros(max_seqs, np.uint32)
+        self.s = Pool._S()
+        lib().orc_pool_init(C.byref(self.s), u32(n_pages), u32(max_seqs), u32(max_pages), u32(page_shift),
+                            ptr(self.free), ptr(self.table), ptr(self.held))
+
+    def reserve(self, slot: int, length: int) -> bool:
+        return lib().orc_pool_reserve(C.byref(self.s), u32(slot), u32(length)) == 0
+
+    def release(self, slot: int) -> None:
+        lib().orc_pool_release(C.byref(self.s), u32(slot))
+
+    def pages(self, slot: int) -> list[int]:
+        return [int(x) for x in self.table[slot, : self.held[slot]]]
+
+
+class StepIO(C.Structure):
+    _fields_ = [("n", u32), ("n_head", u32), ("n_runs", u32), ("tokens", vp), ("tin", vp), ("vis", vp),
+                ("head_rows", vp), ("samples", vp), ("runs", vp), ("attn_runs", vp), ("compact", u32),
+                ("lens", vp), ("feed", vp), ("tree", vp), ("gen", vp), ("k_cache", vp), ("v_cache", vp),
+                ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
+                ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp)]
+
+
+def _chain(row: int) -> int:
+    return row | ((0xFF if row == 0 else row - 1) << 8) | (((2 << row) - 1) << 16)
+
+
+class OracleEngine:
+    """The engine on host memory: page pool, sequence state, plan and step (orc_plan, orc_step).
+
+    `weights`: per layer a dict name -> (w, scales) numpy (int8 + uint16 [m][1], or bf16 bits as
+    uint16 [m][k] with scales None); `embed` uint16 [vocab][hidden]; `scalars` per layer
+    (qkv_scale, o_scale, resid_attn, post_attn, resid_mlp, post_mlp, rope).
+    """
+
+    def __init__(self, L, shape, embed, weights, scalars, *, max_seqs=8, max_seq_len=8192, kv_tokens=None,
+                 page_shift=4, attn_scale=0.125, freq=None):
+        self.L, self.shape = L, shape
+        self.page_shift = page_shift
+        page = 1 << page_shift
+        kv_tokens = kv_tokens if kv_tokens is not None else max_seqs * max_seq_len
+        self.n_pages = -(-kv_tokens // page)
+        self.max_pages = -(-max_seq_len // page)
+        self.max_seqs, self.max_seq_len = max_seqs, max_seq_len
+        s = shape
+        self.k = np.zeros((s.n_layers, self.n_pages, s.n_kv_heads, page, s.head_dim), np.uint16)
+        self.v = np.zeros_like(self.k)
+        self.pool = Pool(self.n_pages, max_seqs, self.max_pages, page_shift)
+        self.lens = np.zeros(max_seqs, np.uint32)
+        self.feed = np.zeros(max_seqs * 16, np.uint32)
+        self.tree = np.array([_chain(i % 16) for i in range(max_seqs * 16)], np.uint32)
+        self.gen = (L.GenState * max_seqs)()
+        for g in self.gen:
+            g.remaining = 0xFFFFFFFF
+        self.seq_len = [0] * max_seqs
+        self.used = [False] * max_seqs
+        self.sampling = [L.SampleRow(0, 0, 0, 0.0, 1.0, 0xFFFFFFFF) for _ in range(max_seqs)]
+        self.attn_scale = attn_scale
+        self.rope = rope_table(freq, max_seq_len + 16)
+        self.embed = np.ascontiguousarray(embed, np.uint16)
+        self._keep = []
+        layers = (L.Layer * s.n_layers)()
+        for i, (lay, sc) in enumerate(zip(weights, scalars)):
+            mats = []
+            for name in ("qkv", "o", "gate_up", "down"):
+                w, scl = lay[name]
+                w = np.ascontiguousarray(w)
+                self._keep.append(w)
+                if scl is not None:
+                    scl = np.ascontiguousarray(scl, np.uint16)
+                    self._keep.append(scl)
+                m, k = w.shape
+                mats.append(L.Matrix(w.ctypes.data, scl.ctypes.data if scl is not None else None, m, k,
+                                     1 if w.dtype == np.int8 else 0, 31 if scl is not None else 0))
+            layers[i] = L.Layer(*mats, *sc[:6], int(sc[6]), 0)
+        self.layers = layers
+
+    # sequences
+    def new_seq(self) -> int:
+        slot = self.used.index(False)
+        self.used[slot] = True
+        self.seq_len[slot] = 0
+        self.lens[slot] = 0
+        g = self.gen[slot]
+        g.remaining, g.done, g.nstop = 0xFFFFFFFF, 0, 0
+        return slot
+
+    def set_sampling(self, slot, temperature=0.0, top_p=1.0, seed=0):
+        self.sampling[slot] = self.L.SampleRow(seed & 0xFFFFFFFF, seed >> 32, 0, temperature, top_p, 0xFFFFFFFF)
+
+    def set_gen(self, slot, remaining=0xFFFFFFFF, stop=(), done=0):
+        g = self.gen[slot]
+        g.remaining, g.done, g.nstop = remaining, done, len(stop)
+        for i, t in enumerate(stop):
+            g.stop[i] = t
+
+    def set_feed(self, slot, length, token):
+        assert self.pool.reserve(slot, length)
+        self.seq_len[slot] = length
+        self.lens[slot] = length
+        self.feed[slot * 16] = token
+
+    def bench_fill(self, slot, n):
+        self.seq_len[slot] += n
+        assert self.pool.reserve(slot, self.seq_len[slot])
+        self.lens[slot] = self.seq_len[slot]
+
+    def step(self, runs, compact=None, want_hidden=False):
+        """runs: (slot, tokens, verify[, head]). Returns (ids, logits, emitted, extra)."""
+        L = self.L
+        n_runs = len(runs)
+        in_runs = np.zeros((n_runs, 4), np.uint32)
+        toks = []
+        for i, r in enumerate(runs):
+            in_runs[i] = (r[0], len(r[1]), 1 if r[2] else 0, r[3] if len(r) > 3 else 1)
+            toks += [int(t) for t in r[1]]
+        n = len(toks)
+        for r in runs:
+            assert self.pool.reserve(r[0], self.seq_len[r[0]] + len(r[1]))
+        in_tokens = np.array(toks, np.uint32)
+        tokens = np.zeros(n, np.uint32)
+        tin = np.zeros(2 * n, np.uint32)
+        vis = np.zeros(n, np.uint32)
+        head_rows = np.zeros(n, np.uint32)
+        samples = (L.SampleRow * max(1, n))()
+        run_in = (L.RunIn * n_runs)()
+        seq_len = np.array(self.seq_len, np.uint32)
+        samp = (L.SampleRow * self.max_seqs)(*self.sampling)
+        n_head = lib().orc_plan(ptr(in_runs), u32(n_runs), ptr(in_tokens), ptr(seq_len), samp, ptr(tokens), ptr(tin),
+                                ptr(vis), ptr(head_rows), samples, run_in)
+        assert n_head >= 0, "plan rejected"
+        attn_runs = np.array([[ri.first, ri.count] for ri in run_in], np.uint32).reshape(-1)
+        branches = any(r[2] and len(r[1]) > 2 for r in runs)
+        meta = np.zeros(2 * n, np.uint32)
+        logits = np.zeros((max(1, n_head), self.shape.vocab), np.float32)
+        out = np.zeros(max(1, n_head), np.uint32)
+        emitted = np.zeros(n_runs, np.uint32)
+        path = np.zeros(n_runs * 16, np.uint32)
+        path_len = np.zeros(n_runs, np.uint32)
+        on_path = np.zeros(n, np.uint32)
+        hidden = np.zeros((n, self.shape.hidden), np.float32) if want_hidden else None
+        io = StepIO()
+        io.n, io.n_head, io.n_runs = n, n_head, n_runs
+        io.tokens, io.tin, io.vis, io.head_rows = ptr(tokens), ptr(tin), ptr(vis), ptr(head_rows)
+        io.samples = C.cast(samples, vp)
+        io.runs = C.cast(run_in, vp)
+        io.attn_runs = ptr(attn_runs)
+        io.compact = int(branches if compact is None else compact)
+        io.lens, io.feed, io.tree = ptr(self.lens), ptr(self.feed), ptr(self.tree)
+        io.gen = C.cast(self.gen, vp)
+        io.k_cache, io.v_cache, io.page_table = ptr(self.k), ptr(self.v), ptr(self.pool.table)
+        io.kv[:] = [1, 0, 0, self.max_seqs, self.page_shift, self.n_pages, self.max_pages, 0]
+        io.rope = ptr(self.rope)
+        io.meta, io.logits, io.out = ptr(meta), ptr(logits), ptr(out)
+        io.emitted, io.path, io.path_len, io.on_path = ptr(emitted), ptr(path), ptr(path_len), ptr(on_path)
+        io.hidden = ptr(hidden)
+        sh = self.shape.c()
+        rc = lib().orc_step(C.byref(sh), ptr(self.embed), self.layers, f32(self.attn_scale), C.byref(io))
+        assert rc == 0
+        for i, r in enumerate(runs):
+            self.seq_len[r[0]] += len(r[1])
+            if r[2]:
+                self.seq_len[r[0]] -= len(r[1]) - min(int(emitted[i]), len(r[1]))
+        extra = dict(tokens=tokens, meta=meta.reshape(n, 2), vis=vis, path=path.reshape(n_runs, 16),
+                     path_len=path_len, on_path=on_path, hidden=hidden, head_rows=head_rows[:n_head])
+        return out[:n_head].copy(), logits[:n_head].copy(), emitted, extra
+
+
+def host_weights(model) -> tuple[np.ndarray, list, list]:
+    """(embed, per-layer weights, per-layer scalars) of a violetto SyntheticModel as numpy."""
+    import torch
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    embed = bits(model.embed)
+    layers = []
+    for lay in model.layers:
+        d = {}
+        for name, (w, s) in lay.items():
+            if s is None:
+                d[name] = (bits(w), None)
+            else:
+                d[name] = (w.detach().cpu().numpy(), bits(s))
+        layers.append(d)
+    scal = [(s.qkv_scale, s.o_scale, s.resid_attn, s.post_attn, s.resid_mlp, s.post_mlp, s.rope)
+            for s in model.scalars]
+    return embed, layers, scal

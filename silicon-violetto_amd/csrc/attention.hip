@@ -1,0 +1,451 @@
+// attention.hip — fused verify attention over the paged KV cache (the reference's
+// attn_verify + attn_dec_reduce, engine/src/kernels.metal:891-1148 and :1316-1362, encoded by
+// encode.rs:233-297).
+//
+// One workgroup (4 waves) per (key split s, kv head g, run r):
+//   - Columns are the run's T tokens x G query heads of kv head g (column c: token c / G,
+//     head g G + c % G), in NCT tiles of 16. Each lane builds its columns' queries in
+//     registers: rms-norm over the head (no gain), RoPE on pairs (2j, 2j+1), j < 32, times
+//     softmax scale * log2 e, split into bf16 hi + lo MFMA operands.
+//   - Splits 0..nsplit-2 own `split` cached keys each; the last split owns the run's new
+//     keys: it norms and ropes them, rounds K and V to bf16, writes them to the cache at
+//     p0 + row and keeps them in LDS.
+//   - Keys go in batches of 32 (wave w takes batches w, w + 4, ...): S^T = K Q^T on
+//     v_mfma_f32_16x16x32_bf16 (two 16-key tiles, hi and lo), p = 2^s for visible keys (no
+//     running max: q and k are rms-normed, so scores are bounded, kernels.metal:804-806),
+//     then O^T += V^T P^T with P (hi, lo) taken straight from the S^T accumulators' layout.
+//     K rows are read as 16-byte slices; each V row is read whole by 16 lanes (8 bytes per
+//     lane for D = 64), and the matrix-core operand takes one of its dims per tile.
+//   - The 4 waves' (l, o) meet in LDS; the split's partial goes to the workspace; the last
+//     split to arrive (agent-scope counter per (run, kv head)) sums the partials in split
+//     order and writes o / l.
+#include "sv_device.h"
+#include "sv_internal.h"
+
+namespace sv {
+
+struct AttnParams {
+  const float* qkv;
+  const uint32_t* meta;
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint32_t* page_table;
+  const float* rope;
+  const uint32_t* runs;
+  const uint32_t* vis;
+  float* out;
+  float* part_o;
+  float* part_l;
+  uint32_t* counters;
+  uint32_t NQ, NKV, G, W, KOFF, VOFF;
+  uint32_t split, max_splits;
+  float scale_log2;
+  uint32_t rope_on;
+  uint32_t page_shift, n_pages, max_pages, layer, maxcols;
+};
+
+// Element offset of kv head g's row at cache position pos (kernels.metal:704-711, global).
+template <int D>
+__device__ __forceinline__ size_t kv_off(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t pos) {
+  const uint32_t page = p.page_table[(size_t)seq * p.max_pages + (pos >> p.page_shift)];
+  return ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
+         (size_t)(pos & ((1u << p.page_shift) - 1u)) * D;
+}
+
+template <int VE>
+struct VWord;
+template <>
+struct VWord<4> {
+  typedef u32x2 type;
+};
+template <>
+struct VWord<8> {
+  typedef u32x4 type;
+};
+
+// One batch of 32 keys [kb, kb + 32) below kend, for this wave: scores, p, and O += V P.
+// NEW: the keys are the run's new ones, in LDS (index key - p0), masked by each column's vis.
+template <int D, int NCT, bool NEW>
+__device__ __forceinline__ void key_batch(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t kb, uint32_t kend,
+                                          uint32_t p0, uint32_t ncols, uint32_t t0, const uint16_t* nk,
+                                          const uint16_t* nv, const bf16x8 (&qh)[NCT][D / 32],
+                                          const bf16x8 (&ql)[NCT][D / 32], f32x4 (&O)[D / 16][NCT],
+                                          float (&lsum)[NCT], int lane) {
+  constexpr int KST = D / 32, VE = D / 16;
+  typedef typename VWord<VE>::type vword;
+  const int c16 = lane & 15, q = lane >> 4;
+  // Row pointers of the two 16-key tiles (a tile never straddles a page: pages hold >= 16).
+  const uint16_t* kt[2];
+  const uint16_t* vt[2];
+  uint32_t tfirst[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+    const uint32_t first = min(kb + 16 * mt, kend - 1);
+    tfirst[mt] = first;
+    if (NEW) {
+      kt[mt] = nk + (size_t)(first - p0) * D;
+      vt[mt] = nv + (size_t)(first - p0) * D;
+    } else {
+      const size_t off = kv_off<D>(p, seq, g, first);
+      kt[mt] = p.kc + off;
+      vt[mt] = p.vc + off;
+    }
+  }
+  // K: lane (c16, q) reads key kb + 16 mt + c16, dims 32 ks + 8 q .. + 7.
+  u32x4 kw[2][KST];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+    const uint32_t key = min(kb + 16 * mt + c16, kend - 1);
+    const uint16_t* kr = kt[mt] + (size_t)(key - tfirst[mt]) * D;
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) kw[mt][ks] = *(const u32x4*)(kr + 32 * ks + 8 * q);
+  }
+  // V: slot j is key kb + 16 (j / 4) + 4 q + j % 4; lane reads its dims VE c16 .. + VE-1.
+  vword vw[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const int mt = j >> 2;
+    const uint32_t key = min(kb + 16 * mt + 4 * q + (j & 3), kend - 1);
+    vw[j] = *(const vword*)(vt[mt] + (size_t)(key - tfirst[mt]) * D + VE * c16);
+  }
+  // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
+  f32x4 S[2][NCT];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const bf16x8 kk = __builtin_bit_cast(bf16x8, kw[mt][ks]);
+        a = mfma16(kk, qh[ct][ks], a);
+        a = mfma16(kk, ql[ct][ks], a);
+      }
+      S[mt][ct] = a;
+    }
+  bf16x8 ph[NCT], pl[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const uint32_t c = 16 * ct + c16;
+    const bool col_ok = c < ncols;
+    uint32_t vbits = 0;
+    if (NEW && col_ok) vbits = p.vis[t0 + c / p.G];
+    float pv[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t key = kb + 16 * mt + 4 * q + i;
+        bool ok = col_ok && key < kend;
+        if (NEW) ok = ok && ((vbits >> (key - p0)) & 1u);
+        const float e = ok ? exp2f(S[mt][ct][i]) : 0.0f;
+        pv[4 * mt + i] = e;
+        lsum[ct] += e;
+      }
+    split8(pv, ph[ct], pl[ct]);
+  }
+  // O^T[dt] (rows: dims VE (4 q + i) + dt) += V^T[dt] P^T.
+#pragma unroll
+  for (int dt = 0; dt < VE; dt++) {
+    u32x4 a;
+    const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) a[jj] = __builtin_amdgcn_perm(vw[2 * jj + 1][dt >> 1], vw[2 * jj][dt >> 1], sel);
+    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      O[dt][ct] = mfma16(av, ph[ct], O[dt][ct]);
+      O[dt][ct] = mfma16(av, pl[ct], O[dt][ct]);
+    }
+  }
+}
+
+template <int D, int NCT>
+__global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
+  constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
+  extern __shared__ float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
+  __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
+  __shared__ uint32_t flag;
+  float* ored = lds;
+  float* lred = lds + 4 * COLS * D;
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c16 = lane & 15, q = lane >> 4;
+  const uint32_t s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  const uint32_t t0 = p.runs[2 * r], T = p.runs[2 * r + 1];
+  const uint32_t seq = p.meta[2 * t0], p0 = p.meta[2 * t0 + 1];
+  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
+  const uint32_t ncols = T * p.G;
+  if (nsplit > p.max_splits) {
+    // The grid has too few splits for this run's context: its output is NaN (never a
+    // partial sum) and the counter is left alone.
+    if (s == 0)
+      for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+        const uint32_t col = idx / D, i = col / p.G, h = g * p.G + col % p.G;
+        p.out[(size_t)(t0 + i) * p.NQ * D + h * D + idx % D] = __builtin_nanf("");
+      }
+    return;
+  }
+  if (s >= nsplit) return;
+  const bool newest = s == nsplit - 1;
+
+  // Queries (kernels.metal:1022-1039 with norm_rope :727-736): k slot j of step ks is dim
+  // 32 ks + 8 q + j.
+  bf16x8 qh[NCT][KST], ql[NCT][KST];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const uint32_t c = 16 * ct + c16;
+    const bool ok = c < ncols;
+    float v[KST][8];
+    uint32_t pos = 0;
+    float ss = 0.0f;
+    if (ok) {
+      const uint32_t i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
+      pos = p.meta[2 * t + 1];
+      const float* qp = p.qkv + (size_t)t * p.W + h * D + 8 * q;
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const f32x4 a = *(const f32x4*)(qp + 32 * ks), b = *(const f32x4*)(qp + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[ks][e] = a[e];
+          v[ks][4 + e] = b[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) v[ks][e] = 0.0f;
+    }
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[ks][e], v[ks][e], ss);
+    ss += __shfl_xor(ss, 16, WAVE);
+    ss += __shfl_xor(ss, 32, WAVE);
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[ks][e] *= inv;
+      if (p.rope_on && ok && 32 * ks + 8 * q < 64) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const uint32_t j = 16 * ks + 4 * q + jj;
+          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + j) * 2);
+          const float a0 = v[ks][2 * jj], a1 = v[ks][2 * jj + 1];
+          v[ks][2 * jj] = cs.x * a0 + cs.y * a1;
+          v[ks][2 * jj + 1] = cs.x * a1 - cs.y * a0;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[ks][e] *= p.scale_log2;
+      split8(v[ks], qh[ct][ks], ql[ct][ks]);
+    }
+  }
+
+  // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
+  // p0 + row and to LDS.
+  if (newest) {
+    constexpr int DE = D / 64;  // dims per lane
+    for (uint32_t i = wv; i < T; i += 4) {
+      const uint32_t t = t0 + i, pos = p.meta[2 * t + 1];
+      const float* kp = p.qkv + (size_t)t * p.W + p.KOFF + g * D;
+      const float* vp = p.qkv + (size_t)t * p.W + p.VOFF + g * D;
+      float kv[DE];
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < DE; e++) {
+        kv[e] = kp[lane + 64 * e];
+        ss = __builtin_fmaf(kv[e], kv[e], ss);
+      }
+      ss = wave_sum(ss);
+      const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
+      const size_t row = kv_off<D>(p, seq, g, p0 + i);
+#pragma unroll
+      for (int e = 0; e < DE; e++) {
+        const uint32_t d = lane + 64 * e;
+        float k = kv[e] * inv;
+        const float other = __shfl_xor(k, 1, WAVE);
+        if (p.rope_on && d < 64) {
+          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
+          k = (d & 1) ? cs.x * k - cs.y * other : cs.x * k + cs.y * other;
+        }
+        const uint16_t kb16 = (uint16_t)to_bf(k), vb16 = (uint16_t)to_bf(vp[d]);
+        p.kc[row + d] = kb16;
+        p.vc[row + d] = vb16;
+        nk[i * D + d] = kb16;
+        nv[i * D + d] = vb16;
+      }
+    }
+  }
+  __syncthreads();
+
+  f32x4 O[VE][NCT];
+  float lsum[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    lsum[ct] = 0.0f;
+#pragma unroll
+    for (int dt = 0; dt < VE; dt++) O[dt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (newest) {
+    if (wv == 0) key_batch<D, NCT, true>(p, seq, g, p0, p0 + T, p0, ncols, t0, nk, nv, qh, ql, O, lsum, lane);
+  } else {
+    const uint32_t kbeg = s * p.split, kend = min(kbeg + p.split, p0);
+    const uint32_t nb = (kend - kbeg + 31) / 32;
+    for (uint32_t b = wv; b < nb; b += 4)
+      key_batch<D, NCT, false>(p, seq, g, kbeg + 32 * b, kend, p0, ncols, t0, nk, nv, qh, ql, O, lsum, lane);
+  }
+
+  // This wave's (l, o) to LDS: lane holds column 16 ct + c16, dims VE (4 q + i) + dt.
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    float l = lsum[ct];
+    l += __shfl_xor(l, 16, WAVE);
+    l += __shfl_xor(l, 32, WAVE);
+    const uint32_t col = 16 * ct + c16;
+    float* od = ored + ((size_t)wv * COLS + col) * D;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int dt = 0; dt < VE; dt++) od[VE * (4 * q + i) + dt] = O[dt][ct][i];
+    if (q == 0) lred[wv * COLS + col] = l;
+  }
+  __syncthreads();
+  const size_t rec = ((size_t)r * p.NKV + g) * p.max_splits + s;
+  float* po = p.part_o + rec * p.maxcols * D;
+  float* pl = p.part_l + rec * p.maxcols;
+  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+    const uint32_t col = idx / D, d = idx % D;
+    po[idx] = ((ored[col * D + d] + ored[(COLS + col) * D + d]) + ored[(2 * COLS + col) * D + d]) +
+              ored[(3 * COLS + col) * D + d];
+  }
+  for (uint32_t idx = tid; idx < ncols; idx += 256)
+    pl[idx] = ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx];
+
+  // The last split of (run, head) merges all (attn_dec_reduce, kernels.metal:1332-1362).
+  if (!arrive_last(&p.counters[r * p.NKV + g], nsplit, &flag)) return;
+  const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
+  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+    const uint32_t col = idx / D, d = idx % D;
+    float o = 0.0f, l = 0.0f;
+    for (uint32_t sp = 0; sp < nsplit; sp++) {
+      o += p.part_o[(rec0 + sp) * p.maxcols * D + idx];
+      l += p.part_l[(rec0 + sp) * p.maxcols + col];
+    }
+    const uint32_t i = col / p.G, h = g * p.G + col % p.G;
+    p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = o / l;
+  }
+}
+
+// Dynamic LDS of up to 4 x 64 x 128 floats (+ l): allow it once per instantiation, outside
+// any graph capture (sv_engine_create calls this; attn_launch does on its first use).
+void attn_init() {
+  static bool done = false;
+  if (done) return;
+  done = true;
+#define SV_ATTR(DD, N)                                                                                       \
+  (void)hipFuncSetAttribute((const void*)attn_verify_kernel<DD, N>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                            (int)((size_t)4 * 16 * N * DD * 4 + (size_t)4 * 16 * N * 4))
+  SV_ATTR(64, 1);
+  SV_ATTR(64, 2);
+  SV_ATTR(64, 3);
+  SV_ATTR(64, 4);
+  SV_ATTR(128, 1);
+  SV_ATTR(128, 2);
+  SV_ATTR(128, 3);
+  SV_ATTR(128, 4);
+#undef SV_ATTR
+}
+
+static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
+  const uint32_t cols = max_run * (sh->n_heads / sh->n_kv_heads);
+  return (cols + 15) / 16 * 16;
+}
+
+size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run) {
+  const size_t maxcols = cols_pad(sh, max_run);
+  size_t b = WS_COUNTER_BYTES;
+  b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * sh->head_dim * 4;
+  b = (b + 255) / 256 * 256;
+  b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * 4;
+  return b;
+}
+
+sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
+                      uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
+                      const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
+                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes) {
+  if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
+    return fail(SV_ERR_ARG, "attn_verify: null pointer");
+  if (n_runs == 0) return SV_OK;
+  const uint32_t D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads;
+  if (D != 64 && D != 128) return fail(SV_ERR_UNSUPPORTED, "attn_verify: head_dim %u (64 or 128 are built)", D);
+  if (NKV == 0 || NQ % NKV) return fail(SV_ERR_ARG, "attn_verify: %u heads over %u kv heads", NQ, NKV);
+  if (!kv->is_global) return fail(SV_ERR_UNSUPPORTED, "attn_verify: local (ring) layers are not built");
+  if (kv->page_shift < 4 || kv->page_shift > 16)
+    return fail(SV_ERR_UNSUPPORTED, "attn_verify: pages of 2^%u tokens (16..65536 are built)", kv->page_shift);
+  if (args->split == 0 || args->split % 32) return fail(SV_ERR_ARG, "attn_verify: split %u (multiple of 32)", args->split);
+  if (max_run == 0 || max_run > SV_MAX_RUN) return fail(SV_ERR_ARG, "attn_verify: max_run %u", max_run);
+  if (!rope && args->rope) return fail(SV_ERR_ARG, "attn_verify: rope table missing");
+  const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;
+  if (nct > 4) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (64 are built)", max_run * NQ / NKV);
+  const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
+  if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
+  AttnParams p;
+  p.qkv = qkv;
+  p.meta = meta;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.page_table = page_table;
+  p.rope = rope;
+  p.runs = runs;
+  p.vis = vis;
+  p.out = out;
+  if ((size_t)n_runs * NKV * 4 > WS_COUNTER_BYTES) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u runs", n_runs);
+  p.counters = (uint32_t*)ws;
+  size_t off = WS_COUNTER_BYTES;
+  p.part_o = (float*)((char*)ws + off);
+  off += (size_t)n_runs * NKV * args->max_splits * maxcols * D * 4;
+  off = (off + 255) / 256 * 256;
+  p.part_l = (float*)((char*)ws + off);
+  p.NQ = NQ;
+  p.NKV = NKV;
+  p.G = NQ / NKV;
+  p.W = (NQ + 2 * NKV) * D;
+  p.KOFF = NQ * D;
+  p.VOFF = (NQ + NKV) * D;
+  p.split = args->split;
+  p.max_splits = args->max_splits;
+  p.scale_log2 = args->scale_log2;
+  p.rope_on = args->rope;
+  p.page_shift = kv->page_shift;
+  p.n_pages = kv->n_pages;
+  p.max_pages = kv->max_pages;
+  p.layer = kv->kv_layer;
+  p.maxcols = maxcols;
+  attn_init();
+  dim3 grid(args->max_splits, NKV, n_runs);
+  const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
+#define SV_ATTN(DD, N) hipLaunchKernelGGL((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
+  if (D == 64) {
+    switch (nct) {
+      case 1: SV_ATTN(64, 1); break;
+      case 2: SV_ATTN(64, 2); break;
+      case 3: SV_ATTN(64, 3); break;
+      default: SV_ATTN(64, 4); break;
+    }
+  } else {
+    switch (nct) {
+      case 1: SV_ATTN(128, 1); break;
+      case 2: SV_ATTN(128, 2); break;
+      case 3: SV_ATTN(128, 3); break;
+      default: SV_ATTN(128, 4); break;
+    }
+  }
+#undef SV_ATTN
+  return check_launch("attn_verify");
+}
+
+}  // namespace sv

@@ -1,0 +1,867 @@
+// engine.cpp — the host side of libsv_verify: the C ABI of include/sv_verify.h.
+//
+// Kernel-level calls wrap the launchers. The engine mirrors the reference's Engine
+// (engine/src/engine.rs), its planner (engine/src/engine/plan.rs), page pool (kv.rs),
+// buffers (buffers.rs) and encoder (encode.rs): it owns the KV cache and the GPU-resident
+// sequence state, lays out a step, encodes it on its HIP stream (or captures it once into a
+// HIP graph and replays it), and reads back what a synchronous step returns.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "sv_internal.h"
+
+namespace sv {
+
+static thread_local std::string g_error;
+
+sv_status fail(sv_status code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+sv_status check_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return SV_OK;
+  return fail(SV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+sv_status check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
+
+}  // namespace sv
+
+using namespace sv;
+
+#define SV_TRY(x)                  \
+  do {                             \
+    const sv_status st_ = (x);     \
+    if (st_ != SV_OK) return st_;  \
+  } while (0)
+#define SV_HIP(x, what) SV_TRY(check_hip((x), (what)))
+
+extern "C" const char* sv_last_error(void) { return g_error.c_str(); }
+
+// ---------------------------------------------------------------- kernel level
+
+extern "C" sv_status sv_embed(void* stream, const sv_shape* shape, const uint16_t* d_table, uint32_t* d_tokens,
+                              float* d_out, const uint32_t* d_tin, uint32_t* d_meta, const uint32_t* d_lens,
+                              const uint32_t* d_feed, const uint32_t* d_tree, uint32_t* d_vis, uint32_t n) {
+  return embed_launch((hipStream_t)stream, shape, d_table, d_tokens, d_out, d_tin, d_meta, d_lens, d_feed, d_tree,
+                      d_vis, n);
+}
+
+extern "C" sv_status sv_rmsnorm_rows(void* stream, const float* d_in, const uint32_t* d_rows, float* d_out, uint32_t n,
+                                     uint32_t hidden) {
+  if (hidden == 0) return fail(SV_ERR_ARG, "rmsnorm_rows: hidden 0");
+  return rmsnorm_rows_launch((hipStream_t)stream, d_in, d_rows, d_out, n, hidden);
+}
+
+extern "C" size_t sv_matmul_workspace_bytes(uint32_t n, uint32_t m, uint32_t k) { return matmul_ws_bytes(n, m, k); }
+
+extern "C" sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_x, const uint32_t* d_x_rows,
+                               float* d_y, const float* d_base, float* d_aux, const sv_mat_args* a, void* d_workspace,
+                               size_t workspace_bytes) {
+  return matmul_launch((hipStream_t)stream, w, d_x, d_x_rows, d_y, d_base, d_aux, a, d_workspace, workspace_bytes);
+}
+
+extern "C" size_t sv_attn_workspace_bytes(const sv_shape* shape, uint32_t n_runs, uint32_t max_splits,
+                                          uint32_t max_run) {
+  if (!shape) return 0;
+  return attn_ws_bytes(shape, n_runs, max_splits, max_run);
+}
+
+extern "C" sv_status sv_attn_verify(void* stream, const sv_shape* shape, const float* d_qkv, const uint32_t* d_meta,
+                                    uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
+                                    const float* d_rope, const sv_kv_args* kv, const sv_attn_args* args,
+                                    const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
+                                    float* d_out, void* d_workspace, size_t workspace_bytes) {
+  return attn_launch((hipStream_t)stream, shape, d_qkv, d_meta, d_k_cache, d_v_cache, d_page_table, d_rope, kv, args,
+                     d_runs, n_runs, max_run, d_vis, d_out, d_workspace, workspace_bytes);
+}
+
+extern "C" sv_status sv_sample(void* stream, const float* d_logits, const sv_sample_row* d_rows, uint32_t* d_out,
+                               const uint32_t* d_meta, uint32_t n_rows, uint32_t vocab) {
+  return sample_launch((hipStream_t)stream, d_logits, d_rows, d_out, d_meta, n_rows, vocab);
+}
+
+extern "C" sv_status sv_accept(void* stream, const sv_run_in* d_runs, const uint32_t* d_tokens, uint32_t* d_out,
+                               uint32_t* d_lens, uint32_t* d_feed, sv_gen_state* d_gen, uint32_t* d_emitted,
+                               uint32_t nruns, const uint32_t* d_tree, uint32_t* d_path, uint32_t* d_path_len,
+                               uint32_t* d_on_path) {
+  return accept_launch((hipStream_t)stream, d_runs, d_tokens, d_out, d_lens, d_feed, d_gen, d_emitted, nruns, d_tree,
+                       d_path, d_path_len, d_on_path);
+}
+
+extern "C" sv_status sv_kv_compact(void* stream, const sv_shape* shape, const sv_run_in* d_runs, uint32_t nruns,
+                                   const uint32_t* d_path, const uint32_t* d_path_len, const uint32_t* d_lens,
+                                   uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
+                                   const sv_kv_args* kv) {
+  return kv_compact_launch((hipStream_t)stream, shape, d_runs, nruns, d_path, d_path_len, d_lens, d_k_cache, d_v_cache,
+                           d_page_table, kv);
+}
+
+extern "C" sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,
+                                     uint32_t* d_feed, const uint32_t* d_trace, const uint32_t* d_trace_len,
+                                     const sv_replay_args* ra, uint32_t* d_tree) {
+  return replay_launch((hipStream_t)stream, d_runs, nruns, d_lens, d_feed, d_trace, d_trace_len, ra, d_tree);
+}
+
+// ---------------------------------------------------------------- the engine
+
+namespace {
+
+// Threadgroups the attention splits aim for per layer (reference: DEC_TGS_PER_CORE x cores,
+// engine.rs:25); MI355X has 256 CUs.
+constexpr uint32_t ATTN_TARGET_WGS = 1024;
+constexpr uint32_t MIN_SPLIT = 128;
+
+struct Plan {
+  uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
+  std::vector<uint32_t> slots;   // per run
+  std::vector<uint32_t> counts;  // per run
+  std::vector<uint32_t> verify;  // per run
+};
+
+template <typename T>
+sv_status dalloc(T** p, size_t count, const char* what) {
+  *p = nullptr;
+  if (count == 0) count = 1;
+  SV_HIP(hipMalloc((void**)p, count * sizeof(T)), what);
+  SV_HIP(hipMemset(*p, 0, count * sizeof(T)), what);
+  return SV_OK;
+}
+
+}  // namespace
+
+struct sv_engine {
+  sv_engine_config cfg{};
+  sv_shape sh{};
+  hipStream_t stream = nullptr;
+  const uint16_t* embed = nullptr;
+  std::vector<sv_layer> layers;
+  std::vector<bool> layer_set;
+  uint32_t n_pages = 0, max_pages = 0, qkv_w = 0;
+
+  // device: KV and sequence state
+  uint16_t* k_cache = nullptr;
+  uint16_t* v_cache = nullptr;
+  size_t kv_elems = 0;
+  uint32_t* page_table = nullptr;
+  float* rope = nullptr;
+  uint32_t *lens = nullptr, *feed = nullptr, *tree = nullptr, *trace = nullptr, *trace_len = nullptr;
+  sv_gen_state* gen = nullptr;
+  // device: one step set (plan.rs writes these per step)
+  uint32_t *tokens = nullptr, *tin = nullptr, *vis = nullptr, *head_rows = nullptr, *attn_runs = nullptr;
+  sv_sample_row* sample_rows = nullptr;
+  sv_run_in* runs = nullptr;
+  uint32_t *out_ids = nullptr, *emitted = nullptr, *meta = nullptr, *path = nullptr, *path_len = nullptr,
+           *on_path = nullptr;
+  // device: activations (buffers.rs Scratch)
+  float *h = nullptr, *qkv = nullptr, *attn = nullptr, *mixed = nullptr, *act = nullptr, *inv = nullptr,
+        *logits = nullptr;
+  void* ws = nullptr;
+  size_t ws_bytes = 0;
+
+  // host: page pool (kv.rs) and sequences (engine.rs Seq)
+  std::vector<uint32_t> free_pages;
+  std::vector<std::vector<uint32_t>> pages;
+  std::vector<uint32_t> seq_len;
+  std::vector<bool> used;
+  std::vector<sv_sample_row> sampling;
+
+  Plan plan;
+  bool planned = false;
+  // sv_profile_step: an event pair around every kernel while `prof` is set.
+  bool prof = false;
+  std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_events;
+
+  sv_status mark_begin(hipEvent_t* ev) {
+    if (!prof) return SV_OK;
+    SV_HIP(hipEventCreate(ev), "event");
+    SV_HIP(hipEventRecord(*ev, stream), "event record");
+    return SV_OK;
+  }
+  sv_status mark_end(int kind, hipEvent_t begin) {
+    if (!prof) return SV_OK;
+    hipEvent_t end;
+    SV_HIP(hipEventCreate(&end), "event");
+    SV_HIP(hipEventRecord(end, stream), "event record");
+    prof_events.push_back({kind, {begin, end}});
+    return SV_OK;
+  }
+#define SV_TIMED(kind, call)          \
+  do {                               \
+    hipEvent_t ev_ = nullptr;        \
+    SV_TRY(mark_begin(&ev_));        \
+    SV_TRY(call);                    \
+    SV_TRY(mark_end((kind), ev_));   \
+  } while (0)
+  sv_replay_args replay{0, 0, 0.0f, 0};
+  hipGraphExec_t graph = nullptr;
+
+  ~sv_engine() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tin, vis,
+                    head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
+                    attn, mixed, act, inv, logits, ws};
+    for (void* b : bufs)
+      if (b) (void)hipFree(b);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+
+  size_t kv_offset_layer() const { return (size_t)n_pages * sh.n_kv_heads * (1u << cfg.page_shift) * sh.head_dim; }
+
+  sv_kv_args kv_args(uint32_t layer) const {
+    sv_kv_args kv{};
+    kv.is_global = 1;
+    kv.kv_layer = layer;
+    kv.max_seqs = cfg.max_seqs;
+    kv.page_shift = cfg.page_shift;
+    kv.n_pages = n_pages;
+    kv.max_pages = max_pages;
+    return kv;
+  }
+
+  // kv.rs:49-56 reserve(): pages until the slot holds `len` positions; the page table
+  // entry goes to the device at once.
+  sv_status reserve(uint32_t slot, uint32_t len) {
+    auto& pg = pages[slot];
+    const size_t before = pg.size();
+    while (((size_t)pg.size() << cfg.page_shift) < len) {
+      if (free_pages.empty()) return fail(SV_ERR_CAPACITY, "global KV pool exhausted");
+      if (pg.size() >= max_pages) return fail(SV_ERR_CAPACITY, "sequence needs more than %u pages", max_pages);
+      pg.push_back(free_pages.back());
+      free_pages.pop_back();
+    }
+    if (pg.size() > before) {
+      SV_HIP(hipMemcpyAsync(page_table + (size_t)slot * max_pages + before, pg.data() + before,
+                            (pg.size() - before) * 4, hipMemcpyHostToDevice, stream),
+             "page table");
+      SV_HIP(hipStreamSynchronize(stream), "page table");
+    }
+    return SV_OK;
+  }
+
+  sv_status ensure_ws(size_t bytes) {
+    if (bytes <= ws_bytes) return SV_OK;
+    if (graph) return fail(SV_ERR_STATE, "workspace must grow after a graph was captured");
+    SV_HIP(hipStreamSynchronize(stream), "workspace");
+    if (ws) SV_HIP(hipFree(ws), "workspace");
+    ws = nullptr;
+    ws_bytes = 0;
+    SV_HIP(hipMalloc(&ws, bytes), "workspace");
+    SV_HIP(hipMemset(ws, 0, bytes), "workspace");
+    ws_bytes = bytes;
+    return SV_OK;
+  }
+
+  sv_status upload(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return SV_OK;
+    SV_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "upload");
+    return SV_OK;
+  }
+
+  sv_status check_ready() const {
+    if (!embed) return fail(SV_ERR_STATE, "no embedding set");
+    for (uint32_t l = 0; l < sh.n_layers; l++)
+      if (!layer_set[l]) return fail(SV_ERR_STATE, "layer %u not set", l);
+    return SV_OK;
+  }
+
+  sv_status matmul(const sv_matrix& w, uint32_t n, const float* x, const uint32_t* x_rows, float* y, uint32_t epi,
+                   uint32_t flags, float scale, float ra, float rb, const float* base, float* aux) {
+    sv_mat_args a{};
+    a.n = n;
+    a.k = w.k;
+    a.m = w.m;
+    a.epi = epi;
+    a.flags = flags;
+    a.vocab_real = sh.vocab_real;
+    a.scale = scale;
+    a.ra = ra;
+    a.rb = rb;
+    a.ksplit = 1;
+    a.kchunk = w.k;
+    a.gshift = w.gshift;
+    return matmul_launch(stream, &w, x, x_rows, y, base, aux, &a, ws, ws_bytes);
+  }
+
+  // encode.rs:99-126 encode_forward + :383-412 encode_tail.
+  sv_status encode(uint32_t flags) {
+    SV_TRY(check_ready());
+    if (!planned) return fail(SV_ERR_STATE, "no plan");
+    const Plan& P = plan;
+    const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
+    SV_TIMED(SV_KIND_EMBED, embed_launch(stream, &sh, embed, tokens, h, tin, meta, lens, feed, tree, vis, n));
+    sv_attn_args aa{};
+    aa.split = P.split;
+    aa.max_splits = P.max_splits;
+    aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
+    for (uint32_t li = 0; li < sh.n_layers; li++) {
+      const sv_layer& L = layers[li];
+      SV_TIMED(SV_KIND_QKV,
+               matmul(L.qkv, n, h, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
+      aa.rope = L.rope;
+      const sv_kv_args kv = kv_args(li);
+      SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
+                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes));
+      SV_TIMED(SV_KIND_O,
+               matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn, h, nullptr));
+      SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
+      SV_TIMED(SV_KIND_DOWN,
+               matmul(L.down, n, act, nullptr, h, SV_EPI_RESID, 0, 1.0f, L.resid_mlp, L.post_mlp, mixed, nullptr));
+    }
+    (void)H;
+    (void)F;
+    (void)NQD;
+    if (P.n_head > 0) {
+      // rmsnorm_rows + the tied head (encode.rs:390-393), the norm folded into the matmul.
+      const sv_matrix head{embed, nullptr, sh.vocab, sh.hidden, SV_FMT_BF16, 0};
+      SV_TIMED(SV_KIND_HEAD, matmul(head, P.n_head, h, head_rows, logits, SV_EPI_HEAD, SV_FLAG_NORM_IN, 1.0f, 0, 0,
+                                    nullptr, nullptr));
+      SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
+    }
+    SV_TIMED(SV_KIND_ACCEPT, accept_launch(stream, runs, tokens, out_ids, lens, feed, gen, emitted, P.n_runs, tree,
+                                           path, path_len, on_path));
+    const bool compact = (flags & SV_STEP_COMPACT) || (P.branches && !(flags & SV_STEP_NO_COMPACT));
+    if (compact) {
+      const sv_kv_args kv = kv_args(0);
+      SV_TIMED(SV_KIND_COMPACT,
+               kv_compact_launch(stream, &sh, runs, P.n_runs, path, path_len, lens, k_cache, v_cache, page_table, &kv));
+    }
+    if (flags & SV_STEP_REPLAY) {
+      sv_replay_args ra = replay;
+      ra.stride = cfg.max_seq_len;
+      ra.vocab = sh.vocab_real;
+      SV_TIMED(SV_KIND_REPLAY, replay_launch(stream, runs, P.n_runs, lens, feed, trace, trace_len, &ra, tree));
+    }
+    return SV_OK;
+  }
+};
+
+extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* rope_freq, sv_engine** out) {
+  if (!cfg || !out || !rope_freq) return fail(SV_ERR_ARG, "engine_create: null pointer");
+  *out = nullptr;
+  const sv_shape& s = cfg->shape;
+  if (s.hidden == 0 || s.hidden % 256 || s.ffn == 0 || s.ffn % 128 || s.n_kv_heads == 0 || s.n_heads % s.n_kv_heads ||
+      (s.head_dim != 64 && s.head_dim != 128) || s.vocab == 0 || s.vocab % 16 || s.vocab_real > s.vocab ||
+      s.n_layers == 0)
+    return fail(SV_ERR_ARG, "engine_create: unsupported shape (hidden %u, heads %u/%u, dim %u, ffn %u, vocab %u)",
+                s.hidden, s.n_heads, s.n_kv_heads, s.head_dim, s.ffn, s.vocab);
+  if ((s.n_heads * s.head_dim) % 256 || ((s.n_heads + 2 * s.n_kv_heads) * s.head_dim) % 16)
+    return fail(SV_ERR_ARG, "engine_create: heads x dim must be a multiple of 256");
+  if (cfg->max_seqs == 0 || cfg->max_step_tokens == 0 || cfg->max_seq_len == 0 || cfg->max_head_rows == 0 ||
+      cfg->kv_tokens == 0)
+    return fail(SV_ERR_ARG, "engine_create: zero capacity");
+  if (cfg->page_shift < 4 || cfg->page_shift > 16) return fail(SV_ERR_ARG, "engine_create: page_shift %u", cfg->page_shift);
+  if (cfg->split_keys % 32) return fail(SV_ERR_ARG, "engine_create: split_keys %u", cfg->split_keys);
+  attn_init();
+  sv_engine* e = new sv_engine();
+  e->cfg = *cfg;
+  e->sh = s;
+  e->layers.resize(s.n_layers);
+  e->layer_set.assign(s.n_layers, false);
+  const uint32_t page = 1u << cfg->page_shift;
+  e->n_pages = (cfg->kv_tokens + page - 1) / page;
+  e->max_pages = (cfg->max_seq_len + page - 1) / page;
+  e->qkv_w = (s.n_heads + 2 * s.n_kv_heads) * s.head_dim;
+  auto bad = [&](sv_status st) {
+    delete e;
+    return st;
+  };
+  if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) return bad(fail(SV_ERR_HIP, "stream"));
+  const uint32_t n = cfg->max_step_tokens, S = cfg->max_seqs, R = cfg->max_head_rows;
+  e->kv_elems = (size_t)s.n_layers * e->kv_offset_layer();
+  sv_status st = SV_OK;
+#define ALLOC(ptr, count)                                 \
+  if ((st = dalloc(&e->ptr, (count), #ptr)) != SV_OK) return bad(st)
+  ALLOC(k_cache, e->kv_elems);
+  ALLOC(v_cache, e->kv_elems);
+  ALLOC(page_table, (size_t)S * e->max_pages);
+  ALLOC(rope, (size_t)(cfg->max_seq_len + SV_FEED_W) * SV_ROPE_PAIRS * 2);
+  ALLOC(lens, S);
+  ALLOC(feed, (size_t)S * SV_FEED_W);
+  ALLOC(tree, (size_t)S * SV_FEED_W);
+  ALLOC(trace, (size_t)S * cfg->max_seq_len);
+  ALLOC(trace_len, S);
+  ALLOC(gen, S);
+  ALLOC(tokens, n);
+  ALLOC(tin, 2 * (size_t)n);
+  ALLOC(vis, n);
+  ALLOC(head_rows, n);
+  ALLOC(attn_runs, 2 * (size_t)S);
+  ALLOC(sample_rows, std::max(n, R));
+  ALLOC(runs, S);
+  ALLOC(out_ids, std::max(n, R));
+  ALLOC(emitted, S);
+  ALLOC(meta, 2 * (size_t)n);
+  ALLOC(path, (size_t)S * SV_FEED_W);
+  ALLOC(path_len, S);
+  ALLOC(on_path, n);
+  ALLOC(h, (size_t)n * s.hidden);
+  ALLOC(qkv, (size_t)n * e->qkv_w);
+  ALLOC(attn, (size_t)n * s.n_heads * s.head_dim);
+  ALLOC(mixed, (size_t)n * s.hidden);
+  ALLOC(act, (size_t)n * s.ffn);
+  ALLOC(inv, n);
+  ALLOC(logits, (size_t)std::max(n, R) * s.vocab);
+#undef ALLOC
+  // RoPE table (engine.rs:394-421): (bf16(cos), bf16(sin)) of float(pos) * freq[j].
+  {
+    const size_t npos = (size_t)cfg->max_seq_len + SV_FEED_W;
+    std::vector<float> tab(npos * SV_ROPE_PAIRS * 2);
+    auto rbf = [](float x) {
+      uint32_t u;
+      memcpy(&u, &x, 4);
+      u += 0x7fffu + ((u >> 16) & 1u);
+      u &= 0xffff0000u;
+      float f;
+      memcpy(&f, &u, 4);
+      return f;
+    };
+    for (size_t pos = 0; pos < npos; pos++)
+      for (uint32_t j = 0; j < SV_ROPE_PAIRS; j++) {
+        const float th = (float)pos * rope_freq[j];
+        tab[(pos * SV_ROPE_PAIRS + j) * 2] = rbf(cosf(th));
+        tab[(pos * SV_ROPE_PAIRS + j) * 2 + 1] = rbf(sinf(th));
+      }
+    if (hipMemcpy(e->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bad(fail(SV_ERR_HIP, "rope table"));
+  }
+  // Chains in every slot's tree (buffers.rs:115-117), open generation state.
+  {
+    std::vector<uint32_t> chains((size_t)S * SV_FEED_W);
+    for (size_t i = 0; i < chains.size(); i++) {
+      const uint32_t row = (uint32_t)(i % SV_FEED_W);
+      chains[i] = row | (row == 0 ? SV_NO_PARENT : row - 1) << 8 | ((2u << row) - 1u) << 16;
+    }
+    if (hipMemcpy(e->tree, chains.data(), chains.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bad(fail(SV_ERR_HIP, "tree"));
+    std::vector<sv_gen_state> g(S);
+    for (auto& x : g) {
+      memset(&x, 0, sizeof x);
+      x.remaining = 0xffffffffu;
+    }
+    if (hipMemcpy(e->gen, g.data(), g.size() * sizeof(sv_gen_state), hipMemcpyHostToDevice) != hipSuccess)
+      return bad(fail(SV_ERR_HIP, "gen"));
+  }
+  // kv.rs:40: free pages (0..n).rev(), popped 0, 1, 2, ...
+  e->free_pages.resize(e->n_pages);
+  for (uint32_t i = 0; i < e->n_pages; i++) e->free_pages[i] = e->n_pages - 1 - i;
+  e->pages.resize(S);
+  e->seq_len.assign(S, 0);
+  e->used.assign(S, false);
+  e->sampling.assign(S, sv_sample_row{0, 0, 0, 0.0f, 1.0f, SV_NO_TOK});
+  // Workspace for the matmuls at the most rows.
+  size_t ws = 0;
+  const uint32_t rows = std::min<uint32_t>(16, std::max(n, R));
+  const uint32_t mk[][2] = {{e->qkv_w, s.hidden}, {s.hidden, s.n_heads * s.head_dim}, {2 * s.ffn, s.hidden},
+                            {s.hidden, s.ffn}, {s.vocab, s.hidden}};
+  for (auto& x : mk) ws = std::max(ws, matmul_ws_bytes(rows, x[0], x[1]));
+  if ((st = e->ensure_ws(ws)) != SV_OK) return bad(st);
+  *out = e;
+  return SV_OK;
+}
+
+extern "C" void sv_engine_destroy(sv_engine* e) {
+  if (!e) return;
+  (void)hipStreamSynchronize(e->stream);
+  delete e;
+}
+
+extern "C" void* sv_engine_stream(sv_engine* e) { return e ? (void*)e->stream : nullptr; }
+
+extern "C" sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed) {
+  if (!e || !d_embed) return fail(SV_ERR_ARG, "set_embed: null pointer");
+  e->embed = d_embed;
+  return SV_OK;
+}
+
+static sv_status check_matrix(const sv_matrix& m, uint32_t rows, uint32_t cols, const char* name) {
+  if (!m.d_w) return fail(SV_ERR_ARG, "%s: no weights", name);
+  if (m.m != rows || m.k != cols) return fail(SV_ERR_ARG, "%s: [%u][%u], expected [%u][%u]", name, m.m, m.k, rows, cols);
+  if (m.format == SV_FMT_I8 && !m.d_scales) return fail(SV_ERR_ARG, "%s: int8 without scales", name);
+  if (m.format != SV_FMT_I8 && m.format != SV_FMT_BF16) return fail(SV_ERR_ARG, "%s: format %u", name, m.format);
+  return SV_OK;
+}
+
+extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_layer* l) {
+  if (!e || !l) return fail(SV_ERR_ARG, "set_layer: null pointer");
+  if (layer >= e->sh.n_layers) return fail(SV_ERR_ARG, "set_layer: layer %u of %u", layer, e->sh.n_layers);
+  const sv_shape& s = e->sh;
+  SV_TRY(check_matrix(l->qkv, e->qkv_w, s.hidden, "qkv"));
+  SV_TRY(check_matrix(l->o, s.hidden, s.n_heads * s.head_dim, "o"));
+  SV_TRY(check_matrix(l->gate_up, 2 * s.ffn, s.hidden, "gate_up"));
+  SV_TRY(check_matrix(l->down, s.hidden, s.ffn, "down"));
+  e->layers[layer] = *l;
+  e->layer_set[layer] = true;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* o) {
+  if (!e || !o) return fail(SV_ERR_ARG, "get_buffers: null pointer");
+  o->d_k_cache = e->k_cache;
+  o->d_v_cache = e->v_cache;
+  o->d_page_table = e->page_table;
+  o->d_lens = e->lens;
+  o->d_feed = e->feed;
+  o->d_tree = e->tree;
+  o->d_gen = e->gen;
+  o->d_trace = e->trace;
+  o->d_trace_len = e->trace_len;
+  o->d_logits = e->logits;
+  o->d_rope = e->rope;
+  o->d_out_ids = e->out_ids;
+  o->d_emitted = e->emitted;
+  o->d_path = e->path;
+  o->d_path_len = e->path_len;
+  o->n_pages = e->n_pages;
+  o->max_pages = e->max_pages;
+  o->kv_bytes = e->kv_elems * 2;
+  return SV_OK;
+}
+
+static sv_status check_slot(sv_engine* e, uint32_t slot) {
+  if (!e) return fail(SV_ERR_ARG, "null engine");
+  if (slot >= e->cfg.max_seqs || !e->used[slot]) return fail(SV_ERR_STATE, "unknown sequence %u", slot);
+  return SV_OK;
+}
+
+extern "C" sv_status sv_new_seq(sv_engine* e, uint32_t* slot) {
+  if (!e || !slot) return fail(SV_ERR_ARG, "new_seq: null pointer");
+  uint32_t s = 0;
+  while (s < e->cfg.max_seqs && e->used[s]) s++;
+  if (s == e->cfg.max_seqs) return fail(SV_ERR_CAPACITY, "no free sequence slot");
+  e->used[s] = true;
+  e->seq_len[s] = 0;
+  e->pages[s].clear();
+  e->sampling[s] = sv_sample_row{0, 0, 0, 0.0f, 1.0f, SV_NO_TOK};
+  const uint32_t zero = 0;
+  sv_gen_state g;
+  memset(&g, 0, sizeof g);
+  g.remaining = 0xffffffffu;
+  SV_TRY(e->upload(e->lens + s, &zero, 4));
+  SV_TRY(e->upload(e->trace_len + s, &zero, 4));
+  SV_TRY(e->upload(e->gen + s, &g, sizeof g));
+  SV_HIP(hipStreamSynchronize(e->stream), "new_seq");
+  *slot = s;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_free_seq(sv_engine* e, uint32_t slot) {
+  SV_TRY(check_slot(e, slot));
+  // kv.rs:58-60 release(): pages pushed back in reverse.
+  auto& pg = e->pages[slot];
+  for (auto it = pg.rbegin(); it != pg.rend(); ++it) e->free_pages.push_back(*it);
+  pg.clear();
+  e->used[slot] = false;
+  e->seq_len[slot] = 0;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_seq_len(sv_engine* e, uint32_t slot, uint32_t* len) {
+  SV_TRY(check_slot(e, slot));
+  if (!len) return fail(SV_ERR_ARG, "seq_len: null pointer");
+  *len = e->seq_len[slot];
+  return SV_OK;
+}
+
+extern "C" sv_status sv_seq_pages(sv_engine* e, uint32_t slot, uint32_t* pages, uint32_t cap, uint32_t* n) {
+  SV_TRY(check_slot(e, slot));
+  const auto& pg = e->pages[slot];
+  if (n) *n = (uint32_t)pg.size();
+  if (pages)
+    for (uint32_t i = 0; i < pg.size() && i < cap; i++) pages[i] = pg[i];
+  return SV_OK;
+}
+
+extern "C" sv_status sv_set_sampling(sv_engine* e, uint32_t slot, float temperature, float top_p, uint64_t seed) {
+  SV_TRY(check_slot(e, slot));
+  // engine.rs:113-120 Sampling::check.
+  const bool t_ok = temperature == 0.0f || (std::isnormal(temperature) && temperature > 0.0f);
+  if (!t_ok || !(top_p > 0.0f && top_p <= 1.0f))
+    return fail(SV_ERR_ARG, "sampling (T %g, top_p %g): needs T 0 or normal positive, 0 < top_p <= 1", temperature,
+                top_p);
+  e->sampling[slot] = sv_sample_row{(uint32_t)seed, (uint32_t)(seed >> 32), 0, temperature, top_p, SV_NO_TOK};
+  return SV_OK;
+}
+
+extern "C" sv_status sv_set_gen(sv_engine* e, uint32_t slot, const sv_gen_state* g) {
+  SV_TRY(check_slot(e, slot));
+  if (!g || g->nstop > SV_MAX_STOP) return fail(SV_ERR_ARG, "set_gen: bad state");
+  SV_TRY(e->upload(e->gen + slot, g, sizeof *g));
+  SV_HIP(hipStreamSynchronize(e->stream), "set_gen");
+  return SV_OK;
+}
+
+extern "C" sv_status sv_bench_fill(sv_engine* e, uint32_t slot, uint32_t len) {
+  SV_TRY(check_slot(e, slot));
+  const uint64_t nl = (uint64_t)e->seq_len[slot] + len;
+  if (nl > e->cfg.max_seq_len) return fail(SV_ERR_CAPACITY, "sequence would reach %llu tokens", (unsigned long long)nl);
+  SV_TRY(e->reserve(slot, (uint32_t)nl));
+  e->seq_len[slot] = (uint32_t)nl;
+  const uint32_t v = (uint32_t)nl;
+  SV_TRY(e->upload(e->lens + slot, &v, 4));
+  SV_HIP(hipStreamSynchronize(e->stream), "bench_fill");
+  return SV_OK;
+}
+
+extern "C" sv_status sv_settle(sv_engine* e, uint32_t slot, uint32_t unused) {
+  SV_TRY(check_slot(e, slot));
+  if (unused > e->seq_len[slot]) return fail(SV_ERR_ARG, "settle: %u unused of %u", unused, e->seq_len[slot]);
+  e->seq_len[slot] -= unused;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_set_feed(sv_engine* e, uint32_t slot, uint32_t len, uint32_t token) {
+  SV_TRY(check_slot(e, slot));
+  if (len > e->cfg.max_seq_len) return fail(SV_ERR_CAPACITY, "set_feed: length %u", len);
+  if (token >= e->sh.vocab) return fail(SV_ERR_ARG, "set_feed: token %u", token);
+  SV_TRY(e->reserve(slot, len));
+  e->seq_len[slot] = len;
+  SV_TRY(e->upload(e->lens + slot, &len, 4));
+  SV_TRY(e->upload(e->feed + (size_t)slot * SV_FEED_W, &token, 4));
+  SV_HIP(hipStreamSynchronize(e->stream), "set_feed");
+  return SV_OK;
+}
+
+extern "C" sv_status sv_set_replay(sv_engine* e, uint32_t seed, float rate) {
+  if (!e) return fail(SV_ERR_ARG, "set_replay: null engine");
+  e->replay.seed = seed;
+  e->replay.rate = rate;
+  return SV_OK;
+}
+
+// plan.rs:47-151 Engine::plan.
+extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_runs, uint32_t extra_keys,
+                             sv_plan_info* info) {
+  if (!e || (!runs_in && n_runs)) return fail(SV_ERR_ARG, "plan: null pointer");
+  if (n_runs == 0) return fail(SV_ERR_ARG, "plan: no runs");
+  if (n_runs > e->cfg.max_seqs) return fail(SV_ERR_CAPACITY, "plan: %u runs", n_runs);
+  if (e->graph) {
+    (void)hipGraphExecDestroy(e->graph);
+    e->graph = nullptr;
+  }
+  SV_HIP(hipStreamSynchronize(e->stream), "plan");
+  uint32_t n = 0;
+  for (uint32_t ri = 0; ri < n_runs; ri++) n += runs_in[ri].count;
+  if (n == 0 || n > e->cfg.max_step_tokens)
+    return fail(SV_ERR_CAPACITY, "step has %u tokens (max %u)", n, e->cfg.max_step_tokens);
+  std::vector<uint32_t> tokens, tin, vis, head_rows, attn_runs;
+  std::vector<sv_sample_row> samples;
+  std::vector<sv_run_in> run_in;
+  Plan P;
+  uint32_t max_cached = 0;
+  for (uint32_t ri = 0; ri < n_runs; ri++) {
+    const sv_run& r = runs_in[ri];
+    SV_TRY(check_slot(e, r.slot));
+    if (r.count == 0 || r.count > SV_MAX_RUN)
+      return fail(SV_ERR_CAPACITY, "%u tokens for one sequence in a step (max %u)", r.count, SV_MAX_RUN);
+    if (!r.tokens) return fail(SV_ERR_ARG, "plan: run %u has no tokens", ri);
+    for (uint32_t j = 0; j < ri; j++)
+      if (runs_in[j].slot == r.slot) return fail(SV_ERR_ARG, "a sequence appears twice in one step");
+    for (uint32_t i = 0; i < r.count; i++) {
+      const uint32_t t = r.tokens[i];
+      if (t >= SV_FEED_ROW ? t - SV_FEED_ROW >= SV_FEED_W : t >= e->sh.vocab)
+        return fail(SV_ERR_ARG, "token id %u out of range", t);
+    }
+    const uint64_t new_len = (uint64_t)e->seq_len[r.slot] + r.count;
+    if (new_len > e->cfg.max_seq_len)
+      return fail(SV_ERR_CAPACITY, "sequence would reach %llu tokens (max %u)", (unsigned long long)new_len,
+                  e->cfg.max_seq_len);
+  }
+  for (uint32_t ri = 0; ri < n_runs; ri++) {
+    const sv_run& r = runs_in[ri];
+    const uint32_t slot = r.slot, count = r.count;
+    SV_TRY(e->reserve(slot, e->seq_len[slot] + count));
+    const uint32_t first_row = (uint32_t)tokens.size();
+    for (uint32_t row = 0; row < count; row++) {
+      tokens.push_back(r.tokens[row]);
+      tin.push_back(slot);
+      tin.push_back(row);
+      vis.push_back(0xffffffffu >> (31 - row));  // causal within the run (plan.rs:81)
+    }
+    const uint32_t first_head = (uint32_t)head_rows.size();
+    if (r.verify)
+      for (uint32_t x = first_row; x < first_row + count; x++) head_rows.push_back(x);
+    else if (r.head)
+      head_rows.push_back(first_row + count - 1);
+    for (uint32_t hx = first_head; hx < head_rows.size(); hx++) {
+      sv_sample_row s = e->sampling[slot];  // engine.rs:134-137 row_of
+      s.pos = 0;
+      s.tok = head_rows[hx];
+      samples.push_back(s);
+    }
+    run_in.push_back(sv_run_in{slot, first_row, count, first_head, (uint32_t)head_rows.size() - first_head,
+                               r.verify ? 1u : 0u});
+    attn_runs.push_back(first_row);
+    attn_runs.push_back(count);
+    max_cached = std::max(max_cached, e->seq_len[slot]);
+    P.max_run = std::max(P.max_run, count);
+    P.branches |= (r.verify && count > 2) ? 1u : 0u;
+    P.slots.push_back(slot);
+    P.counts.push_back(count);
+    P.verify.push_back(r.verify ? 1u : 0u);
+    e->seq_len[slot] += count;
+  }
+  if (head_rows.size() > e->cfg.max_head_rows || head_rows.size() > 16)
+    return fail(SV_ERR_CAPACITY, "%zu head rows (max %u)", head_rows.size(), std::min(16u, e->cfg.max_head_rows));
+  P.n = n;
+  P.n_head = (uint32_t)head_rows.size();
+  P.n_runs = n_runs;
+  // Attention splits (plan.rs:156-164 decode_splits, for 256 CUs): the longest context over
+  // about ATTN_TARGET_WGS workgroups per layer, plus a split of its own for the new keys;
+  // `extra_keys` sizes the grid for replays at later positions.
+  uint32_t split = e->cfg.split_keys;
+  if (split == 0) {
+    const uint32_t want = std::max<uint32_t>(1, ATTN_TARGET_WGS / (n_runs * e->sh.n_kv_heads));
+    split = (max_cached + want - 1) / want;
+    split = std::max<uint32_t>(MIN_SPLIT, (split + 31) / 32 * 32);
+  }
+  P.split = split;
+  P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
+  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, n_runs, P.max_splits, P.max_run)));
+  SV_TRY(e->upload(e->tokens, tokens.data(), tokens.size() * 4));
+  SV_TRY(e->upload(e->tin, tin.data(), tin.size() * 4));
+  SV_TRY(e->upload(e->vis, vis.data(), vis.size() * 4));
+  SV_TRY(e->upload(e->head_rows, head_rows.data(), head_rows.size() * 4));
+  SV_TRY(e->upload(e->sample_rows, samples.data(), samples.size() * sizeof(sv_sample_row)));
+  SV_TRY(e->upload(e->runs, run_in.data(), run_in.size() * sizeof(sv_run_in)));
+  SV_TRY(e->upload(e->attn_runs, attn_runs.data(), attn_runs.size() * 4));
+  SV_HIP(hipStreamSynchronize(e->stream), "plan upload");
+  e->plan = P;
+  e->planned = true;
+  if (info) {
+    info->n_tokens = P.n;
+    info->n_head = P.n_head;
+    info->n_runs = P.n_runs;
+    info->branches = P.branches;
+    info->max_run = P.max_run;
+    info->split = P.split;
+    info->max_splits = P.max_splits;
+  }
+  return SV_OK;
+}
+
+extern "C" sv_status sv_encode(sv_engine* e, uint32_t flags) {
+  if (!e) return fail(SV_ERR_ARG, "encode: null engine");
+  return e->encode(flags);
+}
+
+extern "C" sv_status sv_graph_capture(sv_engine* e, uint32_t flags) {
+  if (!e) return fail(SV_ERR_ARG, "graph_capture: null engine");
+  SV_TRY(e->check_ready());
+  if (!e->planned) return fail(SV_ERR_STATE, "graph_capture: no plan");
+  if (e->graph) {
+    (void)hipGraphExecDestroy(e->graph);
+    e->graph = nullptr;
+  }
+  SV_HIP(hipStreamSynchronize(e->stream), "graph_capture");
+  SV_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+  const sv_status st = e->encode(flags);
+  hipGraph_t g = nullptr;
+  const hipError_t ec = hipStreamEndCapture(e->stream, &g);
+  if (st != SV_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return st;
+  }
+  SV_HIP(ec, "end capture");
+  const hipError_t ei = hipGraphInstantiate(&e->graph, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  SV_HIP(ei, "graph instantiate");
+  return SV_OK;
+}
+
+extern "C" sv_status sv_graph_replay(sv_engine* e, uint32_t count) {
+  if (!e || !e->graph) return fail(SV_ERR_STATE, "graph_replay: no graph");
+  for (uint32_t i = 0; i < count; i++) SV_HIP(hipGraphLaunch(e->graph, e->stream), "graph launch");
+  return SV_OK;
+}
+
+extern "C" sv_status sv_sync(sv_engine* e) {
+  if (!e) return fail(SV_ERR_ARG, "sync: null engine");
+  SV_HIP(hipStreamSynchronize(e->stream), "sync");
+  return SV_OK;
+}
+
+// engine.rs:310-314 step, with generate.rs:446-463 collect: plan, encode, wait, read the
+// head rows' ids (and logits), the tokens each run emitted, and give back a verify run's
+// unused positions (settle).
+extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
+                             float* logits, uint32_t* emitted, sv_plan_info* info) {
+  sv_plan_info pi;
+  SV_TRY(sv_plan(e, runs, n_runs, 0, &pi));
+  if (info) *info = pi;
+  SV_TRY(e->encode(flags));
+  SV_HIP(hipStreamSynchronize(e->stream), "step");
+  std::vector<uint32_t> em(n_runs);
+  SV_HIP(hipMemcpy(em.data(), e->emitted, n_runs * 4, hipMemcpyDeviceToHost), "step emitted");
+  if (ids && pi.n_head) SV_HIP(hipMemcpy(ids, e->out_ids, pi.n_head * 4, hipMemcpyDeviceToHost), "step ids");
+  if (logits && pi.n_head)
+    SV_HIP(hipMemcpy(logits, e->logits, (size_t)pi.n_head * e->sh.vocab * 4, hipMemcpyDeviceToHost), "step logits");
+  if (emitted) memcpy(emitted, em.data(), n_runs * 4);
+  for (uint32_t ri = 0; ri < n_runs; ri++)
+    if (runs[ri].verify) {
+      const uint32_t slot = runs[ri].slot;
+      e->seq_len[slot] -= runs[ri].count - std::min(em[ri], runs[ri].count);
+    }
+  return SV_OK;
+}
+
+extern "C" sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches) {
+  if (!e || !ms || !launches) return fail(SV_ERR_ARG, "profile_step: null pointer");
+  SV_HIP(hipStreamSynchronize(e->stream), "profile_step");
+  e->prof = true;
+  e->prof_events.clear();
+  sv_status st = SV_OK;
+  for (uint32_t r = 0; r < reps && st == SV_OK; r++) st = e->encode(flags);
+  e->prof = false;
+  const hipError_t sync = hipStreamSynchronize(e->stream);
+  for (auto& pe : e->prof_events) {
+    float t = 0.0f;
+    if (st == SV_OK && sync == hipSuccess && hipEventElapsedTime(&t, pe.second.first, pe.second.second) == hipSuccess &&
+        pe.first >= 0 && pe.first < SV_KIND_COUNT) {
+      ms[pe.first] += t;
+      launches[pe.first] += 1;
+    }
+    (void)hipEventDestroy(pe.second.first);
+    (void)hipEventDestroy(pe.second.second);
+  }
+  e->prof_events.clear();
+  SV_TRY(st);
+  SV_HIP(sync, "profile_step");
+  return SV_OK;
+}
+
+// hooks.rs:41-55 sample_logits.
+extern "C" sv_status sv_sample_logits(sv_engine* e, const float* logits, uint32_t rows, const float* temperature,
+                                      const float* top_p, const uint64_t* seed, const uint32_t* pos, uint32_t* ids) {
+  if (!e || !logits || !temperature || !top_p || !seed || !pos || !ids) return fail(SV_ERR_ARG, "sample_logits: null");
+  if (rows == 0 || rows > std::max(e->cfg.max_head_rows, e->cfg.max_step_tokens))
+    return fail(SV_ERR_CAPACITY, "%u rows of logits", rows);
+  std::vector<sv_sample_row> s(rows);
+  for (uint32_t r = 0; r < rows; r++) {
+    const float t = temperature[r], p = top_p[r];
+    if (!(t == 0.0f || (std::isnormal(t) && t > 0.0f)) || !(p > 0.0f && p <= 1.0f))
+      return fail(SV_ERR_ARG, "row %u: T %g top_p %g", r, t, p);
+    s[r] = sv_sample_row{(uint32_t)seed[r], (uint32_t)(seed[r] >> 32), pos[r], t, p, SV_NO_TOK};
+  }
+  SV_HIP(hipStreamSynchronize(e->stream), "sample_logits");
+  SV_TRY(e->upload(e->logits, logits, (size_t)rows * e->sh.vocab * 4));
+  SV_TRY(e->upload(e->sample_rows, s.data(), rows * sizeof(sv_sample_row)));
+  SV_TRY(sample_launch(e->stream, e->logits, e->sample_rows, e->out_ids, e->meta, rows, e->sh.vocab));
+  SV_HIP(hipStreamSynchronize(e->stream), "sample_logits");
+  SV_HIP(hipMemcpy(ids, e->out_ids, rows * 4, hipMemcpyDeviceToHost), "sample_logits ids");
+  e->planned = false;
+  return SV_OK;
+}

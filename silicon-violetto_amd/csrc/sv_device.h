@@ -1,0 +1,132 @@
+// sv_device.h — device-side helpers shared by the HIP kernels of libsv_verify (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sv_verify.h"
+
+namespace sv {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int WAVE = 64;
+constexpr float LOG2E_F = 1.44269504088896340736f;
+
+// bf16 bits -> float (kernels.metal:17).
+__device__ __forceinline__ float bf(uint32_t u16) { return __uint_as_float(u16 << 16); }
+// float -> bf16 bits, round to nearest even on the dropped 16 bits (kernels.metal:23-27).
+__device__ __forceinline__ uint32_t to_bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+
+// 16x16x32 bf16 matrix-core product, fp32 accumulate: c += a (16x32) * b (32x16).
+// Lane l supplies a's row l % 16 and b's column l % 16, each with 8 consecutive k slots
+// of k-group l / 16 (the same slots for a and b); lane l receives c's column l % 16,
+// rows 4 (l / 16) + 0..3.
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Two floats -> their bf16 bits in one word (lo in bits 0-15), round to nearest even.
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) { return to_bf(lo) | (to_bf(hi) << 16); }
+
+// x = hi + lo, both bf16 (hi = x rounded to bf16, lo = the rest rounded): 16 significant
+// bits of x for bf16 matrix-core products.
+__device__ __forceinline__ void split_bf(float x, float& hi, float& lo) {
+  hi = bf(to_bf(x));
+  lo = x - hi;
+}
+
+// Eight floats -> (hi, lo) bf16x8 operands.
+__device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    float h0, l0, h1, l1;
+    split_bf(v[2 * j], h0, l0);
+    split_bf(v[2 * j + 1], h1, l1);
+    h[j] = (__float_as_uint(h0) >> 16) | (__float_as_uint(h1) & 0xffff0000u);
+    l[j] = pack_bf2(l0, l1);
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+
+// Eight signed bytes (two words) -> bf16x8 (exact: |q| <= 128 fits bf16's 8 bits).
+__device__ __forceinline__ bf16x8 i8x8_to_bf(uint32_t w0, uint32_t w1) {
+  u32x4 r;
+  const uint32_t w[2] = {w0, w1};
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const float f0 = (float)(int8_t)(w[j]), f1 = (float)(int8_t)(w[j] >> 8);
+    const float f2 = (float)(int8_t)(w[j] >> 16), f3 = (float)(int8_t)(w[j] >> 24);
+    r[2 * j] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    r[2 * j + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
+  }
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
+  return v;
+}
+
+// The sampler's exp2, bit-identical to the oracle's orc_exp2: Cody-Waite reduction
+// x = n + f, n = rint(x); 2^f by the degree-7 Taylor polynomial of e^(f ln 2) in Horner
+// form with fused multiply-adds; exact scaling by 2^n; results below 2^-125 flush to 0.
+__device__ __forceinline__ float sv_exp2(float x) {
+  if (!(x >= -125.0f)) return 0.0f;
+  if (x > 127.0f) return __builtin_inff();
+  const float nf = __builtin_rintf(x);
+  const float f = x - nf;
+  float p = 1.525273380405984e-05f;
+  p = __builtin_fmaf(p, f, 1.5403530393381608e-04f);
+  p = __builtin_fmaf(p, f, 1.3333558146428443e-03f);
+  p = __builtin_fmaf(p, f, 9.6181291076284772e-03f);
+  p = __builtin_fmaf(p, f, 5.5504108664821580e-02f);
+  p = __builtin_fmaf(p, f, 2.4022650695910071e-01f);
+  p = __builtin_fmaf(p, f, 6.9314718055994531e-01f);
+  p = __builtin_fmaf(p, f, 1.0f);
+  const int n = (int)nf;
+  return p * __uint_as_float((uint32_t)(n + 127) << 23);
+}
+
+// Philox4x32-10 (kernels.metal:1464-1472; Salmon et al. 2011).
+__device__ __forceinline__ u32x4 philox(u32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int i = 0; i < 10; i++) {
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c[0]), lo0 = 0xD2511F53u * c[0];
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c[2]), lo1 = 0xCD9E8D57u * c[2];
+    c = u32x4{hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0};
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// Release this workgroup's global writes, count its arrival at `counter`, and tell whether
+// it arrived last of `expected`; the last one acquires every other's writes and resets the
+// counter for the next launch. All threads of the workgroup must call it.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == expected - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  const bool last = *lds_flag != 0;
+  if (last) __threadfence();
+  return last;
+}
+
+}  // namespace sv

@@ -1,0 +1,52 @@
+// sv_internal.h — host-side declarations shared by the translation units of libsv_verify.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/sv_verify.h"
+
+namespace sv {
+
+// Every workspace starts with this many bytes of arrival counters, zero at rest (each
+// kernel's last workgroup resets the ones it used); partial sums follow. Kernels that run
+// in stream order can share one workspace.
+constexpr size_t WS_COUNTER_BYTES = 65536;
+
+// Record a thread-local error message and return `code` (sv_last_error reads it).
+sv_status fail(sv_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// SV_OK, or SV_ERR_HIP with the launch error of the last kernel.
+sv_status check_launch(const char* what);
+// SV_OK, or SV_ERR_HIP with the message of `e`.
+sv_status check_hip(hipError_t e, const char* what);
+
+size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k);
+sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
+                        const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes);
+
+void attn_init();
+size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
+sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
+                      uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
+                      const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
+                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes);
+
+sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, uint32_t* tokens, float* out,
+                       const uint32_t* tin, uint32_t* meta, const uint32_t* lens, const uint32_t* feed,
+                       const uint32_t* tree, uint32_t* vis, uint32_t n);
+sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
+                              uint32_t hidden);
+sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,
+                        const uint32_t* meta, uint32_t n_rows, uint32_t vocab);
+sv_status accept_launch(hipStream_t stream, const sv_run_in* runs, const uint32_t* tokens, uint32_t* out,
+                        uint32_t* lens, uint32_t* feed, sv_gen_state* gen, uint32_t* emitted, uint32_t nruns,
+                        const uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path);
+sv_status kv_compact_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
+                            const uint32_t* path, const uint32_t* path_len, const uint32_t* lens, uint16_t* k_cache,
+                            uint16_t* v_cache, const uint32_t* page_table, const sv_kv_args* kv);
+sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nruns, const uint32_t* lens,
+                        uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
+                        uint32_t* tree);
+
+}  // namespace sv

@@ -1,0 +1,353 @@
+// tail.hip — the small kernels around the matmuls and attention: embed, rmsnorm_rows, the
+// sampler, accept, kv_compact and the replay drafter (engine/src/kernels.metal:82-131,
+// 1409-1724). The sampler's and accept's results are bit-exact with the oracle: this file is
+// compiled with -ffp-contract=off, and the sampler sums in the reference's fixed order.
+#include "sv_device.h"
+#include "sv_internal.h"
+
+#pragma clang fp contract(off)
+
+namespace sv {
+
+// Sum over a 256-thread workgroup, in a fixed order (waves 0..3).
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int wv = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[wv] = v;
+  __syncthreads();
+  return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// embed (kernels.metal:82-114): one workgroup of 256 per token.
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, uint32_t* tokens, float* out,
+                                                    const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
+                                                    const uint32_t* feed, const uint32_t* tree, uint32_t* vis,
+                                                    uint32_t H, uint32_t vocab) {
+  __shared__ float red[4];
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
+  const uint32_t slot = tin[2 * t];
+  uint32_t tok = tokens[t], depth = tin[2 * t + 1];
+  if (tok >= SV_FEED_ROW) {
+    const uint32_t i = tok - SV_FEED_ROW, node = tree[slot * SV_FEED_W + i];
+    tok = feed[slot * SV_FEED_W + i];
+    depth = node & 0xffu;
+    if (tid == 0) vis[t] = node >> 16;
+  }
+  // An id past the table (only a corrupted feed can make one) reads row vocab - 1.
+  const uint16_t* row = table + (size_t)min(tok, vocab - 1) * H;
+  float ss = 0.0f;
+  for (uint32_t i = tid; i < H; i += 256) {
+    const float v = bf(row[i]);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  const float inv = 1.0f / __builtin_sqrtf(block_sum256(ss, red) / (float)H + SV_RMS_EPS);
+  if (tid == 0) {  // after block_sum256's barriers: every thread has read tokens[t]
+    tokens[t] = tok;
+    meta[2 * t] = slot;
+    meta[2 * t + 1] = lens[slot] + depth;
+  }
+  for (uint32_t i = tid; i < H; i += 256) out[(size_t)t * H + i] = bf(row[i]) * inv;
+}
+
+// rmsnorm_rows (kernels.metal:117-131).
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* in, const uint32_t* rows, float* out,
+                                                           uint32_t H) {
+  __shared__ float red[4];
+  const uint32_t r = blockIdx.x, tid = threadIdx.x;
+  const float* x = in + (size_t)rows[r] * H;
+  float ss = 0.0f;
+  for (uint32_t i = tid; i < H; i += 256) ss = __builtin_fmaf(x[i], x[i], ss);
+  const float inv = 1.0f / __builtin_sqrtf(block_sum256(ss, red) / (float)H + SV_RMS_EPS);
+  for (uint32_t i = tid; i < H; i += 256) out[(size_t)r * H + i] = x[i] * inv;
+}
+
+// ------------------------------------------------------------------ sampler
+
+// kernels.metal:1418-1420: the larger value, ties to the lower id.
+__device__ __forceinline__ void better(float& bv, uint32_t& bi, float v, uint32_t i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// kernels.metal:1484-1501 tg_scan: ex[t] = the sum of v over threads before t, in 32 serial
+// runs of 32 then their bases in order; ex[1024] = the total.
+__device__ __forceinline__ void scan1024(float v, float* ex, float* base, uint32_t tid) {
+  ex[tid] = v;
+  __syncthreads();
+  if (tid < 32) {
+    float acc = 0.0f;
+    for (uint32_t i = 32 * tid; i < 32 * tid + 32; i++) {
+      const float x = ex[i];
+      ex[i] = acc;
+      acc += x;
+    }
+    base[tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.0f;
+    for (uint32_t g = 0; g < 32; g++) {
+      const float x = base[g];
+      base[g] = acc;
+      acc += x;
+    }
+    ex[SV_SAMPLE_THREADS] = acc;
+  }
+  __syncthreads();
+  ex[tid] += base[tid / 32];
+  __syncthreads();
+}
+
+// sample (kernels.metal:1503-1576), with argmax_partial (:1430-1451) folded in: one
+// workgroup of 1024 per row. Thread t owns ids t, t + 1024, ...: the order of every sum.
+__global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const sv_sample_row* rows, uint32_t* out,
+                                                      const uint32_t* meta, uint32_t vocab) {
+  __shared__ float ex[SV_SAMPLE_THREADS + 1];
+  __shared__ float base[32];
+  __shared__ float bvs[16];
+  __shared__ uint32_t bis[16];
+  __shared__ uint32_t pick;
+  const uint32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const sv_sample_row row = rows[r];
+  const uint32_t pos = row.tok == SV_NO_TOK ? row.pos : meta[2 * row.tok + 1] + 1;
+  const float* x = logits + (size_t)r * vocab;
+
+  float lmax = -3.402823466e+38f;
+  uint32_t tok = 0xffffffffu;
+  for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) better(lmax, tok, x[i], i);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float v = __shfl_xor(lmax, o, WAVE);
+    const uint32_t i = __shfl_xor(tok, o, WAVE);
+    better(lmax, tok, v, i);
+  }
+  if (lane == 0) {
+    bvs[wv] = lmax;
+    bis[wv] = tok;
+  }
+  __syncthreads();
+  lmax = bvs[0];
+  tok = bis[0];
+  for (int w = 1; w < 16; w++) better(lmax, tok, bvs[w], bis[w]);
+
+  if (row.temperature > 0.0f) {
+    const float c = LOG2E_F / row.temperature;
+    float s = 0.0f;
+    for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) s += sv_exp2((x[i] - lmax) * c);
+    scan1024(s, ex, base, tid);
+    const float z = ex[SV_SAMPLE_THREADS];
+    float low = -__builtin_inff();
+    for (uint32_t round = 0; round < SV_SAMPLE_ROUNDS; round++) {
+      const u32x4 ph = philox(u32x4{pos, round, 0u, 0u}, row.seed_lo, row.seed_hi);
+      const float target = (float)(ph[0] >> 8) * 0x1p-24f * ex[SV_SAMPLE_THREADS];
+      if (tid == 0) pick = 0xffffffffu;
+      __syncthreads();
+      const float lo = ex[tid];
+      if (lo <= target && target < ex[tid + 1]) {
+        // Re-add this thread's terms in the order of its sum; rounding can leave the
+        // target past them, then the last one counts.
+        float acc = 0.0f;
+        uint32_t j = 0xffffffffu;
+        for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) {
+          const float xi = x[i];
+          if (!(xi > low)) continue;
+          const float e = sv_exp2((xi - lmax) * c);
+          acc += e;
+          if (e > 0.0f) j = i;
+          if (target - lo < acc) break;
+        }
+        pick = j;
+      }
+      __syncthreads();
+      const uint32_t j = pick;
+      if (j == 0xffffffffu) break;
+      const float xj = x[j];
+      if (xj == lmax || row.top_p >= 1.0f) {
+        tok = j;
+        break;
+      }
+      float qs = 0.0f;
+      for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) {
+        const float xi = x[i];
+        if (xi > xj) qs += sv_exp2((xi - lmax) * c);
+      }
+      scan1024(qs, ex, base, tid);
+      if (ex[SV_SAMPLE_THREADS] < row.top_p * z) {
+        tok = j;
+        break;
+      }
+      low = xj;
+    }
+  }
+  if (tid == 0) out[r] = tok;
+}
+
+// ---------------------------------------------------------------- accepting
+
+// accept (kernels.metal:1605-1657): one thread per run. A run that emits nothing (only with
+// remaining = 0 on a slot not marked done) leaves feed alone.
+__global__ __launch_bounds__(64) void accept_kernel(const sv_run_in* runs, const uint32_t* tokens, uint32_t* out,
+                                                    uint32_t* lens, uint32_t* feed, sv_gen_state* gen,
+                                                    uint32_t* emitted, uint32_t nruns, const uint32_t* tree,
+                                                    uint32_t* path, uint32_t* path_len, uint32_t* on_path) {
+  const uint32_t r = blockIdx.x * 64 + threadIdx.x;
+  if (r >= nruns) return;
+  const sv_run_in ru = runs[r];
+  sv_gen_state* gs = &gen[ru.slot];
+  path_len[r] = 0;
+  const uint32_t done = gs->done;
+  for (uint32_t j = 0; j < ru.count; j++) on_path[ru.first + j] = !ru.verify && !done;
+  if (done) {
+    emitted[r] = 0;
+    return;
+  }
+  if (!ru.verify) lens[ru.slot] += ru.count;
+  if (ru.nhead == 0) {
+    emitted[r] = 0;
+    return;
+  }
+  uint32_t first = ru.head0 + ru.nhead - 1, e = 1;
+  uint32_t walk[SV_FEED_W];
+  walk[0] = 0;
+  if (ru.verify) {
+    const uint32_t* node = tree + (size_t)ru.slot * SV_FEED_W;
+    for (uint32_t c = 1, at = 0; c < ru.count; c++) {
+      if (((node[c] >> 8) & 0xffu) == at && tokens[ru.first + c] == out[ru.head0 + at]) walk[e++] = at = c;
+    }
+    for (uint32_t j = 1; j < e; j++) out[ru.head0 + j] = out[ru.head0 + walk[j]];
+    first = ru.head0;
+  }
+  bool stop = false;
+  uint32_t k = 0;
+  const uint32_t remaining = gs->remaining, nstop = gs->nstop;
+  while (k < e && k < remaining && !stop) {
+    const uint32_t t = out[first + k];
+    for (uint32_t j = 0; j < nstop && j < SV_MAX_STOP; j++) stop = stop || t == gs->stop[j];
+    k++;
+  }
+  if (ru.verify) {
+    lens[ru.slot] += k;
+    path_len[r] = k;
+    for (uint32_t j = 0; j < k; j++) {
+      path[r * SV_FEED_W + j] = walk[j];
+      on_path[ru.first + walk[j]] = 1;
+    }
+  }
+  if (k > 0) feed[ru.slot * SV_FEED_W] = out[first + k - 1];
+  gs->remaining = remaining - k;
+  if (stop || remaining - k == 0) gs->done = 1;
+  emitted[r] = k;
+}
+
+// kv_compact (kernels.metal:1659-1693): grid (runs, layers); thread = (kv head, 4 dims).
+// Rows p0 + path[j] -> p0 + j in increasing j: path[j] >= j and increases, so nothing is
+// overwritten before it is read.
+__global__ __launch_bounds__(256) void kv_compact_kernel(const sv_run_in* runs, const uint32_t* path,
+                                                         const uint32_t* path_len, const uint32_t* lens,
+                                                         uint16_t* kc, uint16_t* vc, const uint32_t* page_table,
+                                                         uint32_t NKV, uint32_t D, uint32_t page_shift,
+                                                         uint32_t n_pages, uint32_t max_pages) {
+  const uint32_t r = blockIdx.x, l = blockIdx.y, tid = threadIdx.x;
+  const uint32_t chunks = D / 4;
+  if (tid >= NKV * chunks) return;
+  const uint32_t g = tid / chunks, d0 = (tid % chunks) * 4;
+  const uint32_t k = path_len[r], slot = runs[r].slot, p0 = lens[slot] - k;
+  const uint32_t pmask = (1u << page_shift) - 1u;
+  for (uint32_t j = 1; j < k; j++) {
+    const uint32_t from = path[r * SV_FEED_W + j];
+    if (from == j) continue;
+    const uint32_t ps = page_table[(size_t)slot * max_pages + ((p0 + from) >> page_shift)];
+    const uint32_t pd = page_table[(size_t)slot * max_pages + ((p0 + j) >> page_shift)];
+    const size_t src = ((((size_t)l * n_pages + ps) * NKV + g) << page_shift) * D + (size_t)((p0 + from) & pmask) * D + d0;
+    const size_t dst = ((((size_t)l * n_pages + pd) * NKV + g) << page_shift) * D + (size_t)((p0 + j) & pmask) * D + d0;
+    *(u32x2*)(kc + dst) = *(const u32x2*)(kc + src);
+    *(u32x2*)(vc + dst) = *(const u32x2*)(vc + src);
+  }
+}
+
+// replay_draft (kernels.metal:1705-1724): grid runs, FEED_W threads.
+__global__ __launch_bounds__(64) void replay_kernel(const sv_run_in* runs, uint32_t nruns, const uint32_t* lens,
+                                                    uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len,
+                                                    sv_replay_args ra, uint32_t* tree) {
+  const uint32_t r = blockIdx.x, i = threadIdx.x;
+  if (i == 0 || i >= SV_FEED_W || r >= nruns || runs[r].nhead == 0) return;
+  const uint32_t slot = runs[r].slot, n = trace_len[slot];
+  if (n == 0) return;
+  const uint32_t pos = lens[slot] + i;
+  uint32_t tok = pos < n ? trace[(size_t)slot * ra.stride + pos] : 0u;
+  const u32x4 h = philox(u32x4{pos, 0x5eedu, 0u, 0u}, ra.seed, 0x0dd5u);
+  if ((float)(h[0] >> 8) * 0x1p-24f < ra.rate) tok = (tok + 1) % ra.vocab;
+  feed[slot * SV_FEED_W + i] = tok;
+  tree[slot * SV_FEED_W + i] = i | (i - 1) << 8 | ((2u << i) - 1u) << 16;
+}
+
+// ---------------------------------------------------------------- launchers
+
+sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, uint32_t* tokens, float* out,
+                       const uint32_t* tin, uint32_t* meta, const uint32_t* lens, const uint32_t* feed,
+                       const uint32_t* tree, uint32_t* vis, uint32_t n) {
+  if (!sh || !table || !tokens || !out || !tin || !meta || !lens || !feed || !tree || !vis)
+    return fail(SV_ERR_ARG, "embed: null pointer");
+  if (n == 0) return SV_OK;
+  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, out, tin, meta, lens, feed, tree, vis,
+                     sh->hidden, sh->vocab);
+  return check_launch("embed");
+}
+
+sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
+                              uint32_t hidden) {
+  if (!in || !rows || !out) return fail(SV_ERR_ARG, "rmsnorm_rows: null pointer");
+  if (n == 0) return SV_OK;
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, stream, in, rows, out, hidden);
+  return check_launch("rmsnorm_rows");
+}
+
+sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,
+                        const uint32_t* meta, uint32_t n_rows, uint32_t vocab) {
+  if (!logits || !rows || !out) return fail(SV_ERR_ARG, "sample: null pointer");
+  if (n_rows == 0) return SV_OK;
+  if (vocab == 0) return fail(SV_ERR_ARG, "sample: empty vocabulary");
+  hipLaunchKernelGGL(sample_kernel, dim3(n_rows), dim3(SV_SAMPLE_THREADS), 0, stream, logits, rows, out, meta, vocab);
+  return check_launch("sample");
+}
+
+sv_status accept_launch(hipStream_t stream, const sv_run_in* runs, const uint32_t* tokens, uint32_t* out,
+                        uint32_t* lens, uint32_t* feed, sv_gen_state* gen, uint32_t* emitted, uint32_t nruns,
+                        const uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path) {
+  if (!runs || !tokens || !out || !lens || !feed || !gen || !emitted || !tree || !path || !path_len || !on_path)
+    return fail(SV_ERR_ARG, "accept: null pointer");
+  if (nruns == 0) return SV_OK;
+  hipLaunchKernelGGL(accept_kernel, dim3((nruns + 63) / 64), dim3(64), 0, stream, runs, tokens, out, lens, feed, gen,
+                     emitted, nruns, tree, path, path_len, on_path);
+  return check_launch("accept");
+}
+
+sv_status kv_compact_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
+                            const uint32_t* path, const uint32_t* path_len, const uint32_t* lens, uint16_t* k_cache,
+                            uint16_t* v_cache, const uint32_t* page_table, const sv_kv_args* kv) {
+  if (!sh || !runs || !path || !path_len || !lens || !k_cache || !v_cache || !page_table || !kv)
+    return fail(SV_ERR_ARG, "kv_compact: null pointer");
+  if (nruns == 0) return SV_OK;
+  if (sh->n_kv_heads * sh->head_dim / 4 > 256 || sh->head_dim % 4)
+    return fail(SV_ERR_UNSUPPORTED, "kv_compact: %u kv heads x %u dims", sh->n_kv_heads, sh->head_dim);
+  hipLaunchKernelGGL(kv_compact_kernel, dim3(nruns, sh->n_layers), dim3(256), 0, stream, runs, path, path_len, lens,
+                     k_cache, v_cache, page_table, sh->n_kv_heads, sh->head_dim, kv->page_shift, kv->n_pages,
+                     kv->max_pages);
+  return check_launch("kv_compact");
+}
+
+sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nruns, const uint32_t* lens,
+                        uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
+                        uint32_t* tree) {
+  if (!runs || !lens || !feed || !trace || !trace_len || !ra || !tree) return fail(SV_ERR_ARG, "replay: null pointer");
+  if (nruns == 0) return SV_OK;
+  if (ra->vocab == 0) return fail(SV_ERR_ARG, "replay: vocab 0");
+  hipLaunchKernelGGL(replay_kernel, dim3(nruns), dim3(64), 0, stream, runs, nruns, lens, feed, trace, trace_len, *ra,
+                     tree);
+  return check_launch("replay_draft");
+}
+
+}  // namespace sv

@@ -1,0 +1,134 @@
+"""Synthetic models of the benchmark configurations: shapes, int8/bf16 weights, RoPE.
+
+Weights are random (there is no checkpoint offline): N(0, 0.02), int8 symmetric per output
+channel with bf16 scales (tools/convert.py:41-50 `quantize` with group = k) or bf16, and a
+tied bf16 embedding / head. Generation runs on the given torch device (the GPU for the
+16-layer benchmark, the CPU for parity fixtures).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib as L
+
+
+@dataclass(frozen=True)
+class ModelShape:
+    hidden: int = 2048
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = 64
+    ffn: int = 8192
+    vocab: int = 32000
+    vocab_real: int = 32000
+    n_layers: int = 16
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def c(self) -> L.Shape:
+        return L.Shape(self.hidden, self.n_heads, self.n_kv_heads, self.head_dim, self.ffn, self.vocab,
+                       self.vocab_real, self.n_layers)
+
+    def weight_bytes(self, int8: bool = True) -> int:
+        """Bytes one pass over every matrix reads (model.rs:41-46 Matrix::bytes), head included."""
+        H, F = self.hidden, self.ffn
+        mats = [(self.qkv_width, H), (H, self.n_heads * self.head_dim), (2 * F, H), (H, F)]
+        per = sum(m * k + 2 * m for m, k in mats) if int8 else sum(2 * m * k for m, k in mats)
+        return self.n_layers * per + 2 * self.vocab * H
+
+
+# BASELINE.json configs[0..4] shapes; REFERENCE_SHAPE is the reference's own model
+# (engine/src/model.rs:6-18), kept as a second parity shape.
+CONFIG_SHAPE = ModelShape()
+REFERENCE_SHAPE = ModelShape(hidden=1280, n_heads=10, n_kv_heads=2, head_dim=128, ffn=3328, vocab=151680,
+                             vocab_real=151667, n_layers=48)
+
+
+def rope_freq(theta: float = 500000.0, head_dim: int = 64) -> np.ndarray:
+    """f_j = theta^(-2j / head_dim), j < 32: the 32 pairs of dims 0..63 the kernels rotate."""
+    j = np.arange(L.ROPE_PAIRS, dtype=np.float64)
+    return (theta ** (-2.0 * j / head_dim)).astype(np.float32)
+
+
+def quantize_rows(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """int8 per output channel (tools/convert.py:41-50 with group = k): s = bf16(absmax / 127),
+    q = clamp(round_half_even(w / s), -127, 127). Returns (q int8 [m][k], s bf16 [m][1])."""
+    wf = w.float()
+    s = (wf.abs().amax(-1, keepdim=True) / 127).to(torch.bfloat16)
+    sf = s.float()
+    q = torch.where(sf > 0, wf / sf, torch.zeros((), device=w.device)).round().clamp(-127, 127).to(torch.int8)
+    return q, s
+
+
+@dataclass
+class LayerScalars:
+    qkv_scale: float = 1.0
+    o_scale: float = 1.0
+    resid_attn: float = 1.0
+    post_attn: float = 1.0
+    resid_mlp: float = 1.0
+    post_mlp: float = 1.0
+    rope: int = 1
+
+
+@dataclass
+class SyntheticModel:
+    shape: ModelShape
+    int8: bool
+    device: torch.device
+    embed: torch.Tensor                       # bf16 [vocab][hidden]
+    layers: list[dict] = field(default_factory=list)  # name -> (w, scales or None)
+    scalars: list[LayerScalars] = field(default_factory=list)
+
+    @staticmethod
+    def generate(shape: ModelShape, *, int8: bool = True, seed: int = 0, device: str | torch.device = "cpu",
+                 scalars: LayerScalars | list[LayerScalars] | None = None, std: float = 0.02) -> "SyntheticModel":
+        dev = torch.device(device)
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+
+        def normal(m: int, k: int) -> torch.Tensor:
+            return torch.randn(m, k, generator=g, device=dev, dtype=torch.float32) * std
+
+        H, F = shape.hidden, shape.ffn
+        embed = normal(shape.vocab, H).to(torch.bfloat16)
+        layers = []
+        for _ in range(shape.n_layers):
+            lay = {}
+            for name, (m, k) in (("qkv", (shape.qkv_width, H)), ("o", (H, shape.n_heads * shape.head_dim)),
+                                 ("gate_up", (2 * F, H)), ("down", (H, F))):
+                w = normal(m, k)
+                lay[name] = quantize_rows(w) if int8 else (w.to(torch.bfloat16), None)
+                del w
+            layers.append(lay)
+        if scalars is None:
+            sc = [LayerScalars() for _ in range(shape.n_layers)]
+        elif isinstance(scalars, LayerScalars):
+            sc = [scalars for _ in range(shape.n_layers)]
+        else:
+            sc = list(scalars)
+        return SyntheticModel(shape, int8, dev, embed, layers, sc)
+
+    def to(self, device: str | torch.device) -> "SyntheticModel":
+        dev = torch.device(device)
+        layers = [{k: (w.to(dev), None if s is None else s.to(dev)) for k, (w, s) in lay.items()} for lay in self.layers]
+        return SyntheticModel(self.shape, self.int8, dev, self.embed.to(dev), layers, self.scalars)
+
+    def c_layer(self, i: int) -> L.Layer:
+        """The sv_layer of layer i (device pointers: the model must live on the GPU)."""
+        lay, s = self.layers[i], self.scalars[i]
+
+        def mat(name: str) -> L.Matrix:
+            w, sc = lay[name]
+            m, k = w.shape
+            if sc is None:
+                return L.Matrix(w.data_ptr(), None, m, k, L.FMT_BF16, 0)
+            return L.Matrix(w.data_ptr(), sc.data_ptr(), m, k, L.FMT_I8, 31)
+
+        return L.Layer(mat("qkv"), mat("o"), mat("gate_up"), mat("down"), s.qkv_scale, s.o_scale, s.resid_attn,
+                       s.post_attn, s.resid_mlp, s.post_mlp, s.rope, 0)

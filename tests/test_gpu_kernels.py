@@ -1,0 +1,344 @@
+"""GPU parity of each kernel group against the oracle, through the C ABI (libsv_verify.so).
+
+Integer and sampling results are compared bit for bit; fp32 results within tolerances stated
+per test (fp32 accumulation in a different order, activations as bf16 hi + lo pairs: 16
+significant bits per element)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import banner
+from helpers import bf16_bits, close, to_dev, u16_dev_bf16
+from violetto import _lib as L
+from violetto import kernels as K
+from violetto.model import ModelShape, quantize_rows
+
+pytestmark = pytest.mark.gpu
+
+SH = ModelShape(n_layers=2)  # the configs' layer shapes
+
+
+# ------------------------------------------------------------------------------- matmul
+MM_CASES = [
+    # (m, k, fmt)
+    (3072, 2048, "i8"),   # qkv
+    (2048, 8192, "i8"),   # down: k over 8 workgroups
+    (512, 1280, "i8"),    # the reference's k: a partial workgroup of k slices
+    (256, 3328, "bf16"),  # the reference's FFN k
+    (1024, 2048, "bf16"),
+]
+
+
+@pytest.mark.parametrize("m,k,fmt", MM_CASES)
+@pytest.mark.parametrize("n", [1, 5, 16])
+@pytest.mark.parametrize("epi", [L.EPI_NORM, L.EPI_RESID, L.EPI_SWIGLU, L.EPI_HEAD, L.EPI_RAW])
+def test_matmul(gpu, m, k, fmt, n, epi):
+    banner(f"matmul m={m} k={k} {fmt} n={n} epi={epi}")
+    rng = np.random.default_rng(1000 * n + epi)
+    w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+    if fmt == "i8":
+        q, s = quantize_rows(w)
+        wq, sc = q.numpy(), s.view(torch.int16).numpy().view(np.uint16)
+        mat = K.matrix(q.cuda(), s.cuda(), 31)
+        host_w, host_s, gs = wq, sc, 31
+    else:
+        wb = bf16_bits(w.numpy())
+        mat = K.matrix(u16_dev_bf16(wb))
+        host_w, host_s, gs = wb, None, 0
+    x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
+    base = rng.normal(0, 1, (n, m)).astype(np.float32)
+    flags = L.FLAG_WRITE_INV if epi == L.EPI_NORM else (L.FLAG_NORM_IN if epi in (L.EPI_HEAD, L.EPI_RAW) else 0)
+    if epi == L.EPI_RESID:
+        flags = L.FLAG_WRITE_RAW
+    scale, ra, rb = 0.75, 0.9, 1.3
+    vocab_real = m - 7
+    a = L.MatArgs(n, k, m, epi, flags, vocab_real, scale, ra, rb, 1, k, gs)
+    out_m = m // 2 if epi == L.EPI_SWIGLU else m
+    aux_n = n if epi == L.EPI_NORM else n * m
+    aux_ref = np.zeros(aux_n, np.float32)
+    ref = oracle.matmul(L, host_w, host_s, gs, x, a, base=base if epi == L.EPI_RESID else None, aux=aux_ref)
+    y = torch.zeros(n, out_m, device="cuda")
+    aux = torch.zeros(aux_n, device="cuda")
+    K.matmul(mat, to_dev(x), y, n=n, epi=epi, flags=flags, scale=scale, ra=ra, rb=rb,
+             base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux, vocab_real=vocab_real)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    # Tolerance: |error| <= 2e-5 x the norm of the terms summed (hi/lo split: 2^-17 per term).
+    mag = float(np.abs(ref[np.isfinite(ref)]).max())
+    close(got, ref, atol=5e-5 * max(mag, 1.0), rtol=1e-4, what=f"matmul epi {epi}")
+    if epi in (L.EPI_NORM, L.EPI_RESID):
+        close(aux.cpu().numpy(), aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")
+
+
+def test_matmul_rows_gather(gpu):
+    """x_rows gathers input rows (the head's head_rows)."""
+    banner("matmul gather")
+    rng = np.random.default_rng(7)
+    m, k, n = 512, 2048, 4
+    wb = bf16_bits(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+    x = rng.normal(0, 1, (9, k)).astype(np.float32)
+    rows = np.array([8, 0, 3, 3], np.uint32)
+    a = L.MatArgs(n, k, m, L.EPI_HEAD, L.FLAG_NORM_IN, m, 1.0, 0, 0, 1, k, 0)
+    ref = oracle.matmul(L, wb, None, 0, x, a, x_rows=rows)
+    y = torch.zeros(n, m, device="cuda")
+    K.matmul(K.matrix(u16_dev_bf16(wb)), to_dev(x), y, n=n, epi=L.EPI_HEAD, flags=L.FLAG_NORM_IN,
+             x_rows=to_dev(rows))
+    torch.cuda.synchronize()
+    close(y.cpu().numpy(), ref, atol=1e-4, rtol=1e-5, what="gathered head")
+
+
+def test_matmul_repeat_workspace(gpu):
+    """Counters in a shared workspace stay consistent over many calls (the last workgroup
+    resets them): 20 calls in a row give identical results."""
+    banner("matmul repeat")
+    rng = np.random.default_rng(3)
+    m, k, n = 2048, 8192, 5
+    q, s = quantize_rows(torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32)))
+    mat = K.matrix(q.cuda(), s.cuda(), 31)
+    x = to_dev(rng.normal(0, 1, (n, k)).astype(np.float32))
+    ws = K.Workspace(L.lib().sv_matmul_workspace_bytes(n, m, k))
+    outs = []
+    for _ in range(20):
+        y = torch.zeros(n, m, device="cuda")
+        K.matmul(mat, x, y, n=n, epi=L.EPI_RAW, ws=ws)
+        outs.append(y)
+    torch.cuda.synchronize()
+    for y in outs[1:]:
+        assert torch.equal(y, outs[0])
+    assert int(ws.t[: 65536 // 4].abs().sum()) == 0, "counters left non-zero"
+
+
+# ---------------------------------------------------------------------------- attention
+def make_attn_case(sh: ModelShape, runs_T, p0s, *, seed=0, tree=False, page_shift=4, shuffle=True):
+    rng = np.random.default_rng(seed)
+    D, NQ, NKV = sh.head_dim, sh.n_heads, sh.n_kv_heads
+    W = (NQ + 2 * NKV) * D
+    n = sum(runs_T)
+    page = 1 << page_shift
+    max_len = max(p + t for p, t in zip(p0s, runs_T))
+    max_pages = -(-max_len // page)
+    n_runs = len(runs_T)
+    n_pages = n_runs * max_pages + 3
+    perm = rng.permutation(n_pages) if shuffle else np.arange(n_pages)
+    page_table = perm[: n_runs * max_pages].reshape(n_runs, max_pages).astype(np.uint32)
+    k_cache = bf16_bits(rng.normal(0, 1, (1, n_pages, NKV, page, D)).astype(np.float32))
+    v_cache = bf16_bits(rng.normal(0, 1, (1, n_pages, NKV, page, D)).astype(np.float32))
+    qkv = (rng.normal(0, 1, (n, W)) * rng.uniform(0.2, 3, (n, 1))).astype(np.float32)
+    meta = np.zeros((n, 2), np.uint32)
+    vis = np.zeros(n, np.uint32)
+    runs = np.zeros((n_runs, 2), np.uint32)
+    t = 0
+    for r, (T, p0) in enumerate(zip(runs_T, p0s)):
+        runs[r] = (t, T)
+        if tree:
+            # a random tree over the run's rows: parent of row i is a random earlier row
+            parent = [None] + [int(rng.integers(0, i)) for i in range(1, T)]
+            depth = [0] * T
+            sees = [1] * T
+            for i in range(1, T):
+                depth[i] = depth[parent[i]] + 1
+                sees[i] = sees[parent[i]] | (1 << i)
+        else:
+            depth = list(range(T))
+            sees = [(2 << i) - 1 for i in range(T)]
+        for i in range(T):
+            meta[t + i] = (r, p0 + depth[i])
+            vis[t + i] = sees[i]
+        t += T
+    return dict(qkv=qkv, meta=meta, vis=vis, runs=runs, k=k_cache, v=v_cache, page_table=page_table,
+                n_pages=n_pages, max_pages=max_pages, page_shift=page_shift)
+
+
+ATTN_CASES = [
+    # (run lengths, first positions, split, tree)
+    ([5], [512], 128, False),            # config 0's run
+    ([5], [8192], 256, False),           # config 1's run
+    ([1], [0], 32, False),               # no cached keys
+    ([3, 5, 2], [31, 100, 64], 32, False),
+    ([16], [300], 64, True),             # a 16-row draft tree
+    ([16, 9, 1], [33, 1000, 17], 96, True),
+]
+
+
+@pytest.mark.parametrize("runs_T,p0s,split,tree", ATTN_CASES)
+@pytest.mark.parametrize("rope", [1, 0])
+def test_attn_verify(gpu, runs_T, p0s, split, tree, rope):
+    banner(f"attn runs={runs_T} p0={p0s} split={split} tree={tree} rope={rope}")
+    sh = SH
+    c = make_attn_case(sh, runs_T, p0s, seed=len(runs_T) * 31 + split, tree=tree)
+    freq = oracle.np.asarray((500000.0 ** (-2.0 * np.arange(32) / 64)), np.float32)
+    rope_tab = oracle.rope_table(freq, max(p0s) + 20)
+    kv = L.KvArgs(1, 0, 0, len(runs_T), c["page_shift"], c["n_pages"], c["max_pages"], 0)
+    max_splits = max(-(-p // split) + 1 for p in p0s)
+    args = L.AttnArgs(split, max_splits, 0.125 * 1.4426950408889634, rope, 0, 0, 0, 0, 0)
+    runs_flat = c["runs"].reshape(-1).copy()
+    k_ref, v_ref = c["k"].copy(), c["v"].copy()
+    ref = oracle.attn_verify(L, sh, c["qkv"], c["meta"].reshape(-1).copy(), k_ref, v_ref, c["page_table"], rope_tab,
+                             kv, args, runs_flat, c["vis"])
+    kd, vd = to_dev(c["k"]), to_dev(c["v"])
+    out = torch.zeros(sum(runs_T), sh.n_heads * sh.head_dim, device="cuda")
+    K.attn_verify(sh, to_dev(c["qkv"]), to_dev(c["meta"]), kd, vd, to_dev(c["page_table"]), to_dev(rope_tab), kv,
+                  args, to_dev(runs_flat), len(runs_T), max(runs_T), to_dev(c["vis"]), out)
+    torch.cuda.synchronize()
+    close(out.cpu().numpy(), ref, atol=2e-4, rtol=2e-4, what="attention output")
+    # The new keys/values in the cache: V bit-exact (a rounding of the same fp32), K within one
+    # bf16 step (normed and roped in fp32 here, in double in the oracle).
+    kg, vg = kd.cpu().numpy(), vd.cpu().numpy()
+    assert np.array_equal(vg, v_ref), "V cache differs"
+    dk = np.abs(oracle.bf16_to_f32(kg) - oracle.bf16_to_f32(k_ref))
+    assert (dk <= 2 ** -7 * np.abs(oracle.bf16_to_f32(k_ref)) + 1e-30).all(), "K cache off by more than one step"
+
+
+# ------------------------------------------------------------------------------ sampler
+def sample_rows(n, temps, top_ps, seed=11, pos0=100):
+    rows = []
+    for r in range(n):
+        s = seed * 7919 + r
+        rows.append(L.SampleRow(s & 0xFFFFFFFF, (s >> 32) & 0xFFFFFFFF, pos0 + r, float(temps[r % len(temps)]),
+                                float(top_ps[r % len(top_ps)]), L.NO_TOK))
+    return rows
+
+
+@pytest.mark.parametrize("vocab", [32000, 257, 1024, 151680])
+def test_sample_bit_exact(gpu, vocab):
+    banner(f"sample vocab={vocab}")
+    rng = np.random.default_rng(vocab)
+    n = 24
+    logits = (rng.normal(15.4, 0.6, (n, vocab))).astype(np.float32)
+    logits[3, :] = 7.0                       # all ties: lowest id wins at T = 0
+    logits[4, rng.integers(0, vocab, 5)] = logits[4].max() + 0.5  # tied maxima
+    logits[5, vocab // 2:] = -np.inf         # masked tail (vocab_real)
+    temps = [0.0, 0.7, 1.0, 0.6, 1.5, 0.3]
+    top_ps = [1.0, 1.0, 0.95, 0.9, 0.5, 0.99, 0.7, 1.0]
+    rows = sample_rows(n, temps, top_ps)
+    ref = oracle.sample(L, logits, rows)
+    d_rows = torch.from_numpy(np.frombuffer(bytes((L.SampleRow * n)(*rows)), np.uint8).copy()).cuda()
+    out = torch.zeros(n, dtype=torch.int32, device="cuda")
+    K.sample(to_dev(logits), d_rows, out, None, n, vocab)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().view(np.uint32)
+    assert np.array_equal(got, ref), f"ids differ at rows {np.nonzero(got != ref)[0]}"
+
+
+# --------------------------------------------------------------- accept / compact / replay
+def random_runs(rng, n_runs, max_count=16):
+    """Random verify runs over random trees, with sampled tokens that match some drafts."""
+    runs, tokens, tree, out = [], [], np.zeros(n_runs * 16, np.uint32), []
+    first = head0 = 0
+    for r in range(n_runs):
+        count = int(rng.integers(1, max_count + 1))
+        verify = int(count > 1 or rng.integers(0, 2))
+        parent = [0xFF] + [int(rng.integers(0, i)) for i in range(1, count)]
+        depth = [0] * count
+        sees = [1] * count
+        for i in range(1, count):
+            depth[i] = depth[parent[i]] + 1
+            sees[i] = sees[parent[i]] | (1 << i)
+        for i in range(count):
+            tree[r * 16 + i] = depth[i] | (parent[i] << 8) | (sees[i] << 16)
+        toks = [int(x) for x in rng.integers(0, 6, count)]
+        samp = [int(x) for x in rng.integers(0, 6, count)]
+        nhead = count if verify else int(rng.integers(0, 2))
+        runs.append(L.RunIn(r, first, count, head0, nhead, verify))
+        tokens += toks
+        out += samp[:nhead]
+        first += count
+        head0 += nhead
+    return runs, np.array(tokens, np.uint32), tree, np.array(out, np.uint32)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_accept_compact_bit_exact(gpu, seed):
+    banner(f"accept/compact seed={seed}")
+    rng = np.random.default_rng(seed)
+    n_runs = 12
+    runs, tokens, tree, out = random_runs(rng, n_runs)
+    lens = rng.integers(0, 40, n_runs).astype(np.uint32)
+    feed = rng.integers(0, 100, n_runs * 16).astype(np.uint32)
+    gen = []
+    for r in range(n_runs):
+        g = L.GenState()
+        g.remaining = int(rng.choice([0xFFFFFFFF, 1, 2, 3, 10]))
+        g.done = int(rng.random() < 0.15)
+        g.nstop = int(rng.integers(0, 3))
+        for j in range(g.nstop):
+            g.stop[j] = int(rng.integers(0, 6))
+        gen.append(g)
+    n_tok = len(tokens)
+    o_out, o_lens, o_feed, o_gen, o_em, o_path, o_plen, o_on = oracle.accept(L, runs, tokens, out, lens, feed, gen,
+                                                                             tree, n_tok)
+    d_runs = torch.from_numpy(np.frombuffer(bytes((L.RunIn * n_runs)(*runs)), np.uint8).copy()).cuda()
+    d_gen = torch.from_numpy(np.frombuffer(bytes((L.GenState * n_runs)(*gen)), np.uint8).copy()).cuda()
+    d_out, d_lens, d_feed = to_dev(out.copy()), to_dev(lens.copy()), to_dev(feed.copy())
+    d_em = torch.zeros(n_runs, dtype=torch.int32, device="cuda")
+    d_path = torch.zeros(n_runs * 16, dtype=torch.int32, device="cuda")
+    d_plen = torch.zeros(n_runs, dtype=torch.int32, device="cuda")
+    d_on = torch.zeros(max(1, n_tok), dtype=torch.int32, device="cuda")
+    K.accept(d_runs, to_dev(tokens), d_out, d_lens, d_feed, d_gen, d_em, n_runs, to_dev(tree), d_path, d_plen, d_on)
+    torch.cuda.synchronize()
+    u = lambda t: t.cpu().numpy().view(np.uint32)  # noqa: E731
+    assert np.array_equal(u(d_out), o_out)
+    assert np.array_equal(u(d_lens), o_lens)
+    assert np.array_equal(u(d_feed), o_feed)
+    assert np.array_equal(u(d_em), o_em)
+    assert np.array_equal(u(d_path), o_path)
+    assert np.array_equal(u(d_plen), o_plen)
+    assert np.array_equal(u(d_on)[:n_tok], o_on[:n_tok])
+    assert bytes(d_gen.cpu().numpy()) == bytes((L.GenState * n_runs)(*o_gen))
+
+    # kv_compact on the accepted paths (2 layers, shuffled pages).
+    sh = ModelShape(n_layers=2)
+    page_shift, page = 4, 16
+    max_pages = 8
+    n_pages = n_runs * max_pages
+    perm = rng.permutation(n_pages).astype(np.uint32).reshape(n_runs, max_pages)
+    kc = rng.integers(0, 65535, (2, n_pages, sh.n_kv_heads, page, sh.head_dim)).astype(np.uint16)
+    vc = rng.integers(0, 65535, kc.shape).astype(np.uint16)
+    kv = L.KvArgs(1, 0, 0, n_runs, page_shift, n_pages, max_pages, 0)
+    k_ref, v_ref = kc.copy(), vc.copy()
+    oracle.kv_compact(L, sh, runs, o_path, o_plen, o_lens, k_ref, v_ref, perm, kv)
+    kd, vd = to_dev(kc), to_dev(vc)
+    K.kv_compact(sh, d_runs, n_runs, d_path, d_plen, d_lens, kd, vd, to_dev(perm), kv)
+    torch.cuda.synchronize()
+    assert np.array_equal(kd.cpu().numpy(), k_ref)
+    assert np.array_equal(vd.cpu().numpy(), v_ref)
+
+    # replay drafter after accept
+    stride = 64
+    trace = rng.integers(0, 1000, n_runs * stride).astype(np.uint32)
+    trace_len = rng.integers(0, stride, n_runs).astype(np.uint32)
+    ra = L.ReplayArgs(stride, 77, 0.35, 1000)
+    f_ref, t_ref = o_feed.copy(), tree.copy()
+    oracle.replay_draft(L, runs, o_lens, f_ref, trace, trace_len, ra, t_ref)
+    d_tree = to_dev(tree.copy())
+    K.replay_draft(d_runs, n_runs, d_lens, d_feed, to_dev(trace), to_dev(trace_len), ra, d_tree)
+    torch.cuda.synchronize()
+    assert np.array_equal(u(d_feed), f_ref)
+    assert np.array_equal(u(d_tree), t_ref)
+
+
+def test_embed(gpu):
+    banner("embed")
+    rng = np.random.default_rng(5)
+    sh = ModelShape(vocab=1000, n_layers=1)
+    table = bf16_bits(rng.normal(0, 0.02, (sh.vocab, sh.hidden)).astype(np.float32))
+    tokens = np.array([5, L.FEED_ROW + 0, L.FEED_ROW + 2, L.FEED_ROW + 1, 999], np.uint32)
+    tin = np.array([[0, 0], [1, 0], [1, 1], [1, 2], [2, 0]], np.uint32)
+    lens = np.array([10, 20, 30], np.uint32)
+    feed = rng.integers(0, 1000, 3 * 16).astype(np.uint32)
+    tree = np.array([(i % 16) | ((i % 16 + 3) << 8) | ((i * 37 % 65536) << 16) for i in range(48)], np.uint32)
+    vis = np.array([1, 1, 3, 7, 1], np.uint32)
+    o_tok, o_out, o_meta, o_vis = oracle.embed(L, sh, table, tokens, tin, lens, feed, tree, vis)
+    d_tok, d_vis = to_dev(tokens.copy()), to_dev(vis.copy())
+    d_out = torch.zeros(5, sh.hidden, device="cuda")
+    d_meta = torch.zeros(10, dtype=torch.int32, device="cuda")
+    K.embed(sh, u16_dev_bf16(table), d_tok, d_out, to_dev(tin), d_meta, to_dev(lens), to_dev(feed), to_dev(tree),
+            d_vis, 5)
+    torch.cuda.synchronize()
+    assert np.array_equal(d_tok.cpu().numpy().view(np.uint32), o_tok)
+    assert np.array_equal(d_meta.cpu().numpy().view(np.uint32), o_meta.reshape(-1))
+    assert np.array_equal(d_vis.cpu().numpy().view(np.uint32), o_vis)
+    close(d_out.cpu().numpy(), o_out, atol=1e-5, rtol=1e-5, what="embed rows")
