@@ -1,19 +1,25 @@
 #!/usr/bin/env python3
 """Verified tokens/s of the speculative-decoding verify step on one MI355X.
 
-Workload (configs[1], the metric's single-GPU case): the 16-layer 1B decoder (hidden 2048,
-32/8 heads of 64, SwiGLU 8192, vocab 32000) with random int8 per-output-channel weights and a
-tied bf16 head; one stream with 8192 cached tokens (paged KV, pages of 16, K/V ~ N(0, 1)); a
-linear chain of k = 4 drafts per step; greedy acceptance with rollback of rejected rows.
+Model: the 16-layer 1B decoder of BASELINE.json (hidden 2048, 32/8 heads of 64, SwiGLU 8192,
+vocab 32000), random int8 per-output-channel weights (N(0, 0.02) quantised), tied bf16 head;
+paged KV cache (pages of 16 tokens) filled with N(0, 1) bf16.
+
+`value` is configs[1] (the metric's 1-stream case): one stream at 8192 cached tokens, a
+linear chain of k = 4 drafts per step, greedy acceptance with rollback of rejected rows.
+The line also carries configs[2] (`streams32`): 32 streams with contexts U[1024, 8192],
+page tables shuffled over a shared pool, T = 0.7 sampling with per-stream Philox seeds;
+verify rows = 160.
 
 Drafts come from the reference's replay drafter (kernels.metal:1695-1724): before timing, a
-plain greedy decode records the target's own continuation; each verify step then drafts that
-trace with a seeded 35% mistake rate (per-position agreement ~65%), so acceptance behaves as
-with a real drafter and the emitted tokens must reproduce the trace (checked).
+plain decode (greedy, or sampled with the streams' seeds) records the target's own
+continuation; each verify step then drafts that trace with a seeded 35% mistake rate
+(~65% per-position agreement), so acceptance behaves as with a real drafter and the emitted
+tokens must reproduce the trace (checked: `lossless_trace_check`).
 
-A step is one verify pass over the 5 rows (embed, 16 layers, head, sampler, accept, replay
-drafter), captured once as a HIP graph and replayed back to back; `value` = tokens emitted
-over the timed steps / their wall time, inputs resident in HBM.
+A step is one verify pass (embed, 16 layers, head, sampler, accept + replay drafter),
+captured once as a HIP graph and replayed back to back; value = tokens emitted over the
+timed steps / their wall time, with every input resident in HBM.
 """
 from __future__ import annotations
 
@@ -29,11 +35,154 @@ sys.path.insert(0, str(ROOT / "silicon-violetto_amd"))
 
 METRIC = "verified tok/s @1 & 32 seqs, 8k ctx, k=4; verify-step HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
-KV_BYTES_PER_TOKEN_LAYER = 8 * 64 * 2 * 2  # NKV x D x bf16 x (K, V)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def kv_bytes_per_token(shape) -> int:
+    return shape.n_layers * shape.n_kv_heads * shape.head_dim * 2 * 2  # layers x heads x dims x bf16 x (K, V)
+
+
+def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperature: float, shuffle: bool,
+                 steps: int, warmup: int, profile_reps: int, seed: int):
+    """Build the engine state for `streams` sequences, record their trace, time `steps`
+    graph-replayed verify steps. Returns a dict of results (and the engine for reuse)."""
+    import numpy as np
+    import torch
+
+    import violetto
+    from violetto import _lib as L
+    from violetto.model import rope_freq
+
+    k = args.draft
+    rows = k + 1
+    n_steps = warmup + steps + profile_reps + 4
+    trace_n = rows * n_steps + 32
+    max_ctx = max(ctxs)
+    max_seq_len = max_ctx + trace_n + 64
+    page = 16
+    kv_tokens = sum(-(-(c + trace_n + 64) // page) * page for c in ctxs)
+    freq = rope_freq(500000.0, shape.head_dim)
+    eng = violetto.Engine(shape, max_seqs=streams, max_step_tokens=max(16, streams * rows),
+                          max_seq_len=max_seq_len, max_head_rows=max(16, streams * rows), kv_tokens=kv_tokens,
+                          page_shift=4, attn_scale=0.125, freq=freq)
+    eng.set_model(model)
+    rng = np.random.default_rng(seed)
+    slots = [eng.new_seq() for _ in range(streams)]
+    for s in slots:
+        eng.set_sampling(s, temperature, 1.0, seed * 1000 + s + 1)
+    if shuffle:  # pages taken one at a time by randomly ordered sequences: shuffled tables
+        left = {s: c for s, c in zip(slots, ctxs)}
+        while left:
+            s = int(rng.choice(list(left)))
+            n = min(page, left[s])
+            eng.bench_fill(s, n)
+            left[s] -= n
+            if left[s] == 0:
+                del left[s]
+    else:
+        for s, c in zip(slots, ctxs):
+            eng.bench_fill(s, c)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(seed + 1)
+    kd, vd = eng.kv_cache()
+    for t in (kd, vd):
+        for l0 in range(0, t.shape[0], 4):
+            t[l0:l0 + 4].copy_(torch.randn(t[l0:l0 + 4].shape, generator=gen, device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    first = [int(x) for x in rng.integers(0, shape.vocab_real, streams)]
+
+    # The target's own continuation: plain decode, one row per stream and step.
+    log(f"{streams} stream(s): recording a {trace_n}-token trace per stream")
+    for s, c, t in zip(slots, ctxs, first):
+        eng.set_feed(s, c, t)
+    eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=trace_n + 8)
+    eng.graph_capture(0)
+    feed = eng.view("d_feed", (streams, 16))
+    traces = [[t] for t in first]
+    for _ in range(trace_n):
+        eng.graph_replay(1)
+        eng.sync()
+        col = feed[:, 0].cpu().tolist()
+        for i, s in enumerate(slots):
+            traces[i].append(int(col[s]))
+    tr = eng.view("d_trace", (streams, max_seq_len))
+    tr.zero_()
+    for i, s in enumerate(slots):
+        tr[s, ctxs[i]:ctxs[i] + len(traces[i])] = torch.tensor(traces[i], dtype=torch.int32, device="cuda")
+    tl = eng.view("d_trace_len", (streams,))
+    for i, s in enumerate(slots):
+        tl[s] = ctxs[i] + len(traces[i])
+    torch.cuda.synchronize()
+
+    # Verify steps: [input, d1..dk] per stream from the GPU-fed rows; accept; replay drafts.
+    for s, c, t in zip(slots, ctxs, first):
+        eng.set_feed(s, c, t)
+    eng.set_replay(seed + 7, args.mistake_rate)
+    info = eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots],
+                    extra_keys=rows * n_steps + 8)
+    eng.graph_capture(L.STEP_REPLAY)
+    lens = eng.view("d_lens", (streams,))
+    eng.graph_replay(warmup)
+    eng.sync()
+    len0 = lens.cpu().numpy().astype(np.int64)
+    log(f"split {info.split} keys, grid {info.max_splits} splits; timing {steps} steps")
+    torch.cuda.synchronize()
+    eng.sync()
+    t_a = time.perf_counter()
+    eng.graph_replay(steps)
+    eng.sync()
+    torch.cuda.synchronize()
+    t_b = time.perf_counter()
+    len1 = lens.cpu().numpy().astype(np.int64)
+    emitted = int((len1 - len0).sum())
+    secs = t_b - t_a
+    ms_step = secs / steps * 1e3
+    fed = feed[:, 0].cpu().tolist()
+    lossless = all(int(fed[s]) == traces[i][int(len1[s]) - ctxs[i]] for i, s in enumerate(slots))
+    log(f"{emitted} tokens in {steps} steps ({emitted / steps:.2f}/step), {ms_step:.4f} ms/step, "
+        f"{emitted / secs:.0f} tok/s, traces reproduced: {lossless}")
+
+    prof = eng.profile_step(L.STEP_REPLAY, reps=profile_reps)
+    per_step_ms = {kk: v[0] / profile_reps for kk, v in prof.items() if v[1]}
+    ctx_mid = float(((len0 + len1) / 2).sum())
+    H, F, V = shape.hidden, shape.ffn, shape.vocab
+    n_rows = streams * rows
+    mat_bytes = {"qkv": shape.qkv_width * H + 2 * shape.qkv_width, "o": H * H + 2 * H,
+                 "gate_up": 2 * F * H + 2 * 2 * F, "down": H * F + 2 * H, "head": V * H * 2}
+    attn_bytes = ctx_mid * kv_bytes_per_token(shape) / shape.n_layers + n_rows * 2 * shape.n_kv_heads * \
+        shape.head_dim * 2
+    step_bytes = shape.weight_bytes(int8=True) + shape.n_layers * attn_bytes + n_rows * H * 2
+    flops = 2 * n_rows * (shape.n_layers * sum(v for kk, v in mat_bytes.items() if kk != "head") + V * H)
+    res = dict(eng=eng, kd=kd, vd=vd, traces=traces, ctxs=ctxs, slots=slots, steps=steps, warmup=warmup,
+               emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless, prof=prof,
+               per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
+               flops=flops, info=info, rows=rows)
+    return res
+
+
+def roofline_of(res, profile_reps):
+    prof = res["prof"]
+    dominant = max(prof, key=lambda kk: prof[kk][0])
+    bytes_per_launch = res["mat_bytes"].get(dominant, res["attn_bytes"] if dominant == "attn" else 0)
+    d_ms, d_n = prof[dominant]
+    d_avg_ms = d_ms / d_n
+    achieved = bytes_per_launch / (d_avg_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": int(bytes_per_launch),
+            "avg_launch_us": round(d_avg_ms * 1e3, 3)}
+
+
+def step_roofline(res):
+    gbs = res["step_bytes"] / (res["ms_step"] * 1e-3) / 1e9
+    tflops = res["flops"] / (res["ms_step"] * 1e-3) / 1e12
+    bound_ms = max(res["step_bytes"] / (HBM_PEAK_GBS * 1e9), res["flops"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)) * 1e3
+    return {"bytes_per_step": int(res["step_bytes"]), "achieved_gbs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "flops_per_step": int(res["flops"]), "achieved_tflops": round(tflops, 2),
+            "roofline_ms": round(bound_ms, 4), "frac": round(bound_ms / res["ms_step"], 4)}
 
 
 def main() -> int:
@@ -46,166 +195,99 @@ def main() -> int:
     ap.add_argument("--mistake-rate", type=float, default=0.35)
     ap.add_argument("--profile-reps", type=int, default=5, help="steps timed per kernel with hipEvents")
     ap.add_argument("--cpu-steps", type=int, default=2, help="oracle steps for the CPU baseline (0: skip)")
+    ap.add_argument("--streams32-steps", type=int, default=30, help="timed steps of configs[2] (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {max(args.gpus, world)}); "
-              "streams shard across GPUs with no exchange, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {max(args.gpus, world)} GPUs). "
+              "Streams would shard across GPUs with no exchange per step; see DESIGN.md.", file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
-    import violetto
-    from violetto import _lib as L
-    from violetto.model import CONFIG_SHAPE, SyntheticModel, rope_freq
+    from violetto.model import CONFIG_SHAPE, SyntheticModel
 
     assert torch.cuda.is_available(), "bench.py needs an MI355X"
     shape = CONFIG_SHAPE
-    ctx, k = args.ctx, args.draft
-    rows = k + 1
-    n_steps = args.warmup + args.steps + args.profile_reps + 4
-    trace_n = rows * n_steps + 32
-    max_seq_len = ctx + trace_n + 64
-
-    t_setup = time.perf_counter()
     log(f"generating the 16-layer int8 model on the GPU (seed {args.seed})")
     model = SyntheticModel.generate(shape, int8=True, seed=args.seed, device="cuda")
-    freq = rope_freq(500000.0, shape.head_dim)
-    eng = violetto.Engine(shape, max_seqs=1, max_step_tokens=16, max_seq_len=max_seq_len, max_head_rows=16,
-                          kv_tokens=max_seq_len, page_shift=4, attn_scale=0.125, freq=freq)
-    eng.set_model(model)
-    slot = eng.new_seq()
-    eng.bench_fill(slot, ctx)
-    gen = torch.Generator(device="cuda")
-    gen.manual_seed(args.seed + 1)
-    kd, vd = eng.kv_cache()
-    for t in (kd, vd):
-        t.copy_(torch.randn(t.shape, generator=gen, device="cuda", dtype=torch.float32).to(torch.bfloat16))
-    torch.cuda.synchronize()
-    rng = np.random.default_rng(args.seed)
-    t0 = int(rng.integers(0, shape.vocab_real))
 
-    # The target's greedy continuation (plain decode, one row per step, graph-replayed).
-    log(f"recording a {trace_n}-token greedy trace from position {ctx}")
-    eng.set_feed(slot, ctx, t0)
-    eng.plan([(slot, [L.FEED_ROW], False, 1)], extra_keys=trace_n + 8)
-    eng.graph_capture(0)
-    feed = eng.view("d_feed", (16,))
-    trace = [t0]
-    for _ in range(trace_n):
-        eng.graph_replay(1)
-        eng.sync()
-        trace.append(int(feed[0].item()))
-    tr = eng.view("d_trace", (1, max_seq_len))
-    tr.zero_()
-    tr[0, ctx:ctx + len(trace)] = torch.tensor(trace, dtype=torch.int32, device="cuda")
-    eng.view("d_trace_len", (1,)).fill_(ctx + len(trace))
-    torch.cuda.synchronize()
+    r1 = run_workload(args, model, shape, streams=1, ctxs=[args.ctx], temperature=0.0, shuffle=False,
+                      steps=args.steps, warmup=args.warmup, profile_reps=args.profile_reps, seed=args.seed)
+    log("per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r1["per_step_ms"].items()))
+    cpu = cpu_baseline(args, shape, model, r1) if args.cpu_steps > 0 else None
+    r1["eng"].close()
 
-    # The verify step: run [input, d1..dk] from the GPU-fed rows; accept; replay drafts.
-    eng.set_feed(slot, ctx, t0)
-    eng.set_replay(args.seed + 7, args.mistake_rate)
-    info = eng.plan([(slot, [L.FEED_ROW + i for i in range(rows)], True)], extra_keys=rows * n_steps + 8)
-    eng.graph_capture(L.STEP_REPLAY)
-    lens = eng.view("d_lens", (1,))
-    eng.graph_replay(args.warmup)
-    eng.sync()
-    torch.cuda.synchronize()
-    len0 = int(lens[0].item())
-    log(f"setup {time.perf_counter() - t_setup:.1f} s; split {info.split} keys x {info.max_splits} splits; timing "
-        f"{args.steps} steps")
+    s32 = None
+    if args.streams32_steps > 0:
+        import numpy as np
 
-    torch.cuda.synchronize()
-    eng.sync()
-    t_a = time.perf_counter()
-    eng.graph_replay(args.steps)
-    eng.sync()
-    torch.cuda.synchronize()
-    t_b = time.perf_counter()
-    len1 = int(lens[0].item())
-    emitted = len1 - len0
-    secs = t_b - t_a
-    ms_step = secs / args.steps * 1e3
-    value = emitted / secs
-    # Lossless check: the sequence's next input is the trace's token at its position.
-    lossless = int(feed[0].item()) == trace[len1 - ctx]
-    log(f"{emitted} tokens in {args.steps} steps ({emitted / args.steps:.2f}/step), {ms_step:.4f} ms/step, "
-        f"{value:.0f} tok/s, trace reproduced: {lossless}")
-
-    # Per-kernel durations, hipEvents on the engine's stream around each kernel.
-    prof = eng.profile_step(L.STEP_REPLAY, reps=args.profile_reps)
-    per_step_ms = {kk: v[0] / args.profile_reps for kk, v in prof.items() if v[1]}
-    dominant = max(prof, key=lambda kk: prof[kk][0])
-    H, F, V = shape.hidden, shape.ffn, shape.vocab
-    mat_bytes = {"qkv": shape.qkv_width * H + 2 * shape.qkv_width, "o": H * H + 2 * H,
-                 "gate_up": 2 * F * H + 2 * 2 * F, "down": H * F + 2 * H, "head": V * H * 2}
-    ctx_mid = (len0 + len1) / 2
-    attn_bytes = ctx_mid * KV_BYTES_PER_TOKEN_LAYER + rows * 2 * 8 * 64 * 2
-    bytes_per_launch = mat_bytes.get(dominant, attn_bytes if dominant == "attn" else 0)
-    d_ms, d_n = prof[dominant]
-    d_avg_ms = d_ms / d_n
-    achieved = bytes_per_launch / (d_avg_ms * 1e-3) / 1e9
-    step_bytes = shape.weight_bytes(int8=True) + shape.n_layers * attn_bytes + rows * H * 2
-    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    log("per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in per_step_ms.items()))
-
-    cpu = None
-    if args.cpu_steps > 0:
-        cpu = cpu_baseline(args, shape, model, eng, kd, vd, trace, ctx, rows, freq)
+        rng = np.random.default_rng(args.seed + 100)
+        ctxs = [int(x) for x in rng.integers(1024, 8193, 32)]
+        r2 = run_workload(args, model, shape, streams=32, ctxs=ctxs, temperature=0.7, shuffle=True,
+                          steps=args.streams32_steps, warmup=5, profile_reps=2, seed=args.seed + 1)
+        log("32 streams, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r2["per_step_ms"].items()))
+        s32 = {"value": round(r2["value"], 2), "unit": "verified tok/s", "ms_per_step": round(r2["ms_step"], 5),
+               "steps": r2["steps"], "emitted_per_step": round(r2["emitted"] / r2["steps"], 3),
+               "lossless_trace_check": r2["lossless"],
+               "config": {"workload": "configs[2]: 32 streams, ctx U[1024,8192] (mean %d), shuffled page tables, "
+                                      "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
+                          "rows_per_step": 32 * r2["rows"]},
+               "roofline": roofline_of(r2, 2), "step_roofline": step_roofline(r2),
+               "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r2["per_step_ms"].items()}}
+        r2["eng"].close()
 
     line = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(r1["value"], 2),
         "unit": "verified tok/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
+        "ms_per_step": round(r1["ms_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 weights x fp32 activations (bf16 hi+lo MFMA, fp32 accumulate)",
-        "data": "synthetic (random N(0,0.02) int8 weights, N(0,1) bf16 KV, replayed greedy drafts)",
+        "data": "synthetic (random N(0,0.02) int8 weights, N(0,1) bf16 KV, replayed drafts of the target's own decode)",
         "config": {"workload": "configs[1]: 16-layer int8 1B verify step, 1 stream, 8192 ctx, k=4 chain, greedy, "
-                               "KV rollback", "streams": 1, "ctx": ctx, "k": k, "rows_per_step": rows,
-                   "draft_mistake_rate": args.mistake_rate},
-        "emitted_per_step": round(emitted / args.steps, 3),
-        "lossless_trace_check": lossless,
-        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "bytes_per_launch": int(bytes_per_launch), "avg_launch_us": round(d_avg_ms * 1e3, 3)},
-        "step_roofline": {"bytes_per_step": int(step_bytes), "achieved": round(step_gbs, 1), "peak": HBM_PEAK_GBS,
-                          "unit": "GB/s", "frac": round(step_gbs / HBM_PEAK_GBS, 4)},
-        "kernel_ms_per_step": {kk: round(v, 4) for kk, v in per_step_ms.items()},
+                               "KV rollback", "streams": 1, "ctx": args.ctx, "k": args.draft,
+                   "rows_per_step": r1["rows"], "draft_mistake_rate": args.mistake_rate},
+        "emitted_per_step": round(r1["emitted"] / args.steps, 3),
+        "lossless_trace_check": r1["lossless"],
+        "roofline": roofline_of(r1, args.profile_reps),
+        "step_roofline": step_roofline(r1),
+        "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r1["per_step_ms"].items()},
         "cpu_baseline": cpu,
+        "streams32": s32,
     }
     print(json.dumps(line), flush=True)
-    eng.close()
     return 0
 
 
-def cpu_baseline(args, shape, model, eng, kd, vd, trace, ctx, rows, freq):
+def cpu_baseline(args, shape, model, r1):
     """The oracle's verify step (C, OpenMP over output rows and heads) on this host's cores, on
-    the same workload: args.cpu_steps steps of the 16-layer model at this context."""
+    the configs[1] workload: args.cpu_steps steps of the 16-layer model at its context."""
     import numpy as np
     import torch
 
     sys.path.insert(0, str(ROOT / "oracle"))
     import oracle
     from violetto import _lib as L
+    from violetto.model import rope_freq
 
+    eng, kd, vd, trace, ctx, rows = r1["eng"], r1["kd"], r1["vd"], r1["traces"][0], r1["ctxs"][0], r1["rows"]
     log(f"CPU baseline: copying the model to host, {args.cpu_steps} oracle steps")
     emb, lay, sc = oracle.host_weights(model)
     max_len = ctx + 16 * (args.cpu_steps + 2)
     ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=1, max_seq_len=max_len, kv_tokens=max_len,
-                              attn_scale=0.125, freq=freq)
+                              attn_scale=0.125, freq=rope_freq(500000.0, shape.head_dim))
     s = ref.new_seq()
     ref.bench_fill(s, ctx)
-    pages = eng.seq_pages(0)[: ref.n_pages]
-    assert pages == ref.pool.pages(s)[: len(pages)]
+    ref_pages = ref.pool.pages(s)
+    assert eng.seq_pages(0)[: len(ref_pages)] == ref_pages, "page order differs"
     n = min(ref.n_pages, kd.shape[1])
     ref.k[:, :n] = kd[:, :n].view(torch.int16).cpu().numpy().view(np.uint16)
     ref.v[:, :n] = vd[:, :n].view(torch.int16).cpu().numpy().view(np.uint16)
@@ -217,19 +299,22 @@ def cpu_baseline(args, shape, model, eng, kd, vd, trace, ctx, rows, freq):
     ra = L.ReplayArgs(max_len, args.seed + 7, args.mistake_rate, shape.vocab_real)
     run_in = [L.RunIn(s, 0, rows, 0, rows, 1)]
     oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tr_len, ra, ref.tree)
-    emitted, secs = 0, 0.0
+    emitted, secs, agree = 0, 0.0, True
     for _ in range(args.cpu_steps):
+        pos = int(ref.lens[s])
         t_a = time.perf_counter()
         ids, _, em, _ = ref.step([(s, [L.FEED_ROW + i for i in range(rows)], True)])
         secs += time.perf_counter() - t_a
         emitted += int(em[0])
+        agree = agree and [int(x) for x in ids[: em[0]]] == trace[pos - ctx + 1: pos - ctx + 1 + int(em[0])]
         oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tr_len, ra, ref.tree)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    log(f"CPU: {emitted} tokens in {secs:.2f} s over {args.cpu_steps} steps, {threads} threads")
+    log(f"CPU: {emitted} tokens in {secs:.2f} s over {args.cpu_steps} steps, {threads} threads; "
+        f"oracle tokens = GPU trace: {agree}")
     return {"value": round(emitted / secs, 3), "unit": "verified tok/s", "cores": threads, "kind": "port",
             "sample": f"{args.cpu_steps} verify steps of the configs[1] workload (16 layers, 1 stream, {ctx} ctx, "
                       f"k={rows - 1}) by the C oracle, OpenMP over output rows and attention heads; "
-                      f"{secs / args.cpu_steps:.2f} s/step"}
+                      f"{secs / args.cpu_steps:.2f} s/step; emitted tokens equal the GPU's: {agree}"}
 
 
 if __name__ == "__main__":

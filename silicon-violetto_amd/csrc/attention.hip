@@ -10,17 +10,26 @@
 //   - Splits 0..nsplit-2 own `split` cached keys each; the last split owns the run's new
 //     keys: it norms and ropes them, rounds K and V to bf16, writes them to the cache at
 //     p0 + row and keeps them in LDS.
-//   - Keys go in batches of 32 (wave w takes batches w, w + 4, ...): S^T = K Q^T on
+//   - Keys go in batches of 32 (wave w takes batches w, w + 4, ..., the next one's K/V in
+//     flight while the current one is multiplied; the first is issued before the queries
+//     are built): S^T = K Q^T on
 //     v_mfma_f32_16x16x32_bf16 (two 16-key tiles, hi and lo), p = 2^s for visible keys (no
 //     running max: q and k are rms-normed, so scores are bounded, kernels.metal:804-806),
 //     then O^T += V^T P^T with P (hi, lo) taken straight from the S^T accumulators' layout.
 //     K rows are read as 16-byte slices; each V row is read whole by 16 lanes (8 bytes per
 //     lane for D = 64), and the matrix-core operand takes one of its dims per tile.
-//   - The 4 waves' (l, o) meet in LDS; the split's partial goes to the workspace; the last
-//     split to arrive (agent-scope counter per (run, kv head)) sums the partials in split
-//     order and writes o / l.
+//   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace;
+//     attn_merge_kernel (one workgroup per run and kv head, the next launch) sums the
+//     partials in split order and writes o / l. (A last-arriving-workgroup merge would need
+//     an agent-scope fence, which on gfx950 writes back and invalidates the XCD's L2.)
 #include "sv_device.h"
 #include "sv_internal.h"
+
+#define SV_TRY_LAUNCH(what)                        \
+  do {                                             \
+    const sv_status st_ = check_launch(what);      \
+    if (st_ != SV_OK) return st_;                  \
+  } while (0)
 
 namespace sv {
 
@@ -36,7 +45,6 @@ struct AttnParams {
   float* out;
   float* part_o;
   float* part_l;
-  uint32_t* counters;
   uint32_t NQ, NKV, G, W, KOFF, VOFF;
   uint32_t split, max_splits;
   float scale_log2;
@@ -63,51 +71,57 @@ struct VWord<8> {
   typedef u32x4 type;
 };
 
-// One batch of 32 keys [kb, kb + 32) below kend, for this wave: scores, p, and O += V P.
-// NEW: the keys are the run's new ones, in LDS (index key - p0), masked by each column's vis.
-template <int D, int NCT, bool NEW>
-__device__ __forceinline__ void key_batch(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t kb, uint32_t kend,
-                                          uint32_t p0, uint32_t ncols, uint32_t t0, const uint16_t* nk,
-                                          const uint16_t* nv, const bf16x8 (&qh)[NCT][D / 32],
-                                          const bf16x8 (&ql)[NCT][D / 32], f32x4 (&O)[D / 16][NCT],
-                                          float (&lsum)[NCT], int lane) {
-  constexpr int KST = D / 32, VE = D / 16;
+// One batch of 32 keys [kb, kb + 32) below kend, for one wave: its K and V words (loaded
+// ahead of use) and the products. NEW: the keys are the run's new ones, in LDS (index
+// key - p0), masked by each column's vis.
+template <int D>
+struct KvBatch {
+  static constexpr int KST = D / 32, VE = D / 16;
   typedef typename VWord<VE>::type vword;
+  u32x4 kw[2][KST];  // lane (c16, q): key kb + 16 mt + c16, dims 32 ks + 8 q .. + 7
+  vword vw[8];       // slot j: key kb + 16 (j / 4) + 4 q + j % 4, dims VE c16 .. + VE - 1
+};
+
+template <int D, bool NEW>
+__device__ __forceinline__ void load_batch(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t kb, uint32_t kend,
+                                           uint32_t p0, const uint16_t* nk, const uint16_t* nv, KvBatch<D>& b,
+                                           int lane) {
+  constexpr int KST = D / 32, VE = D / 16;
+  typedef typename KvBatch<D>::vword vword;
   const int c16 = lane & 15, q = lane >> 4;
-  // Row pointers of the two 16-key tiles (a tile never straddles a page: pages hold >= 16).
-  const uint16_t* kt[2];
-  const uint16_t* vt[2];
-  uint32_t tfirst[2];
+  // A tile of 16 keys never straddles a page (pages hold >= 16 keys, kb is a multiple of 32).
 #pragma unroll
   for (int mt = 0; mt < 2; mt++) {
     const uint32_t first = min(kb + 16 * mt, kend - 1);
-    tfirst[mt] = first;
+    const uint16_t* kt;
+    const uint16_t* vt;
     if (NEW) {
-      kt[mt] = nk + (size_t)(first - p0) * D;
-      vt[mt] = nv + (size_t)(first - p0) * D;
+      kt = nk + (size_t)(first - p0) * D;
+      vt = nv + (size_t)(first - p0) * D;
     } else {
       const size_t off = kv_off<D>(p, seq, g, first);
-      kt[mt] = p.kc + off;
-      vt[mt] = p.vc + off;
+      kt = p.kc + off;
+      vt = p.vc + off;
+    }
+    const uint32_t key = min(kb + 16 * mt + c16, kend - 1);
+    const uint16_t* kr = kt + (size_t)(key - first) * D;
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = *(const u32x4*)(kr + 32 * ks + 8 * q);
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      const uint32_t vk = min(kb + 16 * mt + 4 * q + jj, kend - 1);
+      b.vw[4 * mt + jj] = *(const vword*)(vt + (size_t)(vk - first) * D + VE * c16);
     }
   }
-  // K: lane (c16, q) reads key kb + 16 mt + c16, dims 32 ks + 8 q .. + 7.
-  u32x4 kw[2][KST];
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++) {
-    const uint32_t key = min(kb + 16 * mt + c16, kend - 1);
-    const uint16_t* kr = kt[mt] + (size_t)(key - tfirst[mt]) * D;
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++) kw[mt][ks] = *(const u32x4*)(kr + 32 * ks + 8 * q);
-  }
-  // V: slot j is key kb + 16 (j / 4) + 4 q + j % 4; lane reads its dims VE c16 .. + VE-1.
-  vword vw[8];
-#pragma unroll
-  for (int j = 0; j < 8; j++) {
-    const int mt = j >> 2;
-    const uint32_t key = min(kb + 16 * mt + 4 * q + (j & 3), kend - 1);
-    vw[j] = *(const vword*)(vt[mt] + (size_t)(key - tfirst[mt]) * D + VE * c16);
-  }
+}
+
+template <int D, int NCT, bool NEW>
+__device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch<D>& b, uint32_t kb, uint32_t kend,
+                                              uint32_t p0, uint32_t ncols, uint32_t t0,
+                                              const bf16x8 (&qh)[NCT][D / 32], const bf16x8 (&ql)[NCT][D / 32],
+                                              f32x4 (&O)[D / 16][NCT], float (&lsum)[NCT], int lane) {
+  constexpr int KST = D / 32, VE = D / 16;
+  const int c16 = lane & 15, q = lane >> 4;
   // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
   f32x4 S[2][NCT];
 #pragma unroll
@@ -117,7 +131,7 @@ __device__ __forceinline__ void key_batch(const AttnParams& p, uint32_t seq, uin
       f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KST; ks++) {
-        const bf16x8 kk = __builtin_bit_cast(bf16x8, kw[mt][ks]);
+        const bf16x8 kk = __builtin_bit_cast(bf16x8, b.kw[mt][ks]);
         a = mfma16(kk, qh[ct][ks], a);
         a = mfma16(kk, ql[ct][ks], a);
       }
@@ -150,7 +164,7 @@ __device__ __forceinline__ void key_batch(const AttnParams& p, uint32_t seq, uin
     u32x4 a;
     const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
 #pragma unroll
-    for (int jj = 0; jj < 4; jj++) a[jj] = __builtin_amdgcn_perm(vw[2 * jj + 1][dt >> 1], vw[2 * jj][dt >> 1], sel);
+    for (int jj = 0; jj < 4; jj++) a[jj] = __builtin_amdgcn_perm(b.vw[2 * jj + 1][dt >> 1], b.vw[2 * jj][dt >> 1], sel);
     const bf16x8 av = __builtin_bit_cast(bf16x8, a);
 #pragma unroll
     for (int ct = 0; ct < NCT; ct++) {
@@ -165,7 +179,6 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
   extern __shared__ float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
   __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
-  __shared__ uint32_t flag;
   float* ored = lds;
   float* lred = lds + 4 * COLS * D;
 
@@ -187,6 +200,12 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   }
   if (s >= nsplit) return;
   const bool newest = s == nsplit - 1;
+
+  // This wave's first batch of cached keys goes out before the queries are built.
+  const uint32_t kbeg = s * p.split, kend = newest ? p0 : min(kbeg + p.split, p0);
+  const uint32_t nb = newest ? 0u : (kend - kbeg + 31) / 32;
+  KvBatch<D> cur;
+  if ((uint32_t)wv < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kend, p0, nullptr, nullptr, cur, lane);
 
   // Queries (kernels.metal:1022-1039 with norm_rope :727-736): k slot j of step ks is dim
   // 32 ks + 8 q + j.
@@ -290,12 +309,18 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
     for (int dt = 0; dt < VE; dt++) O[dt][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   if (newest) {
-    if (wv == 0) key_batch<D, NCT, true>(p, seq, g, p0, p0 + T, p0, ncols, t0, nk, nv, qh, ql, O, lsum, lane);
+    if (wv == 0) {
+      KvBatch<D> nb0;
+      load_batch<D, true>(p, seq, g, p0, p0 + T, p0, nk, nv, nb0, lane);
+      compute_batch<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane);
+    }
   } else {
-    const uint32_t kbeg = s * p.split, kend = min(kbeg + p.split, p0);
-    const uint32_t nb = (kend - kbeg + 31) / 32;
-    for (uint32_t b = wv; b < nb; b += 4)
-      key_batch<D, NCT, false>(p, seq, g, kbeg + 32 * b, kend, p0, ncols, t0, nk, nv, qh, ql, O, lsum, lane);
+    for (uint32_t b = wv; b < nb; b += 4) {
+      KvBatch<D> nxt;
+      if (b + 4 < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * (b + 4), kend, p0, nullptr, nullptr, nxt, lane);
+      compute_batch<D, NCT, false>(p, cur, kbeg + 32 * b, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
+      cur = nxt;
+    }
   }
 
   // This wave's (l, o) to LDS: lane holds column 16 ct + c16, dims VE (4 q + i) + dt.
@@ -324,19 +349,60 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   for (uint32_t idx = tid; idx < ncols; idx += 256)
     pl[idx] = ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx];
 
-  // The last split of (run, head) merges all (attn_dec_reduce, kernels.metal:1332-1362).
-  if (!arrive_last(&p.counters[r * p.NKV + g], nsplit, &flag)) return;
+}
+
+// attn_dec_reduce (kernels.metal:1316-1362) for the fused verify attention: one workgroup
+// per (run, kv head, column) sums the split partials (plain sums: no running max) and writes
+// o / l. Thread (part, d) adds splits part, part + P, ... eight loads in flight at a time; the
+// P parts are then added in part order. XSA and the gate are off (xsa = 0, gate = 1).
+template <int D>
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
+  constexpr int P = 256 / D;
+  __shared__ float so[P][D];
+  __shared__ float sl[P];
+  const uint32_t r = blockIdx.x, g = blockIdx.y, col = blockIdx.z, tid = threadIdx.x;
+  const uint32_t d = tid % D, part = tid / D;
+  const uint32_t t0 = p.runs[2 * r], T = p.runs[2 * r + 1];
+  const uint32_t ncols = T * p.G;
+  if (col >= ncols) return;
+  const uint32_t p0 = p.meta[2 * t0 + 1];
+  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
+  if (nsplit > p.max_splits) return;  // the attention kernel wrote NaN
   const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
-  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
-    const uint32_t col = idx / D, d = idx % D;
-    float o = 0.0f, l = 0.0f;
-    for (uint32_t sp = 0; sp < nsplit; sp++) {
-      o += p.part_o[(rec0 + sp) * p.maxcols * D + idx];
-      l += p.part_l[(rec0 + sp) * p.maxcols + col];
+  const size_t so_stride = (size_t)p.maxcols * D;
+  const float* po = p.part_o + rec0 * so_stride + (size_t)col * D + d;
+  const float* pl = p.part_l + rec0 * p.maxcols + col;
+  float o = 0.0f, l = 0.0f;
+  uint32_t sp = part;
+  for (; sp + 7 * P < nsplit; sp += 8 * P) {
+    float ov[8], lv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      ov[u] = po[(sp + u * P) * so_stride];
+      lv[u] = pl[(sp + u * P) * p.maxcols];
     }
-    const uint32_t i = col / p.G, h = g * p.G + col % p.G;
-    p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = o / l;
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      o += ov[u];
+      l += lv[u];
+    }
   }
+  for (; sp < nsplit; sp += P) {
+    o += po[sp * so_stride];
+    l += pl[sp * p.maxcols];
+  }
+  so[part][d] = o;
+  if (d == 0) sl[part] = l;
+  __syncthreads();
+  if (part != 0) return;
+  float ot = so[0][d], lt = sl[0];
+#pragma unroll
+  for (int u = 1; u < P; u++) {
+    ot += so[u][d];
+    lt += sl[u];
+  }
+  const uint32_t i = col / p.G, h = g * p.G + col % p.G;
+  p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = ot / lt;
 }
 
 // Dynamic LDS of up to 4 x 64 x 128 floats (+ l): allow it once per instantiation, outside
@@ -366,7 +432,7 @@ static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
 
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run) {
   const size_t maxcols = cols_pad(sh, max_run);
-  size_t b = WS_COUNTER_BYTES;
+  size_t b = 0;
   b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * sh->head_dim * 4;
   b = (b + 255) / 256 * 256;
   b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * 4;
@@ -403,9 +469,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.runs = runs;
   p.vis = vis;
   p.out = out;
-  if ((size_t)n_runs * NKV * 4 > WS_COUNTER_BYTES) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u runs", n_runs);
-  p.counters = (uint32_t*)ws;
-  size_t off = WS_COUNTER_BYTES;
+  size_t off = 0;
   p.part_o = (float*)((char*)ws + off);
   off += (size_t)n_runs * NKV * args->max_splits * maxcols * D * 4;
   off = (off + 255) / 256 * 256;
@@ -445,7 +509,10 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     }
   }
 #undef SV_ATTN
-  return check_launch("attn_verify");
+  SV_TRY_LAUNCH("attn_verify");
+  if (D == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
+  else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
+  return check_launch("attn_merge");
 }
 
 }  // namespace sv

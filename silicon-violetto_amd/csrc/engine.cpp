@@ -56,8 +56,8 @@ extern "C" const char* sv_last_error(void) { return g_error.c_str(); }
 extern "C" sv_status sv_embed(void* stream, const sv_shape* shape, const uint16_t* d_table, uint32_t* d_tokens,
                               float* d_out, const uint32_t* d_tin, uint32_t* d_meta, const uint32_t* d_lens,
                               const uint32_t* d_feed, const uint32_t* d_tree, uint32_t* d_vis, uint32_t n) {
-  return embed_launch((hipStream_t)stream, shape, d_table, d_tokens, d_out, d_tin, d_meta, d_lens, d_feed, d_tree,
-                      d_vis, n);
+  return embed_launch((hipStream_t)stream, shape, d_table, d_tokens, d_tokens, d_out, d_tin, d_meta, d_lens, d_feed,
+                      d_tree, d_vis, n);
 }
 
 extern "C" sv_status sv_rmsnorm_rows(void* stream, const float* d_in, const uint32_t* d_rows, float* d_out, uint32_t n,
@@ -161,7 +161,10 @@ struct sv_engine {
   uint32_t *lens = nullptr, *feed = nullptr, *tree = nullptr, *trace = nullptr, *trace_len = nullptr;
   sv_gen_state* gen = nullptr;
   // device: one step set (plan.rs writes these per step)
-  uint32_t *tokens = nullptr, *tin = nullptr, *vis = nullptr, *head_rows = nullptr, *attn_runs = nullptr;
+  // tokens: the plan's ids (FEED_ROW + i kept, so a captured step can be replayed); tok_res:
+  // the ids embed resolved, which accept compares.
+  uint32_t *tokens = nullptr, *tok_res = nullptr, *tin = nullptr, *vis = nullptr, *head_rows = nullptr,
+           *attn_runs = nullptr;
   sv_sample_row* sample_rows = nullptr;
   sv_run_in* runs = nullptr;
   uint32_t *out_ids = nullptr, *emitted = nullptr, *meta = nullptr, *path = nullptr, *path_len = nullptr,
@@ -211,7 +214,7 @@ struct sv_engine {
 
   ~sv_engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
-    void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tin, vis,
+    void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
                     head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
                     attn, mixed, act, inv, logits, ws};
     for (void* b : bufs)
@@ -302,7 +305,8 @@ struct sv_engine {
     if (!planned) return fail(SV_ERR_STATE, "no plan");
     const Plan& P = plan;
     const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
-    SV_TIMED(SV_KIND_EMBED, embed_launch(stream, &sh, embed, tokens, h, tin, meta, lens, feed, tree, vis, n));
+    SV_TIMED(SV_KIND_EMBED,
+             embed_launch(stream, &sh, embed, tokens, tok_res, h, tin, meta, lens, feed, tree, vis, n));
     sv_attn_args aa{};
     aa.split = P.split;
     aa.max_splits = P.max_splits;
@@ -331,20 +335,15 @@ struct sv_engine {
                                     nullptr, nullptr));
       SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
     }
-    SV_TIMED(SV_KIND_ACCEPT, accept_launch(stream, runs, tokens, out_ids, lens, feed, gen, emitted, P.n_runs, tree,
-                                           path, path_len, on_path));
+    // accept + kv_compact + replay drafter (encode.rs:394-435, 439-451) as one launch.
     const bool compact = (flags & SV_STEP_COMPACT) || (P.branches && !(flags & SV_STEP_NO_COMPACT));
-    if (compact) {
-      const sv_kv_args kv = kv_args(0);
-      SV_TIMED(SV_KIND_COMPACT,
-               kv_compact_launch(stream, &sh, runs, P.n_runs, path, path_len, lens, k_cache, v_cache, page_table, &kv));
-    }
-    if (flags & SV_STEP_REPLAY) {
-      sv_replay_args ra = replay;
-      ra.stride = cfg.max_seq_len;
-      ra.vocab = sh.vocab_real;
-      SV_TIMED(SV_KIND_REPLAY, replay_launch(stream, runs, P.n_runs, lens, feed, trace, trace_len, &ra, tree));
-    }
+    sv_replay_args ra = replay;
+    ra.stride = cfg.max_seq_len;
+    ra.vocab = sh.vocab_real;
+    const sv_kv_args kv0 = kv_args(0);
+    SV_TIMED(SV_KIND_ACCEPT, step_tail_launch(stream, &sh, runs, P.n_runs, tok_res, out_ids, lens, feed, gen, emitted,
+                                              tree, path, path_len, on_path, compact, k_cache, v_cache, page_table,
+                                              &kv0, (flags & SV_STEP_REPLAY) ? &ra : nullptr, trace, trace_len));
     return SV_OK;
   }
 };
@@ -396,6 +395,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   ALLOC(trace_len, S);
   ALLOC(gen, S);
   ALLOC(tokens, n);
+  ALLOC(tok_res, n);
   ALLOC(tin, 2 * (size_t)n);
   ALLOC(vis, n);
   ALLOC(head_rows, n);
@@ -714,8 +714,8 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     P.verify.push_back(r.verify ? 1u : 0u);
     e->seq_len[slot] += count;
   }
-  if (head_rows.size() > e->cfg.max_head_rows || head_rows.size() > 16)
-    return fail(SV_ERR_CAPACITY, "%zu head rows (max %u)", head_rows.size(), std::min(16u, e->cfg.max_head_rows));
+  if (head_rows.size() > e->cfg.max_head_rows)
+    return fail(SV_ERR_CAPACITY, "%zu head rows (max %u)", head_rows.size(), e->cfg.max_head_rows);
   P.n = n;
   P.n_head = (uint32_t)head_rows.size();
   P.n_runs = n_runs;

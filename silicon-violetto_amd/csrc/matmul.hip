@@ -2,21 +2,23 @@
 // group: engine/src/kernels.metal:151-690, chosen by Matmul::for_tokens, encode.rs:33-44).
 //
 // Skinny path (n <= 16 rows, the 1-5 row verify step): weight-streaming on the matrix cores.
-//   - A workgroup is 4 waves; each wave owns one k-slice of KS = 256 and RT tiles of 16
-//     output rows. Its X slice (16 tokens x 256 k, fp32) is loaded once, split into bf16
-//     hi + lo (16 significant bits) and kept in registers as the MFMA B operands, while the
-//     weights stream past: 16 rows x 16 bytes per lane per 64-k block, one dwordx4 each
-//     (int8) or two (bf16), converted to bf16 in registers (int8 is exact in bf16).
+//   - A workgroup of W = 4 or 8 waves owns RT tiles of 16 output rows over the whole of k;
+//     wave w takes the k chunks of 256 numbered w, w + W, ... For each chunk, its X (16
+//     tokens x 256 k, fp32) is loaded once, split into bf16 hi + lo (16 significant bits)
+//     and held in registers as the MFMA B operands while the chunk's weights stream past:
+//     16 rows x 16 bytes per lane per 64-k block, one dwordx4 each (int8) or two (bf16),
+//     converted to bf16 in registers (int8 is exact in bf16); the next chunk's weights are
+//     in flight during the products.
 //   - Products run on v_mfma_f32_16x16x32_bf16 (fp32 accumulate); hi and lo each take one
 //     MFMA, so the fp32 activations lose nothing the tolerance can see, and the VALU only
 //     converts weights (about 1.5 ops per byte, where an fp32 FMA GEMV at 5 rows needs 6).
-//   - The 4 waves' partial sums meet in LDS in a fixed order. When k needs more than one
-//     workgroup (kgroups > 1), each writes its partial to the workspace and the last to
-//     arrive (an agent-scope counter per row group) adds them in workgroup order and runs
-//     the epilogue, so results do not depend on scheduling.
+//   - The waves' partial sums meet in LDS and are added in wave order: no partial sum leaves
+//     the workgroup, so there is no cross-workgroup synchronisation (on gfx950 an agent-scope
+//     fence writes back and invalidates the XCD's whole L2) and results do not depend on
+//     scheduling.
 //   - The sum of squares of X for the folded rms-norm (EPI_NORM/SWIGLU, NORM_IN) rides
 //     along the same path.
-// int8 weights need one scale per k-slice: groups of 256 or more, or one scale per row
+// int8 weights need one scale per k chunk: groups of 256 or more, or one scale per row
 // (per-output-channel, any k).
 #include "sv_device.h"
 #include "sv_internal.h"
@@ -31,59 +33,63 @@ struct MMParams {
   float* y;
   const float* base;
   float* aux;
-  float* part;
-  uint32_t* counters;
-  uint32_t n, k, m, epi, flags, vocab_real, gshift, kgroups, slices, per_row;
+  uint32_t n, k, m, epi, flags, vocab_real, gshift, chunks, per_row;
   float scale, ra, rb;
 };
 
-constexpr int KS = 256;  // k per wave
-constexpr int NBLK = KS / 64;
+constexpr int KC = 256;  // k per chunk: one X chunk in registers, 4 blocks of 64
+constexpr int NBLK = KC / 64;
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-template <int FMT, int RT>
-__global__ __launch_bounds__(256) void mm_skinny(MMParams p) {
+// One workgroup of W waves owns RT tiles of 16 output rows over the whole of k: wave wv
+// takes k chunks wv, wv + W, ... (so no partial sum ever leaves the workgroup).
+template <int FMT, int RT, int W>
+__global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
   constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2;  // dwordx4 loads per lane per 64-k block
+  constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t = lane & 15, q = lane >> 4;
-  const uint32_t xg = blockIdx.x, z = blockIdx.y;
-  const uint32_t slice = z * 4 + wv;
-  const bool active = slice < p.slices;
+  const uint32_t xg = blockIdx.x;
 
-  __shared__ f32x4 red[4][RT][64];
-  __shared__ float ssred[4][16];
-  __shared__ uint32_t flag;
+  __shared__ f32x4 red[W][RT][64];
+  __shared__ float ssred[W][16];
 
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float ss = 0.0f;
-
-  if (active) {
-    const uint32_t kbase = slice * KS;
-    // Weights: lane (t, q) takes row t of each tile, bytes 16 q.. of each 64-k block.
-    u32x4 wr[RT][NBLK * WV];
+  const bool tok = (uint32_t)t < p.n;
+  const float* xrow = p.x + (size_t)(tok ? (p.x_rows ? p.x_rows[t] : (uint32_t)t) : 0u) * p.k + 16 * q;
+  const uint8_t* wbase[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      const size_t row = (size_t)(xg * RT + rt) * 16 + t;
-      const uint8_t* wp = p.w + (row * p.k + kbase) * (FMT == SV_FMT_I8 ? 1 : 2);
+  for (int rt = 0; rt < RT; rt++)
+    wbase[rt] = p.w + ((size_t)((xg * RT + rt) * 16 + t) * p.k) * ESZ + (64 * 0 + 16 * q) * WV;
+  const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
+
+  uint32_t c = wv;
+  u32x4 wr[RT][NBLK * WV];
+  if (c < p.chunks) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
 #pragma unroll
       for (int b = 0; b < NBLK; b++)
 #pragma unroll
         for (int v = 0; v < WV; v++)
-          wr[rt][b * WV + v] = __builtin_nontemporal_load((const u32x4*)(wp + (64 * b + 16 * q) * WV + 16 * v));
-    }
-    // X: token t, k = kbase + 64 b + 16 q + 0..15, as hi/lo bf16 B operands.
+          wr[rt][b * WV + v] =
+              __builtin_nontemporal_load((const u32x4*)(wbase[rt] + ((size_t)c * KC + 64 * b) * ESZ + 16 * v));
+  }
+  for (; c < p.chunks; c += W) {
+    const uint32_t kbase = c * KC;
+    // X chunk: token t, k = kbase + 64 b + 16 q + 0..15, as hi/lo bf16 B operands.
     bf16x8 xh[NBLK][2], xl[NBLK][2];
-    if ((uint32_t)t < p.n) {
-      const float* xr = p.x + (size_t)(p.x_rows ? p.x_rows[t] : t) * p.k + kbase + 16 * q;
+    if (tok) {
 #pragma unroll
       for (int b = 0; b < NBLK; b++) {
         float v[16];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-          const f32x4 f = *(const f32x4*)(xr + 64 * b + 4 * j);
+          const f32x4 f = *(const f32x4*)(xrow + kbase + 64 * b + 4 * j);
           v[4 * j] = f[0];
           v[4 * j + 1] = f[1];
           v[4 * j + 2] = f[2];
@@ -99,35 +105,57 @@ __global__ __launch_bounds__(256) void mm_skinny(MMParams p) {
 #pragma unroll
       for (int b = 0; b < NBLK; b++) xh[b][0] = xh[b][1] = xl[b][0] = xl[b][1] = zero;
     }
+    // Weights of this chunk (loaded), then the next chunk's in flight during the products.
+    u32x4 cur[RT][NBLK * WV];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+      for (int i = 0; i < NBLK * WV; i++) cur[rt][i] = wr[rt][i];
+    const uint32_t cn = c + W;
+    if (cn < p.chunks) {
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int b = 0; b < NBLK; b++)
+#pragma unroll
+          for (int v = 0; v < WV; v++)
+            wr[rt][b * WV + v] =
+                __builtin_nontemporal_load((const u32x4*)(wbase[rt] + ((size_t)cn * KC + 64 * b) * ESZ + 16 * v));
+    }
+    f32x4 part[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) part[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NBLK; b++) {
 #pragma unroll
       for (int rt = 0; rt < RT; rt++) {
         bf16x8 a0, a1;
         if (FMT == SV_FMT_I8) {
-          const u32x4 w = wr[rt][b];
+          const u32x4 w = cur[rt][b];
           a0 = i8x8_to_bf(w[0], w[1]);
           a1 = i8x8_to_bf(w[2], w[3]);
         } else {
-          a0 = __builtin_bit_cast(bf16x8, wr[rt][2 * b]);
-          a1 = __builtin_bit_cast(bf16x8, wr[rt][2 * b + 1]);
+          a0 = __builtin_bit_cast(bf16x8, cur[rt][2 * b]);
+          a1 = __builtin_bit_cast(bf16x8, cur[rt][2 * b + 1]);
         }
-        acc[rt] = mfma16(a0, xh[b][0], acc[rt]);
-        acc[rt] = mfma16(a0, xl[b][0], acc[rt]);
-        acc[rt] = mfma16(a1, xh[b][1], acc[rt]);
-        acc[rt] = mfma16(a1, xl[b][1], acc[rt]);
+        part[rt] = mfma16(a0, xh[b][0], part[rt]);
+        part[rt] = mfma16(a0, xl[b][0], part[rt]);
+        part[rt] = mfma16(a1, xh[b][1], part[rt]);
+        part[rt] = mfma16(a1, xl[b][1], part[rt]);
       }
     }
     if (FMT == SV_FMT_I8) {
-      const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift, gi = p.per_row ? 0u : kbase >> p.gshift;
+      const uint32_t gi = p.per_row ? 0u : kbase >> p.gshift;
 #pragma unroll
       for (int rt = 0; rt < RT; rt++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const size_t row = (size_t)(xg * RT + rt) * 16 + 4 * q + i;
-          acc[rt][i] *= bf(p.scales[row * ng + gi]);
+          part[rt][i] *= bf(p.scales[row * ng + gi]);
         }
     }
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) acc[rt] += part[rt];
   }
   ss += __shfl_xor(ss, 16, WAVE);
   ss += __shfl_xor(ss, 32, WAVE);
@@ -135,36 +163,17 @@ __global__ __launch_bounds__(256) void mm_skinny(MMParams p) {
   for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
   if (q == 0) ssred[wv][t] = ss;
   __syncthreads();
-  if (wv == 0) {
+  if (wv != 0) return;
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) acc[rt] = ((red[0][rt][lane] + red[1][rt][lane]) + red[2][rt][lane]) + red[3][rt][lane];
-    ss = ((ssred[0][t] + ssred[1][t]) + ssred[2][t]) + ssred[3][t];
+  for (int rt = 0; rt < RT; rt++) {
+    f32x4 a = red[0][rt][lane];
+#pragma unroll
+    for (int w = 1; w < W; w++) a += red[w][rt][lane];
+    acc[rt] = a;
   }
-  if (p.kgroups > 1) {
-    // Partials: [xg][z][rt][lane] f32x4, then sums of squares [xg][z][16].
-    const size_t rec = ((size_t)xg * p.kgroups + z);
-    f32x4* pp = (f32x4*)p.part + rec * RT * 64;
-    float* ps = p.part + (size_t)gridDim.x * p.kgroups * RT * 256 + rec * 16;
-    if (wv == 0) {
+  ss = ssred[0][t];
 #pragma unroll
-      for (int rt = 0; rt < RT; rt++) pp[rt * 64 + lane] = acc[rt];
-      if (q == 0) ps[t] = ss;
-    }
-    if (!arrive_last(&p.counters[xg], p.kgroups, &flag)) return;
-    if (wv != 0) return;
-    const f32x4* p0 = (const f32x4*)p.part + (size_t)xg * p.kgroups * RT * 64;
-    const float* s0 = p.part + (size_t)gridDim.x * p.kgroups * RT * 256 + (size_t)xg * p.kgroups * 16;
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) acc[rt] = p0[rt * 64 + lane];
-    ss = s0[t];
-    for (uint32_t zz = 1; zz < p.kgroups; zz++) {
-#pragma unroll
-      for (int rt = 0; rt < RT; rt++) acc[rt] += p0[(zz * RT + rt) * 64 + lane];
-      ss += s0[zz * 16 + t];
-    }
-  } else if (wv != 0) {
-    return;
-  }
+  for (int w = 1; w < W; w++) ss += ssred[w][t];
 
   // Epilogue (kernels.metal:183-209): lane (t, q) holds rows 4 q + 0..3 of each tile.
   if ((uint32_t)t >= p.n) return;
@@ -216,31 +225,312 @@ __global__ __launch_bounds__(256) void mm_skinny(MMParams p) {
   }
 }
 
+// ------------------------------------------------------------------- large n
+// GEMM path (n > 16 rows: many streams, draft trees): a workgroup of 4 waves owns
+// BM = 64 RTW output rows and BN = 16 NT tokens; k goes in chunks of 64.
+//   - X chunk [BN][64] fp32 is read once per workgroup (L2), split into bf16 hi + lo and
+//     written to LDS already in MFMA B-operand lane order (one 16-byte row per lane), so
+//     every operand read is a conflict-free ds_read_b128; double-buffered, one barrier per
+//     chunk.
+//   - Each wave streams its RTW x 16 weight rows straight into registers (16 bytes per lane
+//     per row tile per chunk, the next chunk's in flight), converts int8 to bf16, and runs
+//     RTW x NT x 2 k-steps x 2 (hi, lo) MFMAs per chunk.
+//   - Workgroups that share weight rows (different token blocks) are mapped to the same XCD,
+//     so the second reads the rows from that XCD's L2.
+//   - Sums of squares for the folded rms-norm: each thread owns fixed (token, 8-k group)
+//     pairs for the whole k, added in a fixed order at the end.
+constexpr int GKC = 64;
+
+template <int FMT, int RTW, int NT>
+__global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
+  constexpr int BN = 16 * NT;
+  constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
+  constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;     // dwordx4 per lane per row tile per chunk
+  constexpr int PAIRS = BN * 8;                    // (token, 8-k group) pairs per chunk
+  constexpr int PPT = (PAIRS + 255) / 256;         // pairs per thread
+  // LDS: [2 buffers][NT][2 k-steps][hi, lo][64 lanes] of 16 bytes.
+  __shared__ u32x4 xs[2][NT][2][2][64];
+  __shared__ float ssp[BN][8];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t16 = lane & 15, q = lane >> 4;
+
+  // XCD-aware order: work items (row block, token block) with the same row block go to the
+  // same XCD (workgroup id mod 8) when the count allows.
+  const uint32_t nwg = gridDim.x, g = blockIdx.x;
+  uint32_t item = g;
+  if (nwg % 8 == 0) item = (g % 8) * (nwg / 8) + g / 8;
+  const uint32_t rblk = item / n_tblk, tblk = item % n_tblk;
+  const uint32_t t0 = tblk * BN;
+  const uint32_t row0 = rblk * 64 * RTW + wv * 16 * RTW;  // this wave's first row
+
+  // Weights: lane (t16, q) takes row t16 of each tile, bytes 16 q .. of each 64-k chunk.
+  const uint8_t* wb[RTW];
+#pragma unroll
+  for (int r = 0; r < RTW; r++) wb[r] = p.w + ((size_t)(row0 + 16 * r + t16) * p.k + 16 * q) * ESZ;
+
+  // X pairs of this thread: pair i -> token i / 8, k group i % 8 (k = 8 (i % 8) .. + 7).
+  float ssacc[PPT];
+  const float* xp[PPT];
+  bool pv[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    const int i = tid + 256 * j;
+    const uint32_t tt = t0 + i / 8;
+    pv[j] = i < PAIRS && tt < p.n;
+    xp[j] = p.x + (size_t)(pv[j] ? (p.x_rows ? p.x_rows[tt] : tt) : 0u) * p.k + 8 * (i % 8);
+    ssacc[j] = 0.0f;
+  }
+  auto load_x = [&](uint32_t c, f32x4 (&xr)[PPT][2]) {
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      if (pv[j]) {
+        xr[j][0] = *(const f32x4*)(xp[j] + (size_t)c * GKC);
+        xr[j][1] = *(const f32x4*)(xp[j] + (size_t)c * GKC + 4);
+      } else {
+        xr[j][0] = xr[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  auto store_x = [&](int buf, const f32x4 (&xr)[PPT][2]) {
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      const int i = tid + 256 * j;
+      if (i >= PAIRS) continue;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[e] = xr[j][0][e];
+        v[4 + e] = xr[j][1][e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) ssacc[j] = __builtin_fmaf(v[e], v[e], ssacc[j]);
+      bf16x8 h, l;
+      split8(v, h, l);
+      const int tok = i / 8, g8 = i % 8, qq = g8 >> 1, ks = g8 & 1;
+      const int ln = (tok & 15) + 16 * qq;
+      xs[buf][tok >> 4][ks][0][ln] = __builtin_bit_cast(u32x4, h);
+      xs[buf][tok >> 4][ks][1][ln] = __builtin_bit_cast(u32x4, l);
+    }
+  };
+  const uint32_t nch = p.k / GKC;
+  const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
+
+  f32x4 acc[RTW][NT];
+#pragma unroll
+  for (int r = 0; r < RTW; r++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[r][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 grp[RTW][NT];  // the current scale group's sums (int8 with groups < k)
+
+  f32x4 xr[PPT][2];
+  u32x4 wr[RTW][WL];
+  load_x(0, xr);
+#pragma unroll
+  for (int r = 0; r < RTW; r++)
+#pragma unroll
+    for (int v = 0; v < WL; v++) wr[r][v] = __builtin_nontemporal_load((const u32x4*)(wb[r] + 16 * v));
+  store_x(0, xr);
+  __syncthreads();
+  const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
+#pragma unroll
+  for (int r = 0; r < RTW; r++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) grp[r][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (uint32_t c = 0; c < nch; c++) {
+    const int buf = c & 1;
+    u32x4 cur[RTW][WL];
+#pragma unroll
+    for (int r = 0; r < RTW; r++)
+#pragma unroll
+      for (int v = 0; v < WL; v++) cur[r][v] = wr[r][v];
+    if (c + 1 < nch) {
+      load_x(c + 1, xr);
+#pragma unroll
+      for (int r = 0; r < RTW; r++)
+#pragma unroll
+        for (int v = 0; v < WL; v++)
+          wr[r][v] = __builtin_nontemporal_load((const u32x4*)(wb[r] + (size_t)(c + 1) * GKC * ESZ + 16 * v));
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      bf16x8 a[RTW];
+#pragma unroll
+      for (int r = 0; r < RTW; r++) {
+        if (FMT == SV_FMT_I8) a[r] = i8x8_to_bf(cur[r][0][2 * ks], cur[r][0][2 * ks + 1]);
+        else a[r] = __builtin_bit_cast(bf16x8, cur[r][ks]);
+      }
+#pragma unroll
+      for (int n = 0; n < NT; n++) {
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][ks][0][lane]);
+        const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][ks][1][lane]);
+#pragma unroll
+        for (int r = 0; r < RTW; r++) {
+          grp[r][n] = mfma16(a[r], bh, grp[r][n]);
+          grp[r][n] = mfma16(a[r], bl, grp[r][n]);
+        }
+      }
+    }
+    // Close a scale group (int8 with groups < k): acc += scale * group sums.
+    if (grouped && ((c + 1) * GKC) % (1u << p.gshift) == 0) {
+      const uint32_t gi = (c * GKC) >> p.gshift;
+#pragma unroll
+      for (int r = 0; r < RTW; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const float sc = bf(p.scales[(size_t)(row0 + 16 * r + 4 * q + i) * ng + gi]);
+#pragma unroll
+          for (int n = 0; n < NT; n++) {
+            acc[r][n][i] += sc * grp[r][n][i];
+            grp[r][n][i] = 0.0f;
+          }
+        }
+    }
+    if (c + 1 < nch) store_x(buf ^ 1, xr);
+    __syncthreads();
+  }
+  if (!grouped) {
+#pragma unroll
+    for (int r = 0; r < RTW; r++) {
+      f32x4 sc = f32x4{1.f, 1.f, 1.f, 1.f};
+      if (FMT == SV_FMT_I8)
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = bf(p.scales[(size_t)(row0 + 16 * r + 4 * q + i) * ng]);
+#pragma unroll
+      for (int n = 0; n < NT; n++) acc[r][n] = grp[r][n] * sc;
+    }
+  }
+  // Sums of squares per token: the thread's pairs, then the 8 k groups in order.
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    const int i = tid + 256 * j;
+    if (i < PAIRS) ssp[i / 8][i % 8] = ssacc[j];
+  }
+  __syncthreads();
+
+  // Epilogue (kernels.metal:183-209): lane (t16, q) holds rows 4 q + 0..3 of each row tile
+  // for token t0 + 16 n + t16.
+  const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    const uint32_t tl = 16 * n + t16, t = t0 + tl;
+    if (t >= p.n) continue;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += ssp[tl][e];
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
+    if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && rblk == 0 && wv == 0 && q == 0) p.aux[t] = inv;
+#pragma unroll
+    for (int r = 0; r < RTW; r++) {
+      const uint32_t rowq = row0 + 16 * r + 4 * q;
+      f32x4 v = acc[r][n];
+      const size_t o = (size_t)t * p.m + rowq;
+      switch (p.epi) {
+        case SV_EPI_NORM:
+          *(f32x4*)(p.y + o) = v * (inv * p.scale);
+          break;
+        case SV_EPI_RAW:
+          if (norm_in) v *= inv;
+          *(f32x4*)(p.y + o) = v;
+          break;
+        case SV_EPI_RESID: {
+          if (norm_in) v *= inv;
+          const f32x4 sv = v * p.scale;
+          const f32x4 b = *(const f32x4*)(p.base + o);
+          *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
+          if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
+          break;
+        }
+        case SV_EPI_HEAD: {
+          if (norm_in) v *= inv;
+          f32x4 l;
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            l[i] = rowq + i < p.vocab_real ? 23.0f * sigmoidf_((v[i] + 5.0f) / 7.5f) : -__builtin_inff();
+          *(f32x4*)(p.y + o) = l;
+          break;
+        }
+        case SV_EPI_SWIGLU: {
+          const float sc = inv * p.scale;
+          const float g0 = v[0] * sc, u0 = v[1] * sc, g1 = v[2] * sc, u1 = v[3] * sc;
+          float2 out;
+          out.x = g0 * sigmoidf_(g0) * u0;
+          out.y = g1 * sigmoidf_(g1) * u1;
+          *(float2*)(p.y + (size_t)t * (p.m / 2) + rowq / 2) = out;
+          break;
+        }
+        default:
+          break;
+      }
+    }
+  }
+}
+
 // Row tiles per workgroup: the largest of 4, 2, 1 that divides the tiles and still gives at
 // least 512 workgroups (2 per CU), else 1.
-static int pick_rt(uint32_t tiles, uint32_t kgroups) {
+static int pick_rt(uint32_t tiles) {
   for (int rt = 4; rt > 1; rt /= 2)
-    if (tiles % rt == 0 && (tiles / rt) * kgroups >= 512) return rt;
+    if (tiles % rt == 0 && tiles / rt >= 512) return rt;
   return 1;
+}
+
+// Token tiles per workgroup (BN = 16 NT) and row tiles per wave (BM = 64 RTW) for n rows:
+// the fewest padded tokens, then enough workgroups to fill 256 CUs.
+static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, const MMParams& p) {
+  const int nts[] = {2, 4, 5, 8};
+  int nt = 8;
+  uint32_t best = ~0u;
+  for (int c : nts) {
+    const uint32_t blocks = (p.n + 16 * c - 1) / (16 * c), pad = blocks * 16 * c - p.n;
+    if (pad < best || (pad == best && c > nt)) best = pad, nt = c;
+  }
+  const uint32_t n_tblk = (p.n + 16 * nt - 1) / (16 * nt);
+  int rtw = 1;
+  for (int c = 4; c > 1; c /= 2)
+    if (p.m % (64 * c) == 0 && (p.m / (64 * c)) * n_tblk >= 512) {
+      rtw = c;
+      break;
+    }
+  const uint32_t nwg = p.m / (64 * rtw) * n_tblk;
+#define SV_G(F, R, N) hipLaunchKernelGGL((mm_gemm<F, R, N>), dim3(nwg), dim3(256), 0, stream, p, n_tblk)
+#define SV_G_N(F, R)                \
+  switch (nt) {                     \
+    case 2: SV_G(F, R, 2); break;   \
+    case 4: SV_G(F, R, 4); break;   \
+    case 5: SV_G(F, R, 5); break;   \
+    default: SV_G(F, R, 8); break;  \
+  }
+#define SV_G_R(F)                     \
+  if (rtw == 4) { SV_G_N(F, 4) }      \
+  else if (rtw == 2) { SV_G_N(F, 2) } \
+  else { SV_G_N(F, 1) }
+  if (fmt == SV_FMT_I8) {
+    SV_G_R(SV_FMT_I8)
+  } else {
+    SV_G_R(SV_FMT_BF16)
+  }
+#undef SV_G_R
+#undef SV_G_N
+#undef SV_G
+  return check_launch("matmul (gemm)");
 }
 
 size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
   (void)n;
-  const uint32_t slices = (k + KS - 1) / KS, kgroups = (slices + 3) / 4, tiles = m / 16;
-  size_t b = WS_COUNTER_BYTES;                            // counters
-  b += (size_t)tiles * kgroups * 256 * 4;                 // partial sums
-  b += (size_t)tiles * kgroups * 16 * 4;                  // sums of squares (rt = 1 bound)
-  return b;
+  (void)m;
+  (void)k;
+  return 0;
 }
 
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes) {
+  (void)ws;
+  (void)ws_bytes;
   if (!w || !a || !x || !y || !w->d_w) return fail(SV_ERR_ARG, "matmul: null pointer");
   if (a->k != w->k || a->m != w->m) return fail(SV_ERR_ARG, "matmul: args (m %u, k %u) != matrix (%u, %u)", a->m, a->k, w->m, w->k);
   if (a->n == 0) return SV_OK;
-  if (a->n > 16) return fail(SV_ERR_UNSUPPORTED, "matmul: %u rows: the skinny path takes at most 16", a->n);
-  if (a->k % KS != 0 || a->m % 16 != 0)
-    return fail(SV_ERR_ARG, "matmul: k %u must be a multiple of %d and m %u of 16", a->k, KS, a->m);
+  if (a->n > 16 ? (a->k % GKC != 0 || a->m % 64 != 0) : (a->k % KC != 0 || a->m % 16 != 0))
+    return fail(SV_ERR_ARG, "matmul: k %u must be a multiple of %d and m %u of %d", a->k, a->n > 16 ? GKC : KC, a->m,
+                a->n > 16 ? 64 : 16);
   if (a->epi == SV_EPI_SWIGLU && a->m % 2) return fail(SV_ERR_ARG, "matmul: swiglu needs even m");
   if (a->epi < SV_EPI_NORM || a->epi > SV_EPI_RAW) return fail(SV_ERR_ARG, "matmul: epilogue %u", a->epi);
   if (a->epi == SV_EPI_RESID && !base) return fail(SV_ERR_ARG, "matmul: resid needs base");
@@ -249,9 +539,10 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   if (w->format == SV_FMT_I8) {
     if (!w->d_scales) return fail(SV_ERR_ARG, "matmul: int8 without scales");
     per_row = a->gshift >= 32 || (1ull << a->gshift) >= a->k;
-    if (!per_row && (a->gshift < 8 || a->k % (1u << a->gshift) != 0))
-      return fail(SV_ERR_UNSUPPORTED, "matmul: int8 group 2^%u: groups of at least 256 (or one per row) are built",
-                  a->gshift);
+    const uint32_t min_shift = a->n > 16 ? 6 : 8;
+    if (!per_row && (a->gshift < min_shift || a->k % (1u << a->gshift) != 0))
+      return fail(SV_ERR_UNSUPPORTED, "matmul: int8 group 2^%u: groups of at least %u (or one per row) are built",
+                  a->gshift, 1u << min_shift);
   } else if (w->format != SV_FMT_BF16) {
     return fail(SV_ERR_ARG, "matmul: format %u", w->format);
   }
@@ -274,31 +565,26 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.scale = a->scale;
   p.ra = a->ra;
   p.rb = a->rb;
-  p.slices = a->k / KS;
-  p.kgroups = (p.slices + 3) / 4;
+  p.chunks = a->k / KC;
+  if (a->n > 16) return gemm_launch(stream, w->format, p);
   const uint32_t tiles = a->m / 16;
-  const int rt = pick_rt(tiles, p.kgroups);
-  if (p.kgroups > 1) {
-    const size_t need = matmul_ws_bytes(a->n, a->m, a->k);
-    if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "matmul: workspace %zu < %zu bytes", ws_bytes, need);
-    if ((size_t)tiles * 4 > WS_COUNTER_BYTES) return fail(SV_ERR_UNSUPPORTED, "matmul: %u row tiles", tiles);
-    p.counters = (uint32_t*)ws;
-    p.part = (float*)((char*)ws + WS_COUNTER_BYTES);
-  } else {
-    p.counters = nullptr;
-    p.part = nullptr;
-  }
-  dim3 grid(tiles / rt, p.kgroups);
-#define SV_MM(F, R) hipLaunchKernelGGL((mm_skinny<F, R>), grid, dim3(256), 0, stream, p)
+  const int rt = pick_rt(tiles);
+  const int waves = p.chunks >= 8 ? 8 : 4;
+  dim3 grid(tiles / rt);
+#define SV_MM(F, R, W) hipLaunchKernelGGL((mm_skinny<F, R, W>), grid, dim3(64 * W), 0, stream, p)
+#define SV_MM_W(F, R)        \
+  if (waves == 8) SV_MM(F, R, 8); \
+  else SV_MM(F, R, 4)
   if (w->format == SV_FMT_I8) {
-    if (rt == 4) SV_MM(SV_FMT_I8, 4);
-    else if (rt == 2) SV_MM(SV_FMT_I8, 2);
-    else SV_MM(SV_FMT_I8, 1);
+    if (rt == 4) { SV_MM_W(SV_FMT_I8, 4); }
+    else if (rt == 2) { SV_MM_W(SV_FMT_I8, 2); }
+    else { SV_MM_W(SV_FMT_I8, 1); }
   } else {
-    if (rt == 4) SV_MM(SV_FMT_BF16, 4);
-    else if (rt == 2) SV_MM(SV_FMT_BF16, 2);
-    else SV_MM(SV_FMT_BF16, 1);
+    if (rt == 4) { SV_MM_W(SV_FMT_BF16, 4); }
+    else if (rt == 2) { SV_MM_W(SV_FMT_BF16, 2); }
+    else { SV_MM_W(SV_FMT_BF16, 1); }
   }
+#undef SV_MM_W
 #undef SV_MM
   return check_launch("matmul");
 }

@@ -111,22 +111,4 @@ __device__ __forceinline__ u32x4 philox(u32x4 c, uint32_t k0, uint32_t k1) {
   return c;
 }
 
-// Release this workgroup's global writes, count its arrival at `counter`, and tell whether
-// it arrived last of `expected`; the last one acquires every other's writes and resets the
-// counter for the next launch. All threads of the workgroup must call it.
-__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = old == expected - 1;
-    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    *lds_flag = last;
-  }
-  __syncthreads();
-  const bool last = *lds_flag != 0;
-  if (last) __threadfence();
-  return last;
-}
-
 }  // namespace sv

@@ -9,10 +9,6 @@
 
 namespace sv {
 
-// Every workspace starts with this many bytes of arrival counters, zero at rest (each
-// kernel's last workgroup resets the ones it used); partial sums follow. Kernels that run
-// in stream order can share one workspace.
-constexpr size_t WS_COUNTER_BYTES = 65536;
 
 // Record a thread-local error message and return `code` (sv_last_error reads it).
 sv_status fail(sv_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
@@ -32,9 +28,10 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes);
 
-sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, uint32_t* tokens, float* out,
-                       const uint32_t* tin, uint32_t* meta, const uint32_t* lens, const uint32_t* feed,
-                       const uint32_t* tree, uint32_t* vis, uint32_t n);
+// tokens_out may equal tokens (resolution in place, as the reference's embed).
+sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,
+                       uint32_t* tokens_out, float* out, const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
+                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n);
 sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
                               uint32_t hidden);
 sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,
@@ -48,5 +45,13 @@ sv_status kv_compact_launch(hipStream_t stream, const sv_shape* sh, const sv_run
 sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nruns, const uint32_t* lens,
                         uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
                         uint32_t* tree);
+
+// accept, then (optionally) kv_compact and the replay drafter, one workgroup per run.
+sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
+                           const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed, sv_gen_state* gen,
+                           uint32_t* emitted, uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path,
+                           bool compact, uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table,
+                           const sv_kv_args* kv, const sv_replay_args* ra, const uint32_t* trace,
+                           const uint32_t* trace_len);
 
 }  // namespace sv

@@ -20,7 +20,8 @@ __device__ __forceinline__ float block_sum256(float v, float* red) {
 }
 
 // embed (kernels.metal:82-114): one workgroup of 256 per token.
-__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, uint32_t* tokens, float* out,
+__global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, const uint32_t* tokens,
+                                                    uint32_t* tokens_out, float* out,
                                                     const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
                                                     const uint32_t* feed, const uint32_t* tree, uint32_t* vis,
                                                     uint32_t H, uint32_t vocab) {
@@ -43,7 +44,7 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, uint3
   }
   const float inv = 1.0f / __builtin_sqrtf(block_sum256(ss, red) / (float)H + SV_RMS_EPS);
   if (tid == 0) {  // after block_sum256's barriers: every thread has read tokens[t]
-    tokens[t] = tok;
+    tokens_out[t] = tok;
     meta[2 * t] = slot;
     meta[2 * t + 1] = lens[slot] + depth;
   }
@@ -117,6 +118,7 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const
 
   float lmax = -3.402823466e+38f;
   uint32_t tok = 0xffffffffu;
+#pragma unroll 8
   for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) better(lmax, tok, x[i], i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -136,6 +138,7 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const
   if (row.temperature > 0.0f) {
     const float c = LOG2E_F / row.temperature;
     float s = 0.0f;
+#pragma unroll 8
     for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) s += sv_exp2((x[i] - lmax) * c);
     scan1024(s, ex, base, tid);
     const float z = ex[SV_SAMPLE_THREADS];
@@ -284,16 +287,131 @@ __global__ __launch_bounds__(64) void replay_kernel(const sv_run_in* runs, uint3
   tree[slot * SV_FEED_W + i] = i | (i - 1) << 8 | ((2u << i) - 1u) << 16;
 }
 
+// accept (kernels.metal:1605-1657), then kv_compact (:1659-1693) and the replay drafter
+// (:1705-1724) of the same run, in one workgroup per run: the engine's step tail as one
+// launch. Thread 0 walks the tree exactly as accept_kernel; the path goes through LDS to
+// the threads that move its K/V rows (all layers; element order per thread as kv_compact)
+// and then write the next drafts.
+struct TailParams {
+  const sv_run_in* runs;
+  const uint32_t* tokens;
+  uint32_t* out;
+  uint32_t* lens;
+  uint32_t* feed;
+  sv_gen_state* gen;
+  uint32_t* emitted;
+  const uint32_t* trace;
+  const uint32_t* trace_len;
+  uint32_t* tree;
+  uint32_t* path;
+  uint32_t* path_len;
+  uint32_t* on_path;
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint32_t* page_table;
+  uint32_t nruns, compact, replay;
+  uint32_t n_layers, NKV, D, page_shift, n_pages, max_pages;
+  sv_replay_args ra;
+};
+
+__global__ __launch_bounds__(256) void step_tail_kernel(TailParams p) {
+  __shared__ uint32_t s_path[SV_FEED_W];
+  __shared__ uint32_t s_k, s_len;
+  const uint32_t r = blockIdx.x, tid = threadIdx.x;
+  const sv_run_in ru = p.runs[r];
+  if (tid == 0) {
+    sv_gen_state* gs = &p.gen[ru.slot];
+    p.path_len[r] = 0;
+    const uint32_t done = gs->done;
+    uint32_t k = 0;
+    for (uint32_t j = 0; j < ru.count; j++) p.on_path[ru.first + j] = !ru.verify && !done;
+    if (done) {
+      p.emitted[r] = 0;
+    } else {
+      if (!ru.verify) p.lens[ru.slot] += ru.count;
+      if (ru.nhead == 0) {
+        p.emitted[r] = 0;
+      } else {
+        uint32_t first = ru.head0 + ru.nhead - 1, e = 1;
+        uint32_t walk[SV_FEED_W];
+        walk[0] = 0;
+        if (ru.verify) {
+          const uint32_t* node = p.tree + (size_t)ru.slot * SV_FEED_W;
+          for (uint32_t c = 1, at = 0; c < ru.count; c++) {
+            if (((node[c] >> 8) & 0xffu) == at && p.tokens[ru.first + c] == p.out[ru.head0 + at]) walk[e++] = at = c;
+          }
+          for (uint32_t j = 1; j < e; j++) p.out[ru.head0 + j] = p.out[ru.head0 + walk[j]];
+          first = ru.head0;
+        }
+        bool stop = false;
+        const uint32_t remaining = gs->remaining, nstop = gs->nstop;
+        while (k < e && k < remaining && !stop) {
+          const uint32_t t = p.out[first + k];
+          for (uint32_t j = 0; j < nstop && j < SV_MAX_STOP; j++) stop = stop || t == gs->stop[j];
+          k++;
+        }
+        if (ru.verify) {
+          p.lens[ru.slot] += k;
+          p.path_len[r] = k;
+          for (uint32_t j = 0; j < k; j++) {
+            p.path[r * SV_FEED_W + j] = walk[j];
+            p.on_path[ru.first + walk[j]] = 1;
+            s_path[j] = walk[j];
+          }
+        }
+        if (k > 0) p.feed[ru.slot * SV_FEED_W] = p.out[first + k - 1];
+        gs->remaining = remaining - k;
+        if (stop || remaining - k == 0) gs->done = 1;
+        p.emitted[r] = k;
+      }
+    }
+    s_k = ru.verify ? k : 0;
+    s_len = p.lens[ru.slot];
+  }
+  __syncthreads();
+  const uint32_t k = s_k, len = s_len, slot = ru.slot;
+  if (p.compact && k > 1) {
+    const uint32_t chunks = p.D / 4, per_layer = p.NKV * chunks, p0 = len - k;
+    const uint32_t pmask = (1u << p.page_shift) - 1u;
+    for (uint32_t e = tid; e < p.n_layers * per_layer; e += 256) {
+      const uint32_t l = e / per_layer, g = (e % per_layer) / chunks, d0 = (e % chunks) * 4;
+      for (uint32_t j = 1; j < k; j++) {
+        const uint32_t from = s_path[j];
+        if (from == j) continue;
+        const uint32_t ps = p.page_table[(size_t)slot * p.max_pages + ((p0 + from) >> p.page_shift)];
+        const uint32_t pd = p.page_table[(size_t)slot * p.max_pages + ((p0 + j) >> p.page_shift)];
+        const size_t src = ((((size_t)l * p.n_pages + ps) * p.NKV + g) << p.page_shift) * p.D +
+                           (size_t)((p0 + from) & pmask) * p.D + d0;
+        const size_t dst = ((((size_t)l * p.n_pages + pd) * p.NKV + g) << p.page_shift) * p.D +
+                           (size_t)((p0 + j) & pmask) * p.D + d0;
+        *(u32x2*)(p.kc + dst) = *(const u32x2*)(p.kc + src);
+        *(u32x2*)(p.vc + dst) = *(const u32x2*)(p.vc + src);
+      }
+    }
+  }
+  if (p.replay && tid > 0 && tid < SV_FEED_W && ru.nhead != 0) {
+    const uint32_t n = p.trace_len[slot];
+    if (n != 0) {
+      const uint32_t i = tid, pos = len + i;
+      uint32_t tok = pos < n ? p.trace[(size_t)slot * p.ra.stride + pos] : 0u;
+      const u32x4 h = philox(u32x4{pos, 0x5eedu, 0u, 0u}, p.ra.seed, 0x0dd5u);
+      if ((float)(h[0] >> 8) * 0x1p-24f < p.ra.rate) tok = (tok + 1) % p.ra.vocab;
+      p.feed[slot * SV_FEED_W + i] = tok;
+      p.tree[slot * SV_FEED_W + i] = i | (i - 1) << 8 | ((2u << i) - 1u) << 16;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- launchers
 
-sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, uint32_t* tokens, float* out,
-                       const uint32_t* tin, uint32_t* meta, const uint32_t* lens, const uint32_t* feed,
-                       const uint32_t* tree, uint32_t* vis, uint32_t n) {
-  if (!sh || !table || !tokens || !out || !tin || !meta || !lens || !feed || !tree || !vis)
+sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,
+                       uint32_t* tokens_out, float* out, const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
+                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n) {
+  if (!sh || !table || !tokens || !tokens_out || !out || !tin || !meta || !lens || !feed || !tree || !vis)
     return fail(SV_ERR_ARG, "embed: null pointer");
   if (n == 0) return SV_OK;
-  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, out, tin, meta, lens, feed, tree, vis,
-                     sh->hidden, sh->vocab);
+  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, tokens_out, out, tin, meta, lens, feed,
+                     tree, vis, sh->hidden, sh->vocab);
   return check_launch("embed");
 }
 
@@ -348,6 +466,54 @@ sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nrun
   hipLaunchKernelGGL(replay_kernel, dim3(nruns), dim3(64), 0, stream, runs, nruns, lens, feed, trace, trace_len, *ra,
                      tree);
   return check_launch("replay_draft");
+}
+
+}  // namespace sv
+
+namespace sv {
+
+sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
+                           const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed, sv_gen_state* gen,
+                           uint32_t* emitted, uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path,
+                           bool compact, uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table,
+                           const sv_kv_args* kv, const sv_replay_args* ra, const uint32_t* trace,
+                           const uint32_t* trace_len) {
+  if (nruns == 0) return SV_OK;
+  TailParams p;
+  p.runs = runs;
+  p.tokens = tokens;
+  p.out = out;
+  p.lens = lens;
+  p.feed = feed;
+  p.gen = gen;
+  p.emitted = emitted;
+  p.trace = trace;
+  p.trace_len = trace_len;
+  p.tree = tree;
+  p.path = path;
+  p.path_len = path_len;
+  p.on_path = on_path;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.page_table = page_table;
+  p.nruns = nruns;
+  p.compact = compact ? 1u : 0u;
+  p.replay = ra ? 1u : 0u;
+  p.n_layers = sh->n_layers;
+  p.NKV = sh->n_kv_heads;
+  p.D = sh->head_dim;
+  p.page_shift = kv->page_shift;
+  p.n_pages = kv->n_pages;
+  p.max_pages = kv->max_pages;
+  if (ra) {
+    if (ra->vocab == 0) return fail(SV_ERR_ARG, "step tail: replay vocab 0");
+    p.ra = *ra;
+  } else {
+    p.ra = sv_replay_args{0, 0, 0.0f, 1};
+  }
+  if (p.replay && (!trace || !trace_len)) return fail(SV_ERR_ARG, "step tail: replay without a trace");
+  hipLaunchKernelGGL(step_tail_kernel, dim3(nruns), dim3(256), 0, stream, p);
+  return check_launch("step tail");
 }
 
 }  // namespace sv

@@ -157,7 +157,8 @@ def test_tree_step_compacts(gpu):
     # V rows come from each side's own matmul: equal up to one bf16 rounding step.
     got = oracle.bf16_to_f32(vd.view(torch.int16).cpu().numpy().view(np.uint16))
     want = oracle.bf16_to_f32(ref.v)
-    bad = np.argwhere(np.abs(got - want) > 2 ** -7 * np.abs(want) + 1e-30)
+    # (plus an absolute term for values near zero, whose fp32 projections differ in the last bits)
+    bad = np.argwhere(np.abs(got - want) > 2 ** -7 * np.abs(want) + 1e-4)
     pages = eng.seq_pages(s)
     pos = [(pages.index(int(b[1])) * 16 + int(b[3]) if int(b[1]) in pages else -1, int(b[2])) for b in bad[:12]]
     assert bad.size == 0, (f"V cache (after kv_compact) differs at {len(bad)} elements; (position, kv head) "
