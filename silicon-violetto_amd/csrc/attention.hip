@@ -18,10 +18,14 @@
 //     then O^T += V^T P^T with P (hi, lo) taken straight from the S^T accumulators' layout.
 //     K rows are read as 16-byte slices; each V row is read whole by 16 lanes (8 bytes per
 //     lane for D = 64), and the matrix-core operand takes one of its dims per tile.
-//   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace;
-//     attn_merge_kernel (one workgroup per run and kv head, the next launch) sums the
-//     partials in split order and writes o / l. (A last-arriving-workgroup merge would need
-//     an agent-scope fence, which on gfx950 writes back and invalidates the XCD's L2.)
+//   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace with
+//     coherent (relaxed agent-scope atomic) stores. attn_merge_kernel, the next launch, sums
+//     the partials of each (run, kv head, column) in split order and writes o / l. With
+//     SV_ATTN_MERGE=fused the last split of (run, kv head) to arrive (a relaxed agent-scope
+//     counter: no L2 write-back or invalidate) merges instead, with coherent loads.
+#include <cstdlib>
+#include <cstring>
+
 #include "sv_device.h"
 #include "sv_internal.h"
 
@@ -45,6 +49,7 @@ struct AttnParams {
   float* out;
   float* part_o;
   float* part_l;
+  uint32_t* counters;  // per (run, kv head): fused merge; null: attn_merge_kernel merges
   uint32_t NQ, NKV, G, W, KOFF, VOFF;
   uint32_t split, max_splits;
   float scale_log2;
@@ -343,11 +348,45 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   float* pl = p.part_l + rec * p.maxcols;
   for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
     const uint32_t col = idx / D, d = idx % D;
-    po[idx] = ((ored[col * D + d] + ored[(COLS + col) * D + d]) + ored[(2 * COLS + col) * D + d]) +
-              ored[(3 * COLS + col) * D + d];
+    store_wt(po + idx, ((ored[col * D + d] + ored[(COLS + col) * D + d]) + ored[(2 * COLS + col) * D + d]) +
+                           ored[(3 * COLS + col) * D + d]);
   }
   for (uint32_t idx = tid; idx < ncols; idx += 256)
-    pl[idx] = ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx];
+    store_wt(pl + idx, ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx]);
+  if (!p.counters) return;  // attn_merge_kernel merges
+
+  // The last split of (run, kv head) to arrive merges (attn_dec_reduce, kernels.metal:1316-1362):
+  // plain sums in split order, eight loads in flight per thread.
+  __shared__ uint32_t flag;
+  if (!arrive_last(&p.counters[r * p.NKV + g], nsplit, &flag)) return;
+  const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
+  const size_t so = (size_t)p.maxcols * D;
+  const float* po0 = p.part_o + rec0 * so;
+  const float* pl0 = p.part_l + rec0 * p.maxcols;
+  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+    const uint32_t col = idx / D, d = idx % D;
+    float o = 0.0f, l = 0.0f;
+    uint32_t sp = 0;
+    for (; sp + 8 <= nsplit; sp += 8) {
+      float ov[8], lv[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        ov[u] = load_wt(po0 + (sp + u) * so + idx);
+        lv[u] = load_wt(pl0 + (sp + u) * p.maxcols + col);
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        o += ov[u];
+        l += lv[u];
+      }
+    }
+    for (; sp < nsplit; sp++) {
+      o += load_wt(po0 + sp * so + idx);
+      l += load_wt(pl0 + sp * p.maxcols + col);
+    }
+    const uint32_t i = col / p.G, h = g * p.G + col % p.G;
+    p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = o / l;
+  }
 
 }
 
@@ -432,7 +471,7 @@ static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
 
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run) {
   const size_t maxcols = cols_pad(sh, max_run);
-  size_t b = 0;
+  size_t b = ((size_t)n_runs * sh->n_kv_heads * 4 + 255) / 256 * 256;
   b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * sh->head_dim * 4;
   b = (b + 255) / 256 * 256;
   b += (size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * 4;
@@ -457,6 +496,13 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (!rope && args->rope) return fail(SV_ERR_ARG, "attn_verify: rope table missing");
   const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;
   if (nct > 4) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (64 are built)", max_run * NQ / NKV);
+  // The merge runs as its own launch spread over (run, kv head, column) workgroups; with
+  // SV_ATTN_MERGE=fused the last split of each (run, kv head) merges instead (one launch
+  // less, but one workgroup then walks every split: measured slower at 65 splits).
+  static const bool fused_merge = [] {
+    const char* v = getenv("SV_ATTN_MERGE");
+    return v && strcmp(v, "fused") == 0;
+  }();
   const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
   if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
   AttnParams p;
@@ -469,7 +515,9 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.runs = runs;
   p.vis = vis;
   p.out = out;
-  size_t off = 0;
+  // counters (zero at rest), then the partials
+  p.counters = fused_merge ? (uint32_t*)ws : nullptr;
+  size_t off = ((size_t)n_runs * NKV * 4 + 255) / 256 * 256;
   p.part_o = (float*)((char*)ws + off);
   off += (size_t)n_runs * NKV * args->max_splits * maxcols * D * 4;
   off = (off + 255) / 256 * 256;
@@ -491,6 +539,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.maxcols = maxcols;
   attn_init();
   dim3 grid(args->max_splits, NKV, n_runs);
+  (void)0;
   const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
 #define SV_ATTN(DD, N) hipLaunchKernelGGL((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
   if (D == 64) {
@@ -510,6 +559,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   }
 #undef SV_ATTN
   SV_TRY_LAUNCH("attn_verify");
+  if (fused_merge) return SV_OK;
   if (D == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
   else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
   return check_launch("attn_merge");

@@ -122,8 +122,9 @@ namespace {
 
 // Threadgroups the attention splits aim for per layer (reference: DEC_TGS_PER_CORE x cores,
 // engine.rs:25); MI355X has 256 CUs.
-constexpr uint32_t ATTN_TARGET_WGS = 1024;
+constexpr uint32_t ATTN_TARGET_WGS = 2048;
 constexpr uint32_t MIN_SPLIT = 128;
+constexpr uint32_t MAX_SPLIT = 512;  // at most 4 batches of 32 keys per wave
 
 struct Plan {
   uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
@@ -726,7 +727,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   if (split == 0) {
     const uint32_t want = std::max<uint32_t>(1, ATTN_TARGET_WGS / (n_runs * e->sh.n_kv_heads));
     split = (max_cached + want - 1) / want;
-    split = std::max<uint32_t>(MIN_SPLIT, (split + 31) / 32 * 32);
+    split = std::min<uint32_t>(MAX_SPLIT, std::max<uint32_t>(MIN_SPLIT, (split + 31) / 32 * 32));
   }
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;

@@ -111,4 +111,31 @@ __device__ __forceinline__ u32x4 philox(u32x4 c, uint32_t k0, uint32_t k1) {
   return c;
 }
 
+// Cross-workgroup hand-off without agent-scope fences (on gfx950 such a fence writes back and
+// invalidates the XCD's whole L2, microseconds per workgroup). The producer writes its partial
+// with relaxed agent-scope atomic stores (global_store ... sc1: coherent across XCDs, and
+// unlike volatile ones not serialised), waits for them (workgroup-scope release: s_waitcnt
+// only), then counts its arrival with a relaxed agent-scope atomic; the last of `expected`
+// arrivals reads every partial with relaxed agent-scope atomic loads (sc1, pipelined) and resets
+// the counter for the next launch. All threads of the workgroup must call arrive_last.
+__device__ __forceinline__ void store_wt(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_wt(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = old == expected - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *lds_flag = last;
+  }
+  __syncthreads();
+  return *lds_flag != 0;
+}
+
 }  // namespace sv
