@@ -187,7 +187,10 @@ sv_status sv_rmsnorm_rows(void* stream, const float* d_in, const uint32_t* d_row
  * gemms_*, gemm_*, gemm_splitk_reduce): d_y[t][row] = epilogue(W[row] . x[t]) for
  * t < a->n, with x[t] = d_x[d_x_rows ? d_x_rows[t] : t] (rows of k floats). d_base is
  * [n][m] for EPI_RESID; d_aux is [n] (WRITE_INV) or [n][m] (WRITE_RAW). The kernel variant
- * is chosen from n (the reference's Matmul::for_tokens, encode.rs:33-44). */
+ * is chosen from n (the reference's Matmul::for_tokens, encode.rs:33-44). The workspace
+ * (sv_matmul_workspace_bytes; zero bytes needs none) carries split-k partials: zero-fill it
+ * once; the kernels leave its counters at zero, so calls in stream order may share one, and
+ * calls that overlap in time must not. */
 size_t sv_matmul_workspace_bytes(uint32_t n, uint32_t m, uint32_t k);
 sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_x, const uint32_t* d_x_rows, float* d_y,
                     const float* d_base, float* d_aux, const sv_mat_args* a, void* d_workspace,
@@ -368,7 +371,8 @@ enum {
   SV_KIND_ACCEPT = 8,
   SV_KIND_COMPACT = 9,
   SV_KIND_REPLAY = 10,
-  SV_KIND_COUNT = 11
+  SV_KIND_ATTN_MERGE = 11, /* the attention split merge (its own launch) */
+  SV_KIND_COUNT = 12
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

@@ -19,10 +19,11 @@
 //     K rows are read as 16-byte slices; each V row is read whole by 16 lanes (8 bytes per
 //     lane for D = 64), and the matrix-core operand takes one of its dims per tile.
 //   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace with
-//     coherent (relaxed agent-scope atomic) stores. attn_merge_kernel, the next launch, sums
-//     the partials of each (run, kv head, column) in split order and writes o / l. With
-//     SV_ATTN_MERGE=fused the last split of (run, kv head) to arrive (a relaxed agent-scope
-//     counter: no L2 write-back or invalidate) merges instead, with coherent loads.
+//     coherent stores (sc1: write-through to the agent-coherent level). attn_merge_kernel,
+//     the next launch, sums the partials of each (run, kv head, column) in split order and
+//     writes o / l. With SV_ATTN_MERGE=fused the last split of (run, kv head) to arrive (a
+//     relaxed agent-scope counter: no L2 write-back or invalidate) does the same with
+//     coherent 16-byte loads.
 #include <cstdlib>
 #include <cstring>
 
@@ -180,7 +181,7 @@ __device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch
 }
 
 template <int D, int NCT>
-__global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
   extern __shared__ float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
   __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
@@ -269,37 +270,53 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   }
 
   // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
-  // p0 + row and to LDS.
+  // p0 + row and to LDS. 16 threads per key (DL dims each, rope pairs within a thread), all
+  // keys at once.
   if (newest) {
-    constexpr int DE = D / 64;  // dims per lane
-    for (uint32_t i = wv; i < T; i += 4) {
+    constexpr int DL = D / 16;
+    const uint32_t i = tid >> 4, l16 = tid & 15;
+    if (i < T) {
       const uint32_t t = t0 + i, pos = p.meta[2 * t + 1];
-      const float* kp = p.qkv + (size_t)t * p.W + p.KOFF + g * D;
-      const float* vp = p.qkv + (size_t)t * p.W + p.VOFF + g * D;
-      float kv[DE];
+      const float* kp = p.qkv + (size_t)t * p.W + p.KOFF + g * D + DL * l16;
+      const float* vp = p.qkv + (size_t)t * p.W + p.VOFF + g * D + DL * l16;
+      float kv[DL], vv[DL];
+#pragma unroll
+      for (int e = 0; e < DL; e += 4) {
+        const f32x4 a = *(const f32x4*)(kp + e), b = *(const f32x4*)(vp + e);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          kv[e + j] = a[j];
+          vv[e + j] = b[j];
+        }
+      }
+      const size_t row = kv_off<D>(p, seq, g, p0 + i);
       float ss = 0.0f;
 #pragma unroll
-      for (int e = 0; e < DE; e++) {
-        kv[e] = kp[lane + 64 * e];
-        ss = __builtin_fmaf(kv[e], kv[e], ss);
-      }
-      ss = wave_sum(ss);
-      const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
-      const size_t row = kv_off<D>(p, seq, g, p0 + i);
+      for (int e = 0; e < DL; e++) ss = __builtin_fmaf(kv[e], kv[e], ss);
 #pragma unroll
-      for (int e = 0; e < DE; e++) {
-        const uint32_t d = lane + 64 * e;
-        float k = kv[e] * inv;
-        const float other = __shfl_xor(k, 1, WAVE);
+      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, WAVE);
+      const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
+      uint32_t kb[DL / 2], vb[DL / 2];
+#pragma unroll
+      for (int e = 0; e < DL; e += 2) {
+        const uint32_t d = DL * l16 + e;
+        float k0 = kv[e] * inv, k1 = kv[e + 1] * inv;
         if (p.rope_on && d < 64) {
           const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
-          k = (d & 1) ? cs.x * k - cs.y * other : cs.x * k + cs.y * other;
+          const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
+          k0 = r0;
+          k1 = r1;
         }
-        const uint16_t kb16 = (uint16_t)to_bf(k), vb16 = (uint16_t)to_bf(vp[d]);
-        p.kc[row + d] = kb16;
-        p.vc[row + d] = vb16;
-        nk[i * D + d] = kb16;
-        nv[i * D + d] = vb16;
+        kb[e / 2] = (uint32_t)to_bf(k0) | ((uint32_t)to_bf(k1) << 16);
+        vb[e / 2] = (uint32_t)to_bf(vv[e]) | ((uint32_t)to_bf(vv[e + 1]) << 16);
+      }
+#pragma unroll
+      for (int e = 0; e < DL / 2; e += 2) {
+        const u32x2 kw = u32x2{kb[e], kb[e + 1]}, vw = u32x2{vb[e], vb[e + 1]};
+        *(u32x2*)(p.kc + row + DL * l16 + 2 * e) = kw;
+        *(u32x2*)(p.vc + row + DL * l16 + 2 * e) = vw;
+        *(u32x2*)(nk + i * D + DL * l16 + 2 * e) = kw;
+        *(u32x2*)(nv + i * D + DL * l16 + 2 * e) = vw;
       }
     }
   }
@@ -344,34 +361,39 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
   }
   __syncthreads();
   const size_t rec = ((size_t)r * p.NKV + g) * p.max_splits + s;
-  float* po = p.part_o + rec * p.maxcols * D;
-  float* pl = p.part_l + rec * p.maxcols;
-  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
-    const uint32_t col = idx / D, d = idx % D;
-    store_wt(po + idx, ((ored[col * D + d] + ored[(COLS + col) * D + d]) + ored[(2 * COLS + col) * D + d]) +
-                           ored[(3 * COLS + col) * D + d]);
+  const uint32_t n4 = ncols * D / 4;
+  {
+    const __amdgpu_buffer_rsrc_t po = coherent_rsrc(p.part_o + rec * p.maxcols * D);
+    for (uint32_t i4 = tid; i4 < n4; i4 += 256) {
+      const f32x4* o4 = (const f32x4*)ored;
+      const uint32_t cs = COLS * D / 4;
+      store_wt4(po, i4 * 16, ((o4[i4] + o4[cs + i4]) + o4[2 * cs + i4]) + o4[3 * cs + i4]);
+    }
   }
+  float* pl = p.part_l + rec * p.maxcols;
   for (uint32_t idx = tid; idx < ncols; idx += 256)
     store_wt(pl + idx, ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx]);
   if (!p.counters) return;  // attn_merge_kernel merges
 
   // The last split of (run, kv head) to arrive merges (attn_dec_reduce, kernels.metal:1316-1362):
-  // plain sums in split order, eight loads in flight per thread.
+  // plain sums in split order, 16-byte coherent loads, eight splits in flight per thread.
   __shared__ uint32_t flag;
   if (!arrive_last(&p.counters[r * p.NKV + g], nsplit, &flag)) return;
   const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
-  const size_t so = (size_t)p.maxcols * D;
-  const float* po0 = p.part_o + rec0 * so;
+  const uint32_t so = p.maxcols * D * 4;  // bytes per split partial
+  const __amdgpu_buffer_rsrc_t po0 = coherent_rsrc(p.part_o + rec0 * p.maxcols * D);
   const float* pl0 = p.part_l + rec0 * p.maxcols;
-  for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
-    const uint32_t col = idx / D, d = idx % D;
-    float o = 0.0f, l = 0.0f;
+  for (uint32_t i4 = tid; i4 < n4; i4 += 256) {
+    const uint32_t col = (4 * i4) / D, d = (4 * i4) % D;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    float l = 0.0f;
     uint32_t sp = 0;
     for (; sp + 8 <= nsplit; sp += 8) {
-      float ov[8], lv[8];
+      f32x4 ov[8];
+      float lv[8];
 #pragma unroll
       for (int u = 0; u < 8; u++) {
-        ov[u] = load_wt(po0 + (sp + u) * so + idx);
+        ov[u] = load_wt4(po0, (sp + u) * so + i4 * 16);
         lv[u] = load_wt(pl0 + (sp + u) * p.maxcols + col);
       }
 #pragma unroll
@@ -381,13 +403,12 @@ __global__ __launch_bounds__(256) void attn_verify_kernel(AttnParams p) {
       }
     }
     for (; sp < nsplit; sp++) {
-      o += load_wt(po0 + sp * so + idx);
+      o += load_wt4(po0, sp * so + i4 * 16);
       l += load_wt(pl0 + sp * p.maxcols + col);
     }
     const uint32_t i = col / p.G, h = g * p.G + col % p.G;
-    p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = o / l;
+    *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
   }
-
 }
 
 // attn_dec_reduce (kernels.metal:1316-1362) for the fused verify attention: one workgroup
@@ -469,6 +490,31 @@ static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
   return (cols + 15) / 16 * 16;
 }
 
+// Workgroups of attn_verify_kernel that the device holds at once for this shape (its
+// occupancy per CU x CUs); 0 if the variant is not built.
+uint32_t attn_resident_wgs(const sv_shape* sh, uint32_t max_run) {
+  if (!sh || sh->n_kv_heads == 0 || max_run == 0 || max_run > SV_MAX_RUN) return 0;
+  const uint32_t D = sh->head_dim, nct = cols_pad(sh, max_run) / 16;
+  if ((D != 64 && D != 128) || nct > 4) return 0;
+  attn_init();
+  const void* fn = nullptr;
+  if (D == 64) {
+    const void* f[4] = {(const void*)attn_verify_kernel<64, 1>, (const void*)attn_verify_kernel<64, 2>,
+                        (const void*)attn_verify_kernel<64, 3>, (const void*)attn_verify_kernel<64, 4>};
+    fn = f[nct - 1];
+  } else {
+    const void* f[4] = {(const void*)attn_verify_kernel<128, 1>, (const void*)attn_verify_kernel<128, 2>,
+                        (const void*)attn_verify_kernel<128, 3>, (const void*)attn_verify_kernel<128, 4>};
+    fn = f[nct - 1];
+  }
+  const size_t shm = (size_t)4 * nct * 16 * D * 4 + (size_t)4 * nct * 16 * 4;
+  int per_cu = 0, dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, shm) != hipSuccess)
+    return 0;
+  return (uint32_t)(per_cu * cus);
+}
+
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run) {
   const size_t maxcols = cols_pad(sh, max_run);
   size_t b = ((size_t)n_runs * sh->n_kv_heads * 4 + 255) / 256 * 256;
@@ -481,7 +527,8 @@ size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, u
 sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
-                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes) {
+                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
+                      uint32_t parts) {
   if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
     return fail(SV_ERR_ARG, "attn_verify: null pointer");
   if (n_runs == 0) return SV_OK;
@@ -496,9 +543,9 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (!rope && args->rope) return fail(SV_ERR_ARG, "attn_verify: rope table missing");
   const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;
   if (nct > 4) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (64 are built)", max_run * NQ / NKV);
-  // The merge runs as its own launch spread over (run, kv head, column) workgroups; with
-  // SV_ATTN_MERGE=fused the last split of each (run, kv head) merges instead (one launch
-  // less, but one workgroup then walks every split: measured slower at 65 splits).
+  // The merge runs as its own launch over (run, kv head, column) workgroups (measured
+  // faster at 9-65 splits); with SV_ATTN_MERGE=fused the last split of each (run, kv head)
+  // to arrive merges instead.
   static const bool fused_merge = [] {
     const char* v = getenv("SV_ATTN_MERGE");
     return v && strcmp(v, "fused") == 0;
@@ -538,28 +585,29 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.layer = kv->kv_layer;
   p.maxcols = maxcols;
   attn_init();
-  dim3 grid(args->max_splits, NKV, n_runs);
-  (void)0;
-  const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
+  if (parts & 1) {
+    dim3 grid(args->max_splits, NKV, n_runs);
+    const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
 #define SV_ATTN(DD, N) hipLaunchKernelGGL((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
-  if (D == 64) {
-    switch (nct) {
-      case 1: SV_ATTN(64, 1); break;
-      case 2: SV_ATTN(64, 2); break;
-      case 3: SV_ATTN(64, 3); break;
-      default: SV_ATTN(64, 4); break;
+    if (D == 64) {
+      switch (nct) {
+        case 1: SV_ATTN(64, 1); break;
+        case 2: SV_ATTN(64, 2); break;
+        case 3: SV_ATTN(64, 3); break;
+        default: SV_ATTN(64, 4); break;
+      }
+    } else {
+      switch (nct) {
+        case 1: SV_ATTN(128, 1); break;
+        case 2: SV_ATTN(128, 2); break;
+        case 3: SV_ATTN(128, 3); break;
+        default: SV_ATTN(128, 4); break;
+      }
     }
-  } else {
-    switch (nct) {
-      case 1: SV_ATTN(128, 1); break;
-      case 2: SV_ATTN(128, 2); break;
-      case 3: SV_ATTN(128, 3); break;
-      default: SV_ATTN(128, 4); break;
-    }
-  }
 #undef SV_ATTN
-  SV_TRY_LAUNCH("attn_verify");
-  if (fused_merge) return SV_OK;
+    SV_TRY_LAUNCH("attn_verify");
+  }
+  if (fused_merge || !(parts & 2)) return SV_OK;
   if (D == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
   else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
   return check_launch("attn_merge");

@@ -120,11 +120,32 @@ extern "C" sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint
 
 namespace {
 
-// Threadgroups the attention splits aim for per layer (reference: DEC_TGS_PER_CORE x cores,
-// engine.rs:25); MI355X has 256 CUs.
-constexpr uint32_t ATTN_TARGET_WGS = 2048;
+// Attention split sizes considered (keys per workgroup: multiples of 128, one 32-key batch
+// per wave and step of 128).
 constexpr uint32_t MIN_SPLIT = 128;
-constexpr uint32_t MAX_SPLIT = 512;  // at most 4 batches of 32 keys per wave
+constexpr uint32_t MAX_SPLIT = 1024;
+// Cost model, in eighths of one 32-key batch per wave: a workgroup's fixed latency (launch,
+// page table, first loads, partial store) is about two batches, and the merge adds about an
+// eighth of a batch per split (fitted to measurements at 2k and 8k keys, 1 and 5 rows).
+constexpr uint64_t ATTN_WG_LATENCY = 16;
+constexpr uint64_t ATTN_BATCH = 8;
+constexpr uint64_t ATTN_MERGE_PER_SPLIT = 1;
+
+// Keys per split (plan.rs:156-164 decode_splits, re-derived for this device): the grid is
+// max_splits x kv heads x runs; the split minimises dispatch rounds (grid / workgroups the
+// device holds at once) x per-workgroup cost + merge cost; ties go to the smaller split.
+uint32_t choose_split(uint32_t max_cached, uint32_t pairs, uint32_t resident) {
+  if (resident == 0) resident = 512;
+  uint32_t best = MIN_SPLIT;
+  uint64_t best_cost = ~0ull;
+  for (uint32_t split = MIN_SPLIT; split <= MAX_SPLIT; split += 128) {
+    const uint64_t splits = (max_cached + split - 1) / split + 1;
+    const uint64_t rounds = (splits * pairs + resident - 1) / resident;
+    const uint64_t cost = rounds * (ATTN_WG_LATENCY + ATTN_BATCH * (split / 128)) + ATTN_MERGE_PER_SPLIT * splits;
+    if (cost < best_cost) best_cost = cost, best = split;
+  }
+  return best;
+}
 
 struct Plan {
   uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
@@ -173,8 +194,10 @@ struct sv_engine {
   // device: activations (buffers.rs Scratch)
   float *h = nullptr, *qkv = nullptr, *attn = nullptr, *mixed = nullptr, *act = nullptr, *inv = nullptr,
         *logits = nullptr;
-  void* ws = nullptr;
+  void* ws = nullptr;  // attention split partials
   size_t ws_bytes = 0;
+  void* mm_ws = nullptr;  // matmul split-k hand-off (counters stay zero between launches)
+  size_t mm_ws_bytes = 0;
 
   // host: page pool (kv.rs) and sequences (engine.rs Seq)
   std::vector<uint32_t> free_pages;
@@ -217,7 +240,7 @@ struct sv_engine {
     if (graph) (void)hipGraphExecDestroy(graph);
     void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
                     head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
-                    attn, mixed, act, inv, logits, ws};
+                    attn, mixed, act, inv, logits, ws, mm_ws};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     if (stream) (void)hipStreamDestroy(stream);
@@ -297,7 +320,7 @@ struct sv_engine {
     a.ksplit = 1;
     a.kchunk = w.k;
     a.gshift = w.gshift;
-    return matmul_launch(stream, &w, x, x_rows, y, base, aux, &a, ws, ws_bytes);
+    return matmul_launch(stream, &w, x, x_rows, y, base, aux, &a, mm_ws, mm_ws_bytes);
   }
 
   // encode.rs:99-126 encode_forward + :383-412 encode_tail.
@@ -319,7 +342,9 @@ struct sv_engine {
       aa.rope = L.rope;
       const sv_kv_args kv = kv_args(li);
       SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes));
+                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 1));
+      SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
+                                               attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 2));
       SV_TIMED(SV_KIND_O,
                matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn, h, nullptr));
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
@@ -463,13 +488,17 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   e->seq_len.assign(S, 0);
   e->used.assign(S, false);
   e->sampling.assign(S, sv_sample_row{0, 0, 0, 0.0f, 1.0f, SV_NO_TOK});
-  // Workspace for the matmuls at the most rows.
+  // Workspace for the matmuls: the most any row count up to the step's (head: head rows) needs.
   size_t ws = 0;
-  const uint32_t rows = std::min<uint32_t>(16, std::max(n, R));
-  const uint32_t mk[][2] = {{e->qkv_w, s.hidden}, {s.hidden, s.n_heads * s.head_dim}, {2 * s.ffn, s.hidden},
-                            {s.hidden, s.ffn}, {s.vocab, s.hidden}};
-  for (auto& x : mk) ws = std::max(ws, matmul_ws_bytes(rows, x[0], x[1]));
-  if ((st = e->ensure_ws(ws)) != SV_OK) return bad(st);
+  const uint32_t mk[][3] = {{e->qkv_w, s.hidden, n}, {s.hidden, s.n_heads * s.head_dim, n}, {2 * s.ffn, s.hidden, n},
+                            {s.hidden, s.ffn, n}, {s.vocab, s.hidden, R}};
+  for (auto& x : mk)
+    for (uint32_t rows = 1; rows <= x[2]; rows++) ws = std::max(ws, matmul_ws_bytes(rows, x[0], x[1]));
+  if (ws) {
+    if (hipMalloc(&e->mm_ws, ws) != hipSuccess || hipMemset(e->mm_ws, 0, ws) != hipSuccess)
+      return bad(fail(SV_ERR_HIP, "matmul workspace (%zu bytes)", ws));
+    e->mm_ws_bytes = ws;
+  }
   *out = e;
   return SV_OK;
 }
@@ -720,15 +749,11 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   P.n = n;
   P.n_head = (uint32_t)head_rows.size();
   P.n_runs = n_runs;
-  // Attention splits (plan.rs:156-164 decode_splits, for 256 CUs): the longest context over
-  // about ATTN_TARGET_WGS workgroups per layer, plus a split of its own for the new keys;
-  // `extra_keys` sizes the grid for replays at later positions.
+  // Attention splits: the cached keys of each run in splits of `split`, plus a split of its
+  // own for the new keys; `extra_keys` sizes the grid for replays at later positions.
   uint32_t split = e->cfg.split_keys;
-  if (split == 0) {
-    const uint32_t want = std::max<uint32_t>(1, ATTN_TARGET_WGS / (n_runs * e->sh.n_kv_heads));
-    split = (max_cached + want - 1) / want;
-    split = std::min<uint32_t>(MAX_SPLIT, std::max<uint32_t>(MIN_SPLIT, (split + 31) / 32 * 32));
-  }
+  if (split == 0)
+    split = choose_split(max_cached + extra_keys, n_runs * e->sh.n_kv_heads, attn_resident_wgs(&e->sh, P.max_run));
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
   SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, n_runs, P.max_splits, P.max_run)));

@@ -23,6 +23,8 @@
 #include "sv_device.h"
 #include "sv_internal.h"
 
+#include <algorithm>
+
 namespace sv {
 
 struct MMParams {
@@ -35,6 +37,12 @@ struct MMParams {
   float* aux;
   uint32_t n, k, m, epi, flags, vocab_real, gshift, chunks, per_row;
   float scale, ra, rb;
+  // Split-k hand-off (skinny path with S > 1): counters per row group (zero at rest),
+  // partial sums and sums of squares per (row group, split).
+  uint32_t* counters;
+  float* part;
+  float* ssp;
+  uint32_t splits, tgroups;  // skinny: k splits and 16-token groups
 };
 
 constexpr int KC = 256;  // k per chunk: one X chunk in registers, 4 blocks of 64
@@ -42,32 +50,44 @@ constexpr int NBLK = KC / 64;
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
-// One workgroup of W waves owns RT tiles of 16 output rows over the whole of k: wave wv
-// takes k chunks wv, wv + W, ... (so no partial sum ever leaves the workgroup).
+// One workgroup of W waves owns RT tiles of 16 output rows, one group of 16 tokens and a
+// 1/S share of k: wave wv of split s takes k chunks s W + wv, + S W, ... The waves' sums meet
+// in LDS in wave order; with S > 1 each split's sums go to the workspace with coherent stores
+// and the last split of the (row group, token group) to arrive (relaxed agent-scope counter)
+// adds them in split order and runs the epilogue: deterministic whatever the arrival order.
+// Work items (row group, split, token group) are numbered token group fastest and dealt to
+// the XCDs in contiguous blocks, so token groups that share weight rows share an L2.
 template <int FMT, int RT, int W>
 __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
   constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2;  // dwordx4 loads per lane per 64-k block
   constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int t = lane & 15, q = lane >> 4;
-  const uint32_t xg = blockIdx.x;
+  const uint32_t S = p.splits, TG = p.tgroups, nwg = gridDim.x;
+  uint32_t item = blockIdx.x;
+  if (nwg % 8 == 0) item = (item % 8) * (nwg / 8) + item / 8;
+  const uint32_t tg = item % TG, sp = (item / TG) % S, xg = item / (TG * S);
+  const uint32_t tok0 = 16 * tg, n_loc = min(16u, p.n - tok0);
 
   __shared__ f32x4 red[W][RT][64];
   __shared__ float ssred[W][16];
+  __shared__ uint32_t last_flag;
 
   f32x4 acc[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
   float ss = 0.0f;
-  const bool tok = (uint32_t)t < p.n;
-  const float* xrow = p.x + (size_t)(tok ? (p.x_rows ? p.x_rows[t] : (uint32_t)t) : 0u) * p.k + 16 * q;
+  const bool tok = (uint32_t)t < n_loc;
+  const uint32_t tt = tok0 + t;
+  const float* xrow = p.x + (size_t)(tok ? (p.x_rows ? p.x_rows[tt] : tt) : 0u) * p.k + 16 * q;
   const uint8_t* wbase[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; rt++)
     wbase[rt] = p.w + ((size_t)((xg * RT + rt) * 16 + t) * p.k) * ESZ + (64 * 0 + 16 * q) * WV;
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
+  const uint32_t stride = W * S;
 
-  uint32_t c = wv;
+  uint32_t c = sp * W + wv;
   u32x4 wr[RT][NBLK * WV];
   if (c < p.chunks) {
 #pragma unroll
@@ -79,7 +99,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
           wr[rt][b * WV + v] =
               __builtin_nontemporal_load((const u32x4*)(wbase[rt] + ((size_t)c * KC + 64 * b) * ESZ + 16 * v));
   }
-  for (; c < p.chunks; c += W) {
+  for (; c < p.chunks; c += stride) {
     const uint32_t kbase = c * KC;
     // X chunk: token t, k = kbase + 64 b + 16 q + 0..15, as hi/lo bf16 B operands.
     bf16x8 xh[NBLK][2], xl[NBLK][2];
@@ -111,7 +131,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
       for (int i = 0; i < NBLK * WV; i++) cur[rt][i] = wr[rt][i];
-    const uint32_t cn = c + W;
+    const uint32_t cn = c + stride;
     if (cn < p.chunks) {
 #pragma unroll
       for (int rt = 0; rt < RT; rt++)
@@ -163,28 +183,66 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
   for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
   if (q == 0) ssred[wv][t] = ss;
   __syncthreads();
-  if (wv != 0) return;
+  if (wv == 0) {
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++) {
-    f32x4 a = red[0][rt][lane];
+    for (int rt = 0; rt < RT; rt++) {
+      f32x4 a = red[0][rt][lane];
 #pragma unroll
-    for (int w = 1; w < W; w++) a += red[w][rt][lane];
-    acc[rt] = a;
+      for (int w = 1; w < W; w++) a += red[w][rt][lane];
+      acc[rt] = a;
+    }
+    ss = ssred[0][t];
+#pragma unroll
+    for (int w = 1; w < W; w++) ss += ssred[w][t];
   }
-  ss = ssred[0][t];
+  if (S > 1) {
+    // Split hand-off: partial [group][split][rt][lane] (f32x4), sums of squares [group][split][t].
+    const size_t cell = (size_t)xg * TG + tg;
+    float* part = p.part + (cell * S * RT) * 256;
+    float* ssp = p.ssp + cell * S * 16;
+    if (wv == 0) {
 #pragma unroll
-  for (int w = 1; w < W; w++) ss += ssred[w][t];
+      for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) store_wt(part + ((size_t)sp * RT + rt) * 256 + 4 * lane + i, acc[rt][i]);
+      if (q == 0) store_wt(ssp + sp * 16 + t, ss);
+    }
+    if (!arrive_last(p.counters + cell, S, &last_flag)) return;
+    if (wv != 0) return;
+    f32x4 tot[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) tot[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float sst = 0.0f;
+    for (uint32_t s2 = 0; s2 < S; s2++) {
+      if (s2 == sp) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) tot[rt] += acc[rt];
+        sst += ss;
+        continue;
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) tot[rt][i] += load_wt(part + ((size_t)s2 * RT + rt) * 256 + 4 * lane + i);
+      sst += load_wt(ssp + s2 * 16 + t);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) acc[rt] = tot[rt];
+    ss = sst;
+  } else if (wv != 0) {
+    return;
+  }
 
   // Epilogue (kernels.metal:183-209): lane (t, q) holds rows 4 q + 0..3 of each tile.
-  if ((uint32_t)t >= p.n) return;
+  if ((uint32_t)t >= n_loc) return;
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
-  if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && xg == 0 && q == 0) p.aux[t] = inv;
+  if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && xg == 0 && q == 0) p.aux[tt] = inv;
   const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) {
     const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
     f32x4 v = acc[rt];
-    const size_t o = (size_t)t * p.m + row0;
+    const size_t o = (size_t)tt * p.m + row0;
     switch (p.epi) {
       case SV_EPI_NORM:
         *(f32x4*)(p.y + o) = v * (inv * p.scale);
@@ -216,7 +274,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
         float2 out;
         out.x = g0 * sigmoidf_(g0) * u0;
         out.y = g1 * sigmoidf_(g1) * u1;
-        *(float2*)(p.y + (size_t)t * (p.m / 2) + row0 / 2) = out;
+        *(float2*)(p.y + (size_t)tt * (p.m / 2) + row0 / 2) = out;
         break;
       }
       default:
@@ -465,14 +523,6 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   }
 }
 
-// Row tiles per workgroup: the largest of 4, 2, 1 that divides the tiles and still gives at
-// least 512 workgroups (2 per CU), else 1.
-static int pick_rt(uint32_t tiles) {
-  for (int rt = 4; rt > 1; rt /= 2)
-    if (tiles % rt == 0 && tiles / rt >= 512) return rt;
-  return 1;
-}
-
 // Token tiles per workgroup (BN = 16 NT) and row tiles per wave (BM = 64 RTW) for n rows:
 // the fewest padded tokens, then enough workgroups to fill 256 CUs.
 static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, const MMParams& p) {
@@ -514,37 +564,92 @@ static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, const MMParams& p
   return check_launch("matmul (gemm)");
 }
 
+// Skinny launch shape: RT row tiles per workgroup, W waves, S splits of k.
+struct SkinnyCfg {
+  int rt, w, s;
+};
+SkinnyTune g_skinny_tune;  // all zero: the built-in choice
+
+// Beyond 16 rows the skinny kernel runs one workgroup per 16-token group (weights re-read
+// from L2 per group); measured on MI355X at 160 and 512 rows it beats the LDS-tiled GEMM on
+// matrices of up to 4096 rows (qkv, o, down) and loses on wider ones (gate_up, head).
+constexpr uint32_t SKINNY_MAX_N = 512;
+constexpr uint32_t SKINNY_MAX_M_MANY_ROWS = 4096;
+
+static bool use_skinny(uint32_t n, uint32_t m, uint32_t k) {
+  if (m % 16 || k % KC) return false;
+  if (g_skinny_tune.path) return g_skinny_tune.path == 1;
+  return n <= 16 || (n <= SKINNY_MAX_N && m <= SKINNY_MAX_M_MANY_ROWS);
+}
+
+// Measured on MI355X at 1-5 rows: about 128 KB of weights per workgroup and at least 256
+// workgroups; with more token groups the X chunk dominates a wave's loads, so as many row
+// tiles as possible share it. 8 waves for int8, 4 for bf16 (twice the registers per row);
+// k splits only when the tiles give too few workgroups and every wave still has two chunks.
+static SkinnyCfg pick_skinny(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k) {
+  const uint32_t tiles = m / 16, chunks = k / KC, esz = fmt == SV_FMT_I8 ? 1 : 2, tg = (n + 15) / 16;
+  const size_t max_wg_bytes = tg > 1 ? ~(size_t)0 : (128u << 10);
+  SkinnyCfg c{1, fmt == SV_FMT_I8 ? 8 : 4, 1};
+  for (int rt = 4; rt > 1; rt /= 2)
+    if (tiles % rt == 0 && (tg > 1 || tiles / rt >= 256) && (size_t)rt * 16 * k * esz <= max_wg_bytes) {
+      c.rt = rt;
+      break;
+    }
+  while (c.s < 8 && (tiles / c.rt) * c.s * tg < 256 && (uint32_t)(c.w * c.s * 2) <= chunks) c.s *= 2;
+  if (g_skinny_tune.rt) {
+    c.rt = g_skinny_tune.rt;
+    c.w = g_skinny_tune.w;
+    c.s = g_skinny_tune.s;
+  }
+  return c;
+}
+
+// Workspace layout (skinny, S > 1), per cell (row group, token group): counters [m / 16][TG]
+// u32, then sums of squares [cells][S][16] and partials [cells][S][RT][64][4] fp32.
+static size_t skinny_ws_layout(uint32_t n, uint32_t m, const SkinnyCfg& c, size_t* ss_off, size_t* part_off) {
+  if (c.s <= 1) return 0;
+  const size_t tg = (n + 15) / 16, cells = (size_t)m / (16 * c.rt) * tg;
+  size_t off = ((size_t)(m / 16) * tg * 4 + 255) / 256 * 256;
+  *ss_off = off;
+  off += (cells * c.s * 16 * 4 + 255) / 256 * 256;
+  *part_off = off;
+  off += cells * c.s * c.rt * 256 * 4;
+  return off;
+}
+
 size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
-  (void)n;
-  (void)m;
-  (void)k;
-  return 0;
+  if (n == 0 || !use_skinny(n, m, k)) return 0;
+  size_t a, b;
+  return std::max(skinny_ws_layout(n, m, pick_skinny(SV_FMT_I8, n, m, k), &a, &b),
+                  skinny_ws_layout(n, m, pick_skinny(SV_FMT_BF16, n, m, k), &a, &b));
 }
 
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes) {
-  (void)ws;
-  (void)ws_bytes;
   if (!w || !a || !x || !y || !w->d_w) return fail(SV_ERR_ARG, "matmul: null pointer");
   if (a->k != w->k || a->m != w->m) return fail(SV_ERR_ARG, "matmul: args (m %u, k %u) != matrix (%u, %u)", a->m, a->k, w->m, w->k);
   if (a->n == 0) return SV_OK;
-  if (a->n > 16 ? (a->k % GKC != 0 || a->m % 64 != 0) : (a->k % KC != 0 || a->m % 16 != 0))
-    return fail(SV_ERR_ARG, "matmul: k %u must be a multiple of %d and m %u of %d", a->k, a->n > 16 ? GKC : KC, a->m,
-                a->n > 16 ? 64 : 16);
-  if (a->epi == SV_EPI_SWIGLU && a->m % 2) return fail(SV_ERR_ARG, "matmul: swiglu needs even m");
-  if (a->epi < SV_EPI_NORM || a->epi > SV_EPI_RAW) return fail(SV_ERR_ARG, "matmul: epilogue %u", a->epi);
-  if (a->epi == SV_EPI_RESID && !base) return fail(SV_ERR_ARG, "matmul: resid needs base");
-  if ((a->flags & (SV_FLAG_WRITE_INV | SV_FLAG_WRITE_RAW)) && !aux) return fail(SV_ERR_ARG, "matmul: flags need aux");
   bool per_row = true;
   if (w->format == SV_FMT_I8) {
     if (!w->d_scales) return fail(SV_ERR_ARG, "matmul: int8 without scales");
     per_row = a->gshift >= 32 || (1ull << a->gshift) >= a->k;
-    const uint32_t min_shift = a->n > 16 ? 6 : 8;
-    if (!per_row && (a->gshift < min_shift || a->k % (1u << a->gshift) != 0))
-      return fail(SV_ERR_UNSUPPORTED, "matmul: int8 group 2^%u: groups of at least %u (or one per row) are built",
-                  a->gshift, 1u << min_shift);
   } else if (w->format != SV_FMT_BF16) {
     return fail(SV_ERR_ARG, "matmul: format %u", w->format);
+  }
+  // The skinny kernel takes int8 scales per row or per group of >= 256 (one per k chunk).
+  const bool skinny = use_skinny(a->n, a->m, a->k) && (per_row || a->gshift >= 8);
+  if (!skinny && (a->k % GKC != 0 || a->m % 64 != 0))
+    return fail(SV_ERR_ARG, "matmul: k %u and m %u must be multiples of %d and 16 (or of %d and 64)", a->k, a->m, KC,
+                GKC);
+  if (a->epi == SV_EPI_SWIGLU && a->m % 2) return fail(SV_ERR_ARG, "matmul: swiglu needs even m");
+  if (a->epi < SV_EPI_NORM || a->epi > SV_EPI_RAW) return fail(SV_ERR_ARG, "matmul: epilogue %u", a->epi);
+  if (a->epi == SV_EPI_RESID && !base) return fail(SV_ERR_ARG, "matmul: resid needs base");
+  if ((a->flags & (SV_FLAG_WRITE_INV | SV_FLAG_WRITE_RAW)) && !aux) return fail(SV_ERR_ARG, "matmul: flags need aux");
+  if (!per_row) {
+    const uint32_t min_shift = skinny ? 8 : 6;
+    if (a->gshift < min_shift || a->k % (1u << a->gshift) != 0)
+      return fail(SV_ERR_UNSUPPORTED, "matmul: int8 group 2^%u: groups of at least %u (or one per row) are built",
+                  a->gshift, 1u << min_shift);
   }
   MMParams p;
   p.w = (const uint8_t*)w->d_w;
@@ -566,14 +671,28 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.ra = a->ra;
   p.rb = a->rb;
   p.chunks = a->k / KC;
-  if (a->n > 16) return gemm_launch(stream, w->format, p);
-  const uint32_t tiles = a->m / 16;
-  const int rt = pick_rt(tiles);
-  const int waves = p.chunks >= 8 ? 8 : 4;
-  dim3 grid(tiles / rt);
+  p.counters = nullptr;
+  p.part = p.ssp = nullptr;
+  if (!skinny) return gemm_launch(stream, w->format, p);
+  const SkinnyCfg cfg = pick_skinny(w->format, a->n, a->m, a->k);
+  const int rt = cfg.rt, waves = cfg.w;
+  if ((a->m / 16) % rt != 0 || (rt != 1 && rt != 2 && rt != 4) || (waves != 4 && waves != 8 && waves != 16) || (waves == 16 && rt == 4) ||
+      cfg.s < 1)
+    return fail(SV_ERR_ARG, "matmul: launch shape rt %d, waves %d, splits %d", rt, waves, cfg.s);
+  size_t ss_off = 0, part_off = 0;
+  const size_t need = skinny_ws_layout(a->n, a->m, cfg, &ss_off, &part_off);
+  if (need > 0 && (!ws || ws_bytes < need))
+    return fail(SV_ERR_ARG, "matmul: workspace %zu < %zu bytes (sv_matmul_workspace_bytes)", ws_bytes, need);
+  p.counters = need ? (uint32_t*)ws : nullptr;
+  p.ssp = need ? (float*)((char*)ws + ss_off) : nullptr;
+  p.part = need ? (float*)((char*)ws + part_off) : nullptr;
+  p.splits = cfg.s;
+  p.tgroups = (a->n + 15) / 16;
+  dim3 grid(a->m / 16 / rt * cfg.s * p.tgroups);
 #define SV_MM(F, R, W) hipLaunchKernelGGL((mm_skinny<F, R, W>), grid, dim3(64 * W), 0, stream, p)
-#define SV_MM_W(F, R)        \
-  if (waves == 8) SV_MM(F, R, 8); \
+#define SV_MM_W(F, R)                          \
+  if (waves == 16 && R <= 2) SV_MM(F, R, 16);  \
+  else if (waves == 8) SV_MM(F, R, 8);         \
   else SV_MM(F, R, 4)
   if (w->format == SV_FMT_I8) {
     if (rt == 4) { SV_MM_W(SV_FMT_I8, 4); }

@@ -125,6 +125,20 @@ __device__ __forceinline__ float load_wt(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// 16-byte versions through a buffer resource (sc1 cache policy: the same agent-scope
+// coherence as the relaxed atomics above, four words per access). `base` must be 16-byte
+// aligned; byte offsets below 2 GiB.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+constexpr int SV_CPOL_SC1 = 16;
+__device__ __forceinline__ f32x4 load_wt4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, SV_CPOL_SC1));
+}
+__device__ __forceinline__ void store_wt4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, SV_CPOL_SC1);
+}
+
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();

@@ -18,15 +18,23 @@ sv_status check_launch(const char* what);
 sv_status check_hip(hipError_t e, const char* what);
 
 size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k);
+// Launch-shape override for the skinny matmul (row tiles, waves, k splits; zero: built-in)
+// and the path for more than 16 rows (0: built-in, 1: skinny, 2: GEMM).
+struct SkinnyTune {
+  int rt, w, s, path;
+};
+extern SkinnyTune g_skinny_tune;
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes);
 
 void attn_init();
+uint32_t attn_resident_wgs(const sv_shape* sh, uint32_t max_run);
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
 sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
-                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes);
+                      uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
+                      uint32_t parts = 3);  // bit 0: attention, bit 1: the split merge
 
 // tokens_out may equal tokens (resolution in place, as the reference's embed).
 sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,

@@ -83,6 +83,8 @@ def test_argument_checks_without_gpu():
 def test_workspace_sizes_grow_with_work():
     lib = L.lib()
     # the skinny matmul keeps every partial sum inside its workgroup: no workspace
-    assert lib.sv_matmul_workspace_bytes(5, 2048, 8192) == 0
+    # split-k partials for a skinny matmul with few row tiles and long k; none for the GEMM path
+    assert lib.sv_matmul_workspace_bytes(5, 2048, 8192) > 0
+    assert lib.sv_matmul_workspace_bytes(600, 2048, 8192) == 0
     sh = L.Shape(2048, 32, 8, 64, 8192, 32000, 32000, 16)
     assert lib.sv_attn_workspace_bytes(C.byref(sh), 32, 64, 16) > lib.sv_attn_workspace_bytes(C.byref(sh), 1, 64, 5)

@@ -5,6 +5,8 @@ per test (fp32 accumulation in a different order, activations as bf16 hi + lo pa
 significant bits per element)."""
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -107,6 +109,36 @@ def test_matmul_repeat_workspace(gpu):
     torch.cuda.synchronize()
     for y in outs[1:]:
         assert torch.equal(y, outs[0])
+
+
+@pytest.mark.parametrize("rt,waves,splits", [(1, 8, 2), (1, 4, 8), (2, 8, 4), (4, 4, 2), (2, 16, 1), (1, 16, 2)])
+def test_matmul_skinny_launch_shapes(gpu, rt, waves, splits):
+    """Every skinny launch shape (row tiles, waves, k splits) gives the oracle's result,
+    including the sums of squares carried across splits (EPI_NORM), on two calls that share
+    one workspace. The shape is forced through the library's internal override."""
+    banner(f"matmul launch shape rt={rt} waves={waves} splits={splits}")
+    tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv13g_skinny_tuneE")
+    rng = np.random.default_rng(rt * 100 + waves * 10 + splits)
+    m, k, n = 2048, 8192, 5
+    q, s = quantize_rows(torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32)))
+    mat = K.matrix(q.cuda(), s.cuda(), 31)
+    ws = K.Workspace(32 << 20)
+    try:
+        tune[0], tune[1], tune[2] = rt, waves, splits
+        for call in range(2):
+            x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
+            a = L.MatArgs(n, k, m, L.EPI_NORM, L.FLAG_WRITE_INV, m, 0.75, 0, 0, 1, k, 31)
+            aux_ref = np.zeros(n, np.float32)
+            ref = oracle.matmul(L, q.numpy(), s.view(torch.int16).numpy().view(np.uint16), 31, x, a, aux=aux_ref)
+            y = torch.zeros(n, m, device="cuda")
+            aux = torch.zeros(n, device="cuda")
+            K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_NORM, flags=L.FLAG_WRITE_INV, scale=0.75, aux=aux, ws=ws)
+            torch.cuda.synchronize()
+            close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
+                  what=f"call {call}")
+            close(aux.cpu().numpy(), aux_ref, atol=1e-5, rtol=1e-4, what="inv")
+    finally:
+        tune[0] = tune[1] = tune[2] = 0
 
 
 # ---------------------------------------------------------------------------- attention
