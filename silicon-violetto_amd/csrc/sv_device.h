@@ -114,8 +114,8 @@ __device__ __forceinline__ u32x4 philox(u32x4 c, uint32_t k0, uint32_t k1) {
 // Cross-workgroup hand-off without agent-scope fences (on gfx950 such a fence writes back and
 // invalidates the XCD's whole L2, microseconds per workgroup). The producer writes its partial
 // with relaxed agent-scope atomic stores (global_store ... sc1: coherent across XCDs, and
-// unlike volatile ones not serialised), waits for them (workgroup-scope release: s_waitcnt
-// only), then counts its arrival with a relaxed agent-scope atomic; the last of `expected`
+// unlike volatile ones not serialised), waits for them (s_waitcnt vmcnt(0) in every thread),
+// then counts its arrival with a relaxed agent-scope atomic; the last of `expected`
 // arrivals reads every partial with relaxed agent-scope atomic loads (sc1, pipelined) and resets
 // the counter for the next launch. All threads of the workgroup must call arrive_last.
 __device__ __forceinline__ void store_wt(float* p, float v) {
@@ -139,8 +139,14 @@ __device__ __forceinline__ void store_wt4(__amdgpu_buffer_rsrc_t r, uint32_t byt
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, SV_CPOL_SC1);
 }
 
+// Wait until this thread's memory operations have completed (s_waitcnt vmcnt(0); the gfx9
+// encoding leaves expcnt and lgkmcnt at their maxima). A workgroup-scope release fence does
+// not wait for global stores (the workgroup shares one CU), so a cross-workgroup hand-off
+// needs this before the workgroup barrier that precedes its counter update.
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t expected, uint32_t* lds_flag) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  wait_mem();
   __syncthreads();
   if (threadIdx.x == 0) {
     const uint32_t old = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
