@@ -27,7 +27,7 @@
 #include <cstdlib>
 #include <cstring>
 
-#include "sv_device.h"
+#include "attn_device.h"
 #include "sv_internal.h"
 
 #define SV_TRY_LAUNCH(what)                        \
@@ -37,148 +37,6 @@
   } while (0)
 
 namespace sv {
-
-struct AttnParams {
-  const float* qkv;
-  const uint32_t* meta;
-  uint16_t* kc;
-  uint16_t* vc;
-  const uint32_t* page_table;
-  const float* rope;
-  const uint32_t* runs;
-  const uint32_t* vis;
-  float* out;
-  float* part_o;
-  float* part_l;
-  uint32_t* counters;  // per (run, kv head): fused merge; null: attn_merge_kernel merges
-  uint32_t NQ, NKV, G, W, KOFF, VOFF;
-  uint32_t split, max_splits;
-  float scale_log2;
-  uint32_t rope_on;
-  uint32_t page_shift, n_pages, max_pages, layer, maxcols;
-};
-
-// Element offset of kv head g's row at cache position pos (kernels.metal:704-711, global).
-template <int D>
-__device__ __forceinline__ size_t kv_off(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t pos) {
-  const uint32_t page = p.page_table[(size_t)seq * p.max_pages + (pos >> p.page_shift)];
-  return ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
-         (size_t)(pos & ((1u << p.page_shift) - 1u)) * D;
-}
-
-template <int VE>
-struct VWord;
-template <>
-struct VWord<4> {
-  typedef u32x2 type;
-};
-template <>
-struct VWord<8> {
-  typedef u32x4 type;
-};
-
-// One batch of 32 keys [kb, kb + 32) below kend, for one wave: its K and V words (loaded
-// ahead of use) and the products. NEW: the keys are the run's new ones, in LDS (index
-// key - p0), masked by each column's vis.
-template <int D>
-struct KvBatch {
-  static constexpr int KST = D / 32, VE = D / 16;
-  typedef typename VWord<VE>::type vword;
-  u32x4 kw[2][KST];  // lane (c16, q): key kb + 16 mt + c16, dims 32 ks + 8 q .. + 7
-  vword vw[8];       // slot j: key kb + 16 (j / 4) + 4 q + j % 4, dims VE c16 .. + VE - 1
-};
-
-template <int D, bool NEW>
-__device__ __forceinline__ void load_batch(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t kb, uint32_t kend,
-                                           uint32_t p0, const uint16_t* nk, const uint16_t* nv, KvBatch<D>& b,
-                                           int lane) {
-  constexpr int KST = D / 32, VE = D / 16;
-  typedef typename KvBatch<D>::vword vword;
-  const int c16 = lane & 15, q = lane >> 4;
-  // A tile of 16 keys never straddles a page (pages hold >= 16 keys, kb is a multiple of 32).
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++) {
-    const uint32_t first = min(kb + 16 * mt, kend - 1);
-    const uint16_t* kt;
-    const uint16_t* vt;
-    if (NEW) {
-      kt = nk + (size_t)(first - p0) * D;
-      vt = nv + (size_t)(first - p0) * D;
-    } else {
-      const size_t off = kv_off<D>(p, seq, g, first);
-      kt = p.kc + off;
-      vt = p.vc + off;
-    }
-    const uint32_t key = min(kb + 16 * mt + c16, kend - 1);
-    const uint16_t* kr = kt + (size_t)(key - first) * D;
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = *(const u32x4*)(kr + 32 * ks + 8 * q);
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-      const uint32_t vk = min(kb + 16 * mt + 4 * q + jj, kend - 1);
-      b.vw[4 * mt + jj] = *(const vword*)(vt + (size_t)(vk - first) * D + VE * c16);
-    }
-  }
-}
-
-template <int D, int NCT, bool NEW>
-__device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch<D>& b, uint32_t kb, uint32_t kend,
-                                              uint32_t p0, uint32_t ncols, uint32_t t0,
-                                              const bf16x8 (&qh)[NCT][D / 32], const bf16x8 (&ql)[NCT][D / 32],
-                                              f32x4 (&O)[D / 16][NCT], float (&lsum)[NCT], int lane) {
-  constexpr int KST = D / 32, VE = D / 16;
-  const int c16 = lane & 15, q = lane >> 4;
-  // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
-  f32x4 S[2][NCT];
-#pragma unroll
-  for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-    for (int ct = 0; ct < NCT; ct++) {
-      f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KST; ks++) {
-        const bf16x8 kk = __builtin_bit_cast(bf16x8, b.kw[mt][ks]);
-        a = mfma16(kk, qh[ct][ks], a);
-        a = mfma16(kk, ql[ct][ks], a);
-      }
-      S[mt][ct] = a;
-    }
-  bf16x8 ph[NCT], pl[NCT];
-#pragma unroll
-  for (int ct = 0; ct < NCT; ct++) {
-    const uint32_t c = 16 * ct + c16;
-    const bool col_ok = c < ncols;
-    uint32_t vbits = 0;
-    if (NEW && col_ok) vbits = p.vis[t0 + c / p.G];
-    float pv[8];
-#pragma unroll
-    for (int mt = 0; mt < 2; mt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t key = kb + 16 * mt + 4 * q + i;
-        bool ok = col_ok && key < kend;
-        if (NEW) ok = ok && ((vbits >> (key - p0)) & 1u);
-        const float e = ok ? exp2f(S[mt][ct][i]) : 0.0f;
-        pv[4 * mt + i] = e;
-        lsum[ct] += e;
-      }
-    split8(pv, ph[ct], pl[ct]);
-  }
-  // O^T[dt] (rows: dims VE (4 q + i) + dt) += V^T[dt] P^T.
-#pragma unroll
-  for (int dt = 0; dt < VE; dt++) {
-    u32x4 a;
-    const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
-#pragma unroll
-    for (int jj = 0; jj < 4; jj++) a[jj] = __builtin_amdgcn_perm(b.vw[2 * jj + 1][dt >> 1], b.vw[2 * jj][dt >> 1], sel);
-    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
-#pragma unroll
-    for (int ct = 0; ct < NCT; ct++) {
-      O[dt][ct] = mfma16(av, ph[ct], O[dt][ct]);
-      O[dt][ct] = mfma16(av, pl[ct], O[dt][ct]);
-    }
-  }
-}
 
 template <int D, int NCT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
@@ -213,113 +71,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   KvBatch<D> cur;
   if ((uint32_t)wv < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kend, p0, nullptr, nullptr, cur, lane);
 
-  // Queries (kernels.metal:1022-1039 with norm_rope :727-736): k slot j of step ks is dim
-  // 32 ks + 8 q + j.
   bf16x8 qh[NCT][KST], ql[NCT][KST];
-#pragma unroll
-  for (int ct = 0; ct < NCT; ct++) {
-    const uint32_t c = 16 * ct + c16;
-    const bool ok = c < ncols;
-    float v[KST][8];
-    uint32_t pos = 0;
-    float ss = 0.0f;
-    if (ok) {
-      const uint32_t i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
-      pos = p.meta[2 * t + 1];
-      const float* qp = p.qkv + (size_t)t * p.W + h * D + 8 * q;
-#pragma unroll
-      for (int ks = 0; ks < KST; ks++) {
-        const f32x4 a = *(const f32x4*)(qp + 32 * ks), b = *(const f32x4*)(qp + 32 * ks + 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          v[ks][e] = a[e];
-          v[ks][4 + e] = b[e];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KST; ks++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[ks][e] = 0.0f;
-    }
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[ks][e], v[ks][e], ss);
-    ss += __shfl_xor(ss, 16, WAVE);
-    ss += __shfl_xor(ss, 32, WAVE);
-    const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++) {
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[ks][e] *= inv;
-      if (p.rope_on && ok && 32 * ks + 8 * q < 64) {
-#pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-          const uint32_t j = 16 * ks + 4 * q + jj;
-          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + j) * 2);
-          const float a0 = v[ks][2 * jj], a1 = v[ks][2 * jj + 1];
-          v[ks][2 * jj] = cs.x * a0 + cs.y * a1;
-          v[ks][2 * jj + 1] = cs.x * a1 - cs.y * a0;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[ks][e] *= p.scale_log2;
-      split8(v[ks], qh[ct][ks], ql[ct][ks]);
-    }
-  }
+  build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
 
-  // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
-  // p0 + row and to LDS. 16 threads per key (DL dims each, rope pairs within a thread), all
-  // keys at once.
-  if (newest) {
-    constexpr int DL = D / 16;
-    const uint32_t i = tid >> 4, l16 = tid & 15;
-    if (i < T) {
-      const uint32_t t = t0 + i, pos = p.meta[2 * t + 1];
-      const float* kp = p.qkv + (size_t)t * p.W + p.KOFF + g * D + DL * l16;
-      const float* vp = p.qkv + (size_t)t * p.W + p.VOFF + g * D + DL * l16;
-      float kv[DL], vv[DL];
-#pragma unroll
-      for (int e = 0; e < DL; e += 4) {
-        const f32x4 a = *(const f32x4*)(kp + e), b = *(const f32x4*)(vp + e);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          kv[e + j] = a[j];
-          vv[e + j] = b[j];
-        }
-      }
-      const size_t row = kv_off<D>(p, seq, g, p0 + i);
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < DL; e++) ss = __builtin_fmaf(kv[e], kv[e], ss);
-#pragma unroll
-      for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, WAVE);
-      const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
-      uint32_t kb[DL / 2], vb[DL / 2];
-#pragma unroll
-      for (int e = 0; e < DL; e += 2) {
-        const uint32_t d = DL * l16 + e;
-        float k0 = kv[e] * inv, k1 = kv[e + 1] * inv;
-        if (p.rope_on && d < 64) {
-          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
-          const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
-          k0 = r0;
-          k1 = r1;
-        }
-        kb[e / 2] = (uint32_t)to_bf(k0) | ((uint32_t)to_bf(k1) << 16);
-        vb[e / 2] = (uint32_t)to_bf(vv[e]) | ((uint32_t)to_bf(vv[e + 1]) << 16);
-      }
-#pragma unroll
-      for (int e = 0; e < DL / 2; e += 2) {
-        const u32x2 kw = u32x2{kb[e], kb[e + 1]}, vw = u32x2{vb[e], vb[e + 1]};
-        *(u32x2*)(p.kc + row + DL * l16 + 2 * e) = kw;
-        *(u32x2*)(p.vc + row + DL * l16 + 2 * e) = vw;
-        *(u32x2*)(nk + i * D + DL * l16 + 2 * e) = kw;
-        *(u32x2*)(nv + i * D + DL * l16 + 2 * e) = vw;
-      }
-    }
-  }
+  if (newest) new_keys<D, false>(p, seq, g, t0, T, p0, nk, nv, tid, 256);
   __syncthreads();
 
   f32x4 O[VE][NCT];

@@ -72,6 +72,14 @@ __device__ __forceinline__ bf16x8 i8x8_to_bf(uint32_t w0, uint32_t w1) {
   return __builtin_bit_cast(bf16x8, r);
 }
 
+// Loads through pointers the compiler cannot prove global (read from a struct in memory)
+// would be FLAT loads, which also count against lgkmcnt: every LDS or scalar wait then
+// waits for them too, which defeats loads issued ahead. These cast to the global space.
+typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) const uint16_t g_u16;
+__device__ __forceinline__ u32x4 ldg_nt(const void* p) { return __builtin_nontemporal_load((g_u32x4*)p); }
+__device__ __forceinline__ uint16_t ldg_u16(const uint16_t* p) { return *(g_u16*)p; }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);

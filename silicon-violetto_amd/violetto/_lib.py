@@ -30,7 +30,7 @@ EPI_NORM, EPI_RESID, EPI_SWIGLU, EPI_HEAD, EPI_RAW = 1, 2, 3, 4, 5
 FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
-KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge")
+KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "layers")
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 
@@ -80,7 +80,10 @@ class ReplayArgs(C.Structure):
 class EngineConfig(C.Structure):
     _fields_ = [("shape", Shape), ("max_seqs", u32), ("max_step_tokens", u32), ("max_seq_len", u32),
                 ("max_head_rows", u32), ("kv_tokens", u32), ("page_shift", u32), ("attn_scale", f32),
-                ("split_keys", u32)]
+                ("split_keys", u32), ("options", u32)]
+
+
+ENGINE_STEP_KERNEL = 1
 
 
 class Layer(C.Structure):
@@ -100,7 +103,8 @@ class Run(C.Structure):
 
 
 class PlanInfo(C.Structure):
-    _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits")]
+    _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits",
+                                   "persistent")]
 
 
 P = C.POINTER

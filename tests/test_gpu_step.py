@@ -23,11 +23,12 @@ LOGIT_ATOL, LOGIT_RTOL = 2e-2, 1e-2
 
 
 def build_pair(shape: ModelShape, *, ctx: int, n_seqs: int = 1, seed: int = 0, int8: bool = True, page_shift=4,
-               max_seq_len=1024, scalars=None, shuffle=False):
+               max_seq_len=1024, scalars=None, shuffle=False, step_kernel=True):
     model = SyntheticModel.generate(shape, int8=int8, seed=seed, device="cpu", scalars=scalars)
     freq = rope_freq(500000.0, shape.head_dim)
     eng = Engine(shape, max_seqs=n_seqs, max_step_tokens=16 * n_seqs, max_seq_len=max_seq_len, max_head_rows=16,
-                 kv_tokens=n_seqs * max_seq_len, page_shift=page_shift, attn_scale=0.125, freq=freq)
+                 kv_tokens=n_seqs * max_seq_len, page_shift=page_shift, attn_scale=0.125, freq=freq,
+                 step_kernel=step_kernel)
     gm = model.to("cuda")
     eng.set_model(gm)
     emb, lay, sc = oracle.host_weights(model)
@@ -71,11 +72,13 @@ def compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots):
             assert eng.seq_pages(s) == ref.pool.pages(s)
 
 
-def test_config0_step(gpu):
-    """one layer + head, 512 cached tokens, k = 4 uniform drafts, greedy, seed 0."""
-    banner("config0 step")
+@pytest.mark.parametrize("persistent", [True, False])
+def test_config0_step(gpu, persistent):
+    """configs[0]: one layer + head, 512 cached tokens, k = 4 uniform drafts, greedy, seed 0;
+    the layers as one persistent launch and as separate launches."""
+    banner(f"config0 step persistent={persistent}")
     shape = ModelShape(n_layers=1)
-    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=512, seed=0)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=512, seed=0, step_kernel=persistent)
     s = slots[0]
     tok0 = int(rng.integers(0, shape.vocab))
     eng.set_feed(s, 512, tok0)
@@ -83,19 +86,22 @@ def test_config0_step(gpu):
     drafts = [int(x) for x in rng.integers(0, shape.vocab, 4)]
     run = (s, [L.FEED_ROW] + drafts, True)
     res = eng.step([run], logits=True)
+    assert res.info.persistent == int(persistent)
     ids_r, logits_r, em_r, extra_r = ref.step([run])
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
 
 
+@pytest.mark.parametrize("persistent", [True, False])
 @pytest.mark.parametrize("scalars", [LayerScalars(), LayerScalars(0.8, 1.2, 0.9, 1.1, 0.95, 0.7, 1),
                                      LayerScalars(1.1, 0.9, 1.0, 0.5, 1.0, 1.3, 0)])
-def test_two_layer_steps_with_replayed_drafts(gpu, scalars):
+def test_two_layer_steps_with_replayed_drafts(gpu, scalars, persistent):
     """Two layers, two sequences, three steps: drafts copied from the oracle's own greedy
     continuation (some right, some wrong), so acceptance, emitted counts, lengths and the
     next step's inputs are exercised; KV of rejected rows is overwritten later."""
-    banner(f"two-layer steps {scalars}")
+    banner(f"two-layer steps {scalars} persistent={persistent}")
     shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
-    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[300, 77], n_seqs=2, seed=3, scalars=scalars)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[300, 77], n_seqs=2, seed=3, scalars=scalars,
+                                                 step_kernel=persistent)
     for s in slots:
         t = int(rng.integers(0, shape.vocab_real))
         eng.set_feed(s, ref.seq_len[s], t)
@@ -108,6 +114,7 @@ def test_two_layer_steps_with_replayed_drafts(gpu, scalars):
             runs.append((s, [L.FEED_ROW] + drafts, True))
         ids_r, logits_r, em_r, extra_r = ref.step(runs)
         res = eng.step(runs, logits=True)
+        assert res.info.persistent == int(persistent)
         compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
         assert np.array_equal(res.ids, ids_r), "greedy ids diverged (margins within tolerance)"
 
