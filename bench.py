@@ -164,15 +164,29 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     return res
 
 
-def roofline_of(res, profile_reps):
+def roofline_of(res, profile_reps, workload=None):
+    """The dominant kernel (most algorithmic HBM bytes per step) against the HBM peak: bytes per
+    launch / its mean duration (hipExtLaunchKernelGGL start/stop events around the kernel's own
+    execution, over `profile_reps` steps of the timed workload). `traffic` is the measured HBM
+    bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated) from profiles/hbm_traffic.json
+    when it holds this workload's kernel."""
     prof = res["prof"]
-    dominant = max(prof, key=lambda kk: prof[kk][0])
-    bytes_per_launch = res["mat_bytes"].get(dominant, res["attn_bytes"] if dominant == "attn" else 0)
+    per_launch = dict(res["mat_bytes"])
+    per_launch["attn"] = res["attn_bytes"]
+    per_step = {kk: per_launch[kk] * prof[kk][1] / profile_reps for kk in per_launch if kk in prof and prof[kk][1]}
+    dominant = max(per_step, key=per_step.get)
+    bytes_per_launch = per_launch[dominant]
     d_ms, d_n = prof[dominant]
     d_avg_ms = d_ms / d_n
     achieved = bytes_per_launch / (d_avg_ms * 1e-3) / 1e9
+    traffic = None
+    tf = ROOT / "profiles" / "hbm_traffic.json"
+    if workload and tf.exists():
+        t = json.loads(tf.read_text()).get(workload, {}).get(dominant)
+        if t:
+            traffic = int(t["fetch_bytes"] + t["write_bytes"])
     return {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "bytes_per_launch": int(bytes_per_launch),
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "bytes_per_launch": int(bytes_per_launch),
             "avg_launch_us": round(d_avg_ms * 1e3, 3)}
 
 
@@ -197,6 +211,9 @@ def main() -> int:
     ap.add_argument("--cpu-steps", type=int, default=2, help="oracle steps for the CPU baseline (0: skip)")
     ap.add_argument("--streams32-steps", type=int, default=30, help="timed steps of configs[2] (0: skip)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="end with 4 elementwise passes over 256 MiB (the known-size kernel that scales "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -235,7 +252,7 @@ def main() -> int:
                "config": {"workload": "configs[2]: 32 streams, ctx U[1024,8192] (mean %d), shuffled page tables, "
                                       "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
                           "rows_per_step": 32 * r2["rows"]},
-               "roofline": roofline_of(r2, 2), "step_roofline": step_roofline(r2),
+               "roofline": roofline_of(r2, 2, "configs[2]"), "step_roofline": step_roofline(r2),
                "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r2["per_step_ms"].items()}}
         r2["eng"].close()
 
@@ -257,13 +274,21 @@ def main() -> int:
                    "rows_per_step": r1["rows"], "draft_mistake_rate": args.mistake_rate},
         "emitted_per_step": round(r1["emitted"] / args.steps, 3),
         "lossless_trace_check": r1["lossless"],
-        "roofline": roofline_of(r1, args.profile_reps),
+        "roofline": roofline_of(r1, args.profile_reps, "configs[1]"),
         "step_roofline": step_roofline(r1),
         "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r1["per_step_ms"].items()},
         "cpu_baseline": cpu,
         "streams32": s32,
     }
     print(json.dumps(line), flush=True)
+    if args.calibrate_copy:
+        # an elementwise kernel of known traffic: reads and writes 64 Mi floats (256 MiB each)
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log("calibration: 4 elementwise passes over 256 MiB (read 256 MiB, write 256 MiB each)")
     return 0
 
 

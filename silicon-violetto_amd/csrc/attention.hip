@@ -343,7 +343,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);
     const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
-#define SV_ATTN(DD, N) hipLaunchKernelGGL((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
+#define SV_ATTN(DD, N) launch((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
     if (D == 64) {
       switch (nct) {
         case 1: SV_ATTN(64, 1); break;
@@ -363,8 +363,8 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     SV_TRY_LAUNCH("attn_verify");
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
-  if (D == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
-  else hipLaunchKernelGGL(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
+  if (D == 64) launch(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
+  else launch(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
   return check_launch("attn_merge");
 }
 

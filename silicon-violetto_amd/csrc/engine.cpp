@@ -118,6 +118,10 @@ extern "C" sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint
 
 // ---------------------------------------------------------------- the engine
 
+namespace sv {
+thread_local ProfEvents g_prof;
+}
+
 namespace {
 
 // Attention split sizes considered (keys per workgroup: multiples of 128, one 32-key batch
@@ -221,18 +225,28 @@ struct sv_engine {
   bool prof = false;
   std::vector<std::pair<int, std::pair<hipEvent_t, hipEvent_t>>> prof_events;
 
+  // Each timed kernel's events are taken by sv::launch at the kernel's own start and end.
   sv_status mark_begin(hipEvent_t* ev) {
     if (!prof) return SV_OK;
+    hipEvent_t stop;
     SV_HIP(hipEventCreate(ev), "event");
-    SV_HIP(hipEventRecord(*ev, stream), "event record");
+    SV_HIP(hipEventCreate(&stop), "event");
+    g_prof.start = *ev;
+    g_prof.stop = stop;
+    g_prof.used = false;
     return SV_OK;
   }
   sv_status mark_end(int kind, hipEvent_t begin) {
     if (!prof) return SV_OK;
-    hipEvent_t end;
-    SV_HIP(hipEventCreate(&end), "event");
-    SV_HIP(hipEventRecord(end, stream), "event record");
-    prof_events.push_back({kind, {begin, end}});
+    const hipEvent_t stop = g_prof.stop;
+    const bool used = g_prof.used;
+    g_prof = ProfEvents{};
+    if (!used) {  // nothing launched (an empty step part): no time
+      SV_HIP(hipEventDestroy(begin), "event");
+      SV_HIP(hipEventDestroy(stop), "event");
+      return SV_OK;
+    }
+    prof_events.push_back({kind, {begin, stop}});
     return SV_OK;
   }
 #define SV_TIMED(kind, call)          \

@@ -541,7 +541,7 @@ static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, const MMParams& p
       break;
     }
   const uint32_t nwg = p.m / (64 * rtw) * n_tblk;
-#define SV_G(F, R, N) hipLaunchKernelGGL((mm_gemm<F, R, N>), dim3(nwg), dim3(256), 0, stream, p, n_tblk)
+#define SV_G(F, R, N) launch((mm_gemm<F, R, N>), dim3(nwg), dim3(256), 0, stream, p, n_tblk)
 #define SV_G_N(F, R)                \
   switch (nt) {                     \
     case 2: SV_G(F, R, 2); break;   \
@@ -689,7 +689,7 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.splits = cfg.s;
   p.tgroups = (a->n + 15) / 16;
   dim3 grid(a->m / 16 / rt * cfg.s * p.tgroups);
-#define SV_MM(F, R, W) hipLaunchKernelGGL((mm_skinny<F, R, W>), grid, dim3(64 * W), 0, stream, p)
+#define SV_MM(F, R, W) launch((mm_skinny<F, R, W>), grid, dim3(64 * W), 0, stream, p)
 #define SV_MM_W(F, R)                          \
   if (waves == 16 && R <= 2) SV_MM(F, R, 16);  \
   else if (waves == 8) SV_MM(F, R, 8);         \

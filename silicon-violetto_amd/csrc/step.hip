@@ -840,8 +840,8 @@ sv_status step_launch(hipStream_t stream, const StepLaunch& a) {
   p.mm_counters = (uint32_t*)((char*)a.ws + mmc_off);
   p.mm_part = (float*)((char*)a.ws + mmp_off);
   const size_t lds = step_lds_bytes(D, nct, a.n);
-  if (nct == 1) hipLaunchKernelGGL((step_kernel<64, 1>), dim3(G), dim3(ST), lds, stream, p);
-  else hipLaunchKernelGGL((step_kernel<64, 2>), dim3(G), dim3(ST), lds, stream, p);
+  if (nct == 1) launch((step_kernel<64, 1>), dim3(G), dim3(ST), lds, stream, p);
+  else launch((step_kernel<64, 2>), dim3(G), dim3(ST), lds, stream, p);
   return check_launch("step");
 }
 

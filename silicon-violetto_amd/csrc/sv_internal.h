@@ -1,6 +1,7 @@
 // sv_internal.h — host-side declarations shared by the translation units of libsv_verify.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -8,6 +9,25 @@
 #include "../../include/sv_verify.h"
 
 namespace sv {
+
+// Per-kernel timing (sv_profile_step): when `start` is set, the next launch through sv::launch
+// records the pair at the kernel's own start and end (hipExtLaunchKernelGGL), so the elapsed
+// time is the kernel's execution as a profiler sees it, without the dispatch around it.
+struct ProfEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+extern thread_local ProfEvents g_prof;
+
+template <typename K, typename... A>
+inline void launch(K kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t stream, A... args) {
+  if (g_prof.start && !g_prof.used) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, g_prof.start, g_prof.stop, 0, args...);
+    g_prof.used = true;
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, stream, args...);
+  }
+}
 
 
 // Record a thread-local error message and return `code` (sv_last_error reads it).

@@ -410,7 +410,7 @@ sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* t
   if (!sh || !table || !tokens || !tokens_out || !out || !tin || !meta || !lens || !feed || !tree || !vis)
     return fail(SV_ERR_ARG, "embed: null pointer");
   if (n == 0) return SV_OK;
-  hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, tokens_out, out, tin, meta, lens, feed,
+  launch(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, tokens_out, out, tin, meta, lens, feed,
                      tree, vis, sh->hidden, sh->vocab);
   return check_launch("embed");
 }
@@ -419,7 +419,7 @@ sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_
                               uint32_t hidden) {
   if (!in || !rows || !out) return fail(SV_ERR_ARG, "rmsnorm_rows: null pointer");
   if (n == 0) return SV_OK;
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, stream, in, rows, out, hidden);
+  launch(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, stream, in, rows, out, hidden);
   return check_launch("rmsnorm_rows");
 }
 
@@ -428,7 +428,7 @@ sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample
   if (!logits || !rows || !out) return fail(SV_ERR_ARG, "sample: null pointer");
   if (n_rows == 0) return SV_OK;
   if (vocab == 0) return fail(SV_ERR_ARG, "sample: empty vocabulary");
-  hipLaunchKernelGGL(sample_kernel, dim3(n_rows), dim3(SV_SAMPLE_THREADS), 0, stream, logits, rows, out, meta, vocab);
+  launch(sample_kernel, dim3(n_rows), dim3(SV_SAMPLE_THREADS), 0, stream, logits, rows, out, meta, vocab);
   return check_launch("sample");
 }
 
@@ -438,7 +438,7 @@ sv_status accept_launch(hipStream_t stream, const sv_run_in* runs, const uint32_
   if (!runs || !tokens || !out || !lens || !feed || !gen || !emitted || !tree || !path || !path_len || !on_path)
     return fail(SV_ERR_ARG, "accept: null pointer");
   if (nruns == 0) return SV_OK;
-  hipLaunchKernelGGL(accept_kernel, dim3((nruns + 63) / 64), dim3(64), 0, stream, runs, tokens, out, lens, feed, gen,
+  launch(accept_kernel, dim3((nruns + 63) / 64), dim3(64), 0, stream, runs, tokens, out, lens, feed, gen,
                      emitted, nruns, tree, path, path_len, on_path);
   return check_launch("accept");
 }
@@ -451,7 +451,7 @@ sv_status kv_compact_launch(hipStream_t stream, const sv_shape* sh, const sv_run
   if (nruns == 0) return SV_OK;
   if (sh->n_kv_heads * sh->head_dim / 4 > 256 || sh->head_dim % 4)
     return fail(SV_ERR_UNSUPPORTED, "kv_compact: %u kv heads x %u dims", sh->n_kv_heads, sh->head_dim);
-  hipLaunchKernelGGL(kv_compact_kernel, dim3(nruns, sh->n_layers), dim3(256), 0, stream, runs, path, path_len, lens,
+  launch(kv_compact_kernel, dim3(nruns, sh->n_layers), dim3(256), 0, stream, runs, path, path_len, lens,
                      k_cache, v_cache, page_table, sh->n_kv_heads, sh->head_dim, kv->page_shift, kv->n_pages,
                      kv->max_pages);
   return check_launch("kv_compact");
@@ -463,7 +463,7 @@ sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nrun
   if (!runs || !lens || !feed || !trace || !trace_len || !ra || !tree) return fail(SV_ERR_ARG, "replay: null pointer");
   if (nruns == 0) return SV_OK;
   if (ra->vocab == 0) return fail(SV_ERR_ARG, "replay: vocab 0");
-  hipLaunchKernelGGL(replay_kernel, dim3(nruns), dim3(64), 0, stream, runs, nruns, lens, feed, trace, trace_len, *ra,
+  launch(replay_kernel, dim3(nruns), dim3(64), 0, stream, runs, nruns, lens, feed, trace, trace_len, *ra,
                      tree);
   return check_launch("replay_draft");
 }
@@ -512,7 +512,7 @@ sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_
     p.ra = sv_replay_args{0, 0, 0.0f, 1};
   }
   if (p.replay && (!trace || !trace_len)) return fail(SV_ERR_ARG, "step tail: replay without a trace");
-  hipLaunchKernelGGL(step_tail_kernel, dim3(nruns), dim3(256), 0, stream, p);
+  launch(step_tail_kernel, dim3(nruns), dim3(256), 0, stream, p);
   return check_launch("step tail");
 }
 
