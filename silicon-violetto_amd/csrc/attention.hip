@@ -48,10 +48,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c16 = lane & 15, q = lane >> 4;
   const uint32_t s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
-  const uint32_t t0 = p.runs[2 * r], T = p.runs[2 * r + 1];
-  const uint32_t seq = p.meta[2 * t0], p0 = p.meta[2 * t0 + 1];
-  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
+  uint32_t t0, T, seq;
+  if (p.n_inline) {
+    t0 = p.inl[3 * r];
+    T = p.inl[3 * r + 1];
+    seq = p.inl[3 * r + 2];
+  } else {
+    t0 = p.runs[2 * r];
+    T = p.runs[2 * r + 1];
+    seq = p.meta[2 * t0];
+  }
+  // With the run known up front (the engine's plan), this wave's first batch of the split's
+  // keys is requested before the context length (meta) arrives: the split is taken as full
+  // (kv_off clamps positions to the table and the pool) and keys past the context are masked
+  // by compute_batch's kend. Without it, the batch waits for meta. Either way it is in
+  // flight while the queries are built. The run's visibility masks (for the newest split's
+  // masks) are requested first, into LDS.
+  __shared__ uint32_t svis[SV_MAX_RUN];
+  if (tid < T) svis[tid] = p.vis[t0 + tid];
+  KvBatch<D> cur;
+  const uint32_t kbeg = s * p.split;
+  const bool ahead = p.n_inline && (uint32_t)wv * 32 < p.split;
+  if (ahead) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kbeg + p.split, kbeg + p.split, nullptr, nullptr, cur, lane);
+  const uint32_t p0 = p.meta[2 * t0 + 1];
   const uint32_t ncols = T * p.G;
+  bf16x8 qh[NCT][KST], ql[NCT][KST];
+  build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
+
+  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
   if (nsplit > p.max_splits) {
     // The grid has too few splits for this run's context: its output is NaN (never a
     // partial sum) and the counter is left alone.
@@ -65,14 +89,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   if (s >= nsplit) return;
   const bool newest = s == nsplit - 1;
 
-  // This wave's first batch of cached keys goes out before the queries are built.
-  const uint32_t kbeg = s * p.split, kend = newest ? p0 : min(kbeg + p.split, p0);
+  const uint32_t kend = newest ? p0 : min(kbeg + p.split, p0);
   const uint32_t nb = newest ? 0u : (kend - kbeg + 31) / 32;
-  KvBatch<D> cur;
-  if ((uint32_t)wv < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kend, p0, nullptr, nullptr, cur, lane);
-
-  bf16x8 qh[NCT][KST], ql[NCT][KST];
-  build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
+  if (!ahead && (uint32_t)wv < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kend, p0, nullptr, nullptr, cur, lane);
 
   if (newest) new_keys<D, false>(p, seq, g, t0, T, p0, nk, nv, tid, 256);
   __syncthreads();
@@ -89,7 +108,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
     if (wv == 0) {
       KvBatch<D> nb0;
       load_batch<D, true>(p, seq, g, p0, p0 + T, p0, nk, nv, nb0, lane);
-      compute_batch<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane);
+      compute_batch<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, svis);
     }
   } else {
     for (uint32_t b = wv; b < nb; b += 4) {
@@ -177,35 +196,35 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
   __shared__ float sl[P];
   const uint32_t r = blockIdx.x, g = blockIdx.y, col = blockIdx.z, tid = threadIdx.x;
   const uint32_t d = tid % D, part = tid / D;
-  const uint32_t t0 = p.runs[2 * r], T = p.runs[2 * r + 1];
+  const uint32_t t0 = p.n_inline ? p.inl[3 * r] : p.runs[2 * r];
+  const uint32_t T = p.n_inline ? p.inl[3 * r + 1] : p.runs[2 * r + 1];
   const uint32_t ncols = T * p.G;
   if (col >= ncols) return;
+  // The partials of every split the grid has are requested at once, before the context
+  // length (meta) says how many count; the rest are never added.
   const uint32_t p0 = p.meta[2 * t0 + 1];
-  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
-  if (nsplit > p.max_splits) return;  // the attention kernel wrote NaN
   const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
   const size_t so_stride = (size_t)p.maxcols * D;
   const float* po = p.part_o + rec0 * so_stride + (size_t)col * D + d;
   const float* pl = p.part_l + rec0 * p.maxcols + col;
   float o = 0.0f, l = 0.0f;
-  uint32_t sp = part;
-  for (; sp + 7 * P < nsplit; sp += 8 * P) {
+  for (uint32_t sp = part; sp < p.max_splits; sp += 8 * P) {
     float ov[8], lv[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      ov[u] = po[(sp + u * P) * so_stride];
-      lv[u] = pl[(sp + u * P) * p.maxcols];
+      const bool in = sp + u * P < p.max_splits;
+      ov[u] = in ? po[(sp + u * P) * so_stride] : 0.0f;
+      lv[u] = in ? pl[(sp + u * P) * p.maxcols] : 0.0f;
     }
+    const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;  // after the loads are issued
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      o += ov[u];
-      l += lv[u];
-    }
+    for (int u = 0; u < 8; u++)
+      if (sp + u * P < nsplit) {
+        o += ov[u];
+        l += lv[u];
+      }
   }
-  for (; sp < nsplit; sp += P) {
-    o += po[sp * so_stride];
-    l += pl[sp * p.maxcols];
-  }
+  if ((p0 + p.split - 1) / p.split + 1 > p.max_splits) return;  // the attention kernel wrote NaN
   so[part][d] = o;
   if (d == 0) sl[part] = l;
   __syncthreads();
@@ -283,7 +302,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts) {
+                      uint32_t parts, const uint32_t* host_runs) {
   if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
     return fail(SV_ERR_ARG, "attn_verify: null pointer");
   if (n_runs == 0) return SV_OK;
@@ -339,6 +358,11 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.max_pages = kv->max_pages;
   p.layer = kv->kv_layer;
   p.maxcols = maxcols;
+  p.n_inline = 0;
+  if (host_runs && n_runs <= SV_INLINE_RUNS) {
+    p.n_inline = n_runs;
+    for (uint32_t i = 0; i < 3 * n_runs; i++) p.inl[i] = host_runs[i];
+  }
   attn_init();
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);

@@ -7,6 +7,8 @@
 
 namespace sv {
 
+constexpr uint32_t SV_INLINE_RUNS = 32;
+
 struct AttnParams {
   const float* qkv;
   const uint32_t* meta;
@@ -25,6 +27,11 @@ struct AttnParams {
   float scale_log2;
   uint32_t rope_on;
   uint32_t page_shift, n_pages, max_pages, layer, maxcols;
+  // Runs known to the host when the launch is encoded (the engine's plan): (first token,
+  // rows, sequence slot) per run, so the kernels start without reading runs and meta; 0: read
+  // them from `runs` / `meta`.
+  uint32_t n_inline;
+  uint32_t inl[3 * SV_INLINE_RUNS];
 };
 
 // Step constants of one run, cached in LDS by the persistent step for all layers: positions
@@ -40,7 +47,10 @@ struct RunConsts {
 // Element offset of kv head g's row at cache position pos (kernels.metal:704-711, global).
 template <int D>
 __device__ __forceinline__ size_t kv_off(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t pos) {
-  const uint32_t page = p.page_table[(size_t)seq * p.max_pages + (pos >> p.page_shift)];
+  // Clamped to the table and the pool: keys read ahead of knowing the context length (and
+  // masked later) stay in bounds; valid positions are unchanged.
+  const uint32_t pi = min(pos >> p.page_shift, p.max_pages - 1);
+  const uint32_t page = min(p.page_table[(size_t)seq * p.max_pages + pi], p.n_pages - 1);
   return ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
          (size_t)(pos & ((1u << p.page_shift) - 1u)) * D;
 }
@@ -107,7 +117,7 @@ __device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch
                                               uint32_t p0, uint32_t ncols, uint32_t t0,
                                               const bf16x8 (&qh)[NCT][D / 32], const bf16x8 (&ql)[NCT][D / 32],
                                               f32x4 (&O)[D / 16][NCT], float (&lsum)[NCT], int lane,
-                                              const RunConsts* rc = nullptr) {
+                                              const uint32_t* vis_cached = nullptr) {
   constexpr int KST = D / 32, VE = D / 16;
   const int c16 = lane & 15, q = lane >> 4;
   // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
@@ -131,7 +141,7 @@ __device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch
     const uint32_t c = 16 * ct + c16;
     const bool col_ok = c < ncols;
     uint32_t vbits = 0;
-    if (NEW && col_ok) vbits = rc ? rc->vis[c / p.G] : p.vis[t0 + c / p.G];
+    if (NEW && col_ok) vbits = vis_cached ? vis_cached[c / p.G] : p.vis[t0 + c / p.G];
     float pv[8];
 #pragma unroll
     for (int mt = 0; mt < 2; mt++)
@@ -171,6 +181,95 @@ __device__ __forceinline__ f32x4 ld_act(const float* base, size_t off) {
   return *(const f32x4*)(base + off);
 }
 
+// Raw query words of a lane's columns (loaded) before the norm, RoPE and split.
+template <int D, int NCT>
+struct QRaw {
+  float v[NCT][D / 32][8];
+  uint32_t pos[NCT];
+};
+
+template <int D, int NCT, bool COH>
+__device__ __forceinline__ void qload(const AttnParams& p, uint32_t t0, uint32_t g, uint32_t ncols, QRaw<D, NCT>& r,
+                                      int lane, const RunConsts* rc = nullptr) {
+  constexpr int KST = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const uint32_t c = 16 * ct + c16;
+    r.pos[ct] = 0;
+    if (c < ncols) {
+      const uint32_t i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
+      // with rc: the row index into its tables
+      r.pos[ct] = rc ? i : p.meta[2 * t + 1];
+      const size_t qo = (size_t)t * p.W + h * D + 8 * q;
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const f32x4 a = ld_act<COH>(p.qkv, qo + 32 * ks), b = ld_act<COH>(p.qkv, qo + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          r.v[ct][ks][e] = a[e];
+          r.v[ct][ks][4 + e] = b[e];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) r.v[ct][ks][e] = 0.0f;
+    }
+  }
+}
+
+template <int D, int NCT>
+__device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r, bf16x8 (&qh)[NCT][D / 32],
+                                        bf16x8 (&ql)[NCT][D / 32], int lane, const RunConsts* rc = nullptr) {
+  constexpr int KST = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
+  // Rope words first (all columns), so their loads are in flight together.
+  float2 cs[NCT][KST][4];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        const uint32_t j = 16 * ks + 4 * q + jj;
+        const bool on = p.rope_on && 16 * ct + c16 < ncols && 32 * ks + 8 * q < 64;
+        cs[ct][ks][jj] = !on ? float2{1.0f, 0.0f}
+                         : rc ? rc->rope[r.pos[ct]][j]
+                              : *(const float2*)(p.rope + ((size_t)r.pos[ct] * SV_ROPE_PAIRS + j) * 2);
+      }
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const bool ok = 16 * ct + c16 < ncols;
+    float ss = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+      for (int e = 0; e < 8; e++) ss = __builtin_fmaf(r.v[ct][ks][e], r.v[ct][ks][e], ss);
+    ss += __shfl_xor(ss, 16, WAVE);
+    ss += __shfl_xor(ss, 32, WAVE);
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) {
+      float* v = r.v[ct][ks];
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] *= inv;
+      if (p.rope_on && ok && 32 * ks + 8 * q < 64) {
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const float a0 = v[2 * jj], a1 = v[2 * jj + 1];
+          v[2 * jj] = cs[ct][ks][jj].x * a0 + cs[ct][ks][jj].y * a1;
+          v[2 * jj + 1] = cs[ct][ks][jj].x * a1 - cs[ct][ks][jj].y * a0;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] *= p.scale_log2;
+      split8(v, qh[ct][ks], ql[ct][ks]);
+    }
+  }
+}
+
 // Queries of columns 16 ct + c16 (kernels.metal:1022-1039 with norm_rope :727-736): rms-norm
 // over the head, RoPE on pairs, times softmax scale x log2 e, split into bf16 hi + lo MFMA
 // operands; k slot j of step ks is dim 32 ks + 8 q + j. COH: qkv is read with coherent
@@ -179,62 +278,9 @@ template <int D, int NCT, bool COH>
 __device__ __forceinline__ void build_queries(const AttnParams& p, uint32_t t0, uint32_t g, uint32_t ncols,
                                               bf16x8 (&qh)[NCT][D / 32], bf16x8 (&ql)[NCT][D / 32], int lane,
                                               const RunConsts* rc = nullptr) {
-  constexpr int KST = D / 32;
-  const int c16 = lane & 15, q = lane >> 4;
-#pragma unroll
-  for (int ct = 0; ct < NCT; ct++) {
-    const uint32_t c = 16 * ct + c16;
-    const bool ok = c < ncols;
-    float v[KST][8];
-    uint32_t pos = 0, ci = 0;
-    float ss = 0.0f;
-    if (ok) {
-      const uint32_t i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
-      ci = i;
-      if (!rc) pos = p.meta[2 * t + 1];
-      const size_t qo = (size_t)t * p.W + h * D + 8 * q;
-#pragma unroll
-      for (int ks = 0; ks < KST; ks++) {
-        const f32x4 a = ld_act<COH>(p.qkv, qo + 32 * ks), b = ld_act<COH>(p.qkv, qo + 32 * ks + 4);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          v[ks][e] = a[e];
-          v[ks][4 + e] = b[e];
-        }
-      }
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KST; ks++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[ks][e] = 0.0f;
-    }
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++)
-#pragma unroll
-      for (int e = 0; e < 8; e++) ss = __builtin_fmaf(v[ks][e], v[ks][e], ss);
-    ss += __shfl_xor(ss, 16, WAVE);
-    ss += __shfl_xor(ss, 32, WAVE);
-    const float inv = 1.0f / __builtin_sqrtf(ss / (float)D + SV_RMS_EPS);
-#pragma unroll
-    for (int ks = 0; ks < KST; ks++) {
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[ks][e] *= inv;
-      if (p.rope_on && ok && 32 * ks + 8 * q < 64) {
-#pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-          const uint32_t j = 16 * ks + 4 * q + jj;
-          const float2 cs = rc ? rc->rope[ci][j] : *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + j) * 2);
-          const float a0 = v[ks][2 * jj], a1 = v[ks][2 * jj + 1];
-          v[ks][2 * jj] = cs.x * a0 + cs.y * a1;
-          v[ks][2 * jj + 1] = cs.x * a1 - cs.y * a0;
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) v[ks][e] *= p.scale_log2;
-      split8(v[ks], qh[ct][ks], ql[ct][ks]);
-    }
-  }
-
+  QRaw<D, NCT> r;
+  qload<D, NCT, COH>(p, t0, g, ncols, r, lane, rc);
+  qfinish<D, NCT>(p, ncols, r, qh, ql, lane, rc);
 }
 
 // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
@@ -275,7 +321,8 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
         const uint32_t d = DL * l16 + e;
         float k0 = kv[e] * inv, k1 = kv[e + 1] * inv;
         if (p.rope_on && d < 64) {
-          const float2 cs = rc ? rc->rope[i][d / 2] : *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
+          const float2 cs = rc ? rc->rope[i][d / 2]
+                               : *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
           const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
           k0 = r0;
           k1 = r1;

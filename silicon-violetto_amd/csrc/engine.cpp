@@ -157,6 +157,7 @@ struct Plan {
   std::vector<uint32_t> slots;   // per run
   std::vector<uint32_t> counts;  // per run
   std::vector<uint32_t> verify;  // per run
+  std::vector<uint32_t> inl;     // per run: first token, rows, slot (the attention's inline runs)
 };
 
 template <typename T>
@@ -432,9 +433,10 @@ struct sv_engine {
       aa.rope = L.rope;
       const sv_kv_args kv = kv_args(li);
       SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 1));
+                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data()));
       SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                               attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 2));
+                                               attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 2,
+                                               P.inl.data()));
       SV_TIMED(SV_KIND_O,
                matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn, h, nullptr));
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
@@ -832,6 +834,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     P.branches |= (r.verify && count > 2) ? 1u : 0u;
     P.slots.push_back(slot);
     P.counts.push_back(count);
+    P.inl.insert(P.inl.end(), {first_row, count, slot});
     P.verify.push_back(r.verify ? 1u : 0u);
     e->seq_len[slot] += count;
   }

@@ -50,6 +50,59 @@ constexpr int NBLK = KC / 64;
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Epilogue of the skinny kernels (kernels.metal:183-209): lane (t, q) holds rows 4 q + 0..3
+// of each of the workgroup's RT tiles for token tt; ss: the token's sum of squares over k.
+template <int RT>
+__device__ __forceinline__ void skinny_epilogue(const MMParams& p, const f32x4 (&acc)[RT], float ss, uint32_t xg, int q,
+                                                uint32_t tt) {
+  const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
+  if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && xg == 0 && q == 0) p.aux[tt] = inv;
+  const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+    const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
+    f32x4 v = acc[rt];
+    const size_t o = (size_t)tt * p.m + row0;
+    switch (p.epi) {
+      case SV_EPI_NORM:
+        *(f32x4*)(p.y + o) = v * (inv * p.scale);
+        break;
+      case SV_EPI_RAW:
+        if (norm_in) v *= inv;
+        *(f32x4*)(p.y + o) = v;
+        break;
+      case SV_EPI_RESID: {
+        if (norm_in) v *= inv;
+        const f32x4 sv = v * p.scale;
+        const f32x4 b = *(const f32x4*)(p.base + o);
+        *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
+        if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
+        break;
+      }
+      case SV_EPI_HEAD: {
+        if (norm_in) v *= inv;
+        f32x4 l;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          l[i] = row0 + i < p.vocab_real ? 23.0f * sigmoidf_((v[i] + 5.0f) / 7.5f) : -__builtin_inff();
+        *(f32x4*)(p.y + o) = l;
+        break;
+      }
+      case SV_EPI_SWIGLU: {
+        const float sc = inv * p.scale;
+        const float g0 = v[0] * sc, u0 = v[1] * sc, g1 = v[2] * sc, u1 = v[3] * sc;
+        float2 out;
+        out.x = g0 * sigmoidf_(g0) * u0;
+        out.y = g1 * sigmoidf_(g1) * u1;
+        *(float2*)(p.y + (size_t)tt * (p.m / 2) + row0 / 2) = out;
+        break;
+      }
+      default:
+        break;
+    }
+  }
+}
+
 // One workgroup of W waves owns RT tiles of 16 output rows, one group of 16 tokens and a
 // 1/S share of k: wave wv of split s takes k chunks s W + wv, + S W, ... The waves' sums meet
 // in LDS in wave order; with S > 1 each split's sums go to the workspace with coherent stores
@@ -235,52 +288,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
 
   // Epilogue (kernels.metal:183-209): lane (t, q) holds rows 4 q + 0..3 of each tile.
   if ((uint32_t)t >= n_loc) return;
-  const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
-  if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && xg == 0 && q == 0) p.aux[tt] = inv;
-  const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++) {
-    const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
-    f32x4 v = acc[rt];
-    const size_t o = (size_t)tt * p.m + row0;
-    switch (p.epi) {
-      case SV_EPI_NORM:
-        *(f32x4*)(p.y + o) = v * (inv * p.scale);
-        break;
-      case SV_EPI_RAW:
-        if (norm_in) v *= inv;
-        *(f32x4*)(p.y + o) = v;
-        break;
-      case SV_EPI_RESID: {
-        if (norm_in) v *= inv;
-        const f32x4 sv = v * p.scale;
-        const f32x4 b = *(const f32x4*)(p.base + o);
-        *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
-        if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
-        break;
-      }
-      case SV_EPI_HEAD: {
-        if (norm_in) v *= inv;
-        f32x4 l;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-          l[i] = row0 + i < p.vocab_real ? 23.0f * sigmoidf_((v[i] + 5.0f) / 7.5f) : -__builtin_inff();
-        *(f32x4*)(p.y + o) = l;
-        break;
-      }
-      case SV_EPI_SWIGLU: {
-        const float sc = inv * p.scale;
-        const float g0 = v[0] * sc, u0 = v[1] * sc, g1 = v[2] * sc, u1 = v[3] * sc;
-        float2 out;
-        out.x = g0 * sigmoidf_(g0) * u0;
-        out.y = g1 * sigmoidf_(g1) * u1;
-        *(float2*)(p.y + (size_t)tt * (p.m / 2) + row0 / 2) = out;
-        break;
-      }
-      default:
-        break;
-    }
-  }
+  skinny_epilogue<RT>(p, acc, ss, xg, q, tt);
 }
 
 // ------------------------------------------------------------------- large n
@@ -604,12 +612,16 @@ static SkinnyCfg pick_skinny(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k) {
   return c;
 }
 
-// Workspace layout (skinny, S > 1), per cell (row group, token group): counters [m / 16][TG]
-// u32, then sums of squares [cells][S][16] and partials [cells][S][RT][64][4] fp32.
+// Workspace layout (skinny, S > 1): counters in a region of fixed size at the front (every
+// matmul sharing one workspace finds its counters at zero there, whatever its shape), then per
+// cell (row group, token group) the sums of squares [cells][S][16] and partials
+// [cells][S][RT][64][4] fp32.
+constexpr size_t COUNTER_SLOTS = 16384;
+
 static size_t skinny_ws_layout(uint32_t n, uint32_t m, const SkinnyCfg& c, size_t* ss_off, size_t* part_off) {
   if (c.s <= 1) return 0;
   const size_t tg = (n + 15) / 16, cells = (size_t)m / (16 * c.rt) * tg;
-  size_t off = ((size_t)(m / 16) * tg * 4 + 255) / 256 * 256;
+  size_t off = COUNTER_SLOTS * 4;
   *ss_off = off;
   off += (cells * c.s * 16 * 4 + 255) / 256 * 256;
   *part_off = off;
@@ -681,6 +693,8 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
     return fail(SV_ERR_ARG, "matmul: launch shape rt %d, waves %d, splits %d", rt, waves, cfg.s);
   size_t ss_off = 0, part_off = 0;
   const size_t need = skinny_ws_layout(a->n, a->m, cfg, &ss_off, &part_off);
+  if (need && (size_t)a->m / (16 * rt) * ((a->n + 15) / 16) > COUNTER_SLOTS)
+    return fail(SV_ERR_UNSUPPORTED, "matmul: %u row groups x token groups exceed the hand-off counters", a->m / (16 * rt));
   if (need > 0 && (!ws || ws_bytes < need))
     return fail(SV_ERR_ARG, "matmul: workspace %zu < %zu bytes (sv_matmul_workspace_bytes)", ws_bytes, need);
   p.counters = need ? (uint32_t*)ws : nullptr;

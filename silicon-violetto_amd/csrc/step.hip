@@ -481,7 +481,7 @@ __device__ __forceinline__ void attn_phase(const StepParams& p, uint32_t l, uint
   if (a.wslot == 0 && wv == 0) {
     KvBatch<D> nb0;
     load_batch<D, true>(ap, a.seq, a.hg, a.p0, a.p0 + a.T, a.p0, nk, nv, nb0, lane);
-    compute_batch<D, NCT, true>(ap, nb0, a.p0, a.p0 + a.T, a.p0, ncols, a.t0, qh, ql, O, lsum, lane, rc);
+    compute_batch<D, NCT, true>(ap, nb0, a.p0, a.p0 + a.T, a.p0, ncols, a.t0, qh, ql, O, lsum, lane, rc->vis);
   }
   SUBSTAMP(3);
   ahead();
@@ -810,6 +810,7 @@ sv_status step_launch(hipStream_t stream, const StepLaunch& a) {
   ap.max_pages = a.max_pages;
   ap.layer = 0;
   ap.maxcols = maxcols;
+  ap.n_inline = 0;
   p.n_runs = a.n_runs;
   p.pairs = a.n_runs * NKV;
   p.wpp = G / p.pairs;

@@ -111,6 +111,34 @@ def test_matmul_repeat_workspace(gpu):
         assert torch.equal(y, outs[0])
 
 
+def test_matmul_shared_workspace_across_shapes(gpu):
+    """Matmuls of different shapes, each with k splits, take turns on one workspace (as in an
+    engine step): each finds its hand-off counters at zero and its results match the oracle."""
+    banner("matmul shared workspace")
+    rng = np.random.default_rng(21)
+    n = 5
+    qd, sd = quantize_rows(torch.from_numpy(rng.normal(0, 0.02, (2048, 8192)).astype(np.float32)))
+    down = K.matrix(qd.cuda(), sd.cuda(), 31)
+    wh = bf16_bits(rng.normal(0, 0.02, (32000, 2048)).astype(np.float32))
+    head = K.matrix(u16_dev_bf16(wh))
+    ws = K.Workspace(max(L.lib().sv_matmul_workspace_bytes(n, 2048, 8192), L.lib().sv_matmul_workspace_bytes(n, 32000, 2048)))
+    xd = rng.normal(0, 1, (n, 8192)).astype(np.float32)
+    xh = rng.normal(0, 1, (8, 2048)).astype(np.float32)
+    rows = np.array([3, 0, 7, 1, 5], np.uint32)
+    ad = L.MatArgs(n, 8192, 2048, L.EPI_RAW, 0, 2048, 1.0, 0, 0, 1, 8192, 31)
+    ah = L.MatArgs(n, 2048, 32000, L.EPI_HEAD, L.FLAG_NORM_IN, 32000, 1.0, 0, 0, 1, 2048, 0)
+    ref_d = oracle.matmul(L, qd.numpy(), sd.view(torch.int16).numpy().view(np.uint16), 31, xd, ad)
+    ref_h = oracle.matmul(L, wh, None, 0, xh, ah, x_rows=rows)
+    for rep in range(2):
+        yd = torch.zeros(n, 2048, device="cuda")
+        yh = torch.zeros(n, 32000, device="cuda")
+        K.matmul(down, to_dev(xd), yd, n=n, epi=L.EPI_RAW, ws=ws)
+        K.matmul(head, to_dev(xh), yh, n=n, epi=L.EPI_HEAD, flags=L.FLAG_NORM_IN, x_rows=to_dev(rows), ws=ws)
+        torch.cuda.synchronize()
+        close(yd.cpu().numpy(), ref_d, atol=5e-5 * max(1.0, float(np.abs(ref_d).max())), rtol=1e-4, what=f"down {rep}")
+        close(yh.cpu().numpy(), ref_h, atol=1e-4, rtol=1e-5, what=f"head {rep}")
+
+
 @pytest.mark.parametrize("rt,waves,splits", [(1, 8, 2), (1, 4, 8), (2, 8, 4), (4, 4, 2), (2, 16, 1), (1, 16, 2)])
 def test_matmul_skinny_launch_shapes(gpu, rt, waves, splits):
     """Every skinny launch shape (row tiles, waves, k splits) gives the oracle's result,
