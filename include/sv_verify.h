@@ -64,7 +64,14 @@ enum {
    * rmsnorm_rows (kernels.metal:117-131) folded into the matmul that follows it. */
   SV_FLAG_NORM_IN = 4
 };
-enum { SV_FMT_BF16 = 0, SV_FMT_I8 = 1 };
+enum {
+  SV_FMT_BF16 = 0,
+  SV_FMT_I8 = 1,
+  /* Layout flag, or-ed into a format: weights in 16-row tiles, each tile's 64-k blocks stored
+   * as one contiguous 1 KB (int8) or 2 KB (bf16) in the matrix-core lane order (written by
+   * sv_pack_matrix). Not in the reference: its weights stay row-major (model.rs:22-47). */
+  SV_FMT_TILED = 0x10
+};
 
 typedef enum sv_status {
   SV_OK = 0,
@@ -195,6 +202,12 @@ size_t sv_matmul_workspace_bytes(uint32_t n, uint32_t m, uint32_t k);
 sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_x, const uint32_t* d_x_rows, float* d_y,
                     const float* d_base, float* d_aux, const sv_mat_args* a, void* d_workspace,
                     size_t workspace_bytes);
+
+/* Repacks a row-major matrix into the tiled layout (SV_FMT_TILED) for sv_matmul: d_dst gets
+ * m * k bytes (int8) or 2 m k (bf16), *out the same matrix with format | SV_FMT_TILED and
+ * src's scales. Needs m % 16 == 0 and k % 64 == 0. No counterpart in the reference (its
+ * weights are used as loaded, model.rs:22-47); done once at model load. */
+sv_status sv_pack_matrix(void* stream, const sv_matrix* src, void* d_dst, sv_matrix* out);
 
 /* Fused verify attention (kernels.metal:1008-1148 attn_verify + 1316-1362 attn_dec_reduce;
  * encode.rs:233-297): for each run (d_runs: uint2 (first token, count <= SV_MAX_RUN)),

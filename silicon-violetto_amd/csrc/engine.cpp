@@ -74,6 +74,10 @@ extern "C" sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_
   return matmul_launch((hipStream_t)stream, w, d_x, d_x_rows, d_y, d_base, d_aux, a, d_workspace, workspace_bytes);
 }
 
+extern "C" sv_status sv_pack_matrix(void* stream, const sv_matrix* src, void* d_dst, sv_matrix* out) {
+  return pack_matrix((hipStream_t)stream, src, d_dst, out);
+}
+
 extern "C" size_t sv_attn_workspace_bytes(const sv_shape* shape, uint32_t n_runs, uint32_t max_splits,
                                           uint32_t max_run) {
   if (!shape) return 0;
@@ -176,8 +180,11 @@ struct sv_engine {
   sv_shape sh{};
   hipStream_t stream = nullptr;
   const uint16_t* embed = nullptr;
-  std::vector<sv_layer> layers;
+  sv_matrix head_mat{};  // the tied head (tiled when the shape allows)
+  std::vector<sv_layer> layers;  // as used: matrices repacked into the tiled layout where they fit it
   std::vector<bool> layer_set;
+  std::vector<void*> packed;     // engine-owned tiled copies [layer * 4 + matrix]
+  void* head_tiled = nullptr;    // tiled copy of the tied embedding for the head matmul
   uint32_t n_pages = 0, max_pages = 0, qkv_w = 0;
 
   // device: KV and sequence state
@@ -267,6 +274,9 @@ struct sv_engine {
                     attn, mixed, act, inv, logits, ws, mm_ws, step_ws, step_layers, step_stamps, step_acts};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
+    for (void* b : packed)
+      if (b) (void)hipFree(b);
+    if (head_tiled) (void)hipFree(head_tiled);
     if (stream) (void)hipStreamDestroy(stream);
   }
 
@@ -448,8 +458,7 @@ struct sv_engine {
     (void)NQD;
     if (P.n_head > 0) {
       // rmsnorm_rows + the tied head (encode.rs:390-393), the norm folded into the matmul.
-      const sv_matrix head{embed, nullptr, sh.vocab, sh.hidden, SV_FMT_BF16, 0};
-      SV_TIMED(SV_KIND_HEAD, matmul(head, P.n_head, h, head_rows, logits, SV_EPI_HEAD, SV_FLAG_NORM_IN, 1.0f, 0, 0,
+      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, h, head_rows, logits, SV_EPI_HEAD, SV_FLAG_NORM_IN, 1.0f, 0, 0,
                                     nullptr, nullptr));
       SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
     }
@@ -483,11 +492,13 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   if (cfg->page_shift < 4 || cfg->page_shift > 16) return fail(SV_ERR_ARG, "engine_create: page_shift %u", cfg->page_shift);
   if (cfg->split_keys % 32) return fail(SV_ERR_ARG, "engine_create: split_keys %u", cfg->split_keys);
   attn_init();
+  matmul_init();
   sv_engine* e = new sv_engine();
   e->cfg = *cfg;
   e->sh = s;
   e->layers.resize(s.n_layers);
   e->layer_set.assign(s.n_layers, false);
+  e->packed.assign((size_t)s.n_layers * 4, nullptr);
   const uint32_t page = 1u << cfg->page_shift;
   e->n_pages = (cfg->kv_tokens + page - 1) / page;
   e->max_pages = (cfg->max_seq_len + page - 1) / page;
@@ -603,17 +614,40 @@ extern "C" void sv_engine_destroy(sv_engine* e) {
 
 extern "C" void* sv_engine_stream(sv_engine* e) { return e ? (void*)e->stream : nullptr; }
 
+// A tiled copy of a row-major matrix in *slot (replacing what it held), as *out; a matrix that
+// does not fit the tiled layout, or is tiled already, is used as given. The weight reads of a
+// 1-16 row matmul are then contiguous kilobytes (measured on MI355X: head 31 -> 23 us, down
+// 11.3 -> 9.1 us at 5 rows). Done once, at model load.
+static sv_status pack_into(sv_engine* e, const sv_matrix& in, void** slot, sv_matrix* out) {
+  *out = in;
+  if ((in.format & SV_FMT_TILED) || in.m % 16 || in.k % 64) return SV_OK;
+  const size_t bytes = (size_t)in.m * in.k * (in.format == SV_FMT_I8 ? 1 : 2);
+  if (*slot) {
+    SV_HIP(hipStreamSynchronize(e->stream), "pack: sync");
+    SV_HIP(hipFree(*slot), "pack: free");
+    *slot = nullptr;
+  }
+  SV_HIP(hipMalloc(slot, bytes), "pack: alloc");
+  SV_TRY(pack_matrix(e->stream, &in, *slot, out));
+  SV_HIP(hipStreamSynchronize(e->stream), "pack: sync");
+  return SV_OK;
+}
+
 extern "C" sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed) {
   if (!e || !d_embed) return fail(SV_ERR_ARG, "set_embed: null pointer");
   e->embed = d_embed;
+  const sv_matrix head{d_embed, nullptr, e->sh.vocab, e->sh.hidden, SV_FMT_BF16, 0};
+  SV_TRY(pack_into(e, head, &e->head_tiled, &e->head_mat));
   return SV_OK;
 }
 
 static sv_status check_matrix(const sv_matrix& m, uint32_t rows, uint32_t cols, const char* name) {
   if (!m.d_w) return fail(SV_ERR_ARG, "%s: no weights", name);
   if (m.m != rows || m.k != cols) return fail(SV_ERR_ARG, "%s: [%u][%u], expected [%u][%u]", name, m.m, m.k, rows, cols);
-  if (m.format == SV_FMT_I8 && !m.d_scales) return fail(SV_ERR_ARG, "%s: int8 without scales", name);
-  if (m.format != SV_FMT_I8 && m.format != SV_FMT_BF16) return fail(SV_ERR_ARG, "%s: format %u", name, m.format);
+  const uint32_t fmt = m.format & ~(uint32_t)SV_FMT_TILED;
+  if (fmt == SV_FMT_I8 && !m.d_scales) return fail(SV_ERR_ARG, "%s: int8 without scales", name);
+  if (fmt != SV_FMT_I8 && fmt != SV_FMT_BF16) return fail(SV_ERR_ARG, "%s: format %u", name, m.format);
+  if ((m.format & SV_FMT_TILED) && (m.m % 16 || m.k % 64)) return fail(SV_ERR_ARG, "%s: tiled needs m %% 16, k %% 64", name);
   return SV_OK;
 }
 
@@ -625,7 +659,13 @@ extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_
   SV_TRY(check_matrix(l->o, s.hidden, s.n_heads * s.head_dim, "o"));
   SV_TRY(check_matrix(l->gate_up, 2 * s.ffn, s.hidden, "gate_up"));
   SV_TRY(check_matrix(l->down, s.hidden, s.ffn, "down"));
-  e->layers[layer] = *l;
+  sv_layer used = *l;
+  void** slots = &e->packed[(size_t)layer * 4];
+  SV_TRY(pack_into(e, l->qkv, &slots[0], &used.qkv));
+  SV_TRY(pack_into(e, l->o, &slots[1], &used.o));
+  SV_TRY(pack_into(e, l->gate_up, &slots[2], &used.gate_up));
+  SV_TRY(pack_into(e, l->down, &slots[3], &used.down));
+  e->layers[layer] = used;
   e->layer_set[layer] = true;
   e->step_layers_dirty = true;
   return SV_OK;

@@ -35,7 +35,7 @@ struct MMParams {
   float* y;
   const float* base;
   float* aux;
-  uint32_t n, k, m, epi, flags, vocab_real, gshift, chunks, per_row;
+  uint32_t n, k, m, epi, flags, vocab_real, gshift, chunks, per_row, tiled;
   float scale, ra, rb;
   // Split-k hand-off (skinny path with S > 1): counters per row group (zero at rest),
   // partial sums and sums of squares per (row group, split).
@@ -54,7 +54,7 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __ex
 // of each of the workgroup's RT tiles for token tt; ss: the token's sum of squares over k.
 template <int RT>
 __device__ __forceinline__ void skinny_epilogue(const MMParams& p, const f32x4 (&acc)[RT], float ss, uint32_t xg, int q,
-                                                uint32_t tt) {
+                                                uint32_t tt, const f32x4* base_pre = nullptr) {
   const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
   if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && xg == 0 && q == 0) p.aux[tt] = inv;
   const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
@@ -74,7 +74,7 @@ __device__ __forceinline__ void skinny_epilogue(const MMParams& p, const f32x4 (
       case SV_EPI_RESID: {
         if (norm_in) v *= inv;
         const f32x4 sv = v * p.scale;
-        const f32x4 b = *(const f32x4*)(p.base + o);
+        const f32x4 b = base_pre ? base_pre[rt] : *(const f32x4*)(p.base + o);
         *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
         if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
         break;
@@ -133,10 +133,6 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
   const bool tok = (uint32_t)t < n_loc;
   const uint32_t tt = tok0 + t;
   const float* xrow = p.x + (size_t)(tok ? (p.x_rows ? p.x_rows[tt] : tt) : 0u) * p.k + 16 * q;
-  const uint8_t* wbase[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; rt++)
-    wbase[rt] = p.w + ((size_t)((xg * RT + rt) * 16 + t) * p.k) * ESZ + (64 * 0 + 16 * q) * WV;
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
   const uint32_t stride = W * S;
 
@@ -150,7 +146,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
 #pragma unroll
         for (int v = 0; v < WV; v++)
           wr[rt][b * WV + v] =
-              __builtin_nontemporal_load((const u32x4*)(wbase[rt] + ((size_t)c * KC + 64 * b) * ESZ + 16 * v));
+              ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, xg * RT + rt, c * NBLK + b, v, lane));
   }
   for (; c < p.chunks; c += stride) {
     const uint32_t kbase = c * KC;
@@ -193,7 +189,7 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
 #pragma unroll
           for (int v = 0; v < WV; v++)
             wr[rt][b * WV + v] =
-                __builtin_nontemporal_load((const u32x4*)(wbase[rt] + ((size_t)cn * KC + 64 * b) * ESZ + 16 * v));
+                ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, xg * RT + rt, cn * NBLK + b, v, lane));
     }
     f32x4 part[RT];
 #pragma unroll
@@ -291,6 +287,237 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
   skinny_epilogue<RT>(p, acc, ss, xg, q, tt);
 }
 
+// ------------------------------------------------------------ 1-16 rows, one shot
+// The verify step's matmuls at 1-16 rows: every wave requests everything it will read when
+// it starts (its X, the epilogue's scales and base, then all of its weights), so a launch
+// costs one memory round trip instead of one per dependency.
+//   - A workgroup of W waves owns RT row tiles over the whole of k; wave wv takes the nch
+//     consecutive 256-k chunks from wv nch (nch <= NCH), its weights held in registers.
+//   - X is read densely (lane l: k 4 l .. 4 l + 3 of each token, a contiguous 1 KB per token
+//     and chunk), one chunk ahead; the wave splits it into bf16 hi + lo and writes it to its
+//     own LDS rows, from which each lane reads its MFMA B operands (tokens >= n are zeros).
+//     LDS operations of one wave execute in order, so no barrier is needed between the writes
+//     and the reads.
+//   - Per-row int8 scales multiply the sums once at the end; grouped scales (>= 256) per chunk.
+//   - The waves' sums meet in LDS in wave order; wave 0 runs the epilogue. No partial sum
+//     leaves the workgroup: deterministic, no hand-off.
+constexpr int XROW = KC + 8;  // bf16 per LDS row of one token's hi or lo (16 bytes of padding)
+
+template <int FMT, int RT, int W, int NCH, int NT>
+__global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
+  constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2;
+  constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xs_all[];  // [W][n][hi, lo][XROW]
+  __shared__ f32x4 red[W][RT][64];
+  __shared__ float ssred[W][NT];
+  const int lane = threadIdx.x & 63, t = lane & 15, q = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t n = p.n, nwg = gridDim.x;
+  uint32_t xg = blockIdx.x;
+  if (nwg % 8 == 0) xg = (xg % 8) * (nwg / 8) + xg / 8;
+  uint16_t* xs = xs_all + (size_t)wv * n * 2 * XROW;
+  const uint32_t c0 = wv * NCH;
+  const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
+  const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
+  // Loads go through buffer resources: per-lane offsets xv / wv_off, uniform offsets per load.
+  const __amdgpu_buffer_rsrc_t xrs = coherent_rsrc(p.x), wrs = coherent_rsrc(p.w);
+  const uint32_t xv = 16 * lane;
+  const uint32_t wvo = p.tiled ? 16u * lane : ((uint32_t)t * p.k + 16 * q) * ESZ;
+  const uint32_t tile_bytes = 16 * p.k * ESZ, kb_bytes = p.tiled ? 1024 * ESZ : 64 * ESZ, v_bytes = p.tiled ? 1024 : 16;
+
+  // Loads are unconditional (rows past n and chunks past k re-read valid memory and are
+  // ignored): loads under branches would be waited for one by one.
+  const uint32_t nx = min(n, (uint32_t)NT);
+  uint32_t xrow[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) {
+    const uint32_t ii = (uint32_t)i < nx ? (uint32_t)i : 0u;
+    xrow[i] = p.x_rows ? p.x_rows[ii] : ii;
+  }
+  auto load_x = [&](f32x4 (&dst)[NT], uint32_t c) {
+    c = min(c, p.chunks - 1);
+#pragma unroll
+    for (int i = 0; i < NT; i++) dst[i] = __builtin_bit_cast(f32x4, buf_ld16(xrs, xv, (xrow[i] * p.k + c * KC) * 4));
+  };
+  auto load_gscale = [&](float (&dst)[RT][4], uint32_t c) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        dst[rt][i] = bf(ldg_u16(p.scales + ((size_t)(xg * RT + rt) * 16 + 4 * q + i) * ng + ((c * KC) >> p.gshift)));
+  };
+
+  // 1. the first chunk's X, the epilogue's operands, the first group scales, all weights.
+  f32x4 xr[NT], xn[NT];
+  load_x(xr, c0);
+  f32x4 base_pre[RT];
+  uint2 rsc[RT];
+  if (wv == 0) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+      const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
+      if (FMT == SV_FMT_I8 && p.per_row) rsc[rt] = *(const uint2*)(p.scales + row0);
+      if (p.epi == SV_EPI_RESID && (uint32_t)t < n) base_pre[rt] = *(const f32x4*)(p.base + (size_t)t * p.m + row0);
+    }
+  }
+  float gsc[RT][4];
+  if (grouped && c0 < p.chunks) load_gscale(gsc, c0);
+  u32x4 wr[NCH][RT][NBLK * WV];
+#pragma unroll
+  for (int j = 0; j < NCH; j++) {
+    const uint32_t cj = min(c0 + j, p.chunks - 1);
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+      for (int b = 0; b < NBLK; b++)
+#pragma unroll
+        for (int v = 0; v < WV; v++)
+          wr[j][rt][b * WV + v] =
+              buf_ld16_nt(wrs, wvo, (xg * RT + rt) * tile_bytes + (cj * NBLK + b) * kb_bytes + v * v_bytes);
+  }
+
+  // 2. chunks in order.
+  f32x4 acc[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float ssl[NT];
+#pragma unroll
+  for (int i = 0; i < NT; i++) ssl[i] = 0.0f;
+  const bf16x8 zero = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+  for (int j = 0; j < NCH; j++) {
+    const uint32_t c = c0 + j;
+    if (c >= p.chunks) break;
+    // keep each chunk's conversions and products inside its iteration (register pressure)
+    __builtin_amdgcn_sched_barrier(0);
+    float gnext[RT][4];
+    if (j + 1 < NCH) {
+      load_x(xn, c + 1);
+      if (grouped) load_gscale(gnext, min(c + 1, p.chunks - 1));
+    }
+    // this chunk's X: sums of squares, hi/lo to this wave's LDS rows
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      if ((uint32_t)i >= n) break;
+      const f32x4 v = xr[i];
+      ssl[i] = __builtin_fmaf(v[0], v[0], __builtin_fmaf(v[1], v[1], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[3], v[3], ssl[i]))));
+      float h[4], l[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) split_bf(v[e], h[e], l[e]);
+      const u32x2 hw = u32x2{(__float_as_uint(h[0]) >> 16) | (__float_as_uint(h[1]) & 0xffff0000u),
+                             (__float_as_uint(h[2]) >> 16) | (__float_as_uint(h[3]) & 0xffff0000u)};
+      const u32x2 lw = u32x2{pack_bf2(l[0], l[1]), pack_bf2(l[2], l[3])};
+      *(u32x2*)(xs + (2 * i) * XROW + 4 * lane) = hw;
+      *(u32x2*)(xs + (2 * i + 1) * XROW + 4 * lane) = lw;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f32x4 part[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) part[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NBLK; b++) {
+      bf16x8 xh0 = zero, xh1 = zero, xl0 = zero, xl1 = zero;
+      if ((uint32_t)t < n) {
+        const uint16_t* hp = xs + (2 * t) * XROW + 64 * b + 16 * q;
+        xh0 = *(const bf16x8*)hp;
+        xh1 = *(const bf16x8*)(hp + 8);
+        xl0 = *(const bf16x8*)(hp + XROW);
+        xl1 = *(const bf16x8*)(hp + XROW + 8);
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++) {
+        bf16x8 a0, a1;
+        if (FMT == SV_FMT_I8) {
+          const u32x4 w = wr[j][rt][b];
+          a0 = i8x8_to_bf(w[0], w[1]);
+          a1 = i8x8_to_bf(w[2], w[3]);
+        } else {
+          a0 = __builtin_bit_cast(bf16x8, wr[j][rt][2 * b]);
+          a1 = __builtin_bit_cast(bf16x8, wr[j][rt][2 * b + 1]);
+        }
+        part[rt] = mfma16(a0, xh0, part[rt]);
+        part[rt] = mfma16(a0, xl0, part[rt]);
+        part[rt] = mfma16(a1, xh1, part[rt]);
+        part[rt] = mfma16(a1, xl1, part[rt]);
+      }
+    }
+    // the next chunk's LDS writes stay behind these reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+      if (grouped) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) part[rt][i] *= gsc[rt][i];
+      }
+      acc[rt] += part[rt];
+    }
+    if (j + 1 < NCH) {
+#pragma unroll
+      for (int i = 0; i < NT; i++) xr[i] = xn[i];
+      if (grouped) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) gsc[rt][i] = gnext[rt][i];
+      }
+    }
+  }
+
+  // 3. waves' sums in wave order; sums of squares per token.
+  const bool need_ss = p.epi == SV_EPI_NORM || p.epi == SV_EPI_SWIGLU || (p.flags & SV_FLAG_NORM_IN);
+  if (need_ss) {
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      if ((uint32_t)i >= n) break;
+      const float v = wave_sum(ssl[i]);
+      if (lane == 0) ssred[wv][i] = v;
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
+  __syncthreads();
+  if (wv != 0) return;
+#pragma unroll
+  for (int rt = 0; rt < RT; rt++) {
+    f32x4 a = red[0][rt][lane];
+#pragma unroll
+    for (int w = 1; w < W; w++) a += red[w][rt][lane];
+    if (FMT == SV_FMT_I8 && p.per_row) {
+      a[0] *= bf(rsc[rt].x & 0xffffu);
+      a[1] *= bf(rsc[rt].x >> 16);
+      a[2] *= bf(rsc[rt].y & 0xffffu);
+      a[3] *= bf(rsc[rt].y >> 16);
+    }
+    acc[rt] = a;
+  }
+  if ((uint32_t)t >= n) return;
+  float ss = 0.0f;
+  if (need_ss) {
+    ss = ssred[0][t];
+#pragma unroll
+    for (int w = 1; w < W; w++) ss += ssred[w][t];
+  }
+  skinny_epilogue<RT>(p, acc, ss, xg, q, t, base_pre);
+}
+
+// Tiled copy of a row-major matrix (SV_FMT_TILED): one thread per 16-byte word of the
+// output, in output order (the read side gathers 16-byte pieces of rows).
+__global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* src, uint8_t* dst, uint32_t k, uint32_t esz,
+                                                         size_t words) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= words) return;
+  const uint32_t lane = i % 64;
+  const size_t wi = i / 64;  // (tile, block, v)
+  const uint32_t per_tile = k / 64 * esz;
+  const uint32_t tile = wi / per_tile, bv = wi % per_tile, kb = bv / esz, v = bv % esz;
+  const uint8_t* s = src + ((size_t)(tile * 16 + lane % 16) * k + 64 * kb + 16 * (lane / 16)) * esz + 16 * v;
+  *(u32x4*)(dst + i * 16) = *(const u32x4*)s;
+}
+
 // ------------------------------------------------------------------- large n
 // GEMM path (n > 16 rows: many streams, draft trees): a workgroup of 4 waves owns
 // BM = 64 RTW output rows and BN = 16 NT tokens; k goes in chunks of 64.
@@ -329,9 +556,6 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   const uint32_t row0 = rblk * 64 * RTW + wv * 16 * RTW;  // this wave's first row
 
   // Weights: lane (t16, q) takes row t16 of each tile, bytes 16 q .. of each 64-k chunk.
-  const uint8_t* wb[RTW];
-#pragma unroll
-  for (int r = 0; r < RTW; r++) wb[r] = p.w + ((size_t)(row0 + 16 * r + t16) * p.k + 16 * q) * ESZ;
 
   // X pairs of this thread: pair i -> token i / 8, k group i % 8 (k = 8 (i % 8) .. + 7).
   float ssacc[PPT];
@@ -393,7 +617,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
   for (int r = 0; r < RTW; r++)
 #pragma unroll
-    for (int v = 0; v < WL; v++) wr[r][v] = __builtin_nontemporal_load((const u32x4*)(wb[r] + 16 * v));
+    for (int v = 0; v < WL; v++) wr[r][v] = ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, row0 / 16 + r, 0, v, lane));
   store_x(0, xr);
   __syncthreads();
   const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
@@ -415,7 +639,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       for (int r = 0; r < RTW; r++)
 #pragma unroll
         for (int v = 0; v < WL; v++)
-          wr[r][v] = __builtin_nontemporal_load((const u32x4*)(wb[r] + (size_t)(c + 1) * GKC * ESZ + 16 * v));
+          wr[r][v] = ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, row0 / 16 + r, c + 1, v, lane));
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
@@ -577,6 +801,7 @@ struct SkinnyCfg {
   int rt, w, s;
 };
 SkinnyTune g_skinny_tune;  // all zero: the built-in choice
+int g_mm_variant = -1;
 
 // Beyond 16 rows the skinny kernel runs one workgroup per 16-token group (weights re-read
 // from L2 per group); measured on MI355X at 160 and 512 rows it beats the LDS-tiled GEMM on
@@ -586,7 +811,7 @@ constexpr uint32_t SKINNY_MAX_M_MANY_ROWS = 4096;
 
 static bool use_skinny(uint32_t n, uint32_t m, uint32_t k) {
   if (m % 16 || k % KC) return false;
-  if (g_skinny_tune.path) return g_skinny_tune.path == 1;
+  if (g_skinny_tune.path) return g_skinny_tune.path != 2;
   return n <= 16 || (n <= SKINNY_MAX_N && m <= SKINNY_MAX_M_MANY_ROWS);
 }
 
@@ -630,22 +855,111 @@ static size_t skinny_ws_layout(uint32_t n, uint32_t m, const SkinnyCfg& c, size_
 }
 
 size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
+  matmul_init();
   if (n == 0 || !use_skinny(n, m, k)) return 0;
   size_t a, b;
   return std::max(skinny_ws_layout(n, m, pick_skinny(SV_FMT_I8, n, m, k), &a, &b),
                   skinny_ws_layout(n, m, pick_skinny(SV_FMT_BF16, n, m, k), &a, &b));
 }
 
+// One-shot launch shapes for 1-16 rows (RT row tiles, W waves, NCH chunks per wave), int8
+// and bf16; NT = 8 (n <= 8) or 16 token slots. Measured on MI355X: about 256 workgroups or
+// more, the whole of k in one workgroup (no hand-off), a wave's weights <= 64 registers.
+struct StreamCfg {
+  int rt, w, nch;
+};
+constexpr StreamCfg STREAM_SHAPES[] = {{1, 8, 1}, {2, 8, 1}, {4, 8, 1}, {1, 8, 2}, {2, 8, 2}, {1, 8, 4}};
+
+static bool stream_shape_ok(uint32_t fmt, const StreamCfg& c, uint32_t n) {
+  const int wv = fmt == SV_FMT_I8 ? 1 : 2;
+  if (c.rt * c.nch * wv > 4) return false;  // weights <= 64 registers a wave
+  const size_t lds = (size_t)c.w * n * 2 * XROW * 2 + (size_t)c.w * c.rt * 1024 + (size_t)c.w * (n <= 8 ? 8 : 16) * 4;
+  return lds <= 160 * 1024;
+}
+
+static bool pick_stream(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k, StreamCfg* out) {
+  const uint32_t tiles = m / 16, chunks = k / KC;
+  if (g_skinny_tune.path == 3 && g_skinny_tune.rt) {
+    *out = StreamCfg{g_skinny_tune.rt, g_skinny_tune.w, g_skinny_tune.s};
+    return tiles % out->rt == 0 && (uint32_t)(out->w * out->nch) >= chunks && stream_shape_ok(fmt, *out, n);
+  }
+  for (int w : {8}) {
+    int nch = 1;
+    while ((uint32_t)(nch * w) < chunks) nch *= 2;
+    if (nch > 4) continue;
+    for (int rt : {4, 2, 1}) {
+      const StreamCfg c{rt, w, nch};
+      if (tiles % rt || (rt > 1 && tiles / rt < 256) || !stream_shape_ok(fmt, c, n)) continue;
+      bool listed = false;
+      for (const StreamCfg& sh : STREAM_SHAPES) listed |= sh.rt == rt && sh.w == w && sh.nch == nch;
+      if (!listed) continue;
+      *out = c;
+      return true;
+    }
+  }
+  return false;
+}
+
+// Dynamic LDS (X rows) beyond the default 64 KB needs a per-kernel attribute, which cannot be
+// set while a stream is being captured: matmul_init sets it for every instantiation.
+template <int FMT, int RT, int W, int NCH, int NT>
+static void stream_attr() {
+  const size_t static_lds = (size_t)W * RT * 1024 + (size_t)W * NT * 4;
+  const size_t dyn = std::min((size_t)W * NT * 2 * XROW * 2, (size_t)160 * 1024 - static_lds);
+  (void)hipFuncSetAttribute((const void*)mm_stream<FMT, RT, W, NCH, NT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)dyn);
+}
+
+template <int FMT, int RT, int W, int NCH, int NT>
+static void stream_launch_one(hipStream_t stream, const MMParams& p, uint32_t grid) {
+  launch((mm_stream<FMT, RT, W, NCH, NT>), dim3(grid), dim3(64 * W), (size_t)W * p.n * 2 * XROW * 2, stream, p);
+}
+
+// Calls F<FMT, RT, W, NCH, NT> for the launch shape c (false if it is not built).
+#define SV_STREAM_SHAPES(FMT, NT, CALL)                                        \
+  SV_ST(FMT, NT, 1, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 1, CALL) SV_ST(FMT, NT, 1, 8, 2, CALL) \
+  SV_ST(FMT, NT, 2, 8, 2, CALL) SV_ST(FMT, NT, 1, 8, 4, CALL)                   \
+  if (FMT == SV_FMT_I8) { SV_ST(FMT, NT, 4, 8, 1, CALL) }
+
+template <int FMT, int NT>
+static bool stream_dispatch(hipStream_t stream, const MMParams& p, const StreamCfg& c, uint32_t grid) {
+#define SV_ST(F, N_, R, W_, C_, CALL)                       \
+  if (c.rt == R && c.w == W_ && c.nch == C_) {              \
+    stream_launch_one<F, R, W_, C_, N_>(stream, p, grid);   \
+    return true;                                            \
+  }
+  SV_STREAM_SHAPES(FMT, NT, 0)
+#undef SV_ST
+  return false;
+}
+
+void matmul_init() {
+  static bool done = false;
+  if (done) return;
+  done = true;
+#define SV_ST(F, N_, R, W_, C_, CALL) stream_attr<F, R, W_, C_, N_>();
+  SV_STREAM_SHAPES(SV_FMT_I8, 8, 0)
+  SV_STREAM_SHAPES(SV_FMT_I8, 16, 0)
+  SV_STREAM_SHAPES(SV_FMT_BF16, 8, 0)
+  SV_STREAM_SHAPES(SV_FMT_BF16, 16, 0)
+#undef SV_ST
+  (void)hipGetLastError();  // an attribute the device refused is found by the launch check
+}
+
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes) {
+  matmul_init();
   if (!w || !a || !x || !y || !w->d_w) return fail(SV_ERR_ARG, "matmul: null pointer");
   if (a->k != w->k || a->m != w->m) return fail(SV_ERR_ARG, "matmul: args (m %u, k %u) != matrix (%u, %u)", a->m, a->k, w->m, w->k);
   if (a->n == 0) return SV_OK;
   bool per_row = true;
-  if (w->format == SV_FMT_I8) {
+  const uint32_t fmt = w->format & ~(uint32_t)SV_FMT_TILED;
+  const bool tiled = (w->format & SV_FMT_TILED) != 0;
+  if (tiled && (a->m % 16 || a->k % 64)) return fail(SV_ERR_ARG, "matmul: tiled layout needs m %% 16 == 0, k %% 64 == 0");
+  if (fmt == SV_FMT_I8) {
     if (!w->d_scales) return fail(SV_ERR_ARG, "matmul: int8 without scales");
     per_row = a->gshift >= 32 || (1ull << a->gshift) >= a->k;
-  } else if (w->format != SV_FMT_BF16) {
+  } else if (fmt != SV_FMT_BF16) {
     return fail(SV_ERR_ARG, "matmul: format %u", w->format);
   }
   // The skinny kernel takes int8 scales per row or per group of >= 256 (one per k chunk).
@@ -679,14 +993,32 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.vocab_real = a->vocab_real;
   p.gshift = per_row ? 31 : a->gshift;
   p.per_row = per_row;
+  p.tiled = tiled;
   p.scale = a->scale;
   p.ra = a->ra;
   p.rb = a->rb;
   p.chunks = a->k / KC;
   p.counters = nullptr;
   p.part = p.ssp = nullptr;
-  if (!skinny) return gemm_launch(stream, w->format, p);
-  const SkinnyCfg cfg = pick_skinny(w->format, a->n, a->m, a->k);
+  if (!skinny) {
+    g_mm_variant = 2;
+    return gemm_launch(stream, fmt, p);
+  }
+  StreamCfg sc;
+  const bool stream_ok = a->n <= 16 && g_skinny_tune.path != 1 && (per_row || a->gshift >= 8) &&
+                         pick_stream(fmt, a->n, a->m, a->k, &sc);
+  if (g_skinny_tune.path == 3 && !stream_ok) return fail(SV_ERR_ARG, "matmul: forced one-shot shape does not fit");
+  if (stream_ok) {
+    const uint32_t grid = a->m / 16 / sc.rt;
+    const bool ok = fmt == SV_FMT_I8 ? (a->n <= 8 ? stream_dispatch<SV_FMT_I8, 8>(stream, p, sc, grid)
+                                                  : stream_dispatch<SV_FMT_I8, 16>(stream, p, sc, grid))
+                                     : (a->n <= 8 ? stream_dispatch<SV_FMT_BF16, 8>(stream, p, sc, grid)
+                                                  : stream_dispatch<SV_FMT_BF16, 16>(stream, p, sc, grid));
+    if (!ok) return fail(SV_ERR_ARG, "matmul: launch shape rt %d, waves %d, chunks %d", sc.rt, sc.w, sc.nch);
+    g_mm_variant = 3;
+    return check_launch("matmul");
+  }
+  const SkinnyCfg cfg = pick_skinny(fmt, a->n, a->m, a->k);
   const int rt = cfg.rt, waves = cfg.w;
   if ((a->m / 16) % rt != 0 || (rt != 1 && rt != 2 && rt != 4) || (waves != 4 && waves != 8 && waves != 16) || (waves == 16 && rt == 4) ||
       cfg.s < 1)
@@ -700,6 +1032,7 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.counters = need ? (uint32_t*)ws : nullptr;
   p.ssp = need ? (float*)((char*)ws + ss_off) : nullptr;
   p.part = need ? (float*)((char*)ws + part_off) : nullptr;
+  g_mm_variant = 1;
   p.splits = cfg.s;
   p.tgroups = (a->n + 15) / 16;
   dim3 grid(a->m / 16 / rt * cfg.s * p.tgroups);
@@ -708,7 +1041,7 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   if (waves == 16 && R <= 2) SV_MM(F, R, 16);  \
   else if (waves == 8) SV_MM(F, R, 8);         \
   else SV_MM(F, R, 4)
-  if (w->format == SV_FMT_I8) {
+  if (fmt == SV_FMT_I8) {
     if (rt == 4) { SV_MM_W(SV_FMT_I8, 4); }
     else if (rt == 2) { SV_MM_W(SV_FMT_I8, 2); }
     else { SV_MM_W(SV_FMT_I8, 1); }
@@ -720,6 +1053,21 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
 #undef SV_MM_W
 #undef SV_MM
   return check_launch("matmul");
+}
+
+sv_status pack_matrix(hipStream_t stream, const sv_matrix* src, void* dst, sv_matrix* out) {
+  if (!src || !dst || !out || !src->d_w) return fail(SV_ERR_ARG, "pack_matrix: null pointer");
+  const uint32_t fmt = src->format;
+  if (fmt != SV_FMT_I8 && fmt != SV_FMT_BF16) return fail(SV_ERR_ARG, "pack_matrix: format %u (row-major int8 or bf16)", fmt);
+  if (src->m % 16 || src->k % 64 || src->m == 0) return fail(SV_ERR_ARG, "pack_matrix: m %u, k %u (need m %% 16 == 0, k %% 64 == 0)", src->m, src->k);
+  const uint32_t esz = fmt == SV_FMT_I8 ? 1 : 2;
+  const size_t words = (size_t)src->m * src->k * esz / 16;
+  launch(pack_tiled_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream, (const uint8_t*)src->d_w,
+         (uint8_t*)dst, src->k, esz, words);
+  *out = *src;
+  out->d_w = dst;
+  out->format = fmt | SV_FMT_TILED;
+  return check_launch("pack_matrix");
 }
 
 }  // namespace sv

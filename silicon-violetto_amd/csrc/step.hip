@@ -153,12 +153,11 @@ constexpr int QKV_RT = 1, QKV_S = 1, O_RT = 1, O_S = 1, GU_RT = 4, GU_S = 1, DN_
 template <int FMT>
 __device__ __forceinline__ void load_unit(const StepMat& M, uint32_t tile, uint32_t c, int lane, u32x4* dst) {
   constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2, ESZ = FMT == SV_FMT_I8 ? 1 : 2;
-  const int t = lane & 15, q = lane >> 4;
-  const uint8_t* base = (const uint8_t*)M.w + ((size_t)(tile * 16 + t) * M.k + (size_t)c * SKC) * ESZ + 16 * q * WV;
 #pragma unroll
   for (int b = 0; b < SNBLK; b++)
 #pragma unroll
-    for (int v = 0; v < WV; v++) dst[b * WV + v] = ldg_nt(base + 64 * b * ESZ + 16 * v);
+    for (int v = 0; v < WV; v++)
+      dst[b * WV + v] = ldg_nt(weight_word<ESZ>((const uint8_t*)M.w, M.k, M.tiled, tile, c * SNBLK + b, v, lane));
 }
 
 // Per-phase work shapes (compile time): the matrix's row tiles go in groups of RT to a
@@ -721,7 +720,7 @@ size_t step_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_run) {
 // int8 weights with scales per row or per group of >= 256, and the matrix in the phase's
 // work shape: row tiles in groups of rt, k = splits x 8 waves x 256, groups x splits <= grid.
 static bool mat_ok(const sv_matrix& m, uint32_t G, uint32_t rt, uint32_t splits) {
-  if (m.format != SV_FMT_I8 || !m.d_scales || m.m % (16 * rt) || m.k != splits * SW * SKC || m.m / 16 / rt * splits > G)
+  if ((m.format & ~(uint32_t)SV_FMT_TILED) != SV_FMT_I8 || !m.d_scales || m.m % (16 * rt) || m.k != splits * SW * SKC || m.m / 16 / rt * splits > G)
     return false;
   const bool per_row = m.gshift >= 32 || (1ull << m.gshift) >= m.k;
   return per_row || (m.gshift >= 8 && m.k % (1u << m.gshift) == 0);
@@ -756,8 +755,9 @@ void step_fill_layer(const sv_layer* l, StepLayerHost* out) {
     out->mat[i].scales = m.d_scales;
     out->mat[i].m = m.m;
     out->mat[i].k = m.k;
-    const bool per_row = m.format != SV_FMT_I8 || m.gshift >= 32 || (1ull << m.gshift) >= m.k;
+    const bool per_row = (m.format & ~(uint32_t)SV_FMT_TILED) != SV_FMT_I8 || m.gshift >= 32 || (1ull << m.gshift) >= m.k;
     out->mat[i].per_row = per_row;
+    out->mat[i].tiled = (m.format & SV_FMT_TILED) != 0;
     out->mat[i].gshift = per_row ? 31 : m.gshift;
   }
   out->qkv_scale = l->qkv_scale;

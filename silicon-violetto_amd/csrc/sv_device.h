@@ -80,6 +80,18 @@ typedef __attribute__((address_space(1))) const uint16_t g_u16;
 __device__ __forceinline__ u32x4 ldg_nt(const void* p) { return __builtin_nontemporal_load((g_u32x4*)p); }
 __device__ __forceinline__ uint16_t ldg_u16(const uint16_t* p) { return *(g_u16*)p; }
 
+// Address of lane `lane`'s 16-byte weight word v (bf16: two per block) of 64-k block kb of
+// row tile `tile` (16 rows): lane (t, q) = (lane % 16, lane / 16) takes row 16 tile + t, k
+// 64 kb + 16 q .. + 15 (the MFMA A operand). Row-major [m][k], or tiled (SV_FMT_TILED): each
+// tile's 64-k blocks stored as one contiguous 1 KB (int8) or 2 KB (bf16) in lane order, so
+// a wave's load instruction reads one contiguous kilobyte.
+template <int ESZ>
+__device__ __forceinline__ const uint8_t* weight_word(const uint8_t* w, uint32_t k, bool tiled, uint32_t tile,
+                                                      uint32_t kb, int v, int lane) {
+  if (tiled) return w + (size_t)tile * 16 * k * ESZ + ((size_t)kb * ESZ + v) * 1024 + lane * 16;
+  return w + ((size_t)(tile * 16 + (lane & 15)) * k + 64 * kb + 16 * (lane >> 4)) * ESZ + 16 * v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, WAVE);
@@ -145,6 +157,17 @@ __device__ __forceinline__ f32x4 load_wt4(__amdgpu_buffer_rsrc_t r, uint32_t byt
 }
 __device__ __forceinline__ void store_wt4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, SV_CPOL_SC1);
+}
+
+// Plain and nontemporal 16-byte loads through a buffer resource (coherent_rsrc's descriptor:
+// base + [0, 2 GB)): a per-lane offset in one register and a uniform offset in a scalar
+// register, so a wave with many loads from one base spends no registers on addresses.
+constexpr int SV_CPOL_NT = 2;
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ u32x4 buf_ld16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, SV_CPOL_NT);
 }
 
 // Wait until this thread's memory operations have completed (s_waitcnt vmcnt(0); the gfx9

@@ -43,11 +43,15 @@ size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k);
 struct SkinnyTune {
   int rt, w, s, path;
 };
-extern SkinnyTune g_skinny_tune;
+// The variant of the last matmul launched on this process (1 skinny, 2 GEMM, 3 one-shot): tests.
+extern int g_mm_variant;
+extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave)
+sv_status pack_matrix(hipStream_t stream, const sv_matrix* src, void* dst, sv_matrix* out);
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes);
 
 void attn_init();
+void matmul_init();  // kernel attributes; call outside stream capture
 uint32_t attn_resident_wgs(const sv_shape* sh, uint32_t max_run);
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
 sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
@@ -87,7 +91,7 @@ sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_
 struct StepMat {
   const void* w;
   const uint16_t* scales;
-  uint32_t m, k, per_row, gshift;
+  uint32_t m, k, per_row, gshift, tiled;
 };
 struct StepLayerHost {  // uploaded per layer; the kernel reads it as StepLayerDev
   StepMat mat[4];       // qkv, o, gate_up, down

@@ -29,6 +29,7 @@ ROPE_PAIRS = 32
 EPI_NORM, EPI_RESID, EPI_SWIGLU, EPI_HEAD, EPI_RAW = 1, 2, 3, 4, 5
 FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
+FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
 KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "layers")
 
@@ -115,6 +116,7 @@ PROTOS = {
     "sv_rmsnorm_rows": (C.c_int, [vp, vp, vp, vp, u32, u32]),
     "sv_matmul_workspace_bytes": (C.c_size_t, [u32, u32, u32]),
     "sv_matmul": (C.c_int, [vp, P(Matrix), vp, vp, vp, vp, vp, P(MatArgs), vp, C.c_size_t]),
+    "sv_pack_matrix": (C.c_int, [vp, P(Matrix), vp, P(Matrix)]),
     "sv_attn_workspace_bytes": (C.c_size_t, [P(Shape), u32, u32, u32]),
     "sv_attn_verify": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, P(KvArgs), P(AttnArgs), vp, u32, u32, vp, vp,
                                  vp, C.c_size_t]),

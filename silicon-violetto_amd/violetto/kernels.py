@@ -49,6 +49,14 @@ class Mat:
             assert w.dtype == torch.bfloat16
             self.c = L.Matrix(_p(w), None, m, k, L.FMT_BF16, 0)
 
+    def tiled(self, stream: int | None = None) -> "Mat":
+        """The same matrix in the tiled layout (SV_FMT_TILED), packed on the device."""
+        out = Mat.__new__(Mat)
+        out.w, out.scales = torch.empty_like(self.w), self.scales
+        out.c = L.Matrix()
+        L.check(L.lib().sv_pack_matrix(_stream(stream), C.byref(self.c), _p(out.w), C.byref(out.c)))
+        return out
+
     @property
     def m(self) -> int:
         return self.c.m

@@ -37,8 +37,9 @@ MM_CASES = [
 @pytest.mark.parametrize("m,k,fmt", MM_CASES)
 @pytest.mark.parametrize("n", [1, 5, 16])
 @pytest.mark.parametrize("epi", [L.EPI_NORM, L.EPI_RESID, L.EPI_SWIGLU, L.EPI_HEAD, L.EPI_RAW])
-def test_matmul(gpu, m, k, fmt, n, epi):
-    banner(f"matmul m={m} k={k} {fmt} n={n} epi={epi}")
+@pytest.mark.parametrize("tiled", [False, True])
+def test_matmul(gpu, m, k, fmt, n, epi, tiled):
+    banner(f"matmul m={m} k={k} {fmt} n={n} epi={epi} tiled={tiled}")
     rng = np.random.default_rng(1000 * n + epi)
     w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
     if fmt == "i8":
@@ -50,6 +51,8 @@ def test_matmul(gpu, m, k, fmt, n, epi):
         wb = bf16_bits(w.numpy())
         mat = K.matrix(u16_dev_bf16(wb))
         host_w, host_s, gs = wb, None, 0
+    if tiled:
+        mat = mat.tiled()
     x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
     base = rng.normal(0, 1, (n, m)).astype(np.float32)
     flags = L.FLAG_WRITE_INV if epi == L.EPI_NORM else (L.FLAG_NORM_IN if epi in (L.EPI_HEAD, L.EPI_RAW) else 0)
@@ -67,6 +70,7 @@ def test_matmul(gpu, m, k, fmt, n, epi):
     K.matmul(mat, to_dev(x), y, n=n, epi=epi, flags=flags, scale=scale, ra=ra, rb=rb,
              base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux, vocab_real=vocab_real)
     torch.cuda.synchronize()
+    assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 3, "1-16 rows run the one-shot kernel"
     got = y.cpu().numpy()
     # Tolerance: |error| <= 2e-5 x the norm of the terms summed (hi/lo split: 2^-17 per term).
     mag = float(np.abs(ref[np.isfinite(ref)]).max())
@@ -152,7 +156,7 @@ def test_matmul_skinny_launch_shapes(gpu, rt, waves, splits):
     mat = K.matrix(q.cuda(), s.cuda(), 31)
     ws = K.Workspace(32 << 20)
     try:
-        tune[0], tune[1], tune[2] = rt, waves, splits
+        tune[0], tune[1], tune[2], tune[3] = rt, waves, splits, 1
         for call in range(2):
             x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
             a = L.MatArgs(n, k, m, L.EPI_NORM, L.FLAG_WRITE_INV, m, 0.75, 0, 0, 1, k, 31)
@@ -162,11 +166,59 @@ def test_matmul_skinny_launch_shapes(gpu, rt, waves, splits):
             aux = torch.zeros(n, device="cuda")
             K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_NORM, flags=L.FLAG_WRITE_INV, scale=0.75, aux=aux, ws=ws)
             torch.cuda.synchronize()
+            assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 1, "skinny kernel not launched"
             close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
                   what=f"call {call}")
             close(aux.cpu().numpy(), aux_ref, atol=1e-5, rtol=1e-4, what="inv")
     finally:
-        tune[0] = tune[1] = tune[2] = 0
+        tune[0] = tune[1] = tune[2] = tune[3] = 0
+
+
+@pytest.mark.parametrize("rt,waves,nch", [(1, 8, 1), (2, 8, 1), (4, 8, 1), (1, 8, 2), (2, 8, 2), (1, 8, 4)])
+@pytest.mark.parametrize("n", [3, 12])
+def test_matmul_one_shot_launch_shapes(gpu, rt, waves, nch, n):
+    """Every one-shot launch shape of the 1-16 row kernel (row tiles, waves, chunks per wave;
+    chunks past k and token slots past n are read and discarded) gives the oracle's result,
+    int8 with the sums of squares of EPI_NORM and bf16 with EPI_RESID's base, in both weight
+    layouts. The shape is forced through the library's internal override."""
+    banner(f"matmul one-shot rt={rt} waves={waves} nch={nch} n={n}")
+    tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv13g_skinny_tuneE")
+    rng = np.random.default_rng(rt * 100 + waves * 10 + nch + n)
+    m = 256 * rt
+    k = 256 * waves * nch - 256 * (nch > 1)  # the last wave's last chunk is past k when nch > 1
+    try:
+        tune[0], tune[1], tune[2], tune[3] = rt, waves, nch, 3
+        for fmt in ("i8", "bf16"):
+            if fmt == "bf16" and rt * nch > 2:
+                continue
+            w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+            if fmt == "i8":
+                q, s = quantize_rows(w)
+                host_w, host_s, gs = q.numpy(), s.view(torch.int16).numpy().view(np.uint16), 31
+                mat = K.matrix(q.cuda(), s.cuda(), 31)
+                epi, flags = L.EPI_NORM, L.FLAG_WRITE_INV
+            else:
+                host_w, host_s, gs = bf16_bits(w.numpy()), None, 0
+                mat = K.matrix(u16_dev_bf16(host_w))
+                epi, flags = L.EPI_RESID, 0
+            x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
+            base = rng.normal(0, 1, (n, m)).astype(np.float32)
+            a = L.MatArgs(n, k, m, epi, flags, m, 0.75, 0.9, 1.3, 1, k, gs)
+            aux_ref = np.zeros(n, np.float32)
+            ref = oracle.matmul(L, host_w, host_s, gs, x, a, base=base if epi == L.EPI_RESID else None, aux=aux_ref)
+            for layout in (mat, mat.tiled()):
+                y = torch.zeros(n, m, device="cuda")
+                aux = torch.zeros(n, device="cuda")
+                K.matmul(layout, to_dev(x), y, n=n, epi=epi, flags=flags, scale=0.75, ra=0.9, rb=1.3,
+                         base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux)
+                torch.cuda.synchronize()
+                assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 3, "one-shot kernel not launched"
+                close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
+                      what=f"{fmt} tiled={layout is not mat}")
+                if epi == L.EPI_NORM:
+                    close(aux.cpu().numpy(), aux_ref, atol=1e-5, rtol=1e-4, what="inv")
+    finally:
+        tune[0] = tune[1] = tune[2] = tune[3] = 0
 
 
 # ---------------------------------------------------------------------------- attention
