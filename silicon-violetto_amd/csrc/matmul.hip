@@ -43,7 +43,30 @@ struct MMParams {
   float* part;
   float* ssp;
   uint32_t splits, tgroups;  // skinny: k splits and 16-token groups
+#ifdef SV_MM_STAMPS
+  uint64_t* stamps;  // probe builds: clock stamps of the one-shot kernel, [workgroup][8]
+  uint32_t dbg;      // probe builds: 1 skips the weight loads, 2 the X loads
+#endif
 };
+
+#ifdef SV_MM_STAMPS
+uint64_t* g_mm_stamps = nullptr;
+uint32_t g_mm_dbg = 0;
+#define SV_STAMP(slot)                          \
+  do {                                          \
+    __builtin_amdgcn_sched_barrier(0);          \
+    st[slot] = __builtin_amdgcn_s_memrealtime(); \
+    __builtin_amdgcn_sched_barrier(0);          \
+  } while (0)
+#define X_DBG && !(p.dbg & 2)
+#define W_DBG(v) ((p.dbg & 1) ? 0x80000000u + (v) : (v))
+#else
+#define X_DBG
+#define W_DBG(v) (v)
+#define SV_STAMP(slot) \
+  do {                 \
+  } while (0)
+#endif
 
 constexpr int KC = 256;  // k per chunk: one X chunk in registers, 4 blocks of 64
 constexpr int NBLK = KC / 64;
@@ -289,45 +312,76 @@ __global__ __launch_bounds__(64 * W) void mm_skinny(MMParams p) {
 
 // ------------------------------------------------------------ 1-16 rows, one shot
 // The verify step's matmuls at 1-16 rows: every wave requests everything it will read when
-// it starts (its X, the epilogue's scales and base, then all of its weights), so a launch
-// costs one memory round trip instead of one per dependency.
-//   - A workgroup of W waves owns RT row tiles over the whole of k; wave wv takes the nch
-//     consecutive 256-k chunks from wv nch (nch <= NCH), its weights held in registers.
+// it starts, so a launch costs about one memory round trip instead of one per dependency.
+//   - A workgroup of W waves owns RT row tiles over the whole of k; wave wv takes the NCH
+//     consecutive 256-k chunks from wv NCH, its weights held in registers.
 //   - X is read densely (lane l: k 4 l .. 4 l + 3 of each token, a contiguous 1 KB per token
-//     and chunk), one chunk ahead; the wave splits it into bf16 hi + lo and writes it to its
-//     own LDS rows, from which each lane reads its MFMA B operands (tokens >= n are zeros).
-//     LDS operations of one wave execute in order, so no barrier is needed between the writes
-//     and the reads.
+//     and chunk), XD chunks ahead (all of the wave's chunks when they fit in registers). Every
+//     wave requests its first X chunks before any wave requests weights (an execution barrier,
+//     no wait): a compute unit serves its waves' requests in order, and X is what every chunk
+//     waits for first. The wave splits each chunk into bf16 hi + lo in its own LDS rows, from
+//     which each lane reads its MFMA B operands (token slots >= n are zeros). LDS operations
+//     of one wave execute in order: no barrier between the writes and the reads.
 //   - Per-row int8 scales multiply the sums once at the end; grouped scales (>= 256) per chunk.
+//   - Sums of squares (the folded rms-norm) by DPP row sums and four lane reads per token.
 //   - The waves' sums meet in LDS in wave order; wave 0 runs the epilogue. No partial sum
 //     leaves the workgroup: deterministic, no hand-off.
 constexpr int XROW = KC + 8;  // bf16 per LDS row of one token's hi or lo (16 bytes of padding)
+
+template <int CTRL>
+__device__ __forceinline__ float mov_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// Sum over a full wave, in a fixed order: within rows of 16 lanes by DPP (quad xor 1, xor 2,
+// half-row mirror, row mirror), then the four row sums.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += mov_dpp<0xB1>(v);
+  v += mov_dpp<0x4E>(v);
+  v += mov_dpp<0x141>(v);
+  v += mov_dpp<0x140>(v);
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// X chunks a wave keeps in flight: all NCH if NCH NT <= 24 (<= 96 registers), else fewer.
+constexpr int x_depth(int nch, int nt) { return nch * nt <= 24 ? nch : (2 * nt <= 24 ? 2 : 1); }
 
 template <int FMT, int RT, int W, int NCH, int NT>
 __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2;
   constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
+  constexpr int XD = x_depth(NCH, NT);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_all[];  // [W][n][hi, lo][XROW]
   __shared__ f32x4 red[W][RT][64];
   __shared__ float ssred[W][NT];
   const int lane = threadIdx.x & 63, t = lane & 15, q = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t n = p.n, nwg = gridDim.x;
-  uint32_t xg = blockIdx.x;
-  if (nwg % 8 == 0) xg = (xg % 8) * (nwg / 8) + xg / 8;
+#ifdef SV_MM_STAMPS
+  uint64_t st[8] = {};
+#endif
+  SV_STAMP(0);
+  const uint32_t n = p.n, nwg = gridDim.x, S = p.splits;
+  uint32_t item = blockIdx.x;
+  if (nwg % 8 == 0) item = (item % 8) * (nwg / 8) + item / 8;
+  const uint32_t xg = item / S, sp = item % S;  // row group, k split (the splits of a group share an XCD)
   uint16_t* xs = xs_all + (size_t)wv * n * 2 * XROW;
-  const uint32_t c0 = wv * NCH;
+  const uint32_t c0 = (sp * W + wv) * NCH;
   const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
-  // Loads go through buffer resources: per-lane offsets xv / wv_off, uniform offsets per load.
+  // Loads go through buffer resources: one per-lane offset, a uniform offset per load.
   const __amdgpu_buffer_rsrc_t xrs = coherent_rsrc(p.x), wrs = coherent_rsrc(p.w);
   const uint32_t xv = 16 * lane;
   const uint32_t wvo = p.tiled ? 16u * lane : ((uint32_t)t * p.k + 16 * q) * ESZ;
   const uint32_t tile_bytes = 16 * p.k * ESZ, kb_bytes = p.tiled ? 1024 * ESZ : 64 * ESZ, v_bytes = p.tiled ? 1024 : 16;
 
-  // Loads are unconditional (rows past n and chunks past k re-read valid memory and are
-  // ignored): loads under branches would be waited for one by one.
+  // Loads are unconditional (loads under branches would be waited for one by one): chunks
+  // past k re-read the last chunk and are ignored; token slots past n take a lane offset past
+  // the buffer's range, which the hardware answers with zeros without a memory access.
   const uint32_t nx = min(n, (uint32_t)NT);
+  const uint32_t xv_none = 0x80000000u + xv;
   uint32_t xrow[NT];
 #pragma unroll
   for (int i = 0; i < NT; i++) {
@@ -337,9 +391,11 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   auto load_x = [&](f32x4 (&dst)[NT], uint32_t c) {
     c = min(c, p.chunks - 1);
 #pragma unroll
-    for (int i = 0; i < NT; i++) dst[i] = __builtin_bit_cast(f32x4, buf_ld16(xrs, xv, (xrow[i] * p.k + c * KC) * 4));
+    for (int i = 0; i < NT; i++)
+      dst[i] = __builtin_bit_cast(f32x4, buf_ld16(xrs, (uint32_t)i < nx X_DBG ? xv : xv_none, (xrow[i] * p.k + c * KC) * 4));
   };
   auto load_gscale = [&](float (&dst)[RT][4], uint32_t c) {
+    c = min(c, p.chunks - 1);
 #pragma unroll
     for (int rt = 0; rt < RT; rt++)
 #pragma unroll
@@ -347,9 +403,10 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
         dst[rt][i] = bf(ldg_u16(p.scales + ((size_t)(xg * RT + rt) * 16 + 4 * q + i) * ng + ((c * KC) >> p.gshift)));
   };
 
-  // 1. the first chunk's X, the epilogue's operands, the first group scales, all weights.
-  f32x4 xr[NT], xn[NT];
-  load_x(xr, c0);
+  // 1. X of the first XD chunks, the epilogue's operands; then (all waves) the weights.
+  f32x4 xr[XD][NT];
+#pragma unroll
+  for (int d = 0; d < XD; d++) load_x(xr[d], c0 + d);
   f32x4 base_pre[RT];
   uint2 rsc[RT];
   if (wv == 0) {
@@ -361,7 +418,8 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     }
   }
   float gsc[RT][4];
-  if (grouped && c0 < p.chunks) load_gscale(gsc, c0);
+  if (grouped) load_gscale(gsc, c0);
+  __builtin_amdgcn_s_barrier();
   u32x4 wr[NCH][RT][NBLK * WV];
 #pragma unroll
   for (int j = 0; j < NCH; j++) {
@@ -373,7 +431,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
         for (int v = 0; v < WV; v++)
           wr[j][rt][b * WV + v] =
-              buf_ld16_nt(wrs, wvo, (xg * RT + rt) * tile_bytes + (cj * NBLK + b) * kb_bytes + v * v_bytes);
+              buf_ld16_nt(wrs, W_DBG(wvo), (xg * RT + rt) * tile_bytes + (cj * NBLK + b) * kb_bytes + v * v_bytes);
   }
 
   // 2. chunks in order.
@@ -390,17 +448,17 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     if (c >= p.chunks) break;
     // keep each chunk's conversions and products inside its iteration (register pressure)
     __builtin_amdgcn_sched_barrier(0);
-    float gnext[RT][4];
-    if (j + 1 < NCH) {
-      load_x(xn, c + 1);
-      if (grouped) load_gscale(gnext, min(c + 1, p.chunks - 1));
+    f32x4 (&xc)[NT] = xr[j % XD];
+    // this chunk's X: sums of squares (token slots past n are zeros), hi/lo to the LDS rows
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+      const f32x4 v = xc[i];
+      ssl[i] = __builtin_fmaf(v[0], v[0], __builtin_fmaf(v[1], v[1], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[3], v[3], ssl[i]))));
     }
-    // this chunk's X: sums of squares, hi/lo to this wave's LDS rows
 #pragma unroll
     for (int i = 0; i < NT; i++) {
       if ((uint32_t)i >= n) break;
-      const f32x4 v = xr[i];
-      ssl[i] = __builtin_fmaf(v[0], v[0], __builtin_fmaf(v[1], v[1], __builtin_fmaf(v[2], v[2], __builtin_fmaf(v[3], v[3], ssl[i]))));
+      const f32x4 v = xc[i];
       float h[4], l[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) split_bf(v[e], h[e], l[e]);
@@ -410,9 +468,14 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
       *(u32x2*)(xs + (2 * i) * XROW + 4 * lane) = hw;
       *(u32x2*)(xs + (2 * i + 1) * XROW + 4 * lane) = lw;
     }
+    // the slot is free: the chunk XD ahead goes into it
+    float gnext[RT][4];
+    if (j + XD < NCH) load_x(xr[j % XD], c + XD);
+    if (grouped && j + 1 < NCH) load_gscale(gnext, c + 1);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (j == 0) SV_STAMP(1);
     f32x4 part[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) part[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -443,6 +506,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
         part[rt] = mfma16(a1, xl1, part[rt]);
       }
     }
+    if (j == 0) SV_STAMP(2);
     // the next chunk's LDS writes stay behind these reads
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -455,52 +519,91 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
       }
       acc[rt] += part[rt];
     }
-    if (j + 1 < NCH) {
+    if (grouped && j + 1 < NCH) {
 #pragma unroll
-      for (int i = 0; i < NT; i++) xr[i] = xn[i];
-      if (grouped) {
+      for (int rt = 0; rt < RT; rt++)
 #pragma unroll
-        for (int rt = 0; rt < RT; rt++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) gsc[rt][i] = gnext[rt][i];
-      }
+        for (int i = 0; i < 4; i++) gsc[rt][i] = gnext[rt][i];
     }
   }
 
+  SV_STAMP(3);
   // 3. waves' sums in wave order; sums of squares per token.
   const bool need_ss = p.epi == SV_EPI_NORM || p.epi == SV_EPI_SWIGLU || (p.flags & SV_FLAG_NORM_IN);
   if (need_ss) {
 #pragma unroll
     for (int i = 0; i < NT; i++) {
-      if ((uint32_t)i >= n) break;
-      const float v = wave_sum(ssl[i]);
+      const float v = wave_sum_dpp(ssl[i]);
       if (lane == 0) ssred[wv][i] = v;
     }
   }
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
   __syncthreads();
+  SV_STAMP(4);
+#ifdef SV_MM_STAMPS
+  if (p.stamps && lane == 0) {
+    st[5] = __builtin_amdgcn_s_memrealtime();
+    for (int i = 0; i < 6; i++) p.stamps[((size_t)blockIdx.x * 16 + wv) * 8 + i] = st[i];
+  }
+#endif
   if (wv != 0) return;
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) {
     f32x4 a = red[0][rt][lane];
 #pragma unroll
     for (int w = 1; w < W; w++) a += red[w][rt][lane];
-    if (FMT == SV_FMT_I8 && p.per_row) {
-      a[0] *= bf(rsc[rt].x & 0xffffu);
-      a[1] *= bf(rsc[rt].x >> 16);
-      a[2] *= bf(rsc[rt].y & 0xffffu);
-      a[3] *= bf(rsc[rt].y >> 16);
-    }
     acc[rt] = a;
   }
-  if ((uint32_t)t >= n) return;
   float ss = 0.0f;
-  if (need_ss) {
+  if (need_ss && (uint32_t)t < NT) {
     ss = ssred[0][t];
 #pragma unroll
     for (int w = 1; w < W; w++) ss += ssred[w][t];
   }
+  if (S > 1) {
+    // k splits: each split's sums to the workspace (coherent stores), the last split of the
+    // row group to arrive adds them in split order (wave 0 only: it alone wrote).
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part), srs = coherent_rsrc(p.ssp);
+    const uint32_t pbase = (xg * S) * RT * 1024, sbase = (xg * S) * 64;
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) store_wt4(prs, pbase + (sp * RT + rt) * 1024 + 16 * lane, acc[rt]);
+    if (lane < 16) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ss), srs, sbase + sp * 64 + 4 * lane, 0, SV_CPOL_SC1);
+    wait_mem();
+    uint32_t old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(p.counters + xg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != S - 1) return;
+    if (lane == 0) __hip_atomic_store(p.counters + xg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f32x4 tot[RT];
+    float sst = 0.0f;
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) tot[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s2 = 0; s2 < S; s2++) {
+      if (s2 == sp) {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) tot[rt] += acc[rt];
+        sst += ss;
+      } else {
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) tot[rt] += load_wt4(prs, pbase + (s2 * RT + rt) * 1024 + 16 * lane);
+        sst += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, sbase + s2 * 64 + 4 * t, 0, SV_CPOL_SC1));
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) acc[rt] = tot[rt];
+    ss = sst;
+  }
+  if (FMT == SV_FMT_I8 && p.per_row) {
+#pragma unroll
+    for (int rt = 0; rt < RT; rt++) {
+      acc[rt][0] *= bf(rsc[rt].x & 0xffffu);
+      acc[rt][1] *= bf(rsc[rt].x >> 16);
+      acc[rt][2] *= bf(rsc[rt].y & 0xffffu);
+      acc[rt][3] *= bf(rsc[rt].y >> 16);
+    }
+  }
+  if ((uint32_t)t >= n) return;
   skinny_epilogue<RT>(p, acc, ss, xg, q, t, base_pre);
 }
 
@@ -854,45 +957,48 @@ static size_t skinny_ws_layout(uint32_t n, uint32_t m, const SkinnyCfg& c, size_
   return off;
 }
 
-size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
-  matmul_init();
-  if (n == 0 || !use_skinny(n, m, k)) return 0;
-  size_t a, b;
-  return std::max(skinny_ws_layout(n, m, pick_skinny(SV_FMT_I8, n, m, k), &a, &b),
-                  skinny_ws_layout(n, m, pick_skinny(SV_FMT_BF16, n, m, k), &a, &b));
-}
-
-// One-shot launch shapes for 1-16 rows (RT row tiles, W waves, NCH chunks per wave), int8
-// and bf16; NT = 8 (n <= 8) or 16 token slots. Measured on MI355X: about 256 workgroups or
-// more, the whole of k in one workgroup (no hand-off), a wave's weights <= 64 registers.
+// One-shot launch shapes for 1-16 rows (RT row tiles, W waves, NCH chunks per wave, k split
+// in S = 1 or 2), int8 and bf16; NT = 4, 5, 8 or 16 token slots. Measured on MI355X: the
+// kernel is bound by its compute units' instruction work (weight conversion, X split, MFMA)
+// as much as by memory, so it wants every compute unit busy (>= 256 workgroups), and a
+// wave's weights <= 64 registers.
 struct StreamCfg {
-  int rt, w, nch;
+  int rt, w, nch, s;  // row tiles, waves, chunks per wave, k splits
 };
-constexpr StreamCfg STREAM_SHAPES[] = {{1, 8, 1}, {2, 8, 1}, {4, 8, 1}, {1, 8, 2}, {2, 8, 2}, {1, 8, 4}};
+constexpr StreamCfg STREAM_SHAPES[] = {{1, 8, 1}, {2, 8, 1}, {4, 8, 1}, {1, 8, 2}, {2, 8, 2},
+                                       {1, 8, 4}, {1, 4, 1}, {1, 4, 2}};
 
 static bool stream_shape_ok(uint32_t fmt, const StreamCfg& c, uint32_t n) {
   const int wv = fmt == SV_FMT_I8 ? 1 : 2;
   if (c.rt * c.nch * wv > 4) return false;  // weights <= 64 registers a wave
-  const size_t lds = (size_t)c.w * n * 2 * XROW * 2 + (size_t)c.w * c.rt * 1024 + (size_t)c.w * (n <= 8 ? 8 : 16) * 4;
+  const size_t lds = (size_t)c.w * n * 2 * XROW * 2 + (size_t)c.w * c.rt * 1024 + (size_t)c.w * 16 * 4;
   return lds <= 160 * 1024;
 }
 
+static bool stream_listed(const StreamCfg& c) {
+  for (const StreamCfg& sh : STREAM_SHAPES)
+    if (sh.rt == c.rt && sh.w == c.w && sh.nch == c.nch) return c.s == 1 || c.s == 2;
+  return false;
+}
+
+// Built-in choice: at least 256 workgroups where the matrix allows (more row tiles per
+// workgroup while that holds, else k split in two when each split keeps eight waves busy).
 static bool pick_stream(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k, StreamCfg* out) {
   const uint32_t tiles = m / 16, chunks = k / KC;
   if (g_skinny_tune.path == 3 && g_skinny_tune.rt) {
-    *out = StreamCfg{g_skinny_tune.rt, g_skinny_tune.w, g_skinny_tune.s};
-    return tiles % out->rt == 0 && (uint32_t)(out->w * out->nch) >= chunks && stream_shape_ok(fmt, *out, n);
+    *out = StreamCfg{g_skinny_tune.rt, g_skinny_tune.w, g_skinny_tune.s, std::max(1, g_skinny_tune.splits)};
+    return tiles % out->rt == 0 && (uint32_t)(out->w * out->nch * out->s) >= chunks &&
+           (uint32_t)(out->w * out->nch * (out->s - 1)) < chunks && stream_listed(*out) && stream_shape_ok(fmt, *out, n);
   }
-  for (int w : {8}) {
+  for (int s : {1, 2}) {
+    if (s == 2 && chunks < 16) break;
     int nch = 1;
-    while ((uint32_t)(nch * w) < chunks) nch *= 2;
+    while ((uint32_t)(nch * 8 * s) < chunks) nch *= 2;
     if (nch > 4) continue;
     for (int rt : {4, 2, 1}) {
-      const StreamCfg c{rt, w, nch};
-      if (tiles % rt || (rt > 1 && tiles / rt < 256) || !stream_shape_ok(fmt, c, n)) continue;
-      bool listed = false;
-      for (const StreamCfg& sh : STREAM_SHAPES) listed |= sh.rt == rt && sh.w == w && sh.nch == nch;
-      if (!listed) continue;
+      const StreamCfg c{rt, 8, nch, s};
+      if (tiles % rt || (rt > 1 && tiles / rt < 256) || !stream_shape_ok(fmt, c, n) || !stream_listed(c)) continue;
+      if (s == 1 && tiles / rt < 256 && chunks >= 16) break;  // too few workgroups: try two splits
       *out = c;
       return true;
     }
@@ -900,8 +1006,19 @@ static bool pick_stream(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k, Stream
   return false;
 }
 
-// Dynamic LDS (X rows) beyond the default 64 KB needs a per-kernel attribute, which cannot be
-// set while a stream is being captured: matmul_init sets it for every instantiation.
+size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
+  matmul_init();
+  if (n == 0 || !use_skinny(n, m, k)) return 0;
+  size_t a, b;
+  size_t need = std::max(skinny_ws_layout(n, m, pick_skinny(SV_FMT_I8, n, m, k), &a, &b),
+                         skinny_ws_layout(n, m, pick_skinny(SV_FMT_BF16, n, m, k), &a, &b));
+  StreamCfg c;
+  for (uint32_t fmt : {(uint32_t)SV_FMT_I8, (uint32_t)SV_FMT_BF16})
+    if (n <= 16 && m % 16 == 0 && pick_stream(fmt, n, m, k, &c))
+      need = std::max(need, skinny_ws_layout(n, m, SkinnyCfg{c.rt, c.w, c.s}, &a, &b));
+  return need;
+}
+
 template <int FMT, int RT, int W, int NCH, int NT>
 static void stream_attr() {
   const size_t static_lds = (size_t)W * RT * 1024 + (size_t)W * NT * 4;
@@ -918,8 +1035,8 @@ static void stream_launch_one(hipStream_t stream, const MMParams& p, uint32_t gr
 // Calls F<FMT, RT, W, NCH, NT> for the launch shape c (false if it is not built).
 #define SV_STREAM_SHAPES(FMT, NT, CALL)                                        \
   SV_ST(FMT, NT, 1, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 1, CALL) SV_ST(FMT, NT, 1, 8, 2, CALL) \
-  SV_ST(FMT, NT, 2, 8, 2, CALL) SV_ST(FMT, NT, 1, 8, 4, CALL)                   \
-  if (FMT == SV_FMT_I8) { SV_ST(FMT, NT, 4, 8, 1, CALL) }
+  SV_ST(FMT, NT, 1, 4, 1, CALL) SV_ST(FMT, NT, 1, 4, 2, CALL)                                \
+  if (FMT == SV_FMT_I8) { SV_ST(FMT, NT, 4, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 2, CALL) SV_ST(FMT, NT, 1, 8, 4, CALL) }
 
 template <int FMT, int NT>
 static bool stream_dispatch(hipStream_t stream, const MMParams& p, const StreamCfg& c, uint32_t grid) {
@@ -933,13 +1050,26 @@ static bool stream_dispatch(hipStream_t stream, const MMParams& p, const StreamC
   return false;
 }
 
+// Token slots NT: 4, 5 (the configs' k = 4 drafts + 1), 8 or 16.
+template <int FMT>
+static bool stream_dispatch_n(hipStream_t stream, const MMParams& p, const StreamCfg& c, uint32_t grid) {
+  if (p.n <= 4) return stream_dispatch<FMT, 4>(stream, p, c, grid);
+  if (p.n == 5) return stream_dispatch<FMT, 5>(stream, p, c, grid);
+  if (p.n <= 8) return stream_dispatch<FMT, 8>(stream, p, c, grid);
+  return stream_dispatch<FMT, 16>(stream, p, c, grid);
+}
+
 void matmul_init() {
   static bool done = false;
   if (done) return;
   done = true;
 #define SV_ST(F, N_, R, W_, C_, CALL) stream_attr<F, R, W_, C_, N_>();
+  SV_STREAM_SHAPES(SV_FMT_I8, 4, 0)
+  SV_STREAM_SHAPES(SV_FMT_I8, 5, 0)
   SV_STREAM_SHAPES(SV_FMT_I8, 8, 0)
   SV_STREAM_SHAPES(SV_FMT_I8, 16, 0)
+  SV_STREAM_SHAPES(SV_FMT_BF16, 4, 0)
+  SV_STREAM_SHAPES(SV_FMT_BF16, 5, 0)
   SV_STREAM_SHAPES(SV_FMT_BF16, 8, 0)
   SV_STREAM_SHAPES(SV_FMT_BF16, 16, 0)
 #undef SV_ST
@@ -998,6 +1128,10 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.ra = a->ra;
   p.rb = a->rb;
   p.chunks = a->k / KC;
+#ifdef SV_MM_STAMPS
+  p.stamps = g_mm_stamps;
+  p.dbg = g_mm_dbg;
+#endif
   p.counters = nullptr;
   p.part = p.ssp = nullptr;
   if (!skinny) {
@@ -1009,11 +1143,21 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
                          pick_stream(fmt, a->n, a->m, a->k, &sc);
   if (g_skinny_tune.path == 3 && !stream_ok) return fail(SV_ERR_ARG, "matmul: forced one-shot shape does not fit");
   if (stream_ok) {
-    const uint32_t grid = a->m / 16 / sc.rt;
-    const bool ok = fmt == SV_FMT_I8 ? (a->n <= 8 ? stream_dispatch<SV_FMT_I8, 8>(stream, p, sc, grid)
-                                                  : stream_dispatch<SV_FMT_I8, 16>(stream, p, sc, grid))
-                                     : (a->n <= 8 ? stream_dispatch<SV_FMT_BF16, 8>(stream, p, sc, grid)
-                                                  : stream_dispatch<SV_FMT_BF16, 16>(stream, p, sc, grid));
+    const uint32_t grid = a->m / 16 / sc.rt * sc.s;
+    p.splits = sc.s;
+    p.tgroups = 1;
+    if (sc.s > 1) {
+      size_t ss_off = 0, part_off = 0;
+      const size_t need = skinny_ws_layout(a->n, a->m, SkinnyCfg{sc.rt, sc.w, sc.s}, &ss_off, &part_off);
+      if (a->m / (16 * sc.rt) > COUNTER_SLOTS) return fail(SV_ERR_UNSUPPORTED, "matmul: row groups exceed the counters");
+      if (!ws || ws_bytes < need)
+        return fail(SV_ERR_ARG, "matmul: workspace %zu < %zu bytes (sv_matmul_workspace_bytes)", ws_bytes, need);
+      p.counters = (uint32_t*)ws;
+      p.ssp = (float*)((char*)ws + ss_off);
+      p.part = (float*)((char*)ws + part_off);
+    }
+    const bool ok = fmt == SV_FMT_I8 ? stream_dispatch_n<SV_FMT_I8>(stream, p, sc, grid)
+                                     : stream_dispatch_n<SV_FMT_BF16>(stream, p, sc, grid);
     if (!ok) return fail(SV_ERR_ARG, "matmul: launch shape rt %d, waves %d, chunks %d", sc.rt, sc.w, sc.nch);
     g_mm_variant = 3;
     return check_launch("matmul");

@@ -41,11 +41,11 @@ size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k);
 // Launch-shape override for the skinny matmul (row tiles, waves, k splits; zero: built-in)
 // and the path for more than 16 rows (0: built-in, 1: skinny, 2: GEMM).
 struct SkinnyTune {
-  int rt, w, s, path;
+  int rt, w, s, path, splits;
 };
 // The variant of the last matmul launched on this process (1 skinny, 2 GEMM, 3 one-shot): tests.
 extern int g_mm_variant;
-extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave)
+extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave, splits)
 sv_status pack_matrix(hipStream_t stream, const sv_matrix* src, void* dst, sv_matrix* out);
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,
                         const float* base, float* aux, const sv_mat_args* a, void* ws, size_t ws_bytes);

@@ -174,20 +174,24 @@ def test_matmul_skinny_launch_shapes(gpu, rt, waves, splits):
         tune[0] = tune[1] = tune[2] = tune[3] = 0
 
 
-@pytest.mark.parametrize("rt,waves,nch", [(1, 8, 1), (2, 8, 1), (4, 8, 1), (1, 8, 2), (2, 8, 2), (1, 8, 4)])
-@pytest.mark.parametrize("n", [3, 12])
-def test_matmul_one_shot_launch_shapes(gpu, rt, waves, nch, n):
-    """Every one-shot launch shape of the 1-16 row kernel (row tiles, waves, chunks per wave;
-    chunks past k and token slots past n are read and discarded) gives the oracle's result,
-    int8 with the sums of squares of EPI_NORM and bf16 with EPI_RESID's base, in both weight
-    layouts. The shape is forced through the library's internal override."""
-    banner(f"matmul one-shot rt={rt} waves={waves} nch={nch} n={n}")
-    tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv13g_skinny_tuneE")
-    rng = np.random.default_rng(rt * 100 + waves * 10 + nch + n)
+@pytest.mark.parametrize("rt,waves,nch,splits", [(1, 8, 1, 1), (2, 8, 1, 1), (4, 8, 1, 1), (1, 8, 2, 1), (2, 8, 2, 1),
+                                                (1, 8, 4, 1), (1, 4, 1, 2), (1, 4, 2, 2), (1, 8, 2, 2), (2, 8, 1, 2)])
+@pytest.mark.parametrize("n", [3, 5, 12])
+def test_matmul_one_shot_launch_shapes(gpu, rt, waves, nch, splits, n):
+    """Every one-shot launch shape of the 1-16 row kernel (row tiles, waves, chunks per wave,
+    k splits merged by the last split to arrive; chunks past k and token slots past n are read
+    and discarded) gives the oracle's result, int8 with the sums of squares of EPI_NORM and
+    bf16 with EPI_RESID's base, in both weight layouts, on calls that share one workspace. The
+    shape is forced through the library's internal override."""
+    banner(f"matmul one-shot rt={rt} waves={waves} nch={nch} splits={splits} n={n}")
+    tune = (C.c_int * 5).in_dll(L.lib(), "_ZN2sv13g_skinny_tuneE")
+    rng = np.random.default_rng(rt * 100 + waves * 10 + nch + n + 1000 * splits)
     m = 256 * rt
-    k = 256 * waves * nch - 256 * (nch > 1)  # the last wave's last chunk is past k when nch > 1
+    per_split = waves * nch
+    k = 256 * (per_split * (splits - 1) + per_split - (nch > 1))  # the last split's last chunk is past k when nch > 1
+    ws = K.Workspace(8 << 20)
     try:
-        tune[0], tune[1], tune[2], tune[3] = rt, waves, nch, 3
+        tune[0], tune[1], tune[2], tune[3], tune[4] = rt, waves, nch, 3, splits
         for fmt in ("i8", "bf16"):
             if fmt == "bf16" and rt * nch > 2:
                 continue
@@ -210,7 +214,7 @@ def test_matmul_one_shot_launch_shapes(gpu, rt, waves, nch, n):
                 y = torch.zeros(n, m, device="cuda")
                 aux = torch.zeros(n, device="cuda")
                 K.matmul(layout, to_dev(x), y, n=n, epi=epi, flags=flags, scale=0.75, ra=0.9, rb=1.3,
-                         base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux)
+                         base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux, ws=ws)
                 torch.cuda.synchronize()
                 assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 3, "one-shot kernel not launched"
                 close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
@@ -218,7 +222,7 @@ def test_matmul_one_shot_launch_shapes(gpu, rt, waves, nch, n):
                 if epi == L.EPI_NORM:
                     close(aux.cpu().numpy(), aux_ref, atol=1e-5, rtol=1e-4, what="inv")
     finally:
-        tune[0] = tune[1] = tune[2] = tune[3] = 0
+        tune[0] = tune[1] = tune[2] = tune[3] = tune[4] = 0
 
 
 # ---------------------------------------------------------------------------- attention
