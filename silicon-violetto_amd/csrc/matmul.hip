@@ -459,12 +459,8 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     for (int i = 0; i < NT; i++) {
       if ((uint32_t)i >= n) break;
       const f32x4 v = xc[i];
-      float h[4], l[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++) split_bf(v[e], h[e], l[e]);
-      const u32x2 hw = u32x2{(__float_as_uint(h[0]) >> 16) | (__float_as_uint(h[1]) & 0xffff0000u),
-                             (__float_as_uint(h[2]) >> 16) | (__float_as_uint(h[3]) & 0xffff0000u)};
-      const u32x2 lw = u32x2{pack_bf2(l[0], l[1]), pack_bf2(l[2], l[3])};
+      const u32x2 s01 = split2(v[0], v[1]), s23 = split2(v[2], v[3]);
+      const u32x2 hw = u32x2{s01[0], s23[0]}, lw = u32x2{s01[1], s23[1]};
       *(u32x2*)(xs + (2 * i) * XROW + 4 * lane) = hw;
       *(u32x2*)(xs + (2 * i + 1) * XROW + 4 * lane) = lw;
     }
@@ -623,66 +619,158 @@ __global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* src, uin
 
 // ------------------------------------------------------------------- large n
 // GEMM path (n > 16 rows: many streams, draft trees): a workgroup of 4 waves owns
-// BM = 64 RTW output rows and BN = 16 NT tokens; k goes in chunks of 64.
+// BM = 64 RTW output rows, BN = 16 NT tokens and a 1/S share of k (k splits when the tiles
+// alone give too few workgroups); k goes in chunks of 64.
+//   - Software pipeline D chunks deep: each wave's weights (16 bytes per lane per row tile
+//     per chunk) and each thread's X pairs for chunk c + D are requested while chunk c is
+//     multiplied. Every load is unconditional: chunks past the split's end and token slots
+//     past n use offsets beyond the buffer's range, which the hardware answers with zeros
+//     without a memory access, so no branch makes the compiler wait for a load early.
 //   - X chunk [BN][64] fp32 is read once per workgroup (L2), split into bf16 hi + lo and
-//     written to LDS already in MFMA B-operand lane order (one 16-byte row per lane), so
-//     every operand read is a conflict-free ds_read_b128; double-buffered, one barrier per
-//     chunk.
-//   - Each wave streams its RTW x 16 weight rows straight into registers (16 bytes per lane
-//     per row tile per chunk, the next chunk's in flight), converts int8 to bf16, and runs
+//     written to LDS in MFMA B-operand lane order (one 16-byte row per lane), so every
+//     operand read is a conflict-free ds_read_b128; double-buffered, one barrier per chunk
+//     (an LDS-only wait: weight and X loads stay in flight across it).
+//   - Each wave converts its int8 weights to bf16 in registers (exact) and runs
 //     RTW x NT x 2 k-steps x 2 (hi, lo) MFMAs per chunk.
 //   - Workgroups that share weight rows (different token blocks) are mapped to the same XCD,
-//     so the second reads the rows from that XCD's L2.
+//     so all but the first read the rows from that XCD's L2.
 //   - Sums of squares for the folded rms-norm: each thread owns fixed (token, 8-k group)
 //     pairs for the whole k, added in a fixed order at the end.
+//   - k splits: each split stores its sums (coherent stores) and the last split of the
+//     (row block, token block) to arrive adds them in split order and runs the epilogue.
 constexpr int GKC = 64;
+// Split-k hand-off counters (skinny and GEMM paths): a region of fixed size at the front of the
+// workspace, so every matmul sharing one workspace finds its counters at zero there, whatever
+// its shape.
+constexpr size_t COUNTER_SLOTS = 16384;
 
-template <int FMT, int RTW, int NT>
+// Wait for this thread's LDS operations, then the workgroup barrier. Unlike __syncthreads()
+// this leaves global loads in flight (no vmcnt wait).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Epilogue of the GEMM (kernels.metal:183-209) for one 16-token tile: lane (t16, q) holds rows
+// 4 q + 0..3 of each of the wave's RTW row tiles (first row row0) for token t.
+template <int RTW>
+__device__ __forceinline__ void gemm_epilogue(const MMParams& p, const f32x4 (&acc)[RTW], uint32_t row0, int q,
+                                              uint32_t t, float ss, bool write_inv) {
+  const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
+  if (write_inv && (p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && q == 0) p.aux[t] = inv;
+  const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
+#pragma unroll
+  for (int r = 0; r < RTW; r++) {
+    const uint32_t rowq = row0 + 16 * r + 4 * q;
+    f32x4 v = acc[r];
+    const size_t o = (size_t)t * p.m + rowq;
+    switch (p.epi) {
+      case SV_EPI_NORM:
+        *(f32x4*)(p.y + o) = v * (inv * p.scale);
+        break;
+      case SV_EPI_RAW:
+        if (norm_in) v *= inv;
+        *(f32x4*)(p.y + o) = v;
+        break;
+      case SV_EPI_RESID: {
+        if (norm_in) v *= inv;
+        const f32x4 sv = v * p.scale;
+        const f32x4 b = *(const f32x4*)(p.base + o);
+        *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
+        if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
+        break;
+      }
+      case SV_EPI_HEAD: {
+        if (norm_in) v *= inv;
+        f32x4 l;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          l[i] = rowq + i < p.vocab_real ? 23.0f * sigmoidf_((v[i] + 5.0f) / 7.5f) : -__builtin_inff();
+        *(f32x4*)(p.y + o) = l;
+        break;
+      }
+      case SV_EPI_SWIGLU: {
+        const float sc = inv * p.scale;
+        const float g0 = v[0] * sc, u0 = v[1] * sc, g1 = v[2] * sc, u1 = v[3] * sc;
+        float2 out;
+        out.x = g0 * sigmoidf_(g0) * u0;
+        out.y = g1 * sigmoidf_(g1) * u1;
+        *(float2*)(p.y + (size_t)t * (p.m / 2) + rowq / 2) = out;
+        break;
+      }
+      default:
+        break;
+    }
+  }
+}
+
+template <int FMT, int RTW, int NT, bool GROUPED, int GD>
 __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
+  static_assert(GD % 2 == 0, "chunk parity = slot parity");
   constexpr int BN = 16 * NT;
   constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
-  constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;     // dwordx4 per lane per row tile per chunk
-  constexpr int PAIRS = BN * 8;                    // (token, 8-k group) pairs per chunk
-  constexpr int PPT = (PAIRS + 255) / 256;         // pairs per thread
+  constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;  // dwordx4 per lane per row tile per chunk
+  constexpr int PAIRS = BN * 8;                 // (token, 8-k group) pairs per chunk
+  constexpr int PPT = (PAIRS + 255) / 256;      // pairs per thread
   // LDS: [2 buffers][NT][2 k-steps][hi, lo][64 lanes] of 16 bytes.
   __shared__ u32x4 xs[2][NT][2][2][64];
   __shared__ float ssp[BN][8];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, t16 = lane & 15, q = lane >> 4;
+  __shared__ uint32_t last_flag;
+  const int tid = threadIdx.x, lane = tid & 63, t16 = lane & 15, q = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // XCD-aware order: work items (row block, token block) with the same row block go to the
-  // same XCD (workgroup id mod 8) when the count allows.
-  const uint32_t nwg = gridDim.x, g = blockIdx.x;
-  uint32_t item = g;
-  if (nwg % 8 == 0) item = (g % 8) * (nwg / 8) + g / 8;
-  const uint32_t rblk = item / n_tblk, tblk = item % n_tblk;
+  // Work items (row block, split, token block), token block fastest; consecutive items go
+  // to one XCD (workgroup id mod 8) when the count allows.
+  const uint32_t nwg = gridDim.x, S = p.splits;
+  uint32_t item = blockIdx.x;
+  if (nwg % 8 == 0) item = (item % 8) * (nwg / 8) + item / 8;
+  const uint32_t tblk = item % n_tblk, sp = (item / n_tblk) % S, rblk = item / (n_tblk * S);
   const uint32_t t0 = tblk * BN;
   const uint32_t row0 = rblk * 64 * RTW + wv * 16 * RTW;  // this wave's first row
+  const uint32_t nc = __builtin_amdgcn_readfirstlane(p.k / GKC / S);
+  const uint32_t cb = __builtin_amdgcn_readfirstlane(sp * nc);
 
+  // Buffer resources (offsets below 2 GiB); an offset of 2^31 or more reads zeros.
+  const __amdgpu_buffer_rsrc_t xrs = coherent_rsrc(p.x), wrs = coherent_rsrc(p.w);
+  constexpr uint32_t OOB = 0x80000000u;
   // Weights: lane (t16, q) takes row t16 of each tile, bytes 16 q .. of each 64-k chunk.
-
+  const uint32_t tile0 = row0 / 16;
+  const uint32_t wv_lane = p.tiled ? 16u * lane : ((uint32_t)t16 * p.k + 16 * q) * ESZ;
+  const uint32_t tile_bytes = 16 * p.k * ESZ, chunk_bytes = p.tiled ? 1024 * ESZ : 64 * ESZ,
+                 v_bytes = p.tiled ? 1024 : 16;
   // X pairs of this thread: pair i -> token i / 8, k group i % 8 (k = 8 (i % 8) .. + 7).
-  float ssacc[PPT];
-  const float* xp[PPT];
-  bool pv[PPT];
+  uint32_t xoff[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; j++) {
     const int i = tid + 256 * j;
     const uint32_t tt = t0 + i / 8;
-    pv[j] = i < PAIRS && tt < p.n;
-    xp[j] = p.x + (size_t)(pv[j] ? (p.x_rows ? p.x_rows[tt] : tt) : 0u) * p.k + 8 * (i % 8);
-    ssacc[j] = 0.0f;
+    const bool v = i < PAIRS && tt < p.n;
+    xoff[j] = v ? ((p.x_rows ? p.x_rows[tt] : tt) * p.k + 8 * (i % 8)) * 4 : OOB;
   }
   auto load_x = [&](uint32_t c, f32x4 (&xr)[PPT][2]) {
+    // past the split's end: every lane's offset out of range (the range check covers the
+    // per-lane offset)
+    const uint32_t so = __builtin_amdgcn_readfirstlane((cb + min(c, nc - 1)) * GKC * 4);
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
-      if (pv[j]) {
-        xr[j][0] = *(const f32x4*)(xp[j] + (size_t)c * GKC);
-        xr[j][1] = *(const f32x4*)(xp[j] + (size_t)c * GKC + 4);
-      } else {
-        xr[j][0] = xr[j][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+      const uint32_t vo = c < nc ? xoff[j] : OOB;
+      xr[j][0] = __builtin_bit_cast(f32x4, buf_ld16(xrs, vo, so));
+      xr[j][1] = __builtin_bit_cast(f32x4, buf_ld16(xrs, vo + 16, so));
     }
   };
+  auto load_w = [&](uint32_t c, u32x4 (&wr)[RTW][WL]) {
+    const uint32_t cc = c < nc ? cb + c : 0u;
+    const uint32_t vo = c < nc ? wv_lane : OOB;
+#pragma unroll
+    for (int r = 0; r < RTW; r++)
+#pragma unroll
+      for (int v = 0; v < WL; v++)
+        wr[r][v] = buf_ld16(wrs, vo, __builtin_amdgcn_readfirstlane((tile0 + r) * tile_bytes + cc * chunk_bytes + v * v_bytes));
+  };
+  float ssacc[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; j++) ssacc[j] = 0.0f;
   auto store_x = [&](int buf, const f32x4 (&xr)[PPT][2]) {
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
@@ -704,92 +792,98 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       xs[buf][tok >> 4][ks][1][ln] = __builtin_bit_cast(u32x4, l);
     }
   };
-  const uint32_t nch = p.k / GKC;
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
 
   f32x4 acc[RTW][NT];
+  f32x4 grp[GROUPED ? RTW : 1][GROUPED ? NT : 1];
 #pragma unroll
   for (int r = 0; r < RTW; r++)
 #pragma unroll
     for (int n = 0; n < NT; n++) acc[r][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  f32x4 grp[RTW][NT];  // the current scale group's sums (int8 with groups < k)
-
-  f32x4 xr[PPT][2];
-  u32x4 wr[RTW][WL];
-  load_x(0, xr);
-#pragma unroll
-  for (int r = 0; r < RTW; r++)
-#pragma unroll
-    for (int v = 0; v < WL; v++) wr[r][v] = ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, row0 / 16 + r, 0, v, lane));
-  store_x(0, xr);
-  __syncthreads();
-  const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
-#pragma unroll
-  for (int r = 0; r < RTW; r++)
-#pragma unroll
-    for (int n = 0; n < NT; n++) grp[r][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  for (uint32_t c = 0; c < nch; c++) {
-    const int buf = c & 1;
-    u32x4 cur[RTW][WL];
+  if (GROUPED)
 #pragma unroll
     for (int r = 0; r < RTW; r++)
 #pragma unroll
-      for (int v = 0; v < WL; v++) cur[r][v] = wr[r][v];
-    if (c + 1 < nch) {
-      load_x(c + 1, xr);
+      for (int n = 0; n < NT; n++) grp[GROUPED ? r : 0][GROUPED ? n : 0] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Prologue: chunks 0 .. D-1 requested; chunk 0's X to LDS.
+  f32x4 xr[GD][PPT][2];
+  u32x4 wr[GD][RTW][WL];
+#pragma unroll
+  for (int d = 0; d < GD; d++) {
+    load_w(d, wr[d]);
+    load_x(d, xr[d]);
+  }
+  store_x(0, xr[0]);
+  load_x(GD, xr[0]);
+  lds_barrier();
+
+  // No branch inside the loop (a conditional load would make the compiler wait for every
+  // load in flight): a last partial round of GD runs on zeros (weights and X past the split's
+  // end read as zeros and add exactly nothing).
+  for (uint32_t c0 = 0; c0 < nc; c0 += GD) {
+#pragma unroll
+    for (int d = 0; d < GD; d++) {
+      const uint32_t c = c0 + d;
+      const int buf = d & 1;  // GD is even: chunk parity
+      u32x4 cur[RTW][WL];
 #pragma unroll
       for (int r = 0; r < RTW; r++)
 #pragma unroll
-        for (int v = 0; v < WL; v++)
-          wr[r][v] = ldg_nt(weight_word<ESZ>(p.w, p.k, p.tiled, row0 / 16 + r, c + 1, v, lane));
-    }
+        for (int v = 0; v < WL; v++) cur[r][v] = wr[d][r][v];
+      load_w(c + GD, wr[d]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      bf16x8 a[RTW];
-#pragma unroll
-      for (int r = 0; r < RTW; r++) {
-        if (FMT == SV_FMT_I8) a[r] = i8x8_to_bf(cur[r][0][2 * ks], cur[r][0][2 * ks + 1]);
-        else a[r] = __builtin_bit_cast(bf16x8, cur[r][ks]);
-      }
-#pragma unroll
-      for (int n = 0; n < NT; n++) {
-        const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][ks][0][lane]);
-        const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][ks][1][lane]);
+      for (int ks = 0; ks < 2; ks++) {
+        bf16x8 a[RTW];
 #pragma unroll
         for (int r = 0; r < RTW; r++) {
-          grp[r][n] = mfma16(a[r], bh, grp[r][n]);
-          grp[r][n] = mfma16(a[r], bl, grp[r][n]);
+          if (FMT == SV_FMT_I8) a[r] = i8x8_to_bf(cur[r][0][2 * ks], cur[r][0][2 * ks + 1]);
+          else a[r] = __builtin_bit_cast(bf16x8, cur[r][ks]);
         }
-      }
-    }
-    // Close a scale group (int8 with groups < k): acc += scale * group sums.
-    if (grouped && ((c + 1) * GKC) % (1u << p.gshift) == 0) {
-      const uint32_t gi = (c * GKC) >> p.gshift;
 #pragma unroll
-      for (int r = 0; r < RTW; r++)
+        for (int n = 0; n < NT; n++) {
+          const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][ks][0][lane]);
+          const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][ks][1][lane]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float sc = bf(p.scales[(size_t)(row0 + 16 * r + 4 * q + i) * ng + gi]);
-#pragma unroll
-          for (int n = 0; n < NT; n++) {
-            acc[r][n][i] += sc * grp[r][n][i];
-            grp[r][n][i] = 0.0f;
+          for (int r = 0; r < RTW; r++) {
+            f32x4& g = GROUPED ? grp[GROUPED ? r : 0][GROUPED ? n : 0] : acc[r][n];
+            g = mfma16(a[r], bh, g);
+            g = mfma16(a[r], bl, g);
           }
         }
+      }
+      // Close a scale group (int8 with groups < k): acc += scale * group sums; also at the
+      // split's last chunk when a group straddles two splits (each part scaled: exact).
+      if (GROUPED && c < nc && ((((cb + c) + 1) * GKC) % (1u << p.gshift) == 0 || c + 1 == nc)) {
+        const uint32_t gi = ((cb + c) * GKC) >> p.gshift;
+#pragma unroll
+        for (int r = 0; r < RTW; r++)
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float sc = bf(ldg_u16(p.scales + (size_t)(row0 + 16 * r + 4 * q + i) * ng + gi));
+#pragma unroll
+            for (int n = 0; n < NT; n++) {
+              acc[r][n][i] += sc * grp[GROUPED ? r : 0][GROUPED ? n : 0][i];
+              grp[GROUPED ? r : 0][GROUPED ? n : 0][i] = 0.0f;
+            }
+          }
+      }
+      // Chunk c + 1's X (requested D - 1 chunks ago) to the other buffer, then chunk
+      // c + 1 + D requested into its registers.
+      const int dn = (d + 1) % GD;
+      store_x(buf ^ 1, xr[dn]);
+      load_x(c + 1 + GD, xr[dn]);
+      lds_barrier();
     }
-    if (c + 1 < nch) store_x(buf ^ 1, xr);
-    __syncthreads();
   }
-  if (!grouped) {
+  if (!GROUPED && FMT == SV_FMT_I8) {
 #pragma unroll
     for (int r = 0; r < RTW; r++) {
-      f32x4 sc = f32x4{1.f, 1.f, 1.f, 1.f};
-      if (FMT == SV_FMT_I8)
+      f32x4 sc;
 #pragma unroll
-        for (int i = 0; i < 4; i++) sc[i] = bf(p.scales[(size_t)(row0 + 16 * r + 4 * q + i) * ng]);
+      for (int i = 0; i < 4; i++) sc[i] = bf(ldg_u16(p.scales + (row0 + 16 * r + 4 * q + i)));
 #pragma unroll
-      for (int n = 0; n < NT; n++) acc[r][n] = grp[r][n] * sc;
+      for (int n = 0; n < NT; n++) acc[r][n] *= sc;
     }
   }
   // Sums of squares per token: the thread's pairs, then the 8 k groups in order.
@@ -799,103 +893,170 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
     if (i < PAIRS) ssp[i / 8][i % 8] = ssacc[j];
   }
   __syncthreads();
-
-  // Epilogue (kernels.metal:183-209): lane (t16, q) holds rows 4 q + 0..3 of each row tile
-  // for token t0 + 16 n + t16.
-  const bool norm_in = (p.flags & SV_FLAG_NORM_IN) != 0;
+  float ssn[NT];
 #pragma unroll
   for (int n = 0; n < NT; n++) {
-    const uint32_t tl = 16 * n + t16, t = t0 + tl;
-    if (t >= p.n) continue;
+    const uint32_t tl = 16 * n + t16;
     float ss = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) ss += ssp[tl][e];
-    const float inv = 1.0f / __builtin_sqrtf(ss / (float)p.k + SV_RMS_EPS);
-    if ((p.flags & SV_FLAG_WRITE_INV) && p.epi == SV_EPI_NORM && rblk == 0 && wv == 0 && q == 0) p.aux[t] = inv;
+    ssn[n] = ss;
+  }
+
+  if (S > 1) {
+    // This split's sums to the workspace: [cell][split][256 threads][RTW NT] f32x4 and
+    // [cell][split][BN] sums of squares; the last split of the cell adds them in split order.
+    const uint32_t cell = rblk * n_tblk + tblk;
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part), srs = coherent_rsrc(p.ssp);
+    constexpr uint32_t PER = 256 * RTW * NT * 16;
+    const uint32_t pb = (cell * S) * PER;
 #pragma unroll
-    for (int r = 0; r < RTW; r++) {
-      const uint32_t rowq = row0 + 16 * r + 4 * q;
-      f32x4 v = acc[r][n];
-      const size_t o = (size_t)t * p.m + rowq;
-      switch (p.epi) {
-        case SV_EPI_NORM:
-          *(f32x4*)(p.y + o) = v * (inv * p.scale);
-          break;
-        case SV_EPI_RAW:
-          if (norm_in) v *= inv;
-          *(f32x4*)(p.y + o) = v;
-          break;
-        case SV_EPI_RESID: {
-          if (norm_in) v *= inv;
-          const f32x4 sv = v * p.scale;
-          const f32x4 b = *(const f32x4*)(p.base + o);
-          *(f32x4*)(p.y + o) = b * p.ra + sv * p.rb;
-          if (p.flags & SV_FLAG_WRITE_RAW) *(f32x4*)(p.aux + o) = sv;
-          break;
-        }
-        case SV_EPI_HEAD: {
-          if (norm_in) v *= inv;
-          f32x4 l;
+    for (int r = 0; r < RTW; r++)
 #pragma unroll
-          for (int i = 0; i < 4; i++)
-            l[i] = rowq + i < p.vocab_real ? 23.0f * sigmoidf_((v[i] + 5.0f) / 7.5f) : -__builtin_inff();
-          *(f32x4*)(p.y + o) = l;
-          break;
-        }
-        case SV_EPI_SWIGLU: {
-          const float sc = inv * p.scale;
-          const float g0 = v[0] * sc, u0 = v[1] * sc, g1 = v[2] * sc, u1 = v[3] * sc;
-          float2 out;
-          out.x = g0 * sigmoidf_(g0) * u0;
-          out.y = g1 * sigmoidf_(g1) * u1;
-          *(float2*)(p.y + (size_t)t * (p.m / 2) + rowq / 2) = out;
-          break;
-        }
-        default:
-          break;
-      }
+      for (int n = 0; n < NT; n++) store_wt4(prs, pb + sp * PER + ((r * NT + n) * 256 + tid) * 16, acc[r][n]);
+    if (tid < BN)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ssp[tid][0] + ssp[tid][1] + ssp[tid][2] + ssp[tid][3] +
+                                                            ssp[tid][4] + ssp[tid][5] + ssp[tid][6] + ssp[tid][7]),
+                                            srs, ((cell * S + sp) * BN + tid) * 4, 0, SV_CPOL_SC1);
+    if (!arrive_last(p.counters + cell, S, &last_flag)) return;
+#pragma unroll
+    for (int r = 0; r < RTW; r++)
+#pragma unroll
+      for (int n = 0; n < NT; n++) acc[r][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int n = 0; n < NT; n++) ssn[n] = 0.0f;
+    for (uint32_t s2 = 0; s2 < S; s2++) {
+#pragma unroll
+      for (int r = 0; r < RTW; r++)
+#pragma unroll
+        for (int n = 0; n < NT; n++) acc[r][n] += load_wt4(prs, pb + s2 * PER + ((r * NT + n) * 256 + tid) * 16);
+#pragma unroll
+      for (int n = 0; n < NT; n++)
+        ssn[n] += __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(srs, ((cell * S + s2) * BN + 16 * n + t16) * 4, 0, SV_CPOL_SC1));
     }
+  }
+
+  // Epilogue: lane (t16, q) holds rows 4 q + 0..3 of each row tile for token t0 + 16 n + t16.
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    const uint32_t t = t0 + 16 * n + t16;
+    if (t >= p.n) continue;
+    f32x4 col[RTW];
+#pragma unroll
+    for (int r = 0; r < RTW; r++) col[r] = acc[r][n];
+    gemm_epilogue<RTW>(p, col, row0, q, t, ssn[n], rblk == 0 && wv == 0);
   }
 }
 
-// Token tiles per workgroup (BN = 16 NT) and row tiles per wave (BM = 64 RTW) for n rows:
-// the fewest padded tokens, then enough workgroups to fill 256 CUs.
-static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, const MMParams& p) {
-  const int nts[] = {2, 4, 5, 8};
-  int nt = 8;
-  uint32_t best = ~0u;
-  for (int c : nts) {
-    const uint32_t blocks = (p.n + 16 * c - 1) / (16 * c), pad = blocks * 16 * c - p.n;
-    if (pad < best || (pad == best && c > nt)) best = pad, nt = c;
-  }
-  const uint32_t n_tblk = (p.n + 16 * nt - 1) / (16 * nt);
-  int rtw = 1;
-  for (int c = 4; c > 1; c /= 2)
-    if (p.m % (64 * c) == 0 && (p.m / (64 * c)) * n_tblk >= 512) {
-      rtw = c;
-      break;
+// GEMM launch shape: RTW row tiles per wave (BM = 64 RTW), NT token tiles (BN = 16 NT),
+// S k splits.
+struct GemmCfg {
+  int rtw, nt, s, d;  // d: chunks in flight (4 or 8)
+};
+GemmTune g_gemm_tune;  // all zero: the built-in choice
+
+// Built-in choice, from measurements on MI355X at 40, 160 and 512 rows (qkv, o, gate_up, down
+// int8, the bf16 head): int8 runs 32-token blocks (NT = 2) with two row tiles per wave and two
+// k splits, four when that leaves fewer than 256 workgroups, and one row tile per wave when
+// even four splits leave fewer; bf16 (twice the weight bytes per row) runs the token block with
+// the fewest padded tokens among NT = 3, 5 and 8, unsplit. Scale groups shorter than k: one
+// row tile per wave.
+static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uint32_t k) {
+  if (g_gemm_tune.rtw)
+    return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
+  const uint32_t nch = k / GKC;
+  auto splits_ok = [&](int s) { return nch % s == 0 && nch / s >= 4; };
+  if (fmt != SV_FMT_I8) {
+    GemmCfg c{2, 5, 1, 4};
+    uint32_t best = ~0u;
+    for (int nt : {3, 5, 8}) {
+      const uint32_t pad = (n + 16 * nt - 1) / (16 * nt) * 16 * nt - n;
+      if (pad < best || (pad == best && nt == 5)) best = pad, c.nt = nt;
     }
-  const uint32_t nwg = p.m / (64 * rtw) * n_tblk;
-#define SV_G(F, R, N) launch((mm_gemm<F, R, N>), dim3(nwg), dim3(256), 0, stream, p, n_tblk)
-#define SV_G_N(F, R)                \
-  switch (nt) {                     \
-    case 2: SV_G(F, R, 2); break;   \
-    case 4: SV_G(F, R, 4); break;   \
-    case 5: SV_G(F, R, 5); break;   \
-    default: SV_G(F, R, 8); break;  \
+    if (m % 128 || c.nt == 8) c.rtw = 1;
+    return c;
   }
-#define SV_G_R(F)                     \
-  if (rtw == 4) { SV_G_N(F, 4) }      \
-  else if (rtw == 2) { SV_G_N(F, 2) } \
-  else { SV_G_N(F, 1) }
+  const uint32_t n_tblk = (n + 31) / 32;
+  GemmCfg c{grouped ? 1 : 2, 2, 1, 4};
+  if (m % (64 * c.rtw)) c.rtw = 1;
+  for (int pass = 0; pass < 2; pass++) {
+    const uint32_t cells = m / (64 * c.rtw) * n_tblk;
+    c.s = 1;
+    for (int s : {2, 4})
+      if (splits_ok(s)) {
+        c.s = s;
+        if (cells * s >= 256) break;
+      }
+    if (cells * c.s >= 256 || c.rtw == 1) break;
+    c.rtw = 1;
+  }
+  return c;
+}
+
+static size_t gemm_ws_layout(uint32_t n, uint32_t m, const GemmCfg& c, size_t* ss_off, size_t* part_off) {
+  if (c.s <= 1) return 0;
+  const size_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt), cells = m / (64 * c.rtw) * n_tblk;
+  size_t off = COUNTER_SLOTS * 4;
+  *ss_off = off;
+  off += (cells * c.s * 16 * c.nt * 4 + 255) / 256 * 256;
+  *part_off = off;
+  off += cells * c.s * 256 * c.rtw * c.nt * 16;
+  return off;
+}
+
+static bool gemm_shape_ok(uint32_t m, uint32_t k, const GemmCfg& c) {
+  const bool nt_ok = c.nt == 2 || c.nt == 3 || c.nt == 4 || c.nt == 5 || c.nt == 8;
+  return nt_ok && (c.rtw == 1 || c.rtw == 2) && (c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
+         (k / GKC) % c.s == 0;
+}
+
+template <int FMT, int RTW, int NT, bool GR>
+static void gemm_launch_one(hipStream_t stream, const MMParams& p, int d, uint32_t nwg, uint32_t n_tblk) {
+  if (d == 8 && NT <= 3) launch((mm_gemm<FMT, RTW, NT, GR, (NT <= 3 ? 8 : 4)>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
+  else launch((mm_gemm<FMT, RTW, NT, GR, 4>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
+}
+
+template <int FMT, int RTW, bool GR>
+static void gemm_dispatch_nt(hipStream_t stream, const MMParams& p, int nt, int d, uint32_t nwg, uint32_t n_tblk) {
+  switch (nt) {
+    case 2: gemm_launch_one<FMT, RTW, 2, GR>(stream, p, d, nwg, n_tblk); break;
+    case 3: gemm_launch_one<FMT, RTW, 3, GR>(stream, p, d, nwg, n_tblk); break;
+    case 4: gemm_launch_one<FMT, RTW, 4, GR>(stream, p, d, nwg, n_tblk); break;
+    case 5: gemm_launch_one<FMT, RTW, 5, GR>(stream, p, d, nwg, n_tblk); break;
+    default: gemm_launch_one<FMT, RTW, 8, GR>(stream, p, d, nwg, n_tblk); break;
+  }
+}
+
+static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, MMParams& p, void* ws, size_t ws_bytes) {
+  const bool grouped = fmt == SV_FMT_I8 && !p.per_row;
+  const GemmCfg c = pick_gemm(fmt, grouped, p.n, p.m, p.k);
+  if (!gemm_shape_ok(p.m, p.k, c) || (grouped && c.rtw != 1))
+    return fail(SV_ERR_ARG, "matmul (gemm): launch shape rtw %d, nt %d, splits %d for m %u, k %u", c.rtw, c.nt, c.s,
+                p.m, p.k);
+  if ((size_t)p.m * p.k * (fmt == SV_FMT_I8 ? 1 : 2) >= (1ull << 31) || (size_t)p.n * p.k * 4 >= (1ull << 31))
+    return fail(SV_ERR_UNSUPPORTED, "matmul (gemm): operands of 2 GiB or more");
+  const uint32_t n_tblk = (p.n + 16 * c.nt - 1) / (16 * c.nt), rb = p.m / (64 * c.rtw);
+  size_t ss_off = 0, part_off = 0;
+  const size_t need = gemm_ws_layout(p.n, p.m, c, &ss_off, &part_off);
+  if (need) {
+    if ((size_t)rb * n_tblk > COUNTER_SLOTS) return fail(SV_ERR_UNSUPPORTED, "matmul (gemm): cells exceed the counters");
+    if (!ws || ws_bytes < need)
+      return fail(SV_ERR_ARG, "matmul: workspace %zu < %zu bytes (sv_matmul_workspace_bytes)", ws_bytes, need);
+    p.counters = (uint32_t*)ws;
+    p.ssp = (float*)((char*)ws + ss_off);
+    p.part = (float*)((char*)ws + part_off);
+  }
+  p.splits = c.s;
+  const uint32_t nwg = rb * n_tblk * c.s;
   if (fmt == SV_FMT_I8) {
-    SV_G_R(SV_FMT_I8)
+    if (grouped) gemm_dispatch_nt<SV_FMT_I8, 1, true>(stream, p, c.nt, c.d, nwg, n_tblk);
+    else if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_I8, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);
+    else gemm_dispatch_nt<SV_FMT_I8, 1, false>(stream, p, c.nt, c.d, nwg, n_tblk);
   } else {
-    SV_G_R(SV_FMT_BF16)
+    if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_BF16, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);
+    else gemm_dispatch_nt<SV_FMT_BF16, 1, false>(stream, p, c.nt, c.d, nwg, n_tblk);
   }
-#undef SV_G_R
-#undef SV_G_N
-#undef SV_G
   return check_launch("matmul (gemm)");
 }
 
@@ -906,16 +1067,13 @@ struct SkinnyCfg {
 SkinnyTune g_skinny_tune;  // all zero: the built-in choice
 int g_mm_variant = -1;
 
-// Beyond 16 rows the skinny kernel runs one workgroup per 16-token group (weights re-read
-// from L2 per group); measured on MI355X at 160 and 512 rows it beats the LDS-tiled GEMM on
-// matrices of up to 4096 rows (qkv, o, down) and loses on wider ones (gate_up, head).
-constexpr uint32_t SKINNY_MAX_N = 512;
-constexpr uint32_t SKINNY_MAX_M_MANY_ROWS = 4096;
+// Beyond 16 rows the GEMM path runs; the skinny kernel (one workgroup per 16-token group,
+// weights re-read from L2 per group) can still be forced for more rows (tests).
 
 static bool use_skinny(uint32_t n, uint32_t m, uint32_t k) {
   if (m % 16 || k % KC) return false;
   if (g_skinny_tune.path) return g_skinny_tune.path != 2;
-  return n <= 16 || (n <= SKINNY_MAX_N && m <= SKINNY_MAX_M_MANY_ROWS);
+  return n <= 16;
 }
 
 // Measured on MI355X at 1-5 rows: about 128 KB of weights per workgroup and at least 256
@@ -940,11 +1098,9 @@ static SkinnyCfg pick_skinny(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k) {
   return c;
 }
 
-// Workspace layout (skinny, S > 1): counters in a region of fixed size at the front (every
-// matmul sharing one workspace finds its counters at zero there, whatever its shape), then per
-// cell (row group, token group) the sums of squares [cells][S][16] and partials
-// [cells][S][RT][64][4] fp32.
-constexpr size_t COUNTER_SLOTS = 16384;
+// Workspace layout (skinny, S > 1): the counters region at the front, then per cell (row
+// group, token group) the sums of squares [cells][S][16] and partials [cells][S][RT][64][4]
+// fp32.
 
 static size_t skinny_ws_layout(uint32_t n, uint32_t m, const SkinnyCfg& c, size_t* ss_off, size_t* part_off) {
   if (c.s <= 1) return 0;
@@ -1008,7 +1164,15 @@ static bool pick_stream(uint32_t fmt, uint32_t n, uint32_t m, uint32_t k, Stream
 
 size_t matmul_ws_bytes(uint32_t n, uint32_t m, uint32_t k) {
   matmul_init();
-  if (n == 0 || !use_skinny(n, m, k)) return 0;
+  if (n == 0) return 0;
+  if (!use_skinny(n, m, k)) {
+    size_t a, b, need = 0;
+    if (k % GKC) return 0;
+    for (uint32_t fmt : {(uint32_t)SV_FMT_I8, (uint32_t)SV_FMT_BF16})
+      for (bool grouped : {false, true})
+        if (fmt == SV_FMT_I8 || !grouped) need = std::max(need, gemm_ws_layout(n, m, pick_gemm(fmt, grouped, n, m, k), &a, &b));
+    return need;
+  }
   size_t a, b;
   size_t need = std::max(skinny_ws_layout(n, m, pick_skinny(SV_FMT_I8, n, m, k), &a, &b),
                          skinny_ws_layout(n, m, pick_skinny(SV_FMT_BF16, n, m, k), &a, &b));
@@ -1136,7 +1300,7 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.part = p.ssp = nullptr;
   if (!skinny) {
     g_mm_variant = 2;
-    return gemm_launch(stream, fmt, p);
+    return gemm_launch(stream, fmt, p, ws, ws_bytes);
   }
   StreamCfg sc;
   const bool stream_ok = a->n <= 16 && g_skinny_tune.path != 1 && (per_row || a->gshift >= 8) &&

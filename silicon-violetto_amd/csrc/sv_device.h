@@ -43,16 +43,26 @@ __device__ __forceinline__ void split_bf(float x, float& hi, float& lo) {
   lo = x - hi;
 }
 
+// Two floats -> (hi, lo) bf16 pairs, one word each (element 0 in bits 0-15): hi = x rounded
+// to bf16 (RNE), lo = x - hi rounded, the same values as split_bf. gfx950's packed convert
+// (v_cvt_pk_bf16_f32) rounds two floats in one instruction: 3 VALU ops per element.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// Returns (hi word, lo word).
+__device__ __forceinline__ u32x2 split2(float a, float b) {
+  const uint32_t hw = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+  const float ra = a - __uint_as_float(hw << 16), rb = b - __uint_as_float(hw & 0xffff0000u);
+  return u32x2{hw, __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{ra, rb}), bf16x2))};
+}
+
 // Eight floats -> (hi, lo) bf16x8 operands.
 __device__ __forceinline__ void split8(const float* v, bf16x8& hi, bf16x8& lo) {
   u32x4 h, l;
 #pragma unroll
   for (int j = 0; j < 4; j++) {
-    float h0, l0, h1, l1;
-    split_bf(v[2 * j], h0, l0);
-    split_bf(v[2 * j + 1], h1, l1);
-    h[j] = (__float_as_uint(h0) >> 16) | (__float_as_uint(h1) & 0xffff0000u);
-    l[j] = pack_bf2(l0, l1);
+    const u32x2 w = split2(v[2 * j], v[2 * j + 1]);
+    h[j] = w[0];
+    l[j] = w[1];
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);

@@ -45,6 +45,12 @@ struct SkinnyTune {
 };
 // The variant of the last matmul launched on this process (1 skinny, 2 GEMM, 3 one-shot): tests.
 extern int g_mm_variant;
+// GEMM launch-shape override (row tiles per wave, token tiles, k splits, chunks in flight;
+// zero: built-in).
+struct GemmTune {
+  int rtw, nt, s, d;
+};
+extern GemmTune g_gemm_tune;
 extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave, splits)
 sv_status pack_matrix(hipStream_t stream, const sv_matrix* src, void* dst, sv_matrix* out);
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,

@@ -464,7 +464,7 @@ GEMM_CASES = [
     (16384, 2048, "i8", None),  # gate_up at 32 streams
     (2048, 8192, "i8", None),   # down
     (3072, 2048, "i8", 64),     # int8 groups of 64 (the reference's default)
-    (1280, 1280, "i8", 128),
+    (1280, 1280, "i8", 128),    # 20 chunks of 64 in 4 k splits: groups straddle splits
     (2048, 2048, "bf16", None),
 ]
 
@@ -508,6 +508,59 @@ def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
     close(y.cpu().numpy(), ref, atol=5e-5 * max(mag, 1.0), rtol=1e-4, what=f"gemm epi {epi}")
     if epi in (L.EPI_NORM, L.EPI_RESID):
         close(aux.cpu().numpy(), aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")
+
+
+@pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
+                                                  (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4)])
+@pytest.mark.parametrize("n", [17, 100])
+def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
+    """Every GEMM launch shape (row tiles per wave, token tiles, k splits merged by the last
+    split to arrive, chunks in flight) gives the oracle's result: int8 with EPI_NORM (sums of
+    squares carried across splits, the inverse norm written once) and bf16 with EPI_RESID in
+    the tiled layout, with a row gather, ragged token blocks (17, 100 rows) and a k whose chunk
+    count leaves a partial round of zero chunks (k = 1280: 20 chunks); two calls share one
+    workspace. The shape is forced through the library's internal override."""
+    banner(f"gemm launch shape rtw={rtw} nt={nt} splits={splits} depth={depth} n={n}")
+    tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv11g_gemm_tuneE")
+    rng = np.random.default_rng(rtw * 1000 + nt * 100 + splits * 10 + depth + n)
+    m, k = 384 if rtw == 1 else 512, 1280
+    ws = K.Workspace(16 << 20)
+    try:
+        tune[0], tune[1], tune[2], tune[3] = rtw, nt, splits, depth
+        w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+        q, s = quantize_rows(w)
+        mi8 = K.matrix(q.cuda(), s.cuda(), 31)
+        wb = bf16_bits(w.numpy())
+        mbf = K.matrix(u16_dev_bf16(wb)).tiled()
+        for call in range(2):
+            x = (rng.normal(0, 1, (n + 3, k)) * rng.uniform(0.5, 4, (n + 3, 1))).astype(np.float32)
+            rows = rng.permutation(n + 3)[:n].astype(np.uint32)
+            # int8, EPI_NORM, gathered rows
+            a = L.MatArgs(n, k, m, L.EPI_NORM, L.FLAG_WRITE_INV, m, 0.75, 0, 0, 1, k, 31)
+            aux_ref = np.zeros(n, np.float32)
+            ref = oracle.matmul(L, q.numpy(), s.view(torch.int16).numpy().view(np.uint16), 31, x, a, aux=aux_ref,
+                                x_rows=rows)
+            y = torch.zeros(n, m, device="cuda")
+            aux = torch.zeros(n, device="cuda")
+            K.matmul(mi8, to_dev(x), y, n=n, epi=L.EPI_NORM, flags=L.FLAG_WRITE_INV, scale=0.75, aux=aux,
+                     x_rows=to_dev(rows), ws=ws)
+            torch.cuda.synchronize()
+            assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 2, "GEMM kernel not launched"
+            close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
+                  what=f"int8 call {call}")
+            close(aux.cpu().numpy(), aux_ref, atol=1e-5, rtol=1e-4, what="inv")
+            # bf16 tiled, EPI_RESID
+            base = rng.normal(0, 1, (n, m)).astype(np.float32)
+            xr = x[:n].copy()
+            a = L.MatArgs(n, k, m, L.EPI_RESID, 0, m, 0.5, 1.1, 0.7, 1, k, 0)
+            ref = oracle.matmul(L, wb, None, 0, xr, a, base=base)
+            y = torch.zeros(n, m, device="cuda")
+            K.matmul(mbf, to_dev(xr), y, n=n, epi=L.EPI_RESID, scale=0.5, ra=1.1, rb=0.7, base=to_dev(base), ws=ws)
+            torch.cuda.synchronize()
+            close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
+                  what=f"bf16 call {call}")
+    finally:
+        tune[0] = tune[1] = tune[2] = tune[3] = 0
 
 
 def test_matmul_skinny_groups_of_256(gpu):
