@@ -47,9 +47,12 @@ def kv_bytes_per_token(shape) -> int:
 
 
 def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperature: float, shuffle: bool,
-                 steps: int, warmup: int, profile_reps: int, seed: int):
+                 steps: int, warmup: int, profile_reps: int, seed: int, int8: bool = True, tree: bool = False):
     """Build the engine state for `streams` sequences, record their trace, time `steps`
-    graph-replayed verify steps. Returns a dict of results (and the engine for reuse)."""
+    graph-replayed verify steps. Returns a dict of results (and the engine for reuse).
+
+    tree: each stream verifies the fixed 16-node draft tree TREE_PARENTS every step (node ids
+    random, drawn once; no replay drafter, no trace): the configs[4] workload."""
     import numpy as np
     import torch
 
@@ -58,7 +61,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     from violetto.model import rope_freq
 
     k = args.draft
-    rows = k + 1
+    rows = 16 if tree else k + 1
     n_steps = warmup + steps + profile_reps + 4
     trace_n = rows * n_steps + 32
     max_ctx = max(ctxs)
@@ -68,7 +71,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     freq = rope_freq(500000.0, shape.head_dim)
     eng = violetto.Engine(shape, max_seqs=streams, max_step_tokens=max(16, streams * rows),
                           max_seq_len=max_seq_len, max_head_rows=max(16, streams * rows), kv_tokens=kv_tokens,
-                          page_shift=4, attn_scale=0.125, freq=freq)
+                          page_shift=4, attn_scale=0.125, freq=freq, split_keys=args.split_keys)
     eng.set_model(model)
     rng = np.random.default_rng(seed)
     slots = [eng.new_seq() for _ in range(streams)]
@@ -95,36 +98,61 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     torch.cuda.synchronize()
     first = [int(x) for x in rng.integers(0, shape.vocab_real, streams)]
 
-    # The target's own continuation: plain decode, one row per stream and step.
-    log(f"{streams} stream(s): recording a {trace_n}-token trace per stream")
-    for s, c, t in zip(slots, ctxs, first):
-        eng.set_feed(s, c, t)
-    eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=trace_n + 8)
-    eng.graph_capture(0)
-    feed = eng.view("d_feed", (streams, 16))
-    traces = [[t] for t in first]
-    for _ in range(trace_n):
-        eng.graph_replay(1)
-        eng.sync()
-        col = feed[:, 0].cpu().tolist()
+    traces = None
+    if tree:
+        # The tree (parent, depth, ancestry mask per node: kernels.metal:64-72) and random node ids
+        # as GPU-fed rows; accept leaves them in place (no replay drafter), so every step verifies
+        # the same tree after the stream's newest token.
+        depth = [0] * 16
+        sees = [1] * 16
+        for i in range(1, 16):
+            depth[i] = depth[TREE_PARENTS[i]] + 1
+            sees[i] = sees[TREE_PARENTS[i]] | (1 << i)
+        nodes = np.array([depth[i] | ((0xFF if TREE_PARENTS[i] is None else TREE_PARENTS[i]) << 8) | (sees[i] << 16)
+                          for i in range(16)], np.uint32)
+        d_tree = eng.view("d_tree", (streams, 16))
+        d_feed = eng.view("d_feed", (streams, 16))
+        for s, c, t in zip(slots, ctxs, first):
+            eng.set_feed(s, c, t)
+            ids = np.concatenate([[t], rng.integers(0, shape.vocab_real, 15)]).astype(np.uint32)
+            d_feed[s].copy_(torch.from_numpy(ids.view(np.int32)))
+            d_tree[s].copy_(torch.from_numpy(nodes.view(np.int32)))
+        torch.cuda.synchronize()
+        info = eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots],
+                        extra_keys=rows * n_steps + 8)
+        eng.graph_capture(0)
+        feed = d_feed
+    else:
+        # The target's own continuation: plain decode, one row per stream and step.
+        log(f"{streams} stream(s): recording a {trace_n}-token trace per stream")
+        for s, c, t in zip(slots, ctxs, first):
+            eng.set_feed(s, c, t)
+        eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=trace_n + 8)
+        eng.graph_capture(0)
+        feed = eng.view("d_feed", (streams, 16))
+        traces = [[t] for t in first]
+        for _ in range(trace_n):
+            eng.graph_replay(1)
+            eng.sync()
+            col = feed[:, 0].cpu().tolist()
+            for i, s in enumerate(slots):
+                traces[i].append(int(col[s]))
+        tr = eng.view("d_trace", (streams, max_seq_len))
+        tr.zero_()
         for i, s in enumerate(slots):
-            traces[i].append(int(col[s]))
-    tr = eng.view("d_trace", (streams, max_seq_len))
-    tr.zero_()
-    for i, s in enumerate(slots):
-        tr[s, ctxs[i]:ctxs[i] + len(traces[i])] = torch.tensor(traces[i], dtype=torch.int32, device="cuda")
-    tl = eng.view("d_trace_len", (streams,))
-    for i, s in enumerate(slots):
-        tl[s] = ctxs[i] + len(traces[i])
-    torch.cuda.synchronize()
+            tr[s, ctxs[i]:ctxs[i] + len(traces[i])] = torch.tensor(traces[i], dtype=torch.int32, device="cuda")
+        tl = eng.view("d_trace_len", (streams,))
+        for i, s in enumerate(slots):
+            tl[s] = ctxs[i] + len(traces[i])
+        torch.cuda.synchronize()
 
-    # Verify steps: [input, d1..dk] per stream from the GPU-fed rows; accept; replay drafts.
-    for s, c, t in zip(slots, ctxs, first):
-        eng.set_feed(s, c, t)
-    eng.set_replay(seed + 7, args.mistake_rate)
-    info = eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots],
-                    extra_keys=rows * n_steps + 8)
-    eng.graph_capture(L.STEP_REPLAY)
+        # Verify steps: [input, d1..dk] per stream from the GPU-fed rows; accept; replay drafts.
+        for s, c, t in zip(slots, ctxs, first):
+            eng.set_feed(s, c, t)
+        eng.set_replay(seed + 7, args.mistake_rate)
+        info = eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots],
+                        extra_keys=rows * n_steps + 8)
+        eng.graph_capture(L.STEP_REPLAY)
     lens = eng.view("d_lens", (streams,))
     eng.graph_replay(warmup)
     eng.sync()
@@ -142,7 +170,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     secs = t_b - t_a
     ms_step = secs / steps * 1e3
     fed = feed[:, 0].cpu().tolist()
-    lossless = all(int(fed[s]) == traces[i][int(len1[s]) - ctxs[i]] for i, s in enumerate(slots))
+    lossless = None if tree else all(int(fed[s]) == traces[i][int(len1[s]) - ctxs[i]] for i, s in enumerate(slots))
     log(f"{emitted} tokens in {steps} steps ({emitted / steps:.2f}/step), {ms_step:.4f} ms/step, "
         f"{emitted / secs:.0f} tok/s, traces reproduced: {lossless}")
 
@@ -151,17 +179,35 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     ctx_mid = float(((len0 + len1) / 2).sum())
     H, F, V = shape.hidden, shape.ffn, shape.vocab
     n_rows = streams * rows
-    mat_bytes = {"qkv": shape.qkv_width * H + 2 * shape.qkv_width, "o": H * H + 2 * H,
-                 "gate_up": 2 * F * H + 2 * 2 * F, "down": H * F + 2 * H, "head": V * H * 2}
+    def wbytes(m, kk):  # int8 + one bf16 scale per row, or bf16
+        return m * kk + 2 * m if int8 else 2 * m * kk
+
+    mat_bytes = {"qkv": wbytes(shape.qkv_width, H), "o": wbytes(H, H), "gate_up": wbytes(2 * F, H),
+                 "down": wbytes(H, F), "head": V * H * 2}
     attn_bytes = ctx_mid * kv_bytes_per_token(shape) / shape.n_layers + n_rows * 2 * shape.n_kv_heads * \
         shape.head_dim * 2
-    step_bytes = shape.weight_bytes(int8=True) + shape.n_layers * attn_bytes + n_rows * H * 2
-    flops = 2 * n_rows * (shape.n_layers * sum(v for kk, v in mat_bytes.items() if kk != "head") + V * H)
+    step_bytes = shape.weight_bytes(int8=int8) + shape.n_layers * attn_bytes + n_rows * H * 2
+    mat_elems = {"qkv": shape.qkv_width * H, "o": H * H, "gate_up": 2 * F * H, "down": H * F}
+    flops = 2 * n_rows * (shape.n_layers * sum(mat_elems.values()) + V * H)
     res = dict(eng=eng, kd=kd, vd=vd, traces=traces, ctxs=ctxs, slots=slots, steps=steps, warmup=warmup,
                emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless, prof=prof,
                per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
                flops=flops, info=info, rows=rows)
     return res
+
+
+# configs[4]'s 16-node tree: root 0; children 1-4; two children under each (5-12); one leaf
+# under each of 5, 6, 7 (13-15). The config's 1 + 4 + 8 + 8 = 21 nodes exceed the reference's
+# 16 fed rows per run, so the last level keeps three leaves.
+TREE_PARENTS = [None, 0, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 6, 7]
+
+
+def extra_object(res, workload, rows, reps):
+    return {"value": round(res["value"], 2), "unit": "verified tok/s", "ms_per_step": round(res["ms_step"], 5),
+            "steps": res["steps"], "emitted_per_step": round(res["emitted"] / res["steps"], 3),
+            "lossless_trace_check": res["lossless"], "config": {"workload": workload, "rows_per_step": rows},
+            "roofline": roofline_of(res, reps), "step_roofline": step_roofline(res),
+            "kernel_ms_per_step": {kk: round(v, 4) for kk, v in res["per_step_ms"].items()}}
 
 
 def roofline_of(res, profile_reps, workload=None):
@@ -210,7 +256,11 @@ def main() -> int:
     ap.add_argument("--profile-reps", type=int, default=5, help="steps timed per kernel with hipEvents")
     ap.add_argument("--cpu-steps", type=int, default=2, help="oracle steps for the CPU baseline (0: skip)")
     ap.add_argument("--streams32-steps", type=int, default=30, help="timed steps of configs[2] (0: skip)")
+    ap.add_argument("--long-steps", type=int, default=20,
+                    help="timed steps of configs[3] (bf16 weights, 65536 ctx, 1 and 8 streams; 0: skip)")
+    ap.add_argument("--tree-steps", type=int, default=20, help="timed steps of configs[4] (16-node trees x 32; 0: skip)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--split-keys", type=int, default=0, help="attention keys per split (0: the engine's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with 4 elementwise passes over 256 MiB (the known-size kernel that scales "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE into bytes)")
@@ -256,6 +306,33 @@ def main() -> int:
                "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r2["per_step_ms"].items()}}
         r2["eng"].close()
 
+    s64 = None
+    if args.tree_steps > 0:
+        r4 = run_workload(args, model, shape, streams=32, ctxs=[4096] * 32, temperature=0.7, shuffle=True,
+                          steps=args.tree_steps, warmup=3, profile_reps=2, seed=args.seed + 4, tree=True)
+        log("trees, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r4["per_step_ms"].items()))
+        s64 = extra_object(r4, "configs[4]: 32 streams x 16-node draft tree (random node ids), 4096 ctx, T=0.7 "
+                               "Philox-seeded sample-and-match, accepted path compacted", 32 * 16, 2)
+        r4["eng"].close()
+    del model
+    torch.cuda.empty_cache()
+    long_ctx = None
+    if args.long_steps > 0:
+        log(f"generating the 16-layer bf16 model on the GPU (seed {args.seed})")
+        model16 = SyntheticModel.generate(shape, int8=False, seed=args.seed, device="cuda")
+        long_ctx = {}
+        for streams in (1, 8):
+            r3 = run_workload(args, model16, shape, streams=streams, ctxs=[65536] * streams, temperature=0.0,
+                              shuffle=False, steps=args.long_steps, warmup=3, profile_reps=2, seed=args.seed + 3,
+                              int8=False)
+            log(f"65536 ctx x {streams}, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r3["per_step_ms"].items()))
+            long_ctx[f"streams{streams}"] = extra_object(
+                r3, f"configs[3]: bf16 weights, {streams} stream(s) x 65536 ctx, k=4 chain, greedy, KV rollback",
+                streams * r3["rows"], 2)
+            r3["eng"].close()
+            torch.cuda.empty_cache()
+        del model16
+
     line = {
         "metric": METRIC,
         "value": round(r1["value"], 2),
@@ -279,6 +356,8 @@ def main() -> int:
         "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r1["per_step_ms"].items()},
         "cpu_baseline": cpu,
         "streams32": s32,
+        "long_ctx_bf16": long_ctx,
+        "trees32": s64,
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy:

@@ -958,33 +958,31 @@ GemmTune g_gemm_tune;  // all zero: the built-in choice
 
 // Built-in choice, from measurements on MI355X at 40, 160 and 512 rows (qkv, o, gate_up, down
 // int8, the bf16 head): int8 runs 32-token blocks (NT = 2) with two row tiles per wave and two
-// k splits, four when that leaves fewer than 256 workgroups, and one row tile per wave when
-// even four splits leave fewer; bf16 (twice the weight bytes per row) runs the token block with
-// the fewest padded tokens among NT = 3, 5 and 8, unsplit. Scale groups shorter than k: one
-// row tile per wave.
+// k splits, four when that leaves fewer than 256 workgroups; bf16 (twice the weight bytes per
+// row) runs the token block with the fewest padded tokens among NT = 3 and 5 and the fewest
+// k splits (up to 8) that give 256 workgroups. Either way one row tile per wave when the
+// splits alone cannot reach 256 workgroups, and with int8 scale groups shorter than k.
 static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uint32_t k) {
   if (g_gemm_tune.rtw)
     return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
   const uint32_t nch = k / GKC;
-  auto splits_ok = [&](int s) { return nch % s == 0 && nch / s >= 4; };
-  if (fmt != SV_FMT_I8) {
-    GemmCfg c{2, 5, 1, 4};
+  const bool i8 = fmt == SV_FMT_I8;
+  GemmCfg c{2, 2, 1, 4};
+  if (!i8) {
     uint32_t best = ~0u;
-    for (int nt : {3, 5, 8}) {
+    for (int nt : {3, 5}) {
       const uint32_t pad = (n + 16 * nt - 1) / (16 * nt) * 16 * nt - n;
       if (pad < best || (pad == best && nt == 5)) best = pad, c.nt = nt;
     }
-    if (m % 128 || c.nt == 8) c.rtw = 1;
-    return c;
   }
-  const uint32_t n_tblk = (n + 31) / 32;
-  GemmCfg c{grouped ? 1 : 2, 2, 1, 4};
-  if (m % (64 * c.rtw)) c.rtw = 1;
-  for (int pass = 0; pass < 2; pass++) {
+  if (grouped || m % 128) c.rtw = 1;
+  const uint32_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt);
+  const int s_first = i8 ? 2 : 1, s_last = i8 ? 4 : 8;
+  for (;;) {
     const uint32_t cells = m / (64 * c.rtw) * n_tblk;
     c.s = 1;
-    for (int s : {2, 4})
-      if (splits_ok(s)) {
+    for (int s = s_first; s <= s_last; s *= 2)
+      if (nch % s == 0 && nch / s >= 4) {
         c.s = s;
         if (cells * s >= 256) break;
       }
