@@ -134,7 +134,7 @@ typedef struct sv_kv_args {
 } sv_kv_args;
 
 /* AttnArgs (kernels.rs:72-83, kernels.metal:813-823). Used here: split (cached keys per
- * split, a multiple of 32), max_splits (grid size, at least the most splits any run needs,
+ * split, a multiple of 32, at most 3968), max_splits (grid size, at least the most splits any run needs,
  * counting the split of its new keys), scale_log2 (softmax scale * log2 e), rope. ve,
  * capture, fixed_splits, col_sets and one_round are ignored. */
 typedef struct sv_attn_args {

@@ -70,6 +70,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   const uint32_t kbeg = s * p.split;
   const bool ahead = p.n_inline && (uint32_t)wv * 32 < p.split;
   if (ahead) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kbeg + p.split, kbeg + p.split, nullptr, nullptr, cur, lane);
+  // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
+  // 2 i + mt), requested now with the split taken as full (kv_off clamps into the table; tiles
+  // past the context are masked later): the batch loop takes its tile offsets with readlane
+  // and never waits for a page-table load (such a wait, vmcnt(0), also waits for every K/V
+  // load in flight).
+  // (split <= 3968 keys: at most 31 batches per wave, 62 lanes)
+  const uint32_t nbw_full = p.split / 32 > (uint32_t)wv ? (p.split / 32 - wv + 3) / 4 : 0u;
+  size_t tile_off = 0;
+  if ((uint32_t)lane < 2 * nbw_full)
+    tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
   const uint32_t p0 = p.meta[2 * t0 + 1];
   const uint32_t ncols = T * p.G;
   bf16x8 qh[NCT][KST], ql[NCT][KST];
@@ -113,7 +123,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   } else {
     for (uint32_t b = wv; b < nb; b += 4) {
       KvBatch<D> nxt;
-      if (b + 4 < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * (b + 4), kend, p0, nullptr, nullptr, nxt, lane);
+      // unconditional: past the last batch the keys clamp to kend - 1 (read, never used)
+      const int li = (int)min(2 * ((b + 4 - wv) / 4), 62u);
+      const size_t toffs[2] = {readlane64(tile_off, li), readlane64(tile_off, li + 1)};
+      load_batch<D, false>(p, seq, g, kbeg + 32 * (b + 4), kend, p0, nullptr, nullptr, nxt, lane, toffs);
+      __builtin_amdgcn_sched_barrier(0);  // the next batch's loads go out before this batch's work
       compute_batch<D, NCT, false>(p, cur, kbeg + 32 * b, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
       cur = nxt;
     }
@@ -264,31 +278,6 @@ static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
   return (cols + 15) / 16 * 16;
 }
 
-// Workgroups of attn_verify_kernel that the device holds at once for this shape (its
-// occupancy per CU x CUs); 0 if the variant is not built.
-uint32_t attn_resident_wgs(const sv_shape* sh, uint32_t max_run) {
-  if (!sh || sh->n_kv_heads == 0 || max_run == 0 || max_run > SV_MAX_RUN) return 0;
-  const uint32_t D = sh->head_dim, nct = cols_pad(sh, max_run) / 16;
-  if ((D != 64 && D != 128) || nct > 4) return 0;
-  attn_init();
-  const void* fn = nullptr;
-  if (D == 64) {
-    const void* f[4] = {(const void*)attn_verify_kernel<64, 1>, (const void*)attn_verify_kernel<64, 2>,
-                        (const void*)attn_verify_kernel<64, 3>, (const void*)attn_verify_kernel<64, 4>};
-    fn = f[nct - 1];
-  } else {
-    const void* f[4] = {(const void*)attn_verify_kernel<128, 1>, (const void*)attn_verify_kernel<128, 2>,
-                        (const void*)attn_verify_kernel<128, 3>, (const void*)attn_verify_kernel<128, 4>};
-    fn = f[nct - 1];
-  }
-  const size_t shm = (size_t)4 * nct * 16 * D * 4 + (size_t)4 * nct * 16 * 4;
-  int per_cu = 0, dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, shm) != hipSuccess)
-    return 0;
-  return (uint32_t)(per_cu * cus);
-}
-
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run) {
   const size_t maxcols = cols_pad(sh, max_run);
   size_t b = ((size_t)n_runs * sh->n_kv_heads * 4 + 255) / 256 * 256;
@@ -312,7 +301,8 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (!kv->is_global) return fail(SV_ERR_UNSUPPORTED, "attn_verify: local (ring) layers are not built");
   if (kv->page_shift < 4 || kv->page_shift > 16)
     return fail(SV_ERR_UNSUPPORTED, "attn_verify: pages of 2^%u tokens (16..65536 are built)", kv->page_shift);
-  if (args->split == 0 || args->split % 32) return fail(SV_ERR_ARG, "attn_verify: split %u (multiple of 32)", args->split);
+  if (args->split == 0 || args->split % 32 || args->split > 3968)
+    return fail(SV_ERR_ARG, "attn_verify: split %u (a multiple of 32, at most 3968)", args->split);
   if (max_run == 0 || max_run > SV_MAX_RUN) return fail(SV_ERR_ARG, "attn_verify: max_run %u", max_run);
   if (!rope && args->rope) return fail(SV_ERR_ARG, "attn_verify: rope table missing");
   const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;

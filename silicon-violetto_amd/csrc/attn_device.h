@@ -55,6 +55,12 @@ __device__ __forceinline__ size_t kv_off(const AttnParams& p, uint32_t seq, uint
          (size_t)(pos & ((1u << p.page_shift) - 1u)) * D;
 }
 
+// Lane `l`'s 64-bit value, for a wave-uniform l.
+__device__ __forceinline__ size_t readlane64(size_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)v, l), hi = __builtin_amdgcn_readlane((uint32_t)(v >> 32), l);
+  return ((size_t)hi << 32) | lo;
+}
+
 template <int VE>
 struct VWord;
 template <>

@@ -129,28 +129,38 @@ thread_local ProfEvents g_prof;
 namespace {
 
 // Attention split sizes considered (keys per workgroup: multiples of 128, one 32-key batch
-// per wave and step of 128).
+// per wave and step of 128; at most 3968, the kernel's per-lane page-table prefetch).
 constexpr uint32_t MIN_SPLIT = 128;
-constexpr uint32_t MAX_SPLIT = 1024;
-// Cost model, in eighths of one 32-key batch per wave: a workgroup's fixed latency (launch,
-// page table, first loads, partial store) is about two batches, and the merge adds about an
-// eighth of a batch per split (fitted to measurements at 2k and 8k keys, 1 and 5 rows).
-constexpr uint64_t ATTN_WG_LATENCY = 16;
-constexpr uint64_t ATTN_BATCH = 8;
-constexpr uint64_t ATTN_MERGE_PER_SPLIT = 1;
+constexpr uint32_t MAX_SPLIT = 3968 / 128 * 128;
 
-// Keys per split (plan.rs:156-164 decode_splits, re-derived for this device): the grid is
-// max_splits x kv heads x runs; the split minimises dispatch rounds (grid / workgroups the
-// device holds at once) x per-workgroup cost + merge cost; ties go to the smaller split.
-uint32_t choose_split(uint32_t max_cached, uint32_t pairs, uint32_t resident) {
-  if (resident == 0) resident = 512;
+// Keys per split (plan.rs:156-164 decode_splits, re-derived for this device). The grid is
+// max_splits x kv heads x runs; a run's splits past its context exit at once, so the work is
+// the active workgroups: sum over runs of (its splits + the split of its new keys) x kv heads.
+// Time model, fitted to measurements on MI355X (1-32 streams, 4k-64k keys, 5- and 16-row
+// runs), in microseconds, with b = 32-key batches per wave (split / 128) and k = active
+// workgroups per compute unit (rounded up):
+//   one workgroup per compute unit: its dependent-load chain, 9.7 + 1.2 b;
+//   more: they share the unit's throughput, k (F + 1.05 b), F = 5.3 (<= 32 columns per kv
+//   head) or 19 (more: 4x the query, reduction and partial traffic per workgroup).
+// The larger of the two; ties go to the smaller split. Contexts are counted at the plan's
+// furthest replay (cached + extra keys).
+uint32_t choose_split(const std::vector<uint32_t>& cached, uint32_t extra, uint32_t nkv, uint32_t max_run,
+                      uint32_t group) {
+  static const uint32_t cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return 256u;
+    return (uint32_t)n;
+  }();
+  const double F = max_run * group <= 32 ? 5.3 : 19.0;
   uint32_t best = MIN_SPLIT;
-  uint64_t best_cost = ~0ull;
+  double best_t = 1e300;
   for (uint32_t split = MIN_SPLIT; split <= MAX_SPLIT; split += 128) {
-    const uint64_t splits = (max_cached + split - 1) / split + 1;
-    const uint64_t rounds = (splits * pairs + resident - 1) / resident;
-    const uint64_t cost = rounds * (ATTN_WG_LATENCY + ATTN_BATCH * (split / 128)) + ATTN_MERGE_PER_SPLIT * splits;
-    if (cost < best_cost) best_cost = cost, best = split;
+    uint64_t active = 0;
+    for (uint32_t c : cached) active += ((uint64_t)(c + extra + split - 1) / split + 1) * nkv;
+    const double k = (double)((active + cus - 1) / cus), b = split / 128;
+    const double t = std::max(9.7 + 1.2 * b, k * (F + 1.05 * b));
+    if (t < best_t) best_t = t, best = split;
   }
   return best;
 }
@@ -490,7 +500,8 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
       cfg->kv_tokens == 0)
     return fail(SV_ERR_ARG, "engine_create: zero capacity");
   if (cfg->page_shift < 4 || cfg->page_shift > 16) return fail(SV_ERR_ARG, "engine_create: page_shift %u", cfg->page_shift);
-  if (cfg->split_keys % 32) return fail(SV_ERR_ARG, "engine_create: split_keys %u", cfg->split_keys);
+  if (cfg->split_keys % 32 || cfg->split_keys > 3968)
+    return fail(SV_ERR_ARG, "engine_create: split_keys %u (a multiple of 32, at most 3968)", cfg->split_keys);
   attn_init();
   matmul_init();
   sv_engine* e = new sv_engine();
@@ -825,6 +836,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   std::vector<sv_run_in> run_in;
   Plan P;
   uint32_t max_cached = 0;
+  std::vector<uint32_t> run_cached;
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const sv_run& r = runs_in[ri];
     SV_TRY(check_slot(e, r.slot));
@@ -870,6 +882,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     attn_runs.push_back(first_row);
     attn_runs.push_back(count);
     max_cached = std::max(max_cached, e->seq_len[slot]);
+    run_cached.push_back(e->seq_len[slot]);
     P.max_run = std::max(P.max_run, count);
     P.branches |= (r.verify && count > 2) ? 1u : 0u;
     P.slots.push_back(slot);
@@ -887,7 +900,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   // own for the new keys; `extra_keys` sizes the grid for replays at later positions.
   uint32_t split = e->cfg.split_keys;
   if (split == 0)
-    split = choose_split(max_cached + extra_keys, n_runs * e->sh.n_kv_heads, attn_resident_wgs(&e->sh, P.max_run));
+    split = choose_split(run_cached, extra_keys, e->sh.n_kv_heads, P.max_run, e->sh.n_heads / e->sh.n_kv_heads);
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
   SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, n_runs, P.max_splits, P.max_run)));

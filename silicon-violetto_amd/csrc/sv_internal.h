@@ -58,7 +58,6 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
 
 void attn_init();
 void matmul_init();  // kernel attributes; call outside stream capture
-uint32_t attn_resident_wgs(const sv_shape* sh, uint32_t max_run);
 size_t attn_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
 sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
