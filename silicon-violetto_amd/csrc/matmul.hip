@@ -713,8 +713,11 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;  // dwordx4 per lane per row tile per chunk
   constexpr int PAIRS = BN * 8;                 // (token, 8-k group) pairs per chunk
   constexpr int PPT = (PAIRS + 255) / 256;      // pairs per thread
-  // LDS: [2 buffers][NT][2 k-steps][hi, lo][64 lanes] of 16 bytes.
-  __shared__ u32x4 xs[2][NT][2][2][64];
+  // LDS: [2 buffers][NT][2 k-steps x (hi, lo)][80 slots] of 16 bytes; lane (t, q) of k-step
+  // ks reads slot t + 16 q + 2 (2 q + ks): each quarter-wave reads 16 consecutive slots, and
+  // the writers (8 lanes per token, k groups g = 2 q + ks) land on 16 different bank groups per
+  // 16 lanes (unpadded, the 8 lanes of a token shared 4 banks: an 8-way conflict).
+  __shared__ u32x4 xs[2][NT][4][80];
   __shared__ float ssp[BN][8];
   __shared__ uint32_t last_flag;
   const int tid = threadIdx.x, lane = tid & 63, t16 = lane & 15, q = lane >> 4;
@@ -787,9 +790,9 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       bf16x8 h, l;
       split8(v, h, l);
       const int tok = i / 8, g8 = i % 8, qq = g8 >> 1, ks = g8 & 1;
-      const int ln = (tok & 15) + 16 * qq;
-      xs[buf][tok >> 4][ks][0][ln] = __builtin_bit_cast(u32x4, h);
-      xs[buf][tok >> 4][ks][1][ln] = __builtin_bit_cast(u32x4, l);
+      const int slot = (tok & 15) + 16 * qq + 2 * g8;
+      xs[buf][tok >> 4][2 * ks][slot] = __builtin_bit_cast(u32x4, h);
+      xs[buf][tok >> 4][2 * ks + 1][slot] = __builtin_bit_cast(u32x4, l);
     }
   };
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
@@ -842,8 +845,9 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
         }
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-          const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][ks][0][lane]);
-          const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][ks][1][lane]);
+          const int slot = lane + 2 * (2 * q + ks);
+          const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][2 * ks][slot]);
+          const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][2 * ks + 1][slot]);
 #pragma unroll
           for (int r = 0; r < RTW; r++) {
             f32x4& g = GROUPED ? grp[GROUPED ? r : 0][GROUPED ? n : 0] : acc[r][n];
