@@ -639,6 +639,9 @@ __global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* src, uin
 //   - k splits: each split stores its sums (coherent stores) and the last split of the
 //     (row block, token block) to arrive adds them in split order and runs the epilogue.
 constexpr int GKC = 64;
+#ifndef SV_GEMM_ABLATE
+#define SV_GEMM_ABLATE 0  // probe builds: 1 X split, 2 weight conversion, 3 MFMA, 4 barrier left out
+#endif
 // Split-k hand-off counters (skinny and GEMM paths): a region of fixed size at the front of the
 // workspace, so every matmul sharing one workspace finds its counters at zero there, whatever
 // its shape.
@@ -788,7 +791,12 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
       for (int e = 0; e < 8; e++) ssacc[j] = __builtin_fmaf(v[e], v[e], ssacc[j]);
       bf16x8 h, l;
+#if SV_GEMM_ABLATE == 1
+      h = __builtin_bit_cast(bf16x8, xr[j][0]);
+      l = __builtin_bit_cast(bf16x8, xr[j][1]);
+#else
       split8(v, h, l);
+#endif
       const int tok = i / 8, g8 = i % 8, qq = g8 >> 1, ks = g8 & 1;
       const int slot = (tok & 15) + 16 * qq + 2 * g8;
       xs[buf][tok >> 4][2 * ks][slot] = __builtin_bit_cast(u32x4, h);
@@ -840,7 +848,11 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
         bf16x8 a[RTW];
 #pragma unroll
         for (int r = 0; r < RTW; r++) {
+#if SV_GEMM_ABLATE == 2
+          if (FMT == SV_FMT_I8) a[r] = __builtin_bit_cast(bf16x8, cur[r][0] ^ (uint32_t)ks);
+#else
           if (FMT == SV_FMT_I8) a[r] = i8x8_to_bf(cur[r][0][2 * ks], cur[r][0][2 * ks + 1]);
+#endif
           else a[r] = __builtin_bit_cast(bf16x8, cur[r][ks]);
         }
 #pragma unroll
@@ -851,8 +863,12 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
           for (int r = 0; r < RTW; r++) {
             f32x4& g = GROUPED ? grp[GROUPED ? r : 0][GROUPED ? n : 0] : acc[r][n];
+#if SV_GEMM_ABLATE == 3
+            g += __builtin_bit_cast(f32x4, a[r]) + __builtin_bit_cast(f32x4, bh) + __builtin_bit_cast(f32x4, bl);
+#else
             g = mfma16(a[r], bh, g);
             g = mfma16(a[r], bl, g);
+#endif
           }
         }
       }
@@ -877,7 +893,9 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       const int dn = (d + 1) % GD;
       store_x(buf ^ 1, xr[dn]);
       load_x(c + 1 + GD, xr[dn]);
+#if SV_GEMM_ABLATE != 4
       lds_barrier();
+#endif
     }
   }
   if (!GROUPED && FMT == SV_FMT_I8) {
@@ -965,12 +983,17 @@ GemmTune g_gemm_tune;  // all zero: the built-in choice
 // k splits, four when that leaves fewer than 256 workgroups; bf16 (twice the weight bytes per
 // row) runs the token block with the fewest padded tokens among NT = 3 and 5 and the fewest
 // k splits (up to 8) that give 256 workgroups. Either way one row tile per wave when the
-// splits alone cannot reach 256 workgroups, and with int8 scale groups shorter than k.
+// splits alone cannot reach 256 workgroups, and with int8 scale groups shorter than k. At 384
+// rows and more, matrices with 512 blocks of 256 rows x 64 tokens run those (four row tiles
+// per wave), unsplit.
 static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uint32_t k) {
   if (g_gemm_tune.rtw)
     return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
   const uint32_t nch = k / GKC;
   const bool i8 = fmt == SV_FMT_I8;
+  // Wide matrices at many rows: 256-row x 64-token blocks halve the operand traffic through
+  // L2 (weights re-read per token block, X per row block) where they still fill the device.
+  if (!grouped && n >= 384 && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 63) / 64) >= 512) return GemmCfg{4, 4, 1, 4};
   GemmCfg c{2, 2, 1, 4};
   if (!i8) {
     uint32_t best = ~0u;
@@ -1009,7 +1032,7 @@ static size_t gemm_ws_layout(uint32_t n, uint32_t m, const GemmCfg& c, size_t* s
 
 static bool gemm_shape_ok(uint32_t m, uint32_t k, const GemmCfg& c) {
   const bool nt_ok = c.nt == 2 || c.nt == 3 || c.nt == 4 || c.nt == 5 || c.nt == 8;
-  return nt_ok && (c.rtw == 1 || c.rtw == 2) && (c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
+  return nt_ok && (c.rtw == 1 || c.rtw == 2 || (c.rtw == 4 && c.nt <= 5)) && (c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
          (k / GKC) % c.s == 0;
 }
 
@@ -1026,7 +1049,7 @@ static void gemm_dispatch_nt(hipStream_t stream, const MMParams& p, int nt, int 
     case 3: gemm_launch_one<FMT, RTW, 3, GR>(stream, p, d, nwg, n_tblk); break;
     case 4: gemm_launch_one<FMT, RTW, 4, GR>(stream, p, d, nwg, n_tblk); break;
     case 5: gemm_launch_one<FMT, RTW, 5, GR>(stream, p, d, nwg, n_tblk); break;
-    default: gemm_launch_one<FMT, RTW, 8, GR>(stream, p, d, nwg, n_tblk); break;
+    default: gemm_launch_one<FMT, RTW, (RTW == 4 ? 5 : 8), GR>(stream, p, d, nwg, n_tblk); break;
   }
 }
 
@@ -1053,10 +1076,12 @@ static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, MMParams& p, void
   const uint32_t nwg = rb * n_tblk * c.s;
   if (fmt == SV_FMT_I8) {
     if (grouped) gemm_dispatch_nt<SV_FMT_I8, 1, true>(stream, p, c.nt, c.d, nwg, n_tblk);
+    else if (c.rtw == 4) gemm_dispatch_nt<SV_FMT_I8, 4, false>(stream, p, c.nt, c.d, nwg, n_tblk);
     else if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_I8, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);
     else gemm_dispatch_nt<SV_FMT_I8, 1, false>(stream, p, c.nt, c.d, nwg, n_tblk);
   } else {
-    if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_BF16, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);
+    if (c.rtw == 4) gemm_dispatch_nt<SV_FMT_BF16, 4, false>(stream, p, c.nt, c.d, nwg, n_tblk);
+    else if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_BF16, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);
     else gemm_dispatch_nt<SV_FMT_BF16, 1, false>(stream, p, c.nt, c.d, nwg, n_tblk);
   }
   return check_launch("matmul (gemm)");

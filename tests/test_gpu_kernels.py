@@ -511,7 +511,8 @@ def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
 
 
 @pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
-                                                  (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4)])
+                                                  (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4),
+                                                  (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4)])
 @pytest.mark.parametrize("n", [17, 100])
 def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
     """Every GEMM launch shape (row tiles per wave, token tiles, k splits merged by the last
@@ -523,7 +524,7 @@ def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
     banner(f"gemm launch shape rtw={rtw} nt={nt} splits={splits} depth={depth} n={n}")
     tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv11g_gemm_tuneE")
     rng = np.random.default_rng(rtw * 1000 + nt * 100 + splits * 10 + depth + n)
-    m, k = 384 if rtw == 1 else 512, 1280
+    m, k = {1: 384, 2: 512, 4: 768}[rtw], 1280
     ws = K.Workspace(16 << 20)
     try:
         tune[0], tune[1], tune[2], tune[3] = rtw, nt, splits, depth
