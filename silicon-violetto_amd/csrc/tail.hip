@@ -116,10 +116,24 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const
   const uint32_t pos = row.tok == SV_NO_TOK ? row.pos : meta[2 * row.tok + 1] + 1;
   const float* x = logits + (size_t)r * vocab;
 
+  // The first SAMPLE_CACHED logits of this thread (ids tid, tid + 1024, ...) are requested
+  // together and kept in registers (one memory round trip, and the temperature pass below
+  // reuses them); ids past that are read in the loop.
+  constexpr int SAMPLE_CACHED = 32;
+  float xc[SAMPLE_CACHED];
+#pragma unroll
+  for (int j = 0; j < SAMPLE_CACHED; j++) {
+    const uint32_t i = tid + j * SV_SAMPLE_THREADS;
+    xc[j] = i < vocab ? x[i] : 0.0f;
+  }
   float lmax = -3.402823466e+38f;
   uint32_t tok = 0xffffffffu;
-#pragma unroll 8
-  for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) better(lmax, tok, x[i], i);
+#pragma unroll
+  for (int j = 0; j < SAMPLE_CACHED; j++) {
+    const uint32_t i = tid + j * SV_SAMPLE_THREADS;
+    if (i < vocab) better(lmax, tok, xc[j], i);
+  }
+  for (uint32_t i = tid + SAMPLE_CACHED * SV_SAMPLE_THREADS; i < vocab; i += SV_SAMPLE_THREADS) better(lmax, tok, x[i], i);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const float v = __shfl_xor(lmax, o, WAVE);
@@ -138,8 +152,13 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const
   if (row.temperature > 0.0f) {
     const float c = LOG2E_F / row.temperature;
     float s = 0.0f;
-#pragma unroll 8
-    for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) s += sv_exp2((x[i] - lmax) * c);
+#pragma unroll
+    for (int j = 0; j < SAMPLE_CACHED; j++) {
+      const uint32_t i = tid + j * SV_SAMPLE_THREADS;
+      if (i < vocab) s += sv_exp2((xc[j] - lmax) * c);
+    }
+    for (uint32_t i = tid + SAMPLE_CACHED * SV_SAMPLE_THREADS; i < vocab; i += SV_SAMPLE_THREADS)
+      s += sv_exp2((x[i] - lmax) * c);
     scan1024(s, ex, base, tid);
     const float z = ex[SV_SAMPLE_THREADS];
     float low = -__builtin_inff();
