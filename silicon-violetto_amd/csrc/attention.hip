@@ -58,28 +58,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
     T = p.runs[2 * r + 1];
     seq = p.meta[2 * t0];
   }
-  // With the run known up front (the engine's plan), this wave's first batch of the split's
-  // keys is requested before the context length (meta) arrives: the split is taken as full
-  // (kv_off clamps positions to the table and the pool) and keys past the context are masked
-  // by compute_batch's kend. Without it, the batch waits for meta. Either way it is in
-  // flight while the queries are built. The run's visibility masks (for the newest split's
-  // masks) are requested first, into LDS.
+  // The run's visibility masks (for the newest split's masks) are requested first, into LDS.
   __shared__ uint32_t svis[SV_MAX_RUN];
   if (tid < T) svis[tid] = p.vis[t0 + tid];
   KvBatch<D> cur;
   const uint32_t kbeg = s * p.split;
-  const bool ahead = p.n_inline && (uint32_t)wv * 32 < p.split;
-  if (ahead) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kbeg + p.split, kbeg + p.split, nullptr, nullptr, cur, lane);
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
-  // 2 i + mt), requested now with the split taken as full (kv_off clamps into the table; tiles
-  // past the context are masked later): the batch loop takes its tile offsets with readlane
-  // and never waits for a page-table load (such a wait, vmcnt(0), also waits for every K/V
-  // load in flight).
+  // 2 i + mt), requested at once with the split taken as full (kv_off clamps into the table;
+  // tiles past the context are masked later): the batch loop takes its tile offsets with
+  // readlane and never waits for a page-table load (such a wait, vmcnt(0), also waits for every
+  // K/V load in flight). The wave's first batch is requested as soon as they arrive, before
+  // the context length (meta) and while the queries are built; it is read whether or not the
+  // split has keys there (inside its page) and used only if it does.
   // (split <= 3968 keys: at most 31 batches per wave, 62 lanes)
   const uint32_t nbw_full = p.split / 32 > (uint32_t)wv ? (p.split / 32 - wv + 3) / 4 : 0u;
   size_t tile_off = 0;
   if ((uint32_t)lane < 2 * nbw_full)
     tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
+  {
+    const size_t toffs[2] = {readlane64(tile_off, 0), readlane64(tile_off, 1)};
+    load_batch_tiles<D>(p, toffs, cur, lane);
+  }
   const uint32_t p0 = p.meta[2 * t0 + 1];
   const uint32_t ncols = T * p.G;
   bf16x8 qh[NCT][KST], ql[NCT][KST];
@@ -101,7 +100,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
 
   const uint32_t kend = newest ? p0 : min(kbeg + p.split, p0);
   const uint32_t nb = newest ? 0u : (kend - kbeg + 31) / 32;
-  if (!ahead && (uint32_t)wv < nb) load_batch<D, false>(p, seq, g, kbeg + 32 * wv, kend, p0, nullptr, nullptr, cur, lane);
 
   if (newest) new_keys<D, false>(p, seq, g, t0, T, p0, nk, nv, tid, 256);
   __syncthreads();
@@ -123,12 +121,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   } else {
     for (uint32_t b = wv; b < nb; b += 4) {
       KvBatch<D> nxt;
-      // unconditional: past the last batch the keys clamp to kend - 1 (read, never used)
+      // unconditional: past the split's last batch the tiles are read and never used
       const int li = (int)min(2 * ((b + 4 - wv) / 4), 62u);
       const size_t toffs[2] = {readlane64(tile_off, li), readlane64(tile_off, li + 1)};
-      load_batch<D, false>(p, seq, g, kbeg + 32 * (b + 4), kend, p0, nullptr, nullptr, nxt, lane, toffs);
+      load_batch_tiles<D>(p, toffs, nxt, lane);
       __builtin_amdgcn_sched_barrier(0);  // the next batch's loads go out before this batch's work
-      compute_batch<D, NCT, false>(p, cur, kbeg + 32 * b, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
+      const uint32_t kb = kbeg + 32 * b;
+      if (kb + 32 <= kend) compute_batch<D, NCT, false, true>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
+      else compute_batch<D, NCT, false>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
       cur = nxt;
     }
   }
