@@ -31,6 +31,13 @@
  *   orc_step                    the lossless-speculation invariant (bench_spec.rs:119-139):
  *                               greedy verify with replayed drafts emits the plain-decode
  *                               tokens.
+ *   orc_rope_table              float64 cos/sin of the same float32 angle rounded to bf16 by
+ *                               torch: equal except one bf16 step at rounding boundaries.
+ *   orc_embed, orc_rmsnorm_rows a hand-built feed/tree resolution case; outputs collinear with
+ *                               the input row, mean square 1 / (1 + eps / ms), constant-row
+ *                               closed form.
+ *   orc_replay_draft            rate 0 replays the trace, rate 1 shifts every id by one, runs
+ *                               without head rows untouched, chain node encoding.
  */
 #include "oracle.h"
 

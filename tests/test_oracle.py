@@ -453,3 +453,140 @@ def test_lossless_speculation_on_the_oracle():
         ids, _, em, extra = spec.step([(s, [L.FEED_ROW] + drafts, True)])
         got += [int(t) for t in ids[: em[0]]]
     assert got[:20] == trace[:20]
+
+
+# ------------------------------------------------- rope table, embed, rmsnorm_rows, replay
+def bf16_round_torch(x: np.ndarray) -> np.ndarray:
+    """float -> bf16 (round to nearest even) -> float, by torch (independent of the oracle)."""
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).float().numpy()
+
+
+def test_rope_freq_closed_form():
+    """f_j = theta^(-2 j / 64) (model.rs:81, tools/convert.py:59-61), as float32."""
+    from violetto.model import rope_freq
+
+    f = rope_freq(500000.0, 64)
+    want = np.array([500000.0 ** (-2.0 * j / 64) for j in range(32)])
+    assert f.dtype == np.float32 and f.shape == (32,)
+    assert np.all(np.abs(f.astype(np.float64) - want) <= np.spacing(np.float32(want)).astype(np.float64))
+    assert f[0] == 1.0 and np.all(np.diff(f) < 0)
+
+
+def test_rope_table_against_float64_trig():
+    """engine.rs:394-421: tab[pos][j] = (bf16(cos th), bf16(sin th)), th = f32(pos) * f_j in
+    float32. Pinned against float64 cos/sin of the same float32 angle, rounded to bf16 by
+    torch: equal except where the float32 library value and the exact one straddle a bf16
+    rounding boundary (then one bf16 step apart, and the exact value within 2^-22 relative of
+    that boundary)."""
+    from violetto.model import rope_freq
+
+    f = rope_freq(500000.0, 64)
+    pos = np.arange(0, 70000, 7, dtype=np.float32)  # every 7th position up to past 65536
+    n = int(pos[-1]) + 1
+    tab = O.rope_table(f, n)[pos.astype(np.int64)]
+    th = (pos[:, None] * f[None, :]).astype(np.float32)  # float32 product, as the reference
+    exact = np.stack([np.cos(th.astype(np.float64)), np.sin(th.astype(np.float64))], -1)
+    want = bf16_round_torch(exact.astype(np.float32))
+    diff = tab != want
+    assert tab[0, 0, 0] == 1.0 and tab[0, 0, 1] == 0.0  # pos 0: cos 1, sin 0 (sign convention)
+    assert np.all(np.isfinite(tab)) and np.all(np.abs(tab) <= 1.0)
+    if diff.any():
+        e = exact[diff]
+        step = np.abs(np.spacing(bf16_round_torch(e.astype(np.float32)).astype(np.float32))) * 65536.0
+        assert np.all(np.abs(tab[diff] - want[diff]) <= step * 1.0001), "off by more than one bf16 step"
+        # the exact value sits at a rounding boundary: (value - boundary) tiny relative to the value
+        mid = (tab[diff].astype(np.float64) + want[diff].astype(np.float64)) / 2
+        assert np.all(np.abs(e - mid) <= 2.0 ** -22 * np.abs(e) + 1e-30)
+    assert diff.mean() < 1e-3
+
+
+def test_embed_resolution_and_norm_properties():
+    """kernels.metal:82-114: GPU-fed rows take their id from feed[slot][i] and depth/vis from
+    the tree node; meta = (slot, lens[slot] + depth); out = row / rms(row) (no gain, eps
+    2^-23): collinear with the bf16 row, mean square 1 / (1 + eps / ms), and for a constant row
+    c the closed form c / sqrt(c^2 + eps)."""
+    shape = ModelShape(n_layers=1, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=64,
+                       vocab_real=64)
+    rng = np.random.default_rng(3)
+    table = (rng.normal(0, 0.02, (64, 256)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    table[5] = 0x3F40  # a constant row: 0.75
+    feed = np.zeros((2, 16), np.uint32)
+    tree = np.zeros((2, 16), np.uint32)
+    feed[1, :3] = [9, 5, 33]
+    # node i: depth | parent << 8 | sees << 16 (kernels.metal:64-72): 0 root, 1 and 2 children of 0
+    tree[1, :3] = [0 | (0xFF << 8) | (1 << 16), 1 | (0 << 8) | (0b011 << 16), 1 | (0 << 8) | (0b101 << 16)]
+    lens = np.array([40, 100], np.uint32)
+    tokens = [7, L.FEED_ROW + 0, L.FEED_ROW + 1, L.FEED_ROW + 2, 5]
+    tin = np.array([[0, 0], [1, 0], [1, 1], [1, 2], [0, 1]], np.uint32)
+    vis0 = np.array([0xAA, 0, 0, 0, 0xBB], np.uint32)
+    tok, out, meta, vis = O.embed(L, shape, table, tokens, tin, lens, feed.reshape(-1), tree.reshape(-1), vis0)
+    assert list(tok) == [7, 9, 5, 33, 5]
+    assert meta.tolist() == [[0, 40], [1, 100], [1, 101], [1, 101], [0, 41]]
+    assert list(vis) == [0xAA, 0b001, 0b011, 0b101, 0xBB]  # CPU rows keep theirs
+    rows = (table.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    eps = 2.0 ** -23
+    for t, tk in enumerate(tok):
+        r = rows[tk]
+        o = out[t].astype(np.float64)
+        ms = np.mean(r * r)
+        assert abs(np.mean(o * o) - 1.0 / (1.0 + eps / ms)) < 1e-5
+        cos = np.dot(o, r) / np.linalg.norm(o) / np.linalg.norm(r)
+        assert cos > 1 - 1e-12
+    assert np.all(out[4] == np.float32(0.75 / np.sqrt(0.75 ** 2 + eps)))
+
+
+def test_rmsnorm_rows_gather_and_properties():
+    """kernels.metal:117-131: out[r] = in[rows[r]] / rms (no gain): gathered in rows' order,
+    collinear, mean square 1 / (1 + eps / ms); a zero row stays zero."""
+    rng = np.random.default_rng(4)
+    x = (rng.normal(0, 1, (6, 128)) * rng.uniform(0.01, 30, (6, 1))).astype(np.float32)
+    x[2] = 0.0
+    rows = np.array([4, 0, 2, 4], np.uint32)
+    out = np.zeros((4, 128), np.float32)
+    O.lib().orc_rmsnorm_rows(O.ptr(x), O.ptr(rows), O.ptr(out), C.c_uint32(4), C.c_uint32(128))
+    eps = 2.0 ** -23
+    for r, src in enumerate(rows):
+        v = x[src].astype(np.float64)
+        o = out[r].astype(np.float64)
+        if not v.any():
+            assert not o.any()
+            continue
+        ms = np.mean(v * v)
+        assert abs(np.mean(o * o) - 1.0 / (1.0 + eps / ms)) < 1e-5
+        assert np.dot(o, v) / np.linalg.norm(o) / np.linalg.norm(v) > 1 - 1e-12
+    assert np.array_equal(out[0], out[3])
+
+
+def test_replay_draft_rules():
+    """kernels.metal:1695-1724: drafts i = 1..15 replay trace[lens + i]; with probability rate
+    (Philox4x32-10 of (pos, 0x5eed) under (seed, 0x0dd5), top 24 bits) the id is replaced by
+    id + 1 mod vocab; positions past the trace read 0; the tree becomes the chain; runs with
+    no head rows are left alone; feed[slot][0] is untouched."""
+    stride, vocab = 64, 50
+    trace = np.zeros((3, stride), np.uint32)
+    trace[0, :40] = np.arange(40) % vocab
+    trace[1, :64] = (np.arange(64) * 7 + 3) % vocab
+    trace_len = np.array([40, 64, 0], np.uint32)
+    lens = np.array([30, 10, 5], np.uint32)
+    runs = [L.RunIn(0, 0, 5, 0, 5, 1), L.RunIn(1, 5, 5, 5, 0, 1), L.RunIn(2, 10, 1, 10, 1, 0)]
+
+    def run(rate, seed=11):
+        feed = np.full(3 * 16, 777, np.uint32)
+        tree = np.full(3 * 16, 0xDEAD, np.uint32)
+        O.replay_draft(L, runs, lens, feed, trace.reshape(-1), trace_len, L.ReplayArgs(stride, seed, rate, vocab), tree)
+        return feed.reshape(3, 16), tree.reshape(3, 16)
+
+    f0, t0 = run(0.0)
+    want = np.array([trace[0, 30 + i] if 30 + i < 40 else 0 for i in range(1, 16)])
+    assert np.array_equal(f0[0, 1:], want) and f0[0, 0] == 777
+    assert np.all(f0[1] == 777) and np.all(t0[1] == 0xDEAD)  # no head rows: untouched
+    assert np.all(f0[2] == 777)  # empty trace: untouched
+    for i in range(1, 16):
+        assert t0[0, i] == i | ((i - 1) << 8) | (((2 << i) - 1) << 16)
+    f1, _ = run(1.0)
+    assert np.array_equal(f1[0, 1:], (want + 1) % vocab)
+    # an intermediate rate mixes the two, per position, the same way for the same seed
+    fa, _ = run(0.5, seed=3)
+    fb, _ = run(0.5, seed=3)
+    assert np.array_equal(fa, fb)
+    assert set(np.nonzero(fa[0, 1:] != want)[0]) == set(np.nonzero(fa[0, 1:] == (want + 1) % vocab)[0])
