@@ -985,7 +985,7 @@ GemmTune g_gemm_tune;  // all zero: the built-in choice
 // k splits (up to 8) that give 256 workgroups. Either way one row tile per wave when the
 // splits alone cannot reach 256 workgroups, and with int8 scale groups shorter than k. At 384
 // rows and more, matrices with 512 blocks of 256 rows x 64 tokens run those (four row tiles
-// per wave), unsplit.
+// per wave, two chunks in flight), unsplit.
 static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uint32_t k) {
   if (g_gemm_tune.rtw)
     return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
@@ -993,7 +993,8 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
   const bool i8 = fmt == SV_FMT_I8;
   // Wide matrices at many rows: 256-row x 64-token blocks halve the operand traffic through
   // L2 (weights re-read per token block, X per row block) where they still fill the device.
-  if (!grouped && n >= 384 && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 63) / 64) >= 512) return GemmCfg{4, 4, 1, 4};
+  // Two chunks in flight (not four) keep that shape at two waves per SIMD.
+  if (!grouped && n >= 384 && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 63) / 64) >= 512) return GemmCfg{4, 4, 1, 2};
   GemmCfg c{2, 2, 1, 4};
   if (!i8) {
     uint32_t best = ~0u;
@@ -1032,13 +1033,14 @@ static size_t gemm_ws_layout(uint32_t n, uint32_t m, const GemmCfg& c, size_t* s
 
 static bool gemm_shape_ok(uint32_t m, uint32_t k, const GemmCfg& c) {
   const bool nt_ok = c.nt == 2 || c.nt == 3 || c.nt == 4 || c.nt == 5 || c.nt == 8;
-  return nt_ok && (c.rtw == 1 || c.rtw == 2 || (c.rtw == 4 && c.nt <= 5)) && (c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
+  return nt_ok && (c.rtw == 1 || c.rtw == 2 || (c.rtw == 4 && c.nt <= 5)) && (c.d == 2 || c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
          (k / GKC) % c.s == 0;
 }
 
 template <int FMT, int RTW, int NT, bool GR>
 static void gemm_launch_one(hipStream_t stream, const MMParams& p, int d, uint32_t nwg, uint32_t n_tblk) {
   if (d == 8 && NT <= 3) launch((mm_gemm<FMT, RTW, NT, GR, (NT <= 3 ? 8 : 4)>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
+  else if (d == 2 && RTW == 4) launch((mm_gemm<FMT, RTW, NT, GR, 2>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
   else launch((mm_gemm<FMT, RTW, NT, GR, 4>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
 }
 

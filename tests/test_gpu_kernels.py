@@ -512,7 +512,7 @@ def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
 
 @pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
                                                   (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4),
-                                                  (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4)])
+                                                  (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4), (4, 4, 2, 2), (4, 3, 1, 2)])
 @pytest.mark.parametrize("n", [17, 100])
 def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
     """Every GEMM launch shape (row tiles per wave, token tiles, k splits merged by the last
