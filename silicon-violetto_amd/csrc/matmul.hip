@@ -1004,6 +1004,7 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
     }
   }
   if (grouped || m % 128) c.rtw = 1;
+  if (i8) c.d = 2;  // measured: as fast or faster than four chunks in flight (more waves per SIMD)
   const uint32_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt);
   const int s_first = i8 ? 2 : 1, s_last = i8 ? 4 : 8;
   for (;;) {
@@ -1040,7 +1041,7 @@ static bool gemm_shape_ok(uint32_t m, uint32_t k, const GemmCfg& c) {
 template <int FMT, int RTW, int NT, bool GR>
 static void gemm_launch_one(hipStream_t stream, const MMParams& p, int d, uint32_t nwg, uint32_t n_tblk) {
   if (d == 8 && NT <= 3) launch((mm_gemm<FMT, RTW, NT, GR, (NT <= 3 ? 8 : 4)>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
-  else if (d == 2 && RTW == 4) launch((mm_gemm<FMT, RTW, NT, GR, 2>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
+  else if (d == 2) launch((mm_gemm<FMT, RTW, NT, GR, 2>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
   else launch((mm_gemm<FMT, RTW, NT, GR, 4>), dim3(nwg), dim3(256), 0, stream, p, n_tblk);
 }
 
