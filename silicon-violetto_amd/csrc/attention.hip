@@ -20,7 +20,7 @@
 //     lane for D = 64), and the matrix-core operand takes one of its dims per tile.
 //   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace with
 //     coherent stores (sc1: write-through to the agent-coherent level). attn_merge_kernel,
-//     the next launch, sums the partials of each (run, kv head, column) in split order and
+//     the next launch, sums the partials of each (run, kv head) output in split order and
 //     writes o / l. With SV_ATTN_MERGE=fused the last split of (run, kv head) to arrive (a
 //     relaxed agent-scope counter: no L2 write-back or invalidate) does the same with
 //     coherent 16-byte loads.
@@ -199,36 +199,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   }
 }
 
-// attn_dec_reduce (kernels.metal:1316-1362) for the fused verify attention: one workgroup
-// per (run, kv head, column) sums the split partials (plain sums: no running max) and writes
-// o / l. Thread (part, d) adds splits part, part + P, ... eight loads in flight at a time; the
-// P parts are then added in part order. XSA and the gate are off (xsa = 0, gate = 1).
+// attn_dec_reduce (kernels.metal:1316-1362) for the fused verify attention: plain sums over
+// the splits (no running max) of four consecutive outputs (column, dims d .. d + 3) of one
+// (run, kv head), then o / l. A workgroup of 256 threads is P parts x 256 / P output groups:
+// part j adds splits j, j + P, ... (at most eight, all requested at once, before the context
+// length in meta says how many count), then the parts are added in part order through LDS.
+// P grows with the grid's splits (long contexts at one stream), so no thread waits for more
+// than one round of loads. XSA and the gate are off (xsa = 0, gate = 1).
 template <int D>
-__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
-  constexpr int P = 256 / D;
-  __shared__ float so[P][D];
-  __shared__ float sl[P];
-  const uint32_t r = blockIdx.x, g = blockIdx.y, col = blockIdx.z, tid = threadIdx.x;
-  const uint32_t d = tid % D, part = tid / D;
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t P) {
+  __shared__ f32x4 so[256];
+  __shared__ float sl[256];
+  const uint32_t G4 = 256 / P, part = threadIdx.x / G4, gi = threadIdx.x % G4;
+  const uint32_t r = blockIdx.x, g = blockIdx.y, i4 = blockIdx.z * G4 + gi;
   const uint32_t t0 = p.n_inline ? p.inl[3 * r] : p.runs[2 * r];
   const uint32_t T = p.n_inline ? p.inl[3 * r + 1] : p.runs[2 * r + 1];
   const uint32_t ncols = T * p.G;
-  if (col >= ncols) return;
-  // The partials of every split the grid has are requested at once, before the context
-  // length (meta) says how many count; the rest are never added.
+  const bool live = 4 * i4 < ncols * D;
+  const uint32_t col = live ? (4 * i4) / D : 0u, d = (4 * i4) % D;
   const uint32_t p0 = p.meta[2 * t0 + 1];
   const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
   const size_t so_stride = (size_t)p.maxcols * D;
   const float* po = p.part_o + rec0 * so_stride + (size_t)col * D + d;
   const float* pl = p.part_l + rec0 * p.maxcols + col;
-  float o = 0.0f, l = 0.0f;
+  f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+  float l = 0.0f;
   for (uint32_t sp = part; sp < p.max_splits; sp += 8 * P) {
-    float ov[8], lv[8];
+    f32x4 ov[8];
+    float lv[8];
 #pragma unroll
     for (int u = 0; u < 8; u++) {
-      const bool in = sp + u * P < p.max_splits;
-      ov[u] = in ? po[(sp + u * P) * so_stride] : 0.0f;
-      lv[u] = in ? pl[(sp + u * P) * p.maxcols] : 0.0f;
+      const uint32_t x = sp + u * P;
+      const bool in = live && x < p.max_splits;
+      ov[u] = in ? *(const f32x4*)(po + x * so_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
+      lv[u] = in ? pl[x * p.maxcols] : 0.0f;
     }
     const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;  // after the loads are issued
 #pragma unroll
@@ -238,19 +242,19 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
         l += lv[u];
       }
   }
-  if ((p0 + p.split - 1) / p.split + 1 > p.max_splits) return;  // the attention kernel wrote NaN
-  so[part][d] = o;
-  if (d == 0) sl[part] = l;
-  __syncthreads();
-  if (part != 0) return;
-  float ot = so[0][d], lt = sl[0];
-#pragma unroll
-  for (int u = 1; u < P; u++) {
-    ot += so[u][d];
-    lt += sl[u];
+  if (P > 1) {
+    so[threadIdx.x] = o;
+    sl[threadIdx.x] = l;
+    __syncthreads();
+    if (part != 0) return;
+    for (uint32_t j = 1; j < P; j++) {
+      o += so[j * G4 + gi];
+      l += sl[j * G4 + gi];
+    }
   }
+  if (!live || (p0 + p.split - 1) / p.split + 1 > p.max_splits) return;  // NaN written by the attention
   const uint32_t i = col / p.G, h = g * p.G + col % p.G;
-  p.out[(size_t)(t0 + i) * p.NQ * D + h * D + d] = ot / lt;
+  *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
 }
 
 // Dynamic LDS of up to 4 x 64 x 128 floats (+ l): allow it once per instantiation, outside
@@ -377,8 +381,12 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     SV_TRY_LAUNCH("attn_verify");
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
-  if (D == 64) launch(attn_merge_kernel<64>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
-  else launch(attn_merge_kernel<128>, dim3(n_runs, NKV, maxcols), dim3(256), 0, stream, p);
+  // parts: enough that a thread adds at most eight splits (a power of two, up to 64)
+  uint32_t P = 1;
+  while (P < 64 && 8 * P < args->max_splits) P *= 2;
+  const uint32_t G4 = 256 / P, mz = (maxcols * D / 4 + G4 - 1) / G4;
+  if (D == 64) launch(attn_merge_kernel<64>, dim3(n_runs, NKV, mz), dim3(256), 0, stream, p, P);
+  else launch(attn_merge_kernel<128>, dim3(n_runs, NKV, mz), dim3(256), 0, stream, p, P);
   return check_launch("attn_merge");
 }
 
