@@ -41,7 +41,7 @@ namespace sv {
 template <int D, int NCT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
-  extern __shared__ float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
+  extern __shared__ __attribute__((aligned(16))) float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
   __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
   float* ored = lds;
   float* lred = lds + 4 * COLS * D;
@@ -61,8 +61,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   // The run's visibility masks (for the newest split's masks) are requested first, into LDS.
   __shared__ uint32_t svis[SV_MAX_RUN];
   if (tid < T) svis[tid] = p.vis[t0 + tid];
-  KvBatch<D> cur;
+  KvBatchT<D> cur;
   const uint32_t kbeg = s * p.split;
+  // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
+  uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
   // 2 i + mt), requested at once with the split taken as full (kv_off clamps into the table;
   // tiles past the context are masked later): the batch loop takes its tile offsets with
@@ -77,7 +79,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
     tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
   {
     const size_t toffs[2] = {readlane64(tile_off, 0), readlane64(tile_off, 1)};
-    load_batch_tiles<D>(p, toffs, cur, lane);
+    load_batch_tiles_t<D>(p, toffs, cur, lane);
   }
   const uint32_t p0 = p.meta[2 * t0 + 1];
   const uint32_t ncols = T * p.G;
@@ -114,26 +116,27 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   }
   if (newest) {
     if (wv == 0) {
-      KvBatch<D> nb0;
-      load_batch<D, true>(p, seq, g, p0, p0 + T, p0, nk, nv, nb0, lane);
-      compute_batch<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, svis);
+      KvBatchT<D> nb0;
+      load_batch_new_t<D>(nk, nv, p0, p0 + T, p0, nb0, lane);
+      compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, svis);
     }
   } else {
     for (uint32_t b = wv; b < nb; b += 4) {
-      KvBatch<D> nxt;
+      KvBatchT<D> nxt;
       // unconditional: past the split's last batch the tiles are read and never used
       const int li = (int)min(2 * ((b + 4 - wv) / 4), 62u);
       const size_t toffs[2] = {readlane64(tile_off, li), readlane64(tile_off, li + 1)};
-      load_batch_tiles<D>(p, toffs, nxt, lane);
+      load_batch_tiles_t<D>(p, toffs, nxt, lane);
       __builtin_amdgcn_sched_barrier(0);  // the next batch's loads go out before this batch's work
       const uint32_t kb = kbeg + 32 * b;
-      if (kb + 32 <= kend) compute_batch<D, NCT, false, true>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
-      else compute_batch<D, NCT, false>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane);
+      if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+      else compute_batch_t<D, NCT, false>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
       cur = nxt;
     }
   }
 
-  // This wave's (l, o) to LDS: lane holds column 16 ct + c16, dims VE (4 q + i) + dt.
+  __syncthreads();  // every wave's V stage read before the reduction buffer (over it) is written
+  // This wave's (l, o) to LDS: lane holds column 16 ct + c16, dims 16 dt + 4 q + i.
 #pragma unroll
   for (int ct = 0; ct < NCT; ct++) {
     float l = lsum[ct];
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int dt = 0; dt < VE; dt++) od[VE * (4 * q + i) + dt] = O[dt][ct][i];
+      for (int dt = 0; dt < VE; dt++) od[16 * dt + 4 * q + i] = O[dt][ct][i];
     if (q == 0) lred[wv * COLS + col] = l;
   }
   __syncthreads();

@@ -137,6 +137,9 @@ __device__ __forceinline__ void load_batch_tiles(const AttnParams& p, const size
     for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = buf_ld16(krs, ko + 64 * ks, 0);
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
+#ifdef SV_ATTN_ABLATE_V
+      if constexpr (VE == 4) { b.vw[4 * mt + jj] = vword{b.kw[mt][0][jj], b.kw[mt][0][(jj + 1) & 3]}; continue; }
+#endif
       if constexpr (VE == 4)
         b.vw[4 * mt + jj] = __builtin_bit_cast(vword, __builtin_amdgcn_raw_buffer_load_b64(vrs, vo + jj * D * 2, 0, 0));
       else
@@ -212,6 +215,139 @@ __device__ __forceinline__ void compute_batch(const AttnParams& p, const KvBatch
   }
 }
 
+
+// ----------------------------------------------------------------------------------------
+// The attention kernel's batches carry V as the tile's own bytes (coalesced 16-byte loads) and
+// transpose it on the way into the matrix cores through a wave-private LDS stage with gfx950's
+// transposing LDS read (ds_read_b64_tr_b16: within each group of 16 lanes, lane j receives
+// element j % 4 of the 8-byte rows addressed by lanes j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4).
+// Output tile dt of O^T then holds dims 16 dt + row.
+template <int D>
+struct KvBatchT {
+  static constexpr int KST = D / 32, NV = D / 32;
+  u32x4 kw[2][KST];  // lane (c16, q): key kb + 16 mt + c16, dims 32 ks + 8 q .. + 7
+  u32x4 vr[2][NV];   // tile mt (keys kb + 16 mt ..): its bytes 16 lane + 1024 v (rows of 2 D bytes)
+};
+
+// Cached batch through per-tile buffer descriptors (load_batch_tiles' contract).
+template <int D>
+__device__ __forceinline__ void load_batch_tiles_t(const AttnParams& p, const size_t* toff, KvBatchT<D>& b, int lane) {
+  constexpr int KST = D / 32, NV = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
+  const uint32_t ko = (uint32_t)(c16 * D + 8 * q) * 2;
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+    const __amdgpu_buffer_rsrc_t krs = coherent_rsrc(p.kc + toff[mt]), vrs = coherent_rsrc(p.vc + toff[mt]);
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = buf_ld16(krs, ko + 64 * ks, 0);
+#pragma unroll
+    for (int v = 0; v < NV; v++) b.vr[mt][v] = buf_ld16(vrs, 16 * lane + 1024 * v, 0);
+  }
+}
+
+// The run's new keys from LDS (nk / nv: [T][D], key p0 + row), keys clamped to kend - 1.
+template <int D>
+__device__ __forceinline__ void load_batch_new_t(const uint16_t* nk, const uint16_t* nv, uint32_t kb, uint32_t kend,
+                                                 uint32_t p0, KvBatchT<D>& b, int lane) {
+  constexpr int KST = D / 32, NV = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++) {
+    const uint32_t key = min(kb + 16 * mt + c16, kend - 1);
+#pragma unroll
+    for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = *(const u32x4*)(nk + (size_t)(key - p0) * D + 32 * ks + 8 * q);
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      const uint32_t byte = 16 * lane + 1024 * v, row = byte / (2 * D), col = (byte % (2 * D)) / 2;
+      const uint32_t vk = min(kb + 16 * mt + row, kend - 1);
+      b.vr[mt][v] = *(const u32x4*)(nv + (size_t)(vk - p0) * D + col);
+    }
+  }
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// compute_batch's semantics with V through the wave's LDS stage (2 tiles x 16 x D bf16).
+// Keys at or past kend that a partial batch read from their page get V rows of zero, so
+// whatever the cache holds there cannot reach the sums (p is 0 for them).
+template <int D, int NCT, bool NEW, bool FULL = false>
+__device__ __forceinline__ void compute_batch_t(const AttnParams& p, const KvBatchT<D>& b, uint32_t kb, uint32_t kend,
+                                                uint32_t p0, uint32_t ncols, uint32_t t0,
+                                                const bf16x8 (&qh)[NCT][D / 32], const bf16x8 (&ql)[NCT][D / 32],
+                                                f32x4 (&O)[D / 16][NCT], float (&lsum)[NCT], int lane, uint16_t* stage,
+                                                const uint32_t* vis_cached = nullptr) {
+  constexpr int KST = D / 32, VE = D / 16, NV = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
+  // V into the stage first (its LDS writes overlap the score products).
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      u32x4 w = b.vr[mt][v];
+      if (!FULL && !NEW) {
+        const uint32_t row = (16 * lane + 1024 * v) / (2 * D);
+        if (kb + 16 * mt + row >= kend) w = u32x4{0u, 0u, 0u, 0u};
+      }
+      *(u32x4*)((char*)stage + mt * 32 * D + 16 * lane + 1024 * v) = w;
+    }
+  // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
+  f32x4 S[2][NCT];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const bf16x8 kk = __builtin_bit_cast(bf16x8, b.kw[mt][ks]);
+        a = mfma16(kk, qh[ct][ks], a);
+        a = mfma16(kk, ql[ct][ks], a);
+      }
+      S[mt][ct] = a;
+    }
+  bf16x8 ph[NCT], pl[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const uint32_t c = 16 * ct + c16;
+    const bool col_ok = c < ncols;
+    uint32_t vbits = 0;
+    if (NEW && col_ok) vbits = vis_cached ? vis_cached[c / p.G] : p.vis[t0 + c / p.G];
+    float pv[8];
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t key = kb + 16 * mt + 4 * q + i;
+        float e = __builtin_amdgcn_exp2f(S[mt][ct][i]);
+        if (!FULL) {
+          bool ok = col_ok && key < kend;
+          if (NEW) ok = ok && ((vbits >> (key - p0)) & 1u);
+          e = ok ? e : 0.0f;
+        }
+        pv[4 * mt + i] = e;
+        lsum[ct] += e;
+      }
+    split8(pv, ph[ct], pl[ct]);
+  }
+  // O^T[dt] (rows: dims 16 dt + 4 q + i) += V^T[dt] P^T; the A operand's k slots 4 mt + t are
+  // keys kb + 16 mt + 4 q + t (P's layout), read transposed: lane (i, q) addresses key
+  // 4 q + i / 4 of tile mt, dims 16 dt + 4 (i % 4) .. + 3.
+  const uint32_t rd = (uint32_t)(4 * q + c16 / 4) * 2 * D + (uint32_t)(4 * (c16 % 4)) * 2;
+#pragma unroll
+  for (int dt = 0; dt < VE; dt++) {
+    const i16x4 h0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((char*)stage + rd + 32 * dt));
+    const i16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((char*)stage + 32 * D + rd + 32 * dt));
+    const u32x4 a = u32x4{__builtin_bit_cast(u32x2, h0)[0], __builtin_bit_cast(u32x2, h0)[1],
+                          __builtin_bit_cast(u32x2, h1)[0], __builtin_bit_cast(u32x2, h1)[1]};
+    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      O[dt][ct] = mfma16(av, ph[ct], O[dt][ct]);
+      O[dt][ct] = mfma16(av, pl[ct], O[dt][ct]);
+    }
+  }
+}
 
 // fp32 activation words at element offset `off` (a multiple of 4): plain, or coherent (sc1)
 // when they were written earlier in the same launch by another workgroup.
