@@ -316,6 +316,46 @@ def sample_rows(n, temps, top_ps, seed=11, pos0=100):
     return rows
 
 
+@pytest.mark.parametrize("runs_T,p0s,split,tree", [([5], [515], 128, False), ([3, 5, 2], [31, 100, 64], 32, False),
+                                                   ([16], [300], 64, True)])
+def test_attn_verify_garbage_past_context(gpu, runs_T, p0s, split, tree):
+    """Cache slots past each run's context (the rest of its last page, and never-used pages) hold
+    NaN bit patterns, as a caller's uninitialised cache may: keys there are read inside their
+    page but masked, their V rows zeroed, so the output is finite and matches the oracle."""
+    banner(f"attn garbage runs={runs_T} p0={p0s} split={split} tree={tree}")
+    sh = SH
+    c = make_attn_case(sh, runs_T, p0s, seed=len(runs_T) * 7 + split, tree=tree)
+    page = 1 << c["page_shift"]
+    nan = np.uint16(0x7FC0)
+    used = set()
+    for r, p0 in enumerate(p0s):
+        for pos in range(c["max_pages"] * page):
+            pg = int(c["page_table"][r, pos // page])
+            if pos < p0:
+                used.add(pg)
+            else:
+                c["k"][0, pg, :, pos % page, :] = nan
+                c["v"][0, pg, :, pos % page, :] = nan
+    for pg in range(c["n_pages"]):
+        if pg not in used and pg not in set(c["page_table"].reshape(-1).tolist()):
+            c["k"][0, pg] = nan
+            c["v"][0, pg] = nan
+    freq = oracle.np.asarray((500000.0 ** (-2.0 * np.arange(32) / 64)), np.float32)
+    rope_tab = oracle.rope_table(freq, max(p0s) + 20)
+    kv = L.KvArgs(1, 0, 0, len(runs_T), c["page_shift"], c["n_pages"], c["max_pages"], 0)
+    max_splits = max(-(-p // split) + 1 for p in p0s)
+    args = L.AttnArgs(split, max_splits, 0.125 * 1.4426950408889634, 1, 0, 0, 0, 0, 0)
+    runs_flat = c["runs"].reshape(-1).copy()
+    ref = oracle.attn_verify(L, sh, c["qkv"], c["meta"].reshape(-1).copy(), c["k"].copy(), c["v"].copy(),
+                             c["page_table"], rope_tab, kv, args, runs_flat, c["vis"])
+    assert np.all(np.isfinite(ref))
+    out = torch.zeros(sum(runs_T), sh.n_heads * sh.head_dim, device="cuda")
+    K.attn_verify(sh, to_dev(c["qkv"]), to_dev(c["meta"]), to_dev(c["k"]), to_dev(c["v"]), to_dev(c["page_table"]),
+                  to_dev(rope_tab), kv, args, to_dev(runs_flat), len(runs_T), max(runs_T), to_dev(c["vis"]), out)
+    torch.cuda.synchronize()
+    close(out.cpu().numpy(), ref, atol=2e-4, rtol=2e-4, what="attention output over garbage")
+
+
 @pytest.mark.parametrize("vocab", [32000, 257, 1024, 151680])
 def test_sample_bit_exact(gpu, vocab):
     banner(f"sample vocab={vocab}")
