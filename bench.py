@@ -32,9 +32,6 @@ from pathlib import Path
 
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "silicon-violetto_amd"))
-if os.environ.get("SV_LIB"):  # PROBE
-    import violetto._lib as _L
-    _L.LIB_PATH = Path(os.environ["SV_LIB"])
 
 METRIC = "verified tok/s @1 & 32 seqs, 8k ctx, k=4; verify-step HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0

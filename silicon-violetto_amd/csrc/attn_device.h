@@ -137,9 +137,6 @@ __device__ __forceinline__ void load_batch_tiles(const AttnParams& p, const size
     for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = buf_ld16(krs, ko + 64 * ks, 0);
 #pragma unroll
     for (int jj = 0; jj < 4; jj++) {
-#ifdef SV_ATTN_ABLATE_V
-      if constexpr (VE == 4) { b.vw[4 * mt + jj] = vword{b.kw[mt][0][jj], b.kw[mt][0][(jj + 1) & 3]}; continue; }
-#endif
       if constexpr (VE == 4)
         b.vw[4 * mt + jj] = __builtin_bit_cast(vword, __builtin_amdgcn_raw_buffer_load_b64(vrs, vo + jj * D * 2, 0, 0));
       else

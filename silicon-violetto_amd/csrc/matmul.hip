@@ -639,9 +639,6 @@ __global__ __launch_bounds__(256) void pack_tiled_kernel(const uint8_t* src, uin
 //   - k splits: each split stores its sums (coherent stores) and the last split of the
 //     (row block, token block) to arrive adds them in split order and runs the epilogue.
 constexpr int GKC = 64;
-#ifndef SV_GEMM_ABLATE
-#define SV_GEMM_ABLATE 0  // probe builds: 1 X split, 2 weight conversion, 3 MFMA, 4 barrier left out
-#endif
 // Split-k hand-off counters (skinny and GEMM paths): a region of fixed size at the front of the
 // workspace, so every matmul sharing one workspace finds its counters at zero there, whatever
 // its shape.
@@ -792,12 +789,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
       for (int e = 0; e < 8; e++) ssacc[j] = __builtin_fmaf(v[e], v[e], ssacc[j]);
       bf16x8 h, l;
-#if SV_GEMM_ABLATE == 1
-      h = __builtin_bit_cast(bf16x8, xr[j][0]);
-      l = __builtin_bit_cast(bf16x8, xr[j][1]);
-#else
       split8(v, h, l);
-#endif
       const int tok = i / 8, g8 = i % 8, qq = g8 >> 1, ks = g8 & 1;
       const int slot = (tok & 15) + 16 * qq + 2 * g8;
       xs[buf][tok >> 4][2 * ks][slot] = __builtin_bit_cast(u32x4, h);
@@ -849,11 +841,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
         bf16x8 a[RTW];
 #pragma unroll
         for (int r = 0; r < RTW; r++) {
-#if SV_GEMM_ABLATE == 2
-          if (FMT == SV_FMT_I8) a[r] = __builtin_bit_cast(bf16x8, cur[r][0] ^ (uint32_t)ks);
-#else
           if (FMT == SV_FMT_I8) a[r] = i8x8_to_bf(cur[r][0][2 * ks], cur[r][0][2 * ks + 1]);
-#endif
           else a[r] = __builtin_bit_cast(bf16x8, cur[r][ks]);
         }
 #pragma unroll
@@ -864,12 +852,8 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
           for (int r = 0; r < RTW; r++) {
             f32x4& g = GROUPED ? grp[GROUPED ? r : 0][GROUPED ? n : 0] : acc[r][n];
-#if SV_GEMM_ABLATE == 3
-            g += __builtin_bit_cast(f32x4, a[r]) + __builtin_bit_cast(f32x4, bh) + __builtin_bit_cast(f32x4, bl);
-#else
             g = mfma16(a[r], bh, g);
             g = mfma16(a[r], bl, g);
-#endif
           }
         }
       }
@@ -894,9 +878,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       const int dn = (d + 1) % GD;
       store_x(buf ^ 1, xr[dn]);
       load_x(c + 1 + GD, xr[dn]);
-#if SV_GEMM_ABLATE != 4
       lds_barrier();
-#endif
     }
   }
   if (!GROUPED && FMT == SV_FMT_I8) {
