@@ -38,8 +38,15 @@
 
 namespace sv {
 
-template <int D, int NCT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
+// Batches per wave of the all-in-flight variant (splits of at most 128 x this many keys).
+constexpr int SV_ATTN_NBW = 4;
+
+// NBW = 0: each wave keeps one batch in flight ahead of the one it multiplies (any split).
+// NBW > 0 (splits of at most 128 NBW keys, grids of about one workgroup per CU): each wave
+// requests all of its batches at once, after the queries, positions and page-table words (one
+// round trip) and the rope words, and builds the queries while they arrive.
+template <int D, int NCT, int NBW, bool INL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NBW == 0 && D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
   extern __shared__ __attribute__((aligned(16))) float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
   __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
@@ -49,18 +56,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c16 = lane & 15, q = lane >> 4;
   const uint32_t s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
   uint32_t t0, T, seq;
-  if (p.n_inline) {
-    t0 = p.inl[3 * r];
-    T = p.inl[3 * r + 1];
-    seq = p.inl[3 * r + 2];
-  } else {
-    t0 = p.runs[2 * r];
-    T = p.runs[2 * r + 1];
-    seq = p.meta[2 * t0];
-  }
-  // The run's visibility masks (for the newest split's masks) are requested first, into LDS.
+  run_header<INL>(p, r, t0, T, seq);
+  // The run's visibility masks (the newest split's masks): requested with the first loads and
+  // put in LDS once those have arrived (before the barrier that precedes their use), so no
+  // round trip is spent on them alone.
   __shared__ uint32_t svis[SV_MAX_RUN];
-  if (tid < T) svis[tid] = p.vis[t0 + tid];
+  const uint32_t visw = p.vis[t0 + min((uint32_t)tid, T - 1)];
   KvBatchT<D> cur;
   const uint32_t kbeg = s * p.split;
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
@@ -75,16 +76,95 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
   // (split <= 3968 keys: at most 31 batches per wave, 62 lanes)
   const uint32_t nbw_full = p.split / 32 > (uint32_t)wv ? (p.split / 32 - wv + 3) / 4 : 0u;
   size_t tile_off = 0;
-  if ((uint32_t)lane < 2 * nbw_full)
-    tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
-  {
-    const size_t toffs[2] = {readlane64(tile_off, 0), readlane64(tile_off, 1)};
-    load_batch_tiles_t<D>(p, toffs, cur, lane);
-  }
-  const uint32_t p0 = p.meta[2 * t0 + 1];
   const uint32_t ncols = T * p.G;
   bf16x8 qh[NCT][KST], ql[NCT][KST];
-  build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
+  uint32_t p0;
+  KvBatchT<D> bt[NBW > 0 ? NBW : 1];
+  if constexpr (NBW == 0) {
+    if ((uint32_t)lane < 2 * nbw_full)
+      tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
+    {
+      const size_t toffs[2] = {readlane64(tile_off, 0), readlane64(tile_off, 1)};
+      load_batch_tiles_t<D>(p, toffs, cur, lane);
+    }
+    p0 = p.meta[2 * t0 + 1];
+    build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
+    if (tid < T) svis[tid] = visw;
+  } else {
+    // Queries, positions and page-table words in one round trip; then the rope words, then
+    // every batch of the wave (slots past the split's batches read nothing); the queries are
+    // built once the rope words are in, while the batches stream.
+    // 1. One round trip: query words and positions of the lane's columns (a column past the
+    //    run's reads the last column's words and is zeroed), this wave's page-table words
+    //    (lane 2 i + mt: tile mt of batch i, index clamped into the table) and p0.
+    QRaw<D, NCT> qr;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      const uint32_t c = min(16u * ct + c16, ncols - 1), i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
+      qr.pos[ct] = p.meta[2 * t + 1];
+      const size_t qo = (size_t)t * p.W + h * D + 8 * q;
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const f32x4 a = *(const f32x4*)(p.qkv + qo + 32 * ks), b = *(const f32x4*)(p.qkv + qo + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          qr.v[ct][ks][e] = a[e];
+          qr.v[ct][ks][4 + e] = b[e];
+        }
+      }
+    }
+    const uint32_t tpos = kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1);
+    const uint32_t pword = p.page_table[(size_t)seq * p.max_pages + min(tpos >> p.page_shift, p.max_pages - 1)];
+    p0 = p.meta[2 * t0 + 1];
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. Rope words (they need the positions), then every batch of the wave (they need the
+    //    page words; slots past the split's batches read nothing).
+    //    Rope words through a descriptor whose range is empty without rope (zeros, no
+    //    access), so no branch splits the loads' accounting.
+    float2 cs[NCT][KST][4];
+    const __amdgpu_buffer_rsrc_t rrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.rope), 0, p.rope_on ? 0x7fffffff : 0, 0x00020000);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const uint32_t j = 16 * ks + 4 * q + jj;
+          const bool on = p.rope_on && 32 * ks + 8 * q < 64;
+          const uint32_t off = (qr.pos[ct] * SV_ROPE_PAIRS + j) * 8 + (on ? 0u : 0x80000000u);
+          cs[ct][ks][jj] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rrs, off, 0, 0));
+        }
+    if ((uint32_t)lane < 2 * nbw_full) {
+      const uint32_t page = min(pword, p.n_pages - 1);
+      tile_off = ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
+                 (size_t)(tpos & ((1u << p.page_shift) - 1u)) * D;
+    }
+#pragma unroll
+    for (int i = 0; i < NBW; i++) {
+      const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
+      load_batch_tiles_t<D>(p, toffs, bt[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < T) svis[tid] = visw;
+    // 3. The queries, while the batches stream (columns past the run's are zero; no rope is
+    //    the identity rotation).
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++)
+          if (!(p.rope_on && 32 * ks + 8 * q < 64)) cs[ct][ks][jj] = float2{1.0f, 0.0f};
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++)
+      if (16u * ct + c16 >= ncols)
+#pragma unroll
+        for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) qr.v[ct][ks][e] = 0.0f;
+    qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane);
+  }
 
   const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
   if (nsplit > p.max_splits) {
@@ -119,6 +199,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
       KvBatchT<D> nb0;
       load_batch_new_t<D>(nk, nv, p0, p0 + T, p0, nb0, lane);
       compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, svis);
+    }
+  } else if constexpr (NBW > 0) {
+#pragma unroll
+    for (int i = 0; i < NBW; i++) {
+      const uint32_t b = wv + 4 * i, kb = kbeg + 32 * b;
+      if (b < nb) {
+        if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+        else compute_batch_t<D, NCT, false>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+      }
     }
   } else {
     for (uint32_t b = wv; b < nb; b += 4) {
@@ -209,14 +298,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((D == 64 &&
 // length in meta says how many count), then the parts are added in part order through LDS.
 // P grows with the grid's splits (long contexts at one stream), so no thread waits for more
 // than one round of loads. XSA and the gate are off (xsa = 0, gate = 1).
-template <int D>
+template <int D, bool INL>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t P) {
   __shared__ f32x4 so[256];
   __shared__ float sl[256];
   const uint32_t G4 = 256 / P, part = threadIdx.x / G4, gi = threadIdx.x % G4;
   const uint32_t r = blockIdx.x, g = blockIdx.y, i4 = blockIdx.z * G4 + gi;
-  const uint32_t t0 = p.n_inline ? p.inl[3 * r] : p.runs[2 * r];
-  const uint32_t T = p.n_inline ? p.inl[3 * r + 1] : p.runs[2 * r + 1];
+  uint32_t t0, T, seq;
+  run_header<INL>(p, r, t0, T, seq);
   const uint32_t ncols = T * p.G;
   const bool live = 4 * i4 < ncols * D;
   const uint32_t col = live ? (4 * i4) / D : 0u, d = (4 * i4) % D;
@@ -266,9 +355,15 @@ void attn_init() {
   static bool done = false;
   if (done) return;
   done = true;
-#define SV_ATTR(DD, N)                                                                                       \
-  (void)hipFuncSetAttribute((const void*)attn_verify_kernel<DD, N>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+#define SV_ATTR2(DD, N, B, I)                                                                                      \
+  (void)hipFuncSetAttribute((const void*)attn_verify_kernel<DD, N, B, I>, hipFuncAttributeMaxDynamicSharedMemorySize, \
                             (int)((size_t)4 * 16 * N * DD * 4 + (size_t)4 * 16 * N * 4))
+#define SV_ATTR1(DD, N, B) \
+  SV_ATTR2(DD, N, B, true); \
+  SV_ATTR2(DD, N, B, false)
+#define SV_ATTR(DD, N) SV_ATTR1(DD, N, 0)
+  SV_ATTR1(64, 1, SV_ATTN_NBW);
+  SV_ATTR1(64, 2, SV_ATTN_NBW);
   SV_ATTR(64, 1);
   SV_ATTR(64, 2);
   SV_ATTR(64, 3);
@@ -278,7 +373,21 @@ void attn_init() {
   SV_ATTR(128, 3);
   SV_ATTR(128, 4);
 #undef SV_ATTR
+#undef SV_ATTR1
+#undef SV_ATTR2
 }
+
+// Compute units of the current device (the all-batches-in-flight choice).
+static uint32_t attn_cus() {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+  }
+  return (uint32_t)cus;
+}
+int g_attn_allin = -1;  // -1: by shape; 0 / 1: force the one-batch-ahead / all-batches variant where built
 
 static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
   const uint32_t cols = max_run * (sh->n_heads / sh->n_kv_heads);
@@ -364,8 +473,21 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);
     const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
-#define SV_ATTN(DD, N) launch((attn_verify_kernel<DD, N>), grid, dim3(256), shm, stream, p)
-    if (D == 64) {
+    const bool inl = p.n_inline != 0;
+#define SV_ATTN3(DD, N, B)                                                          \
+  do {                                                                              \
+    if (inl) launch((attn_verify_kernel<DD, N, B, true>), grid, dim3(256), shm, stream, p);  \
+    else launch((attn_verify_kernel<DD, N, B, false>), grid, dim3(256), shm, stream, p);     \
+  } while (0)
+#define SV_ATTN(DD, N) SV_ATTN3(DD, N, 0)
+    // All of a wave's batches in flight where the grid is about one workgroup per CU (latency,
+    // not throughput, bounds it) and a wave has at most SV_ATTN_NBW batches.
+    const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW;
+    const bool allin = fits && (g_attn_allin == 1 || (g_attn_allin < 0 && (size_t)args->max_splits * NKV * n_runs <= attn_cus()));
+    if (allin) {
+      if (nct == 1) SV_ATTN3(64, 1, SV_ATTN_NBW);
+      else SV_ATTN3(64, 2, SV_ATTN_NBW);
+    } else if (D == 64) {
       switch (nct) {
         case 1: SV_ATTN(64, 1); break;
         case 2: SV_ATTN(64, 2); break;
@@ -381,6 +503,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
       }
     }
 #undef SV_ATTN
+#undef SV_ATTN3
     SV_TRY_LAUNCH("attn_verify");
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
@@ -388,8 +511,14 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   uint32_t P = 1;
   while (P < 64 && 8 * P < args->max_splits) P *= 2;
   const uint32_t G4 = 256 / P, mz = (maxcols * D / 4 + G4 - 1) / G4;
-  if (D == 64) launch(attn_merge_kernel<64>, dim3(n_runs, NKV, mz), dim3(256), 0, stream, p, P);
-  else launch(attn_merge_kernel<128>, dim3(n_runs, NKV, mz), dim3(256), 0, stream, p, P);
+  const dim3 mg(n_runs, NKV, mz);
+  if (D == 64) {
+    if (p.n_inline) launch(attn_merge_kernel<64, true>, mg, dim3(256), 0, stream, p, P);
+    else launch(attn_merge_kernel<64, false>, mg, dim3(256), 0, stream, p, P);
+  } else {
+    if (p.n_inline) launch(attn_merge_kernel<128, true>, mg, dim3(256), 0, stream, p, P);
+    else launch(attn_merge_kernel<128, false>, mg, dim3(256), 0, stream, p, P);
+  }
   return check_launch("attn_merge");
 }
 

@@ -34,6 +34,22 @@ struct AttnParams {
   uint32_t inl[3 * SV_INLINE_RUNS];
 };
 
+// Run r's first token, rows and sequence slot: from the kernel arguments (INL: the launch
+// carries the runs, read by scalar loads issued with the other arguments, so no round trip is
+// spent on the header alone) or from runs / meta.
+template <bool INL>
+__device__ __forceinline__ void run_header(const AttnParams& p, uint32_t r, uint32_t& t0, uint32_t& T, uint32_t& seq) {
+  if constexpr (INL) {
+    t0 = p.inl[3 * r];
+    T = p.inl[3 * r + 1];
+    seq = p.inl[3 * r + 2];
+  } else {
+    t0 = p.runs[2 * r];
+    T = p.runs[2 * r + 1];
+    seq = p.meta[2 * t0];
+  }
+}
+
 // Step constants of one run, cached in LDS by the persistent step for all layers: positions
 // and visibility of its T new rows, the layer-0 cache element offset of each new key (for
 // kv head g), and the rope (cos, sin) of each row's position.
@@ -227,18 +243,21 @@ struct KvBatchT {
 };
 
 // Cached batch through per-tile buffer descriptors (load_batch_tiles' contract).
+// oob = 2^31 turns every load into a range-checked miss: zeros, no memory access (a batch
+// slot past the split's last batch).
 template <int D>
-__device__ __forceinline__ void load_batch_tiles_t(const AttnParams& p, const size_t* toff, KvBatchT<D>& b, int lane) {
+__device__ __forceinline__ void load_batch_tiles_t(const AttnParams& p, const size_t* toff, KvBatchT<D>& b, int lane,
+                                                   uint32_t oob = 0) {
   constexpr int KST = D / 32, NV = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
-  const uint32_t ko = (uint32_t)(c16 * D + 8 * q) * 2;
+  const uint32_t ko = (uint32_t)(c16 * D + 8 * q) * 2 + oob, vo = 16u * lane + oob;
 #pragma unroll
   for (int mt = 0; mt < 2; mt++) {
     const __amdgpu_buffer_rsrc_t krs = coherent_rsrc(p.kc + toff[mt]), vrs = coherent_rsrc(p.vc + toff[mt]);
 #pragma unroll
     for (int ks = 0; ks < KST; ks++) b.kw[mt][ks] = buf_ld16(krs, ko + 64 * ks, 0);
 #pragma unroll
-    for (int v = 0; v < NV; v++) b.vr[mt][v] = buf_ld16(vrs, 16 * lane + 1024 * v, 0);
+    for (int v = 0; v < NV; v++) b.vr[mt][v] = buf_ld16(vrs, vo + 1024 * v, 0);
   }
 }
 
@@ -393,13 +412,12 @@ __device__ __forceinline__ void qload(const AttnParams& p, uint32_t t0, uint32_t
   }
 }
 
+// The rope words of a lane's columns (all columns requested together).
 template <int D, int NCT>
-__device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r, bf16x8 (&qh)[NCT][D / 32],
-                                        bf16x8 (&ql)[NCT][D / 32], int lane, const RunConsts* rc = nullptr) {
+__device__ __forceinline__ void qrope_load(const AttnParams& p, uint32_t ncols, const QRaw<D, NCT>& r,
+                                           float2 (&cs)[NCT][D / 32][4], int lane, const RunConsts* rc = nullptr) {
   constexpr int KST = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
-  // Rope words first (all columns), so their loads are in flight together.
-  float2 cs[NCT][KST][4];
 #pragma unroll
   for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
@@ -412,6 +430,15 @@ __device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRa
                          : rc ? rc->rope[r.pos[ct]][j]
                               : *(const float2*)(p.rope + ((size_t)r.pos[ct] * SV_ROPE_PAIRS + j) * 2);
       }
+}
+
+// Norm, RoPE (words from qrope_load), scale and hi/lo split of the raw queries.
+template <int D, int NCT>
+__device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r,
+                                           const float2 (&cs)[NCT][D / 32][4], bf16x8 (&qh)[NCT][D / 32],
+                                           bf16x8 (&ql)[NCT][D / 32], int lane) {
+  constexpr int KST = D / 32;
+  const int c16 = lane & 15, q = lane >> 4;
 #pragma unroll
   for (int ct = 0; ct < NCT; ct++) {
     const bool ok = 16 * ct + c16 < ncols;
@@ -441,6 +468,14 @@ __device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRa
       split8(v, qh[ct][ks], ql[ct][ks]);
     }
   }
+}
+
+template <int D, int NCT>
+__device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r, bf16x8 (&qh)[NCT][D / 32],
+                                        bf16x8 (&ql)[NCT][D / 32], int lane, const RunConsts* rc = nullptr) {
+  float2 cs[NCT][D / 32][4];
+  qrope_load<D, NCT>(p, ncols, r, cs, lane, rc);
+  qfinish_cs<D, NCT>(p, ncols, r, cs, qh, ql, lane);
 }
 
 // Queries of columns 16 ct + c16 (kernels.metal:1022-1039 with norm_rope :727-736): rms-norm

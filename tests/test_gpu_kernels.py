@@ -274,13 +274,28 @@ ATTN_CASES = [
     ([3, 5, 2], [31, 100, 64], 32, False),
     ([16], [300], 64, True),             # a 16-row draft tree
     ([16, 9, 1], [33, 1000, 17], 96, True),
+    ([5], [8192], 384, False),           # config 1's split: three batches per wave
+    ([5, 4], [1000, 2047], 512, False),  # four batches per wave, a partial last split
+    ([2], [700], 160, False),            # five batches: waves with one and two
 ]
 
 
 @pytest.mark.parametrize("runs_T,p0s,split,tree", ATTN_CASES)
 @pytest.mark.parametrize("rope", [1, 0])
-def test_attn_verify(gpu, runs_T, p0s, split, tree, rope):
-    banner(f"attn runs={runs_T} p0={p0s} split={split} tree={tree} rope={rope}")
+@pytest.mark.parametrize("allin", [1, 0])
+def test_attn_verify(gpu, runs_T, p0s, split, tree, rope, allin):
+    """Both cached-key variants (all of a wave's batches in flight, where built: up to 32
+    columns per kv head and 512 keys per split; one batch ahead) against the oracle."""
+    banner(f"attn runs={runs_T} p0={p0s} split={split} tree={tree} rope={rope} allin={allin}")
+    sel = C.c_int.in_dll(L.lib(), "_ZN2sv12g_attn_allinE")
+    sel.value = allin
+    try:
+        _attn_verify_case(runs_T, p0s, split, tree, rope)
+    finally:
+        sel.value = -1
+
+
+def _attn_verify_case(runs_T, p0s, split, tree, rope):
     sh = SH
     c = make_attn_case(sh, runs_T, p0s, seed=len(runs_T) * 31 + split, tree=tree)
     freq = oracle.np.asarray((500000.0 ** (-2.0 * np.arange(32) / 64)), np.float32)
