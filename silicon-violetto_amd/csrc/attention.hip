@@ -40,13 +40,21 @@ namespace sv {
 
 // Batches per wave of the all-in-flight variant (splits of at most 128 x this many keys).
 constexpr int SV_ATTN_NBW = 4;
+// Batch slots per wave of the streaming variant: one batch is multiplied while the other is in
+// flight (three or four slots measured no faster at 64 columns per kv head, which is bound by
+// its chain of products and exponentials, not by loads in flight).
+constexpr int ATTN_RING = 2;
+// Waves per SIMD the register budget allows: three up to 32 columns per kv head (streaming
+// variant), two otherwise for D = 64 (64 columns fit in 228 registers without spills; 3 %
+// faster than one wave per SIMD on the trees), one for D = 128.
+constexpr int attn_waves(int D, int NCT, int NBW) { return (NBW == 0 && D == 64 && NCT <= 2) ? 3 : (D == 64 ? 2 : 1); }
 
 // NBW = 0: each wave keeps one batch in flight ahead of the one it multiplies (any split).
 // NBW > 0 (splits of at most 128 NBW keys, grids of about one workgroup per CU): each wave
 // requests all of its batches at once, after the queries, positions and page-table words (one
 // round trip) and the rope words, and builds the queries while they arrive.
 template <int D, int NCT, int NBW, bool INL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NBW == 0 && D == 64 && NCT <= 2) ? 3 : 1))) void attn_verify_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(D, NCT, NBW)))) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
   extern __shared__ __attribute__((aligned(16))) float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
   __shared__ uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
@@ -62,7 +70,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NBW == 0 &
   // round trip is spent on them alone.
   __shared__ uint32_t svis[SV_MAX_RUN];
   const uint32_t visw = p.vis[t0 + min((uint32_t)tid, T - 1)];
-  KvBatchT<D> cur;
+  constexpr int R = ATTN_RING;
+  KvBatchT<D> ring[NBW == 0 ? R : 1];
   const uint32_t kbeg = s * p.split;
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
   uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
@@ -83,9 +92,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NBW == 0 &
   if constexpr (NBW == 0) {
     if ((uint32_t)lane < 2 * nbw_full)
       tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
-    {
-      const size_t toffs[2] = {readlane64(tile_off, 0), readlane64(tile_off, 1)};
-      load_batch_tiles_t<D>(p, toffs, cur, lane);
+#pragma unroll
+    for (int i = 0; i < R - 1; i++) {
+      const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
+      load_batch_tiles_t<D>(p, toffs, ring[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
     }
     p0 = p.meta[2 * t0 + 1];
     build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
@@ -210,17 +220,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((NBW == 0 &
       }
     }
   } else {
-    for (uint32_t b = wv; b < nb; b += 4) {
-      KvBatchT<D> nxt;
-      // unconditional: past the split's last batch the tiles are read and never used
-      const int li = (int)min(2 * ((b + 4 - wv) / 4), 62u);
-      const size_t toffs[2] = {readlane64(tile_off, li), readlane64(tile_off, li + 1)};
-      load_batch_tiles_t<D>(p, toffs, nxt, lane);
-      __builtin_amdgcn_sched_barrier(0);  // the next batch's loads go out before this batch's work
-      const uint32_t kb = kbeg + 32 * b;
-      if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
-      else compute_batch_t<D, NCT, false>(p, cur, kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
-      cur = nxt;
+    // The wave's j-th batch (wv + 4 j of the split) lives in slot j % R; the batch R - 1 ahead
+    // is requested (slots past the wave's last batch read nothing) before batch j is multiplied.
+    const uint32_t nbw = nb > (uint32_t)wv ? (nb - wv + 3) / 4 : 0u;
+    for (uint32_t j0 = 0; j0 < nbw; j0 += R) {
+#pragma unroll
+      for (int i = 0; i < R; i++) {
+        const uint32_t j = j0 + i, jn = j + R - 1;
+        const int li = (int)min(2 * jn, 62u);
+        const size_t toffs[2] = {readlane64(tile_off, li), readlane64(tile_off, li + 1)};
+        load_batch_tiles_t<D>(p, toffs, ring[(i + R - 1) % R], lane, jn < nbw ? 0u : 0x80000000u);
+        __builtin_amdgcn_sched_barrier(0);  // the loads go out before this batch's work
+        if (j < nbw) {
+          const uint32_t kb = kbeg + 32 * (wv + 4 * j);
+          if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+          else compute_batch_t<D, NCT, false>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+        }
+      }
     }
   }
 
