@@ -973,7 +973,6 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
   if (g_gemm_tune.rtw)
     return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
   const uint32_t nch = k / GKC;
-  const bool i8 = fmt == SV_FMT_I8;
   // Wide matrices at many rows: 256-row x 64-token blocks halve the operand traffic through
   // L2 (weights re-read per token block, X per row block) where they still fill the device.
   // Two chunks in flight (not four) keep that shape at two waves per SIMD.
@@ -981,20 +980,37 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
   // Below that, 256-row x 32-token blocks without splits where they still make 512 workgroups
   // (measured on gate_up at 256 and 320 rows: 3-25% faster than 128-row blocks in splits).
   if (!grouped && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 31) / 32) >= 512) return GemmCfg{4, 2, 1, 2};
-  GemmCfg c{2, 2, 1, 4};
-  if (!i8) {
+  // Long reductions (k of 8192 or more): the largest row block (256, 128, 64 rows) that makes
+  // 512 workgroups with four or eight k splits (measured on the down projection at 24-512
+  // rows: up to 30 % faster than fewer splits or smaller blocks).
+  if (nch >= 128) {
+    for (int rtw : {4, 2, 1}) {
+      if (rtw > 1 && (grouped || m % (64u * rtw))) continue;
+      const uint32_t cells = m / (64u * rtw) * ((n + 31) / 32);
+      for (int s : {4, 8})
+        if (nch % s == 0 && cells * s >= 512) return GemmCfg{rtw, 2, s, 2};
+    }
+    for (int s : {8, 4, 2})
+      if (nch % s == 0) return GemmCfg{1, 2, s, 2};
+    return GemmCfg{1, 2, 1, 2};
+  }
+  // Otherwise 128-row x 32-token blocks, two chunks in flight (more waves per SIMD; measured as
+  // fast or faster than 48- and 80-token blocks with four in flight for bf16 too), except for
+  // weights too large to stay cached between token blocks (the 131 MB bf16 head): there every
+  // token block re-reads them from HBM, so 48- or 80-token blocks (the one padding n least),
+  // four chunks in flight and up to eight splits.
+  GemmCfg c{2, 2, 1, 2};
+  int s_first = 2, s_last = 4;
+  if ((uint64_t)m * k * (fmt == SV_FMT_I8 ? 1 : 2) > (96ull << 20)) {
     uint32_t best = ~0u;
     for (int nt : {3, 5}) {
       const uint32_t pad = (n + 16 * nt - 1) / (16 * nt) * 16 * nt - n;
       if (pad < best || (pad == best && nt == 5)) best = pad, c.nt = nt;
     }
+    c.d = 4, s_first = 1, s_last = 8;
   }
   if (grouped || m % 128) c.rtw = 1;
-  if (i8) c.d = 2;  // measured: as fast or faster than four chunks in flight (more waves per SIMD)
   const uint32_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt);
-  // Long int8 reductions (k of 8192) run at least four splits of at most 32 chunks each:
-  // measured faster on the down projection than two splits, at the same or fewer workgroups.
-  const int s_first = i8 ? (nch >= 128 ? 4 : 2) : 1, s_last = i8 ? 4 : 8;
   for (;;) {
     const uint32_t cells = m / (64 * c.rtw) * n_tblk;
     c.s = 1;
