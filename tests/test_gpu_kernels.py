@@ -277,6 +277,8 @@ ATTN_CASES = [
     ([5], [8192], 384, False),           # config 1's split: three batches per wave
     ([5, 4], [1000, 2047], 512, False),  # four batches per wave, a partial last split
     ([2], [700], 160, False),            # five batches: waves with one and two
+    ([5, 1, 3, 5, 2, 4], [4000, 0, 17, 9000, 1, 2500], 256, False),  # empty and one-key contexts among long ones
+    ([4] * 40, [37 * i for i in range(40)], 128, False),              # 40 runs (not inline), short contexts
 ]
 
 
