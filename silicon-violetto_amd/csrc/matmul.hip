@@ -977,6 +977,20 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
   // L2 (weights re-read per token block, X per row block) where they still fill the device.
   // Two chunks in flight (not four) keep that shape at two waves per SIMD.
   if (!grouped && n >= 384 && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 63) / 64) >= 384) return GemmCfg{4, 4, 1, 2};
+  // Weights too large to stay cached between token blocks (the 131 MB bf16 head) are re-read
+  // from HBM by every token block: below that shape, the fewest token blocks (48 or 80 tokens,
+  // whichever pads n least), no k splits, four chunks in flight for 48 tokens (measured with
+  // the weights cold: 20-25 % faster than 32-token blocks or split k at 40 and 160 rows).
+  if (!grouped && (uint64_t)m * k * (fmt == SV_FMT_I8 ? 1 : 2) > (96ull << 20)) {
+    GemmCfg c{m % 128 ? 1 : 2, 3, 1, 4};
+    uint32_t best = ~0u;
+    for (int nt : {3, 5}) {
+      const uint32_t pad = (n + 16 * nt - 1) / (16 * nt) * 16 * nt - n;
+      if (pad < best || (pad == best && nt == 5)) best = pad, c.nt = nt;
+    }
+    if (c.nt == 5) c.d = 2;
+    return c;
+  }
   // Below that, 256-row x 32-token blocks without splits where they still make 512 workgroups
   // (measured on gate_up at 256 and 320 rows: 3-25% faster than 128-row blocks in splits).
   if (!grouped && m % 256 == 0 && (uint64_t)(m / 256) * ((n + 31) / 32) >= 512) return GemmCfg{4, 2, 1, 2};
@@ -995,20 +1009,9 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
     return GemmCfg{1, 2, 1, 2};
   }
   // Otherwise 128-row x 32-token blocks, two chunks in flight (more waves per SIMD; measured as
-  // fast or faster than 48- and 80-token blocks with four in flight for bf16 too), except for
-  // weights too large to stay cached between token blocks (the 131 MB bf16 head): there every
-  // token block re-reads them from HBM, so 48- or 80-token blocks (the one padding n least),
-  // four chunks in flight and up to eight splits.
+  // fast or faster than 48- and 80-token blocks with four in flight for bf16 too).
   GemmCfg c{2, 2, 1, 2};
-  int s_first = 2, s_last = 4;
-  if ((uint64_t)m * k * (fmt == SV_FMT_I8 ? 1 : 2) > (96ull << 20)) {
-    uint32_t best = ~0u;
-    for (int nt : {3, 5}) {
-      const uint32_t pad = (n + 16 * nt - 1) / (16 * nt) * 16 * nt - n;
-      if (pad < best || (pad == best && nt == 5)) best = pad, c.nt = nt;
-    }
-    c.d = 4, s_first = 1, s_last = 8;
-  }
+  const int s_first = 2, s_last = 4;
   if (grouped || m % 128) c.rtw = 1;
   const uint32_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt);
   for (;;) {
