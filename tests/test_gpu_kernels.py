@@ -569,19 +569,22 @@ def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
 
 @pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
                                                   (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4),
-                                                  (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4), (4, 4, 2, 2), (4, 3, 1, 2)])
+                                                  (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4), (4, 4, 2, 2), (4, 3, 1, 2),
+                                                  (4, 2, 4, 2), (4, 2, 1, 2), (2, 2, 4, 2), (1, 2, 2, 2), (2, 5, 1, 2),
+                                                  (2, 2, 8, 2), (1, 2, 8, 2), (4, 2, 8, 2)])
 @pytest.mark.parametrize("n", [17, 100])
 def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
     """Every GEMM launch shape (row tiles per wave, token tiles, k splits merged by the last
     split to arrive, chunks in flight) gives the oracle's result: int8 with EPI_NORM (sums of
     squares carried across splits, the inverse norm written once) and bf16 with EPI_RESID in
     the tiled layout, with a row gather, ragged token blocks (17, 100 rows) and a k whose chunk
-    count leaves a partial round of zero chunks (k = 1280: 20 chunks); two calls share one
-    workspace. The shape is forced through the library's internal override."""
+    count leaves a partial round of zero chunks (k = 1280: 20 chunks; 2560 = 40 chunks for eight
+    splits, five each); two calls share one workspace. The shape is forced through the
+    library's internal override."""
     banner(f"gemm launch shape rtw={rtw} nt={nt} splits={splits} depth={depth} n={n}")
     tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv11g_gemm_tuneE")
     rng = np.random.default_rng(rtw * 1000 + nt * 100 + splits * 10 + depth + n)
-    m, k = {1: 384, 2: 512, 4: 768}[rtw], 1280
+    m, k = {1: 384, 2: 512, 4: 768}[rtw], (2560 if splits == 8 else 1280)
     ws = K.Workspace(16 << 20)
     try:
         tune[0], tune[1], tune[2], tune[3] = rtw, nt, splits, depth
