@@ -7,9 +7,10 @@
 //     head g G + c % G), in NCT tiles of 16. Each lane builds its columns' queries in
 //     registers: rms-norm over the head (no gain), RoPE on pairs (2j, 2j+1), j < 32, times
 //     softmax scale * log2 e, split into bf16 hi + lo MFMA operands.
-//   - Splits 0..nsplit-2 own `split` cached keys each; the last split owns the run's new
-//     keys: it norms and ropes them, rounds K and V to bf16, writes them to the cache at
-//     p0 + row and keeps them in LDS.
+//   - Splits own `split` cached keys each. The run's new keys (norm, RoPE, K and V rounded to
+//     bf16, written to the cache at p0 + row and kept in LDS) go to a split of their own after
+//     the cached ones (all-in-flight variant) or to the last cached split, after its batches
+//     (streaming variant; without cached keys the one split holds only them).
 //   - Keys go in batches of 32 (wave w takes batches w, w + 4, ..., the next one's K/V in
 //     flight while the current one is multiplied; the first is issued before the queries
 //     are built): S^T = K Q^T on
@@ -48,6 +49,13 @@ constexpr int ATTN_RING = 2;
 // variant), two otherwise for D = 64 (64 columns fit in 228 registers without spills; 3 %
 // faster than one wave per SIMD on the trees), one for D = 128.
 constexpr int attn_waves(int D, int NCT, int NBW) { return (NBW == 0 && D == 64 && NCT <= 2) ? 3 : (D == 64 ? 2 : 1); }
+// Whether a run's new keys get a split of their own. All-in-flight variant: yes (it runs beside
+// the cached splits on an otherwise idle CU). Streaming variant up to 32 columns per kv head:
+// no, the last cached split takes them (a split of new keys alone is a short workgroup that
+// holds a resident slot and pushes cached splits into a later round: configs[2] attention 3 %
+// faster). Wider runs: yes (their splits are bound by their own products, and the extra
+// workgroup adds parallelism: the trees 2 % faster).
+constexpr bool attn_newest_own(int NCT, int NBW) { return NBW > 0 || NCT >= 3; }
 
 // NBW = 0: each wave keeps one batch in flight ahead of the one it multiplies (any split).
 // NBW > 0 (splits of at most 128 NBW keys, grids of about one workgroup per CU): each wave
@@ -176,7 +184,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane);
   }
 
-  const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;
+  const uint32_t nsplit = attn_nsplit(p, p0);
   if (nsplit > p.max_splits) {
     // The grid has too few splits for this run's context: its output is NaN (never a
     // partial sum) and the counter is left alone.
@@ -188,7 +196,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     return;
   }
   if (s >= nsplit) return;
-  const bool newest = s == nsplit - 1;
+  // newest: a split of the new keys alone; takes_new: the last cached split also takes them
+  // (attn_newest_own; the launch sets p.newest_own to match).
+  const bool newest = attn_newest_own(NCT, NBW) && s == nsplit - 1, takes_new = !attn_newest_own(NCT, NBW) && s == nsplit - 1;
 
   const uint32_t kend = newest ? p0 : min(kbeg + p.split, p0);
   const uint32_t nb = newest ? 0u : (kend - kbeg + 31) / 32;
@@ -236,6 +246,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
           if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
           else compute_batch_t<D, NCT, false>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
         }
+      }
+    }
+    if (takes_new) {
+      // The run's new keys after this split's cached ones: to the cache and LDS (no other
+      // workgroup reads positions p0 on), then wave 0 multiplies them (the barrier orders every
+      // wave's batches before it).
+      new_keys<D, false>(p, seq, g, t0, T, p0, nk, nv, tid, 256);
+      __syncthreads();
+      if (wv == 0) {
+        KvBatchT<D> nb0;
+        load_batch_new_t<D>(nk, nv, p0, p0 + T, p0, nb0, lane);
+        compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, svis);
       }
     }
   }
@@ -342,7 +364,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t 
       ov[u] = in ? *(const f32x4*)(po + x * so_stride) : f32x4{0.f, 0.f, 0.f, 0.f};
       lv[u] = in ? pl[x * p.maxcols] : 0.0f;
     }
-    const uint32_t nsplit = (p0 + p.split - 1) / p.split + 1;  // after the loads are issued
+    const uint32_t nsplit = attn_nsplit(p, p0);  // after the loads are issued
 #pragma unroll
     for (int u = 0; u < 8; u++)
       if (sp + u * P < nsplit) {
@@ -360,7 +382,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t 
       l += sl[j * G4 + gi];
     }
   }
-  if (!live || (p0 + p.split - 1) / p.split + 1 > p.max_splits) return;  // NaN written by the attention
+  if (!live || attn_nsplit(p, p0) > p.max_splits) return;  // NaN written by the attention
   const uint32_t i = col / p.G, h = g * p.G + col % p.G;
   *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
 }
@@ -481,11 +503,18 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.layer = kv->kv_layer;
   p.maxcols = maxcols;
   p.n_inline = 0;
+  p.newest_own = 1;
   if (host_runs && n_runs <= SV_INLINE_RUNS) {
     p.n_inline = n_runs;
     for (uint32_t i = 0; i < 3 * n_runs; i++) p.inl[i] = host_runs[i];
   }
   attn_init();
+  // All of a wave's batches in flight where the grid is about one workgroup per CU (latency,
+  // not throughput, bounds it) and a wave has at most SV_ATTN_NBW batches. The new keys' split
+  // follows attn_newest_own for the variant launched.
+  const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW;
+  const bool allin = fits && (g_attn_allin == 1 || (g_attn_allin < 0 && (size_t)args->max_splits * NKV * n_runs <= attn_cus()));
+  p.newest_own = attn_newest_own((int)nct, allin ? SV_ATTN_NBW : 0) ? 1u : 0u;
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);
     const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
@@ -496,10 +525,6 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     else launch((attn_verify_kernel<DD, N, B, false>), grid, dim3(256), shm, stream, p);     \
   } while (0)
 #define SV_ATTN(DD, N) SV_ATTN3(DD, N, 0)
-    // All of a wave's batches in flight where the grid is about one workgroup per CU (latency,
-    // not throughput, bounds it) and a wave has at most SV_ATTN_NBW batches.
-    const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW;
-    const bool allin = fits && (g_attn_allin == 1 || (g_attn_allin < 0 && (size_t)args->max_splits * NKV * n_runs <= attn_cus()));
     if (allin) {
       if (nct == 1) SV_ATTN3(64, 1, SV_ATTN_NBW);
       else SV_ATTN3(64, 2, SV_ATTN_NBW);

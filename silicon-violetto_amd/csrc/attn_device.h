@@ -32,7 +32,16 @@ struct AttnParams {
   // them from `runs` / `meta`.
   uint32_t n_inline;
   uint32_t inl[3 * SV_INLINE_RUNS];
+  // 1: a run's new keys have a split of their own (after its cached splits); 0: its last cached
+  // split (or the only split, without cached keys) takes them too.
+  uint32_t newest_own;
 };
+
+// Splits of a run with p0 cached keys.
+__device__ __forceinline__ uint32_t attn_nsplit(const AttnParams& p, uint32_t p0) {
+  const uint32_t c = (p0 + p.split - 1) / p.split;
+  return p.newest_own ? c + 1 : (c ? c : 1u);
+}
 
 // Run r's first token, rows and sequence slot: from the kernel arguments (INL: the launch
 // carries the runs, read by scalar loads issued with the other arguments, so no round trip is
