@@ -811,6 +811,7 @@ sv_status step_launch(hipStream_t stream, const StepLaunch& a) {
   ap.layer = 0;
   ap.maxcols = maxcols;
   ap.n_inline = 0;
+  ap.newest_own = 1;  // this kernel's attention keeps the new keys apart (its own phases)
   p.n_runs = a.n_runs;
   p.pairs = a.n_runs * NKV;
   p.wpp = G / p.pairs;
