@@ -269,7 +269,8 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for {max(args.gpus, world)} GPUs). "
-              "Streams would shard across GPUs with no exchange per step; see DESIGN.md.", file=sys.stderr)
+              "Streams would shard across GPUs (one engine and page pool per GPU, a full weight "
+              "replica each) with no exchange per step.", file=sys.stderr)
         return 2
 
     import torch
