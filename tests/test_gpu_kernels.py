@@ -297,14 +297,13 @@ def test_attn_verify(gpu, runs_T, p0s, split, tree, rope, allin):
         sel.value = -1
 
 
-def _attn_verify_case(runs_T, p0s, split, tree, rope):
-    sh = SH
+def _attn_verify_case(runs_T, p0s, split, tree, rope, sh=SH):
     c = make_attn_case(sh, runs_T, p0s, seed=len(runs_T) * 31 + split, tree=tree)
     freq = oracle.np.asarray((500000.0 ** (-2.0 * np.arange(32) / 64)), np.float32)
     rope_tab = oracle.rope_table(freq, max(p0s) + 20)
     kv = L.KvArgs(1, 0, 0, len(runs_T), c["page_shift"], c["n_pages"], c["max_pages"], 0)
     max_splits = max(-(-p // split) + 1 for p in p0s)
-    args = L.AttnArgs(split, max_splits, 0.125 * 1.4426950408889634, rope, 0, 0, 0, 0, 0)
+    args = L.AttnArgs(split, max_splits, sh.head_dim ** -0.5 * 1.4426950408889634, rope, 0, 0, 0, 0, 0)
     runs_flat = c["runs"].reshape(-1).copy()
     k_ref, v_ref = c["k"].copy(), c["v"].copy()
     ref = oracle.attn_verify(L, sh, c["qkv"], c["meta"].reshape(-1).copy(), k_ref, v_ref, c["page_table"], rope_tab,
@@ -321,6 +320,19 @@ def _attn_verify_case(runs_T, p0s, split, tree, rope):
     assert np.array_equal(vg, v_ref), "V cache differs"
     dk = np.abs(oracle.bf16_to_f32(kg) - oracle.bf16_to_f32(k_ref))
     assert (dk <= 2 ** -7 * np.abs(oracle.bf16_to_f32(k_ref)) + 1e-30).all(), "K cache off by more than one step"
+
+
+SH128 = ModelShape(n_layers=2, n_heads=16, n_kv_heads=4, head_dim=128)
+
+
+@pytest.mark.parametrize("runs_T,p0s,split,tree", [([5], [700], 128, False), ([3, 5, 2], [31, 100, 64], 32, False),
+                                                   ([16], [300], 64, True)])
+@pytest.mark.parametrize("rope", [1, 0])
+def test_attn_verify_head_dim_128(gpu, runs_T, p0s, split, tree, rope):
+    """The head_dim 128 instantiations (16 query heads over 4 kv heads: 4 to 64 columns per kv
+    head; RoPE on dims 0..63 only, as the table has 32 pairs) against the oracle."""
+    banner(f"attn D=128 runs={runs_T} p0={p0s} split={split} tree={tree} rope={rope}")
+    _attn_verify_case(runs_T, p0s, split, tree, rope, sh=SH128)
 
 
 # ------------------------------------------------------------------------------ sampler
