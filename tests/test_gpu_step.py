@@ -23,12 +23,12 @@ LOGIT_ATOL, LOGIT_RTOL = 2e-2, 1e-2
 
 
 def build_pair(shape: ModelShape, *, ctx: int, n_seqs: int = 1, seed: int = 0, int8: bool = True, page_shift=4,
-               max_seq_len=1024, scalars=None, shuffle=False, step_kernel=True):
+               max_seq_len=1024, scalars=None, shuffle=False, step_kernel=True, split_keys=0, max_head_rows=16):
     model = SyntheticModel.generate(shape, int8=int8, seed=seed, device="cpu", scalars=scalars)
     freq = rope_freq(500000.0, shape.head_dim)
-    eng = Engine(shape, max_seqs=n_seqs, max_step_tokens=16 * n_seqs, max_seq_len=max_seq_len, max_head_rows=16,
+    eng = Engine(shape, max_seqs=n_seqs, max_step_tokens=16 * n_seqs, max_seq_len=max_seq_len, max_head_rows=max_head_rows,
                  kv_tokens=n_seqs * max_seq_len, page_shift=page_shift, attn_scale=0.125, freq=freq,
-                 step_kernel=step_kernel)
+                 step_kernel=step_kernel, split_keys=split_keys)
     gm = model.to("cuda")
     eng.set_model(gm)
     emb, lay, sc = oracle.host_weights(model)
@@ -115,6 +115,32 @@ def test_two_layer_steps_with_replayed_drafts(gpu, scalars, persistent):
         ids_r, logits_r, em_r, extra_r = ref.step(runs)
         res = eng.step(runs, logits=True)
         assert res.info.persistent == int(persistent)
+        compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
+        assert np.array_equal(res.ids, ids_r), "greedy ids diverged (margins within tolerance)"
+
+
+def test_multi_stream_steps(gpu):
+    """Eight sequences (contexts 64-1100) over two layers, three steps of 1-5 drafts each: 17+
+    verify rows (the GEMM path for every matmul) and, with 128-key splits, more attention
+    workgroups than CUs (the streaming variant, each run's last cached split taking its new
+    keys), against the oracle engine."""
+    banner("multi-stream steps")
+    shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
+    ctxs = [300, 1100, 517, 64, 800, 999, 128, 640]
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=ctxs, n_seqs=8, seed=7, max_seq_len=1200,
+                                                 step_kernel=False, split_keys=128, max_head_rows=64)
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ref.seq_len[s], t)
+        ref.set_feed(s, ref.seq_len[s], t)
+    for step in range(3):
+        runs = []
+        for s in slots:
+            k = int(rng.integers(1, 6))
+            runs.append((s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, k)], True))
+        ids_r, logits_r, em_r, extra_r = ref.step(runs)
+        res = eng.step(runs, logits=True)
+        assert sum(len(r[1]) for r in runs) > 16, "the step must take the GEMM path"
         compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
         assert np.array_equal(res.ids, ids_r), "greedy ids diverged (margins within tolerance)"
 
