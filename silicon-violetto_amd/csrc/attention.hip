@@ -41,14 +41,14 @@ namespace sv {
 
 // Batches per wave of the all-in-flight variant (splits of at most 128 x this many keys).
 constexpr int SV_ATTN_NBW = 4;
-// Batch slots per wave of the streaming variant: one batch is multiplied while the other is in
-// flight (three or four slots measured no faster at 64 columns per kv head, which is bound by
-// its chain of products and exponentials, not by loads in flight).
-constexpr int ATTN_RING = 2;
-// Waves per SIMD the register budget allows: three up to 32 columns per kv head (streaming
-// variant), two otherwise for D = 64 (64 columns fit in 228 registers without spills; 3 %
-// faster than one wave per SIMD on the trees), one for D = 128.
-constexpr int attn_waves(int D, int NCT, int NBW) { return (NBW == 0 && D == 64 && NCT <= 2) ? 3 : (D == 64 ? 2 : 1); }
+// Batch slots per wave of the streaming variant: one batch is multiplied while the others are in
+// flight. Up to 32 columns per kv head three slots at two waves per SIMD (measured 1-3 % faster
+// than two slots at three waves per SIMD at 32 streams and 65536 x 8); wider runs two (a third
+// does not fit two waves per SIMD, and at one wave per SIMD it measured no faster).
+constexpr int attn_ring(int NCT) { return NCT <= 2 ? 3 : 2; }
+// Waves per SIMD the register budget allows: two for D = 64 (64 columns fit in 228 registers
+// without spills; 3 % faster than one wave per SIMD on the trees), one for D = 128.
+constexpr int attn_waves(int D, int, int) { return D == 64 ? 2 : 1; }
 // Whether a run's new keys get a split of their own. All-in-flight variant: yes (it runs beside
 // the cached splits on an otherwise idle CU). Streaming variant up to 32 columns per kv head:
 // no, the last cached split takes them (a split of new keys alone is a short workgroup that
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   // round trip is spent on them alone.
   __shared__ uint32_t svis[SV_MAX_RUN];
   const uint32_t visw = p.vis[t0 + min((uint32_t)tid, T - 1)];
-  constexpr int R = ATTN_RING;
+  constexpr int R = attn_ring(NCT);
   KvBatchT<D> ring[NBW == 0 ? R : 1];
   const uint32_t kbeg = s * p.split;
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
