@@ -90,3 +90,15 @@ def test_workspace_sizes_grow_with_work():
     assert lib.sv_matmul_workspace_bytes(0, 2048, 8192) == 0
     sh = L.Shape(2048, 32, 8, 64, 8192, 32000, 32000, 16)
     assert lib.sv_attn_workspace_bytes(C.byref(sh), 32, 64, 16) > lib.sv_attn_workspace_bytes(C.byref(sh), 1, 64, 5)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says so (before any GPU work)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parent.parent
+    out = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=60, cwd=root)
+    assert out.returncode == 2
+    assert "one GPU" in out.stderr
