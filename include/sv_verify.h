@@ -262,14 +262,8 @@ typedef struct sv_engine_config {
   uint32_t page_shift;      /* log2 tokens per page (reference: 7; configs: 4)  */
   float attn_scale;         /* softmax scale (reference ATTN_SCALE, model.rs:19) */
   uint32_t split_keys;      /* cached keys per attention split, multiple of 32; 0: auto */
-  uint32_t options;         /* SV_ENGINE_* bits                                 */
+  uint32_t options;         /* reserved: 0                                      */
 } sv_engine_config;
-
-/* sv_engine_config.options: run all layers of a step in one persistent launch (grid
- * barriers between phases) where it applies (int8 layers of the 1B shape, steps of <= 16
- * rows); otherwise every pipeline group is its own launch. No counterpart in the reference
- * (its encoder always issues one dispatch per pipeline). */
-#define SV_ENGINE_STEP_KERNEL 1u
 
 /* One decoder layer (model.rs:49-67): matrices and scalars. rope: whether the layer's
  * q/k get RoPE (the reference ropes its local layers only, encode.rs:237). */
@@ -346,7 +340,6 @@ typedef struct sv_plan_info {
   uint32_t branches;   /* some verify run has > 2 rows: kv_compact runs */
   uint32_t max_run;
   uint32_t split, max_splits;
-  uint32_t persistent; /* the layers run as one persistent launch (see SV_ENGINE_STEP_KERNEL) */
 } sv_plan_info;
 
 enum {
@@ -393,8 +386,7 @@ enum {
   SV_KIND_COMPACT = 9,
   SV_KIND_REPLAY = 10,
   SV_KIND_ATTN_MERGE = 11, /* the attention split merge (its own launch) */
-  SV_KIND_LAYERS = 12,     /* all layers in one persistent launch (steps of <= 16 rows) */
-  SV_KIND_COUNT = 13
+  SV_KIND_COUNT = 12
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

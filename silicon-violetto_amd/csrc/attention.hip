@@ -22,7 +22,7 @@
 //   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace with
 //     coherent stores (sc1: write-through to the agent-coherent level). attn_merge_kernel,
 //     the next launch, sums the partials of each (run, kv head) output in split order and
-//     writes o / l. With SV_ATTN_MERGE=fused the last split of (run, kv head) to arrive (a
+//     writes o / l. With g_attn_fused_merge set the last split of (run, kv head) to arrive (a
 //     relaxed agent-scope counter: no L2 write-back or invalidate) does the same with
 //     coherent 16-byte loads.
 #include <cstdlib>
@@ -425,6 +425,7 @@ static uint32_t attn_cus() {
   }
   return (uint32_t)cus;
 }
+bool g_attn_fused_merge = false;  // tests: the last split to arrive merges (measured slower)
 int g_attn_allin = -1;  // -1: by shape; 0 / 1: force the one-batch-ahead / all-batches variant where built
 
 static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
@@ -462,12 +463,9 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;
   if (nct > 4) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (64 are built)", max_run * NQ / NKV);
   // The merge runs as its own launch over (run, kv head, column) workgroups (measured
-  // faster at 9-65 splits); with SV_ATTN_MERGE=fused the last split of each (run, kv head)
+  // faster at 9-65 splits); with g_attn_fused_merge set the last split of each (run, kv head)
   // to arrive merges instead.
-  static const bool fused_merge = [] {
-    const char* v = getenv("SV_ATTN_MERGE");
-    return v && strcmp(v, "fused") == 0;
-  }();
+  const bool fused_merge = g_attn_fused_merge;
   const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
   if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
   AttnParams p;

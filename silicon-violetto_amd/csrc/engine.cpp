@@ -167,11 +167,13 @@ uint32_t choose_split(const std::vector<uint32_t>& cached, uint32_t extra, uint3
 
 struct Plan {
   uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
-  bool step_kernel = false;  // all layers in one persistent launch (step.hip)
   std::vector<uint32_t> slots;   // per run
   std::vector<uint32_t> counts;  // per run
   std::vector<uint32_t> verify;  // per run
   std::vector<uint32_t> inl;     // per run: first token, rows, slot (the attention's inline runs)
+  // Steps this plan may run (encodes, graph replays, profiled steps): each advances a run by at
+  // most its row count, and every position it can reach has a reserved page.
+  uint64_t budget = 0, issued = 0;
 };
 
 template <typename T>
@@ -221,14 +223,6 @@ struct sv_engine {
   size_t ws_bytes = 0;
   void* mm_ws = nullptr;  // matmul split-k hand-off (counters stay zero between launches)
   size_t mm_ws_bytes = 0;
-  void* step_ws = nullptr;  // persistent step: barrier words, counters, partials (zeroed once)
-  size_t step_ws_bytes = 0;
-  StepLayerHost* step_layers = nullptr;  // device copy of the layers for the persistent step
-  bool step_layers_dirty = true;
-  // SV_STEP_STAMPS=1: the persistent step records workgroup 0's clock at every phase end and
-  // barrier exit; sv_step prints the per-phase averages to stderr (a developer aid).
-  uint64_t* step_stamps = nullptr;
-  void* step_acts = nullptr;  // per-layer activation slices of the persistent step
 
   // host: page pool (kv.rs) and sequences (engine.rs Seq)
   std::vector<uint32_t> free_pages;
@@ -281,7 +275,7 @@ struct sv_engine {
     if (graph) (void)hipGraphExecDestroy(graph);
     void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
                     head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
-                    attn, mixed, act, inv, logits, ws, mm_ws, step_ws, step_layers, step_stamps, step_acts};
+                    attn, mixed, act, inv, logits, ws, mm_ws};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     for (void* b : packed)
@@ -336,45 +330,6 @@ struct sv_engine {
     return SV_OK;
   }
 
-  sv_status ensure_step(size_t bytes) {
-    if (bytes > step_ws_bytes) {
-      if (graph) return fail(SV_ERR_STATE, "step workspace must grow after a graph was captured");
-      SV_HIP(hipStreamSynchronize(stream), "step workspace");
-      if (step_ws) SV_HIP(hipFree(step_ws), "step workspace");
-      step_ws = nullptr;
-      step_ws_bytes = 0;
-      SV_HIP(hipMalloc(&step_ws, bytes), "step workspace");
-      SV_HIP(hipMemset(step_ws, 0, bytes), "step workspace");
-      step_ws_bytes = bytes;
-    }
-    static const bool stamps_on = [] {
-      const char* v = getenv("SV_STEP_STAMPS");
-      return v && strcmp(v, "1") == 0;
-    }();
-    if (!step_acts) SV_HIP(hipMalloc(&step_acts, step_acts_bytes(&sh)), "step activations");
-    if (stamps_on && !step_stamps) SV_HIP(hipMalloc((void**)&step_stamps, (size_t)(10 * sh.n_layers + 8 + 40) * 8), "stamps");
-    if (step_layers_dirty) {
-      std::vector<StepLayerHost> h(sh.n_layers);
-      for (uint32_t l = 0; l < sh.n_layers; l++) step_fill_layer(&layers[l], &h[l]);
-      if (!step_layers) SV_HIP(hipMalloc((void**)&step_layers, h.size() * sizeof(StepLayerHost)), "step layers");
-      SV_HIP(hipMemcpy(step_layers, h.data(), h.size() * sizeof(StepLayerHost), hipMemcpyHostToDevice), "step layers");
-      step_layers_dirty = false;
-    }
-    return SV_OK;
-  }
-
-  // A persistent step whose barrier wait ran out of time leaves a non-zero error word.
-  sv_status check_step_error() {
-    if (!step_ws) return SV_OK;
-    uint32_t err = 0;
-    SV_HIP(hipMemcpy(&err, (char*)step_ws + step_err_offset(), 4, hipMemcpyDeviceToHost), "step error word");
-    if (err) {
-      SV_HIP(hipMemset((char*)step_ws + step_err_offset(), 0, 4), "step error word");
-      return fail(SV_ERR_HIP, "persistent step: a grid barrier timed out (workgroups not co-resident?)");
-    }
-    return SV_OK;
-  }
-
   sv_status upload(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return SV_OK;
     SV_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "upload");
@@ -406,6 +361,17 @@ struct sv_engine {
     return matmul_launch(stream, &w, x, x_rows, y, base, aux, &a, mm_ws, mm_ws_bytes);
   }
 
+  // Counts `steps` more runs of the plan against its page reservation.
+  sv_status issue(uint64_t steps) {
+    if (!planned) return fail(SV_ERR_STATE, "no plan");
+    if (plan.issued + steps > plan.budget)
+      return fail(SV_ERR_CAPACITY,
+                  "the plan's pages cover %llu steps (%llu run): plan again, with more extra_keys for replays",
+                  (unsigned long long)plan.budget, (unsigned long long)plan.issued);
+    plan.issued += steps;
+    return SV_OK;
+  }
+
   // encode.rs:99-126 encode_forward + :383-412 encode_tail.
   sv_status encode(uint32_t flags) {
     SV_TRY(check_ready());
@@ -418,35 +384,7 @@ struct sv_engine {
     aa.split = P.split;
     aa.max_splits = P.max_splits;
     aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
-    if (P.step_kernel) {
-      StepLaunch sl{};
-      sl.sh = &sh;
-      sl.layers = step_layers;
-      sl.n = n;
-      sl.fmt = SV_FMT_I8;
-      sl.h = h;
-      sl.inv = inv;
-      sl.acts = step_acts;
-      sl.meta = meta;
-      sl.kc = k_cache;
-      sl.vc = v_cache;
-      sl.page_table = page_table;
-      sl.rope = rope;
-      sl.runs = attn_runs;
-      sl.n_runs = P.n_runs;
-      sl.max_run = P.max_run;
-      sl.vis = vis;
-      const sv_kv_args kv = kv_args(0);
-      sl.page_shift = kv.page_shift;
-      sl.n_pages = kv.n_pages;
-      sl.max_pages = kv.max_pages;
-      sl.scale_log2 = aa.scale_log2;
-      sl.ws = step_ws;
-      sl.ws_bytes = step_ws_bytes;
-      sl.stamps = step_stamps;
-      SV_TIMED(SV_KIND_LAYERS, step_launch(stream, sl));
-    }
-    for (uint32_t li = 0; li < sh.n_layers && !P.step_kernel; li++) {
+    for (uint32_t li = 0; li < sh.n_layers; li++) {
       const sv_layer& L = layers[li];
       SV_TIMED(SV_KIND_QKV,
                matmul(L.qkv, n, h, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
@@ -499,6 +437,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   if (cfg->max_seqs == 0 || cfg->max_step_tokens == 0 || cfg->max_seq_len == 0 || cfg->max_head_rows == 0 ||
       cfg->kv_tokens == 0)
     return fail(SV_ERR_ARG, "engine_create: zero capacity");
+  if (cfg->options != 0) return fail(SV_ERR_ARG, "engine_create: options %u (none are defined)", cfg->options);
   if (cfg->page_shift < 4 || cfg->page_shift > 16) return fail(SV_ERR_ARG, "engine_create: page_shift %u", cfg->page_shift);
   if (cfg->split_keys % 32 || cfg->split_keys > 3968)
     return fail(SV_ERR_ARG, "engine_create: split_keys %u (a multiple of 32, at most 3968)", cfg->split_keys);
@@ -678,7 +617,6 @@ extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_
   SV_TRY(pack_into(e, l->down, &slots[3], &used.down));
   e->layers[layer] = used;
   e->layer_set[layer] = true;
-  e->step_layers_dirty = true;
   return SV_OK;
 }
 
@@ -855,10 +793,21 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
       return fail(SV_ERR_CAPACITY, "sequence would reach %llu tokens (max %u)", (unsigned long long)new_len,
                   e->cfg.max_seq_len);
   }
+  // Pages for every position a replay of this plan can reach: the step's own rows plus
+  // `extra_keys` more (capped at the sequence limit). A replay reads no host state, so the
+  // number of steps the plan may run is bounded by the run with the least headroom.
+  uint64_t budget = UINT64_MAX;
+  for (uint32_t ri = 0; ri < n_runs; ri++) {
+    const sv_run& r = runs_in[ri];
+    const uint64_t want = std::min<uint64_t>((uint64_t)e->seq_len[r.slot] + r.count + extra_keys, e->cfg.max_seq_len);
+    budget = std::min<uint64_t>(budget, (want - e->seq_len[r.slot]) / r.count);
+  }
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const sv_run& r = runs_in[ri];
     const uint32_t slot = r.slot, count = r.count;
-    SV_TRY(e->reserve(slot, e->seq_len[slot] + count));
+    const uint32_t want = (uint32_t)std::min<uint64_t>((uint64_t)e->seq_len[slot] + count + extra_keys,
+                                                       e->cfg.max_seq_len);
+    SV_TRY(e->reserve(slot, want));
     const uint32_t first_row = (uint32_t)tokens.size();
     for (uint32_t row = 0; row < count; row++) {
       tokens.push_back(r.tokens[row]);
@@ -894,6 +843,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   if (head_rows.size() > e->cfg.max_head_rows)
     return fail(SV_ERR_CAPACITY, "%zu head rows (max %u)", head_rows.size(), e->cfg.max_head_rows);
   P.n = n;
+  P.budget = budget;
   P.n_head = (uint32_t)head_rows.size();
   P.n_runs = n_runs;
   // Attention splits: the cached keys of each run in splits of `split`, plus a split of its
@@ -904,9 +854,6 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
   SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, n_runs, P.max_splits, P.max_run)));
-  P.step_kernel = (e->cfg.options & SV_ENGINE_STEP_KERNEL) && e->check_ready() == SV_OK &&
-                  step_supported(&e->sh, e->layers.data(), n, n_runs, P.max_run);
-  if (P.step_kernel) SV_TRY(e->ensure_step(step_ws_bytes(&e->sh, n_runs, P.max_run)));
   SV_TRY(e->upload(e->tokens, tokens.data(), tokens.size() * 4));
   SV_TRY(e->upload(e->tin, tin.data(), tin.size() * 4));
   SV_TRY(e->upload(e->vis, vis.data(), vis.size() * 4));
@@ -925,13 +872,13 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     info->max_run = P.max_run;
     info->split = P.split;
     info->max_splits = P.max_splits;
-    info->persistent = P.step_kernel ? 1u : 0u;
   }
   return SV_OK;
 }
 
 extern "C" sv_status sv_encode(sv_engine* e, uint32_t flags) {
   if (!e) return fail(SV_ERR_ARG, "encode: null engine");
+  SV_TRY(e->issue(1));
   return e->encode(flags);
 }
 
@@ -961,6 +908,7 @@ extern "C" sv_status sv_graph_capture(sv_engine* e, uint32_t flags) {
 
 extern "C" sv_status sv_graph_replay(sv_engine* e, uint32_t count) {
   if (!e || !e->graph) return fail(SV_ERR_STATE, "graph_replay: no graph");
+  SV_TRY(e->issue(count));
   for (uint32_t i = 0; i < count; i++) SV_HIP(hipGraphLaunch(e->graph, e->stream), "graph launch");
   return SV_OK;
 }
@@ -968,7 +916,7 @@ extern "C" sv_status sv_graph_replay(sv_engine* e, uint32_t count) {
 extern "C" sv_status sv_sync(sv_engine* e) {
   if (!e) return fail(SV_ERR_ARG, "sync: null engine");
   SV_HIP(hipStreamSynchronize(e->stream), "sync");
-  return e->check_step_error();
+  return SV_OK;
 }
 
 // engine.rs:310-314 step, with generate.rs:446-463 collect: plan, encode, wait, read the
@@ -979,39 +927,9 @@ extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, 
   sv_plan_info pi;
   SV_TRY(sv_plan(e, runs, n_runs, 0, &pi));
   if (info) *info = pi;
+  SV_TRY(e->issue(1));
   SV_TRY(e->encode(flags));
   SV_HIP(hipStreamSynchronize(e->stream), "step");
-  SV_TRY(e->check_step_error());
-  if (e->step_stamps && pi.persistent) {
-    // phases per layer: qkv, attention, o, gate_up, down; stamp 2i = workgroup 0 reaches
-    // barrier i, 2i + 1 = it leaves (stamp 0: start)
-    const uint32_t L = e->sh.n_layers, nb = 5 * L - 1;
-    std::vector<uint64_t> st(2 * nb + 4);
-    SV_HIP(hipMemcpy(st.data(), e->step_stamps, st.size() * 8, hipMemcpyDeviceToHost), "stamps");
-    double work[5] = {}, wait[5] = {};
-    for (uint32_t i = 1; i <= nb; i++) {
-      const uint32_t ph = (i - 1) % 5;
-      const uint64_t begin = i == 1 ? st[0] : st[2 * (i - 1) + 1];
-      work[ph] += (double)(st[2 * i] - begin) * 0.01;
-      wait[ph] += (double)(st[2 * i + 1] - st[2 * i]) * 0.01;
-    }
-    const double total = (double)(st[2 * (nb + 1)] - st[0]) * 0.01;
-    fprintf(stderr, "[step stamps] total %.1f us; per layer (wg0 work / barrier wait, us):", total);
-    const char* nm[5] = {"qkv", "attn", "o", "gate_up", "down"};
-    for (int ph = 0; ph < 5; ph++) fprintf(stderr, " %s %.2f/%.2f", nm[ph], work[ph] / L, wait[ph] / L);
-    fprintf(stderr, "\n");
-    if (L > 1) {
-      std::vector<uint64_t> sub(40);
-      SV_HIP(hipMemcpy(sub.data(), e->step_stamps + 10 * L + 8, 40 * 8, hipMemcpyDeviceToHost), "stamps");
-      for (int ph = 0; ph < 5; ph++) {
-        fprintf(stderr, "[step stamps] layer 1 %s:", nm[ph]);
-        for (int k = 1; k < 8; k++)
-          if (sub[8 * ph + k] > sub[8 * ph] && sub[8 * ph + k] - sub[8 * ph] < 100000000)
-            fprintf(stderr, " s%d +%.2f", k, (double)(sub[8 * ph + k] - sub[8 * ph]) * 0.01);
-        fprintf(stderr, "\n");
-      }
-    }
-  }
   std::vector<uint32_t> em(n_runs);
   SV_HIP(hipMemcpy(em.data(), e->emitted, n_runs * 4, hipMemcpyDeviceToHost), "step emitted");
   if (ids && pi.n_head) SV_HIP(hipMemcpy(ids, e->out_ids, pi.n_head * 4, hipMemcpyDeviceToHost), "step ids");
@@ -1029,6 +947,7 @@ extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, 
 extern "C" sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches) {
   if (!e || !ms || !launches) return fail(SV_ERR_ARG, "profile_step: null pointer");
   SV_HIP(hipStreamSynchronize(e->stream), "profile_step");
+  SV_TRY(e->issue(reps));
   e->prof = true;
   e->prof_events.clear();
   sv_status st = SV_OK;

@@ -43,30 +43,8 @@ struct MMParams {
   float* part;
   float* ssp;
   uint32_t splits, tgroups;  // skinny: k splits and 16-token groups
-#ifdef SV_MM_STAMPS
-  uint64_t* stamps;  // probe builds: clock stamps of the one-shot kernel, [workgroup][8]
-  uint32_t dbg;      // probe builds: 1 skips the weight loads, 2 the X loads
-#endif
 };
 
-#ifdef SV_MM_STAMPS
-uint64_t* g_mm_stamps = nullptr;
-uint32_t g_mm_dbg = 0;
-#define SV_STAMP(slot)                          \
-  do {                                          \
-    __builtin_amdgcn_sched_barrier(0);          \
-    st[slot] = __builtin_amdgcn_s_memrealtime(); \
-    __builtin_amdgcn_sched_barrier(0);          \
-  } while (0)
-#define X_DBG && !(p.dbg & 2)
-#define W_DBG(v) ((p.dbg & 1) ? 0x80000000u + (v) : (v))
-#else
-#define X_DBG
-#define W_DBG(v) (v)
-#define SV_STAMP(slot) \
-  do {                 \
-  } while (0)
-#endif
 
 constexpr int KC = 256;  // k per chunk: one X chunk in registers, 4 blocks of 64
 constexpr int NBLK = KC / 64;
@@ -359,10 +337,6 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   __shared__ float ssred[W][NT];
   const int lane = threadIdx.x & 63, t = lane & 15, q = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-#ifdef SV_MM_STAMPS
-  uint64_t st[8] = {};
-#endif
-  SV_STAMP(0);
   const uint32_t n = p.n, nwg = gridDim.x, S = p.splits;
   uint32_t item = blockIdx.x;
   if (nwg % 8 == 0) item = (item % 8) * (nwg / 8) + item / 8;
@@ -392,7 +366,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     c = min(c, p.chunks - 1);
 #pragma unroll
     for (int i = 0; i < NT; i++)
-      dst[i] = __builtin_bit_cast(f32x4, buf_ld16(xrs, (uint32_t)i < nx X_DBG ? xv : xv_none, (xrow[i] * p.k + c * KC) * 4));
+      dst[i] = __builtin_bit_cast(f32x4, buf_ld16(xrs, (uint32_t)i < nx ? xv : xv_none, (xrow[i] * p.k + c * KC) * 4));
   };
   auto load_gscale = [&](float (&dst)[RT][4], uint32_t c) {
     c = min(c, p.chunks - 1);
@@ -431,7 +405,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
         for (int v = 0; v < WV; v++)
           wr[j][rt][b * WV + v] =
-              buf_ld16_nt(wrs, W_DBG(wvo), (xg * RT + rt) * tile_bytes + (cj * NBLK + b) * kb_bytes + v * v_bytes);
+              buf_ld16_nt(wrs, wvo, (xg * RT + rt) * tile_bytes + (cj * NBLK + b) * kb_bytes + v * v_bytes);
   }
 
   // 2. chunks in order.
@@ -471,7 +445,6 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (j == 0) SV_STAMP(1);
     f32x4 part[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) part[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -502,7 +475,6 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
         part[rt] = mfma16(a1, xl1, part[rt]);
       }
     }
-    if (j == 0) SV_STAMP(2);
     // the next chunk's LDS writes stay behind these reads
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -523,7 +495,6 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     }
   }
 
-  SV_STAMP(3);
   // 3. waves' sums in wave order; sums of squares per token.
   const bool need_ss = p.epi == SV_EPI_NORM || p.epi == SV_EPI_SWIGLU || (p.flags & SV_FLAG_NORM_IN);
   if (need_ss) {
@@ -536,13 +507,6 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
   __syncthreads();
-  SV_STAMP(4);
-#ifdef SV_MM_STAMPS
-  if (p.stamps && lane == 0) {
-    st[5] = __builtin_amdgcn_s_memrealtime();
-    for (int i = 0; i < 6; i++) p.stamps[((size_t)blockIdx.x * 16 + wv) * 8 + i] = st[i];
-  }
-#endif
   if (wv != 0) return;
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) {
@@ -1329,10 +1293,6 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   p.ra = a->ra;
   p.rb = a->rb;
   p.chunks = a->k / KC;
-#ifdef SV_MM_STAMPS
-  p.stamps = g_mm_stamps;
-  p.dbg = g_mm_dbg;
-#endif
   p.counters = nullptr;
   p.part = p.ssp = nullptr;
   if (!skinny) {

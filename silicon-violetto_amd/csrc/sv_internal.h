@@ -92,41 +92,5 @@ sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_
                            const sv_kv_args* kv, const sv_replay_args* ra, const uint32_t* trace,
                            const uint32_t* trace_len);
 
-// Persistent verify step (step.hip): all layers in one launch for steps of <= 16 rows.
-struct StepMat {
-  const void* w;
-  const uint16_t* scales;
-  uint32_t m, k, per_row, gshift, tiled;
-};
-struct StepLayerHost {  // uploaded per layer; the kernel reads it as StepLayerDev
-  StepMat mat[4];       // qkv, o, gate_up, down
-  float qkv_scale, o_scale, resid_attn, post_attn, resid_mlp, post_mlp;
-  uint32_t rope;
-};
-struct StepLaunch {
-  const sv_shape* sh;
-  const void* layers;  // device StepLayerHost[n_layers]
-  uint32_t n, fmt;
-  float *h, *inv;  // h: the layers' input and output; inv: the first layer's qkv norm factors
-  void* acts;      // step_acts_bytes: per-layer activation slices
-  const uint32_t* meta;
-  uint16_t *kc, *vc;
-  const uint32_t* page_table;
-  const float* rope;
-  const uint32_t* runs;
-  uint32_t n_runs, max_run;
-  const uint32_t* vis;
-  uint32_t page_shift, n_pages, max_pages;
-  float scale_log2;
-  void* ws;  // step_ws_bytes, zero-filled once
-  size_t ws_bytes;
-  void* stamps;  // optional: uint64 clock stamps (2 per barrier + 4), null: off
-};
-bool step_supported(const sv_shape* sh, const sv_layer* layers, uint32_t n, uint32_t n_runs, uint32_t max_run);
-size_t step_ws_bytes(const sv_shape* sh, uint32_t n_runs, uint32_t max_run);
-size_t step_acts_bytes(const sv_shape* sh);
-size_t step_err_offset();
-void step_fill_layer(const sv_layer* l, StepLayerHost* out);
-sv_status step_launch(hipStream_t stream, const StepLaunch& a);
 
 }  // namespace sv

@@ -281,8 +281,9 @@ __global__ __launch_bounds__(256) void kv_compact_kernel(const sv_run_in* runs, 
   for (uint32_t j = 1; j < k; j++) {
     const uint32_t from = path[r * SV_FEED_W + j];
     if (from == j) continue;
-    const uint32_t ps = page_table[(size_t)slot * max_pages + ((p0 + from) >> page_shift)];
-    const uint32_t pd = page_table[(size_t)slot * max_pages + ((p0 + j) >> page_shift)];
+    // (clamped to the pool: a page table entry never reserved cannot send the copy out of it)
+    const uint32_t ps = min(page_table[(size_t)slot * max_pages + ((p0 + from) >> page_shift)], n_pages - 1);
+    const uint32_t pd = min(page_table[(size_t)slot * max_pages + ((p0 + j) >> page_shift)], n_pages - 1);
     const size_t src = ((((size_t)l * n_pages + ps) * NKV + g) << page_shift) * D + (size_t)((p0 + from) & pmask) * D + d0;
     const size_t dst = ((((size_t)l * n_pages + pd) * NKV + g) << page_shift) * D + (size_t)((p0 + j) & pmask) * D + d0;
     *(u32x2*)(kc + dst) = *(const u32x2*)(kc + src);
@@ -397,8 +398,8 @@ __global__ __launch_bounds__(256) void step_tail_kernel(TailParams p) {
       for (uint32_t j = 1; j < k; j++) {
         const uint32_t from = s_path[j];
         if (from == j) continue;
-        const uint32_t ps = p.page_table[(size_t)slot * p.max_pages + ((p0 + from) >> p.page_shift)];
-        const uint32_t pd = p.page_table[(size_t)slot * p.max_pages + ((p0 + j) >> p.page_shift)];
+        const uint32_t ps = min(p.page_table[(size_t)slot * p.max_pages + ((p0 + from) >> p.page_shift)], p.n_pages - 1);
+        const uint32_t pd = min(p.page_table[(size_t)slot * p.max_pages + ((p0 + j) >> p.page_shift)], p.n_pages - 1);
         const size_t src = ((((size_t)l * p.n_pages + ps) * p.NKV + g) << p.page_shift) * p.D +
                            (size_t)((p0 + from) & pmask) * p.D + d0;
         const size_t dst = ((((size_t)l * p.n_pages + pd) * p.NKV + g) << p.page_shift) * p.D +

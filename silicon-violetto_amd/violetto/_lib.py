@@ -31,7 +31,7 @@ FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
 FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
-KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "layers")
+KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge")
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 
@@ -84,9 +84,6 @@ class EngineConfig(C.Structure):
                 ("split_keys", u32), ("options", u32)]
 
 
-ENGINE_STEP_KERNEL = 1
-
-
 class Layer(C.Structure):
     _fields_ = [("qkv", Matrix), ("o", Matrix), ("gate_up", Matrix), ("down", Matrix), ("qkv_scale", f32),
                 ("o_scale", f32), ("resid_attn", f32), ("post_attn", f32), ("resid_mlp", f32), ("post_mlp", f32),
@@ -104,8 +101,7 @@ class Run(C.Structure):
 
 
 class PlanInfo(C.Structure):
-    _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits",
-                                   "persistent")]
+    _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits")]
 
 
 P = C.POINTER

@@ -37,12 +37,12 @@ class StepResult:
 class Engine:
     def __init__(self, shape: ModelShape, *, max_seqs: int = 8, max_step_tokens: int = 64, max_seq_len: int = 8192,
                  max_head_rows: int = 16, kv_tokens: int | None = None, page_shift: int = 4, attn_scale: float = 0.125,
-                 split_keys: int = 0, freq: np.ndarray | None = None, step_kernel: bool = False):
+                 split_keys: int = 0, freq: np.ndarray | None = None):
         self.shape = shape
         self.lib = L.lib()
         cfg = L.EngineConfig(shape.c(), max_seqs, max_step_tokens, max_seq_len, max_head_rows,
                              kv_tokens if kv_tokens is not None else max_seqs * max_seq_len, page_shift, attn_scale,
-                             split_keys, L.ENGINE_STEP_KERNEL if step_kernel else 0)
+                             split_keys, 0)
         self.cfg = cfg
         f = np.ascontiguousarray(freq if freq is not None else rope_freq(500000.0, shape.head_dim), dtype=np.float32)
         self.freq = f

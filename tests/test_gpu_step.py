@@ -6,6 +6,8 @@ oracle's top-1 margin exceeds 2e-2; accepted counts, emitted ids, paths, lengths
 tables bit-exact."""
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import pytest
 import torch
@@ -23,12 +25,12 @@ LOGIT_ATOL, LOGIT_RTOL = 2e-2, 1e-2
 
 
 def build_pair(shape: ModelShape, *, ctx: int, n_seqs: int = 1, seed: int = 0, int8: bool = True, page_shift=4,
-               max_seq_len=1024, scalars=None, shuffle=False, step_kernel=True, split_keys=0, max_head_rows=16):
+               max_seq_len=1024, scalars=None, shuffle=False, split_keys=0, max_head_rows=16, fast_kv=False):
     model = SyntheticModel.generate(shape, int8=int8, seed=seed, device="cpu", scalars=scalars)
     freq = rope_freq(500000.0, shape.head_dim)
     eng = Engine(shape, max_seqs=n_seqs, max_step_tokens=16 * n_seqs, max_seq_len=max_seq_len, max_head_rows=max_head_rows,
                  kv_tokens=n_seqs * max_seq_len, page_shift=page_shift, attn_scale=0.125, freq=freq,
-                 step_kernel=step_kernel, split_keys=split_keys)
+                 split_keys=split_keys)
     gm = model.to("cuda")
     eng.set_model(gm)
     emb, lay, sc = oracle.host_weights(model)
@@ -40,18 +42,34 @@ def build_pair(shape: ModelShape, *, ctx: int, n_seqs: int = 1, seed: int = 0, i
         a, b = eng.new_seq(), ref.new_seq()
         assert a == b
         slots.append(a)
-    if shuffle:  # take pages in a shuffled order: reserve/release scratch sequences
-        pass
     ctxs = [ctx] * n_seqs if np.isscalar(ctx) else list(ctx)
-    for s, c in zip(slots, ctxs):
-        eng.bench_fill(s, c)
-        ref.bench_fill(s, c)
+    if shuffle:  # pages taken a page at a time by randomly ordered sequences: shuffled tables
+        left = dict(zip(slots, ctxs))
+        while left:
+            s = int(rng.choice(list(left)))
+            n = min(1 << page_shift, left[s])
+            eng.bench_fill(s, n)
+            ref.bench_fill(s, n)
+            left[s] -= n
+            if left[s] == 0:
+                del left[s]
+    else:
+        for s, c in zip(slots, ctxs):
+            eng.bench_fill(s, c)
+            ref.bench_fill(s, c)
+    for s in slots:
         assert eng.seq_pages(s) == ref.pool.pages(s), "page tables differ"
-    # cached K/V ~ N(0, 1) bf16 at every reserved page (same values on both sides)
+    # cached K/V bf16 at every reserved page (same values on both sides): N(0, 1), or for large
+    # caches random bf16 of magnitude [2^-7, 2) with random sign, drawn as bits
     kd, vd = eng.kv_cache()
-    kv_host = rng.normal(0, 1, (2,) + tuple(kd.shape)).astype(np.float32)
-    bits = oracle.np.asarray(kv_host.view(np.uint32) + 0x7FFF + ((kv_host.view(np.uint32) >> 16) & 1), np.uint32) >> 16
-    bits = bits.astype(np.uint16)
+    if fast_kv:
+        size = (2,) + tuple(kd.shape)
+        bits = (rng.integers(0x3C00, 0x4000, size, dtype=np.uint16) |
+                (rng.integers(0, 2, size, dtype=np.uint16) << np.uint16(15)))
+    else:
+        kv_host = rng.normal(0, 1, (2,) + tuple(kd.shape)).astype(np.float32)
+        bits = np.asarray(kv_host.view(np.uint32) + 0x7FFF + ((kv_host.view(np.uint32) >> 16) & 1), np.uint32) >> 16
+        bits = bits.astype(np.uint16)
     ref.k[...] = bits[0]
     ref.v[...] = bits[1]
     kd.copy_(torch.from_numpy(bits[0].view(np.int16)).cuda().view(torch.bfloat16))
@@ -72,13 +90,11 @@ def compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots):
             assert eng.seq_pages(s) == ref.pool.pages(s)
 
 
-@pytest.mark.parametrize("persistent", [True, False])
-def test_config0_step(gpu, persistent):
-    """configs[0]: one layer + head, 512 cached tokens, k = 4 uniform drafts, greedy, seed 0;
-    the layers as one persistent launch and as separate launches."""
-    banner(f"config0 step persistent={persistent}")
+def test_config0_step(gpu):
+    """one layer + head, 512 cached tokens, k = 4 uniform drafts, greedy, seed 0."""
+    banner("config0 step")
     shape = ModelShape(n_layers=1)
-    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=512, seed=0, step_kernel=persistent)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=512, seed=0)
     s = slots[0]
     tok0 = int(rng.integers(0, shape.vocab))
     eng.set_feed(s, 512, tok0)
@@ -86,22 +102,20 @@ def test_config0_step(gpu, persistent):
     drafts = [int(x) for x in rng.integers(0, shape.vocab, 4)]
     run = (s, [L.FEED_ROW] + drafts, True)
     res = eng.step([run], logits=True)
-    assert res.info.persistent == int(persistent)
     ids_r, logits_r, em_r, extra_r = ref.step([run])
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
 
 
-@pytest.mark.parametrize("persistent", [True, False])
 @pytest.mark.parametrize("scalars", [LayerScalars(), LayerScalars(0.8, 1.2, 0.9, 1.1, 0.95, 0.7, 1),
                                      LayerScalars(1.1, 0.9, 1.0, 0.5, 1.0, 1.3, 0)])
-def test_two_layer_steps_with_replayed_drafts(gpu, scalars, persistent):
+def test_two_layer_steps_with_replayed_drafts(gpu, scalars):
     """Two layers, two sequences, three steps: drafts copied from the oracle's own greedy
     continuation (some right, some wrong), so acceptance, emitted counts, lengths and the
     next step's inputs are exercised; KV of rejected rows is overwritten later."""
-    banner(f"two-layer steps {scalars} persistent={persistent}")
+    banner(f"two-layer steps {scalars}")
     shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
     model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[300, 77], n_seqs=2, seed=3, scalars=scalars,
-                                                 step_kernel=persistent)
+                                                 )
     for s in slots:
         t = int(rng.integers(0, shape.vocab_real))
         eng.set_feed(s, ref.seq_len[s], t)
@@ -114,7 +128,6 @@ def test_two_layer_steps_with_replayed_drafts(gpu, scalars, persistent):
             runs.append((s, [L.FEED_ROW] + drafts, True))
         ids_r, logits_r, em_r, extra_r = ref.step(runs)
         res = eng.step(runs, logits=True)
-        assert res.info.persistent == int(persistent)
         compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
         assert np.array_equal(res.ids, ids_r), "greedy ids diverged (margins within tolerance)"
 
@@ -128,7 +141,7 @@ def test_multi_stream_steps(gpu):
     shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
     ctxs = [300, 1100, 517, 64, 800, 999, 128, 640]
     model, gm, eng, ref, slots, rng = build_pair(shape, ctx=ctxs, n_seqs=8, seed=7, max_seq_len=1200,
-                                                 step_kernel=False, split_keys=128, max_head_rows=64)
+                                                 split_keys=128, max_head_rows=64)
     for s in slots:
         t = int(rng.integers(0, shape.vocab_real))
         eng.set_feed(s, ref.seq_len[s], t)
@@ -214,3 +227,271 @@ def test_sample_logits_seam(gpu):
                         float(tops[i]), L.NO_TOK) for i in range(8)]
     want = oracle.sample(L, logits, rows)
     assert np.array_equal(got, want)
+
+
+# ------------------------------------------------------------------ sampled steps (T > 0)
+def sample_rows_of(ref, extra) -> list:
+    """Each head row's sampler row with its position explicit (engine.rs:134-137 row_of: a step
+    row samples at meta[row].y + 1 with its sequence's seed), for the oracle sampler."""
+    rows = []
+    for t in extra["head_rows"]:
+        slot, pos = (int(v) for v in extra["meta"][t])
+        sr = ref.sampling[slot]
+        rows.append(L.SampleRow(sr.seed_lo, sr.seed_hi, pos + 1, sr.temperature, sr.top_p, L.NO_TOK))
+    return rows
+
+
+def check_sampled(got_ids, got_logits, want_ids, want_logits, rows, what) -> np.ndarray:
+    """Sampled ids against the oracle. The GPU's draws must equal the oracle sampler's on the
+    GPU's own logits, and the oracle step's draws the oracle sampler's on its logits (both bit
+    for bit); the logits agree within the tolerance. Rows where the two sides' draws still
+    differ are draws that the logits' rounding difference moved across an edge of the ordered
+    CDF; they are returned (the caller bounds and reports them)."""
+    close(got_logits, want_logits, LOGIT_ATOL, LOGIT_RTOL, f"{what} logits")
+    assert np.array_equal(oracle.sample(L, got_logits, rows), got_ids), f"{what}: GPU draws != sampler on GPU logits"
+    assert np.array_equal(oracle.sample(L, want_logits, rows), want_ids), f"{what}: oracle step draws != sampler"
+    return np.flatnonzero(got_ids != want_ids)
+
+
+def read_head(eng, n_head):
+    torch.cuda.synchronize()
+    ids = eng.view("d_out_ids", (n_head,)).cpu().numpy().view(np.uint32).copy()
+    logits = eng.view("d_logits", (n_head, eng.shape.vocab), torch.float32).cpu().numpy().copy()
+    return ids, logits
+
+
+def dev_u32(eng, name, shape) -> np.ndarray:
+    torch.cuda.synchronize()
+    return eng.view(name, shape).cpu().numpy().view(np.uint32).copy()
+
+
+def put_u32(eng, name, arr) -> None:
+    eng.view(name, arr.shape).copy_(torch.from_numpy(np.ascontiguousarray(arr, np.uint32).view(np.int32)).cuda())
+    torch.cuda.synchronize()
+
+
+def reserve_like_plan(ref, runs, extra_keys) -> None:
+    """The oracle's pool takes the pages sv_plan reserves for replays of a plan (each run's rows
+    plus extra_keys positions, in run order), so both page tables stay equal."""
+    for r in runs:
+        s = r[0]
+        assert ref.pool.reserve(s, min(ref.seq_len[s] + len(r[1]) + extra_keys, ref.max_seq_len))
+
+
+def resync(eng, ref, slots) -> None:
+    """After a draw that crossed a CDF edge the two sides' sequences differ: continue from the
+    GPU's state (lengths, feed, tree, generation state and KV cache)."""
+    S = ref.max_seqs
+    ref.lens[:] = dev_u32(eng, "d_lens", (S,))
+    ref.feed[:] = dev_u32(eng, "d_feed", (S * 16,))
+    ref.tree[:] = dev_u32(eng, "d_tree", (S * 16,))
+    g = dev_u32(eng, "d_gen", (S, C.sizeof(L.GenState) // 4))
+    C.memmove(ref.gen, g.ctypes.data, g.nbytes)
+    kd, vd = eng.kv_cache()
+    ref.k[...] = kd.view(torch.int16).cpu().numpy().view(np.uint16)
+    ref.v[...] = vd.view(torch.int16).cpu().numpy().view(np.uint16)
+    for s in slots:
+        ref.seq_len[s] = int(ref.lens[s])
+
+
+@pytest.mark.parametrize("top_p", [1.0, 0.9])
+def test_sampled_graph_replay_multi_stream(gpu, top_p):
+    """configs[2]'s path at reduced size: 8 streams (contexts 64-1100, shuffled page tables), T in
+    {0.5, 0.7, 1.0, 1.3}, captured once as a HIP graph and replayed, as bench.py times it.
+    First a plain sampled decode records each stream's continuation (14 replays of one row per
+    stream); then verify steps of k = 4 drafts from the replay drafter over that continuation
+    (35% wrong), 4 replays. After every replay the GPU's draws, emitted counts, lengths, feed,
+    drafts and page tables equal the oracle engine's (bit-exact; a draw moved across a CDF edge
+    by the logits' rounding is counted, and both sides continue from the GPU's state), and every
+    verify step emits the recorded continuation (the lossless property)."""
+    banner(f"sampled graph replay, 8 streams, top_p={top_p}")
+    shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
+    ctxs = [300, 1100, 517, 64, 800, 999, 128, 640]
+    S, k, trace_n, steps, rate, max_len = 8, 4, 24, 4, 0.35, 1300
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=ctxs, n_seqs=S, seed=11, max_seq_len=max_len,
+                                                 shuffle=True, max_head_rows=64)
+    temps = [0.7, 0.7, 1.0, 0.7, 0.5, 0.7, 1.3, 0.7]
+    for i, s in enumerate(slots):
+        eng.set_sampling(s, temps[i], top_p, 1000 + 7 * i)
+        ref.set_sampling(s, temps[i], top_p, 1000 + 7 * i)
+    first = [int(x) for x in rng.integers(0, shape.vocab_real, S)]
+    for s, c, t in zip(slots, ctxs, first):
+        eng.set_feed(s, c, t)
+        ref.set_feed(s, c, t)
+    edges, draws = 0, 0
+    diverged = set()
+
+    def one(runs, what, after=None):
+        nonlocal edges, draws
+        eng.graph_replay(1)
+        eng.sync()
+        ids_r, logits_r, em_r, extra = ref.step(runs)
+        if after:
+            after()
+        got_ids, got_logits = read_head(eng, len(ids_r))
+        e = check_sampled(got_ids, got_logits, ids_r, logits_r, sample_rows_of(ref, extra), what)
+        draws += len(ids_r)
+        if e.size:
+            edges += e.size
+            diverged.update(int(extra["meta"][extra["head_rows"][i]][0]) for i in e)
+            resync(eng, ref, slots)
+            return
+        assert np.array_equal(dev_u32(eng, "d_emitted", (S,))[: len(runs)], em_r), f"{what}: emitted"
+        assert np.array_equal(dev_u32(eng, "d_lens", (S,)), ref.lens), f"{what}: lengths"
+        assert np.array_equal(dev_u32(eng, "d_feed", (S * 16,)), ref.feed), f"{what}: feed / drafts"
+        for s in slots:
+            assert eng.seq_pages(s) == ref.pool.pages(s), f"{what}: page table of {s}"
+
+    # 1. the plain sampled decode that records each stream's continuation
+    runs1 = [(s, [L.FEED_ROW], False, 1) for s in slots]
+    eng.plan(runs1, extra_keys=trace_n + 8)
+    reserve_like_plan(ref, runs1, trace_n + 8)
+    eng.graph_capture(0)
+    traces = [[t] for t in first]
+    for i in range(trace_n):
+        one(runs1, f"decode {i}")
+        col = dev_u32(eng, "d_feed", (S, 16))[:, 0]
+        for j, s in enumerate(slots):
+            traces[j].append(int(col[s]))
+    # 2. verify steps drafting that continuation
+    tr = np.zeros((S, max_len), np.uint32)
+    tl = np.zeros(S, np.uint32)
+    for j, (s, c) in enumerate(zip(slots, ctxs)):
+        tr[s, c:c + len(traces[j])] = traces[j]
+        tl[s] = c + len(traces[j])
+    put_u32(eng, "d_trace", tr)
+    put_u32(eng, "d_trace_len", tl)
+    for s, c, t in zip(slots, ctxs, first):
+        eng.set_feed(s, c, t)
+        ref.set_feed(s, c, t)
+    ra = L.ReplayArgs(max_len, 77, rate, shape.vocab_real)
+    eng.set_replay(77, rate)
+    run_in = [L.RunIn(s, 0, k + 1, 0, k + 1, 1) for s in slots]
+    oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tl, ra, ref.tree)
+    put_u32(eng, "d_feed", ref.feed)
+    put_u32(eng, "d_tree", ref.tree)
+    runs2 = [(s, [L.FEED_ROW + i for i in range(k + 1)], True) for s in slots]
+    eng.plan(runs2, extra_keys=(k + 1) * steps + 8)
+    reserve_like_plan(ref, runs2, (k + 1) * steps + 8)
+    eng.graph_capture(L.STEP_REPLAY)
+    accepted = 0
+    for i in range(steps):
+        before = ref.lens.copy()
+        one(runs2, f"verify {i}", lambda: oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tl, ra, ref.tree))
+        lens = dev_u32(eng, "d_lens", (S,))
+        feed = dev_u32(eng, "d_feed", (S, 16))
+        accepted += int((lens - before)[slots].sum()) - S
+        for j, (s, c) in enumerate(zip(slots, ctxs)):
+            if s not in diverged:
+                assert feed[s, 0] == traces[j][lens[s] - c], f"verify {i}: stream {s} left its continuation"
+    print(f"  {draws} draws, {edges} moved across a CDF edge by rounding; {accepted} drafts accepted", flush=True)
+    assert edges <= 2, f"{edges} of {draws} draws differ"
+    assert accepted > 0, "no draft was accepted"
+    # The plan reserved pages for (4 + 1) x 4 + 8 positions past the first step: 6 steps in
+    # all. A replay past them is refused before it runs (it would write unreserved pages).
+    eng.graph_replay(2)
+    with pytest.raises(L.SvError, match="pages cover 6 steps"):
+        eng.graph_replay(1)
+    eng.close()
+
+
+TREE16 = [None, 0, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 6, 7]  # configs[4]'s tree (16 nodes)
+
+
+def tree_nodes(parents) -> np.ndarray:
+    depth, sees = [0] * len(parents), [1] * len(parents)
+    for i in range(1, len(parents)):
+        depth[i] = depth[parents[i]] + 1
+        sees[i] = sees[parents[i]] | (1 << i)
+    return np.array([depth[i] | ((0xFF if parents[i] is None else parents[i]) << 8) | (sees[i] << 16)
+                     for i in range(len(parents))], np.uint32)
+
+
+def test_sampled_tree_step_accepts_planted_path(gpu):
+    """Four streams verify configs[4]'s 16-node tree at T = 0.7 (top-p 1 and 0.9) through
+    sv_step. The drafts along root -> 2 -> 7 -> 15 are set, level by level, to what the oracle
+    samples at their parents, so multi-candidate sample-and-match accepts a path that is not a
+    prefix of the rows and kv_compact moves it. Draws, emitted counts, paths, lengths and page
+    tables are bit-exact; the V cache after compaction matches within one bf16 step."""
+    banner("sampled tree step with a planted path")
+    shape = ModelShape(n_layers=2, vocab=2048, vocab_real=2048)
+    ctxs = [200, 333, 90, 512]
+    S = 4
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=ctxs, n_seqs=S, seed=13, max_seq_len=600,
+                                                 shuffle=True, max_head_rows=64)
+    for i, s in enumerate(slots):
+        eng.set_sampling(s, 0.7, (1.0, 0.9)[i % 2], 31 + i)
+        ref.set_sampling(s, 0.7, (1.0, 0.9)[i % 2], 31 + i)
+    nodes = tree_nodes(TREE16)
+    for s, c in zip(slots, ctxs):
+        t0 = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, c, t0)
+        ref.set_feed(s, c, t0)
+        ref.feed[s * 16 + 1:s * 16 + 16] = rng.integers(0, shape.vocab_real, 15)
+        ref.tree[s * 16:s * 16 + 16] = nodes
+    runs = [(s, [L.FEED_ROW + i for i in range(16)], True) for s in slots]
+    for parent, child in ((0, 2), (2, 7), (7, 15)):  # probe on the oracle, then roll it back
+        saved = (ref.lens.copy(), ref.feed.copy(), ref.tree.copy(), list(ref.seq_len), bytes(ref.gen))
+        ids = ref.step(runs)[0]
+        ref.lens[:], ref.feed[:], ref.tree[:] = saved[0], saved[1], saved[2]
+        ref.seq_len[:] = saved[3]
+        C.memmove(ref.gen, saved[4], len(saved[4]))
+        for j, s in enumerate(slots):
+            ref.feed[s * 16 + child] = ids[16 * j + parent]
+    put_u32(eng, "d_feed", ref.feed)
+    put_u32(eng, "d_tree", ref.tree)
+    res = eng.step(runs, logits=True)
+    ids_r, logits_r, em_r, extra = ref.step(runs)
+    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "tree step")
+    print(f"  {len(ids_r)} draws, {e.size} across a CDF edge; emitted {list(em_r)}", flush=True)
+    assert e.size == 0, f"draws {e} moved across a CDF edge (rerun with another seed)"
+    assert (em_r >= 4).all(), "the planted path root -> 2 -> 7 -> 15 is accepted"
+    assert np.array_equal(res.emitted, em_r)
+    assert np.array_equal(dev_u32(eng, "d_path", (S, 16))[: len(runs)], extra["path"])
+    assert np.array_equal(dev_u32(eng, "d_lens", (S,)), ref.lens)
+    for s in slots:
+        assert eng.seq_len(s) == ref.seq_len[s] and eng.seq_pages(s) == ref.pool.pages(s)
+    kd, vd = eng.kv_cache()
+    got = oracle.bf16_to_f32(vd.view(torch.int16).cpu().numpy().view(np.uint16))
+    want = oracle.bf16_to_f32(ref.v)
+    assert (np.abs(got - want) <= 2 ** -7 * np.abs(want) + 1e-4).all(), "V cache after kv_compact"
+    eng.close()
+
+
+def test_trees_32_streams_full_layer(gpu):
+    """configs[4]'s step shape at one layer: 32 streams x the 16-node tree (512 verify rows: the
+    GEMM launch shapes and attention grid configs[4] uses), 4096 cached tokens each on shuffled
+    pages, random node ids, T = 0.7 sample-and-match, compaction where a path is accepted.
+    Draws (CDF-edge rows counted), emitted counts, paths, lengths and page tables against the
+    oracle; logits within 2e-2 / 1e-2."""
+    banner("32 streams x 16-node trees, one full layer")
+    shape = ModelShape(n_layers=1, vocab=4096, vocab_real=4096)
+    S, ctx = 32, 4096
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[ctx] * S, n_seqs=S, seed=17, max_seq_len=ctx + 64,
+                                                 shuffle=True, max_head_rows=16 * S, fast_kv=True)
+    nodes = tree_nodes(TREE16)
+    for i, s in enumerate(slots):
+        eng.set_sampling(s, 0.7, 1.0, 500 + i)
+        ref.set_sampling(s, 0.7, 1.0, 500 + i)
+        t0 = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ctx, t0)
+        ref.set_feed(s, ctx, t0)
+        ref.feed[s * 16 + 1:s * 16 + 16] = rng.integers(0, shape.vocab_real, 15)
+        ref.tree[s * 16:s * 16 + 16] = nodes
+    put_u32(eng, "d_feed", ref.feed)
+    put_u32(eng, "d_tree", ref.tree)
+    runs = [(s, [L.FEED_ROW + i for i in range(16)], True) for s in slots]
+    res = eng.step(runs, logits=True)
+    assert res.info.n_tokens == 512
+    ids_r, logits_r, em_r, extra = ref.step(runs)
+    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "trees32")
+    print(f"  {len(ids_r)} draws, {e.size} across a CDF edge; emitted {int(em_r.sum())}", flush=True)
+    assert e.size <= 1
+    ok = np.ones(S, bool)
+    ok[[int(extra["meta"][extra["head_rows"][i]][0]) for i in e]] = False
+    assert np.array_equal(res.emitted[ok], em_r[ok])
+    assert np.array_equal(dev_u32(eng, "d_path", (S, 16))[ok], extra["path"][ok])
+    for j, s in enumerate(slots):
+        if ok[j]:
+            assert eng.seq_len(s) == ref.seq_len[s] and eng.seq_pages(s) == ref.pool.pages(s)
+    eng.close()

@@ -179,7 +179,23 @@ def textbook_attention(q, K, V, scale):
     return (p[:, None] * V).sum(0) / p.sum()
 
 
-def test_attention_against_textbook_softmax():
+def rotate_pairs(x, cs):
+    """RoPE as a complex product, written from the reference's own Python statement of it
+    (tools/spec/drafter.py:33-38): dims (2j, 2j + 1) as z_j = x_2j + i x_2j+1 become z_j (cos - i sin),
+    i.e. (c a0 + s a1, c a1 - s a0); cs holds (cos, sin) per pair."""
+    z = x[0::2].astype(np.complex128) + 1j * x[1::2]
+    z = z * (cs[:, 0] - 1j * cs[:, 1])
+    out = np.empty_like(x, dtype=np.float64)
+    out[0::2], out[1::2] = z.real, z.imag
+    return out
+
+
+@pytest.mark.parametrize("theta", [None, 500000.0])
+def test_attention_against_textbook_softmax(theta):
+    """Attention against max-subtracted natural-exp softmax in float64, with RoPE off (theta None:
+    zero frequencies, the identity) and on (theta 500000: the queries and new keys rotated at
+    their own positions as complex products). A wrong pair layout, sign or table row for q or k
+    changes the scores and fails this."""
     sh = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=64, vocab_real=64, n_layers=1)
     rng = np.random.default_rng(0)
     D, NQ, NKV = 64, 4, 2
@@ -193,7 +209,7 @@ def test_attention_against_textbook_softmax():
     qkv = rng.normal(0, 1, (T, W)).astype(np.float32)
     meta = np.array([0, p0, 0, p0 + 1, 0, p0 + 2], np.uint32)
     vis = np.array([1, 3, 5], np.uint32)  # row 2 sees row 0 and itself only
-    freq = np.zeros(32, np.float32)  # theta = 0: RoPE is the identity
+    freq = np.zeros(32, np.float32) if theta is None else (theta ** (-2.0 * np.arange(32) / 64)).astype(np.float32)
     rope = O.rope_table(freq, p0 + 4)
     kv = L.KvArgs(1, 0, 0, 1, page_shift, n_pages, 4, 0)
     scale = 0.125
@@ -204,11 +220,14 @@ def test_attention_against_textbook_softmax():
     def rms(v):
         return v / np.sqrt((v.astype(np.float64) ** 2).mean() + L.RMS_EPS)
 
+    def roped(v, pos):  # the table (pinned against float64 trig) at the row's own position
+        return rotate_pairs(rms(v), rope[pos].reshape(32, 2).astype(np.float64))
+
     def cached(cache, pos, g):
         page_i = table[0, pos >> page_shift]
         return O.bf16_to_f32(cache[0, page_i, g, pos & (page - 1)]).astype(np.float64)
 
-    new_k = [[O.bf16_to_f32(to_bf_array(rms(qkv[i, NQ * D + g * D: NQ * D + (g + 1) * D]).astype(np.float32)))
+    new_k = [[O.bf16_to_f32(to_bf_array(roped(qkv[i, NQ * D + g * D: NQ * D + (g + 1) * D], p0 + i).astype(np.float32)))
               for g in range(NKV)] for i in range(T)]
     new_v = [[O.bf16_to_f32(to_bf_array(qkv[i, (NQ + NKV) * D + g * D:(NQ + NKV) * D + (g + 1) * D]))
               for g in range(NKV)] for i in range(T)]
@@ -217,7 +236,7 @@ def test_attention_against_textbook_softmax():
             g = h // (NQ // NKV)
             keys = [cached(k_cache, j, g) for j in range(p0)] + [new_k[j][g] for j in range(T) if vis[i] >> j & 1]
             vals = [cached(v_cache, j, g) for j in range(p0)] + [new_v[j][g] for j in range(T) if vis[i] >> j & 1]
-            want = textbook_attention(rms(qkv[i, h * D:(h + 1) * D]), np.array(keys), np.array(vals), scale)
+            want = textbook_attention(roped(qkv[i, h * D:(h + 1) * D], p0 + i), np.array(keys), np.array(vals), scale)
             np.testing.assert_allclose(out[i, h * D:(h + 1) * D], want, rtol=1e-5, atol=1e-6)
     # the new keys landed at p0 + row, through the page table
     for i in range(T):
