@@ -42,6 +42,13 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def sample_order(tok: int, vocab: int) -> int:
+    """Position of id `tok` in the sampler's fixed order: thread t of 1024 owns ids t, t + 1024,
+    ... in turn (kernels.metal:1484-1576)."""
+    t, j = tok % 1024, tok // 1024
+    return t * (vocab // 1024) + min(t, vocab % 1024) + j
+
+
 def kv_bytes_per_token(shape) -> int:
     return shape.n_layers * shape.n_kv_heads * shape.head_dim * 2 * 2  # layers x heads x dims x bf16 x (K, V)
 
@@ -154,8 +161,35 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
                         extra_keys=rows * n_steps + 8)
         eng.graph_capture(L.STEP_REPLAY)
     lens = eng.view("d_lens", (streams,))
-    eng.graph_replay(warmup)
-    eng.sync()
+    divergences = []
+    if tree:
+        eng.graph_replay(warmup)
+        eng.sync()
+    else:
+        # Warm-up steps one at a time, each stream's emitted tokens checked against its plain
+        # decode. Where they first differ, the distance between the drawn and the recorded id in
+        # the sampler's fixed order says what moved the draw: 1 is the neighbouring id (a CDF edge
+        # that the two computations' fp32 rounding put on different sides of the uniform).
+        outv = eng.view("d_out_ids", (streams * rows,))
+        seen = set()
+        for w in range(warmup):
+            before = lens.cpu().numpy().astype(np.int64)
+            eng.graph_replay(1)
+            eng.sync()
+            after = lens.cpu().numpy().astype(np.int64)
+            out = outv.cpu().numpy().view(np.uint32)
+            for i, s in enumerate(slots):
+                if s in seen:
+                    continue
+                got = [int(x) for x in out[rows * i: rows * i + after[s] - before[s]]]
+                off = int(before[s]) - ctxs[i] + 1
+                want = traces[i][off: off + len(got)]
+                if got != want:
+                    m = next(j for j in range(len(got)) if j >= len(want) or got[j] != want[j])
+                    seen.add(s)
+                    divergences.append({"stream": s, "step": w, "position": int(before[s]) + m,
+                                        "order_distance": None if m >= len(want) else
+                                        abs(sample_order(got[m], shape.vocab) - sample_order(want[m], shape.vocab))})
     len0 = lens.cpu().numpy().astype(np.int64)
     log(f"split {info.split} keys, grid {info.max_splits} splits; timing {steps} steps")
     torch.cuda.synchronize()
@@ -195,7 +229,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     flops = 2 * n_rows * (shape.n_layers * sum(mat_elems.values()) + V * H)
     res = dict(eng=eng, kd=kd, vd=vd, traces=traces, ctxs=ctxs, slots=slots, steps=steps, warmup=warmup,
                emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless,
-               lossless_streams=None if tree else sum(same), prof=prof,
+               lossless_streams=None if tree else sum(same), divergences=divergences, prof=prof,
                per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
                flops=flops, info=info, rows=rows)
     return res
@@ -300,11 +334,12 @@ def main() -> int:
         rng = np.random.default_rng(args.seed + 100)
         ctxs = [int(x) for x in rng.integers(1024, 8193, 32)]
         r2 = run_workload(args, model, shape, streams=32, ctxs=ctxs, temperature=0.7, shuffle=True,
-                          steps=args.streams32_steps, warmup=5, profile_reps=2, seed=args.seed + 1)
+                          steps=args.streams32_steps, warmup=8, profile_reps=2, seed=args.seed + 1)
         log("32 streams, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r2["per_step_ms"].items()))
         s32 = {"value": round(r2["value"], 2), "unit": "verified tok/s", "ms_per_step": round(r2["ms_step"], 5),
                "steps": r2["steps"], "emitted_per_step": round(r2["emitted"] / r2["steps"], 3),
                "lossless_trace_check": r2["lossless"], "lossless_streams": r2["lossless_streams"],
+               "warmup_divergences": r2["divergences"],
                "config": {"workload": "configs[2]: 32 streams, ctx U[1024,8192] (mean %d), shuffled page tables, "
                                       "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
                           "rows_per_step": 32 * r2["rows"]},

@@ -169,8 +169,9 @@ __global__ __launch_bounds__(1024) void sample_kernel(const float* logits, const
       __syncthreads();
       const float lo = ex[tid];
       if (lo <= target && target < ex[tid + 1]) {
-        // Re-add this thread's terms in the order of its sum; rounding can leave the
-        // target past them, then the last one counts.
+        // Walk this thread's ids again, summing exactly as the scan did, until the sum
+        // passes the target's offset into this thread's share. If fp32 rounding leaves the
+        // offset beyond the re-sum, the thread's last nonzero term is the pick.
         float acc = 0.0f;
         uint32_t j = 0xffffffffu;
         for (uint32_t i = tid; i < vocab; i += SV_SAMPLE_THREADS) {

@@ -241,16 +241,34 @@ def sample_rows_of(ref, extra) -> list:
     return rows
 
 
-def check_sampled(got_ids, got_logits, want_ids, want_logits, rows, what) -> np.ndarray:
+def compacted(draws, head0s, paths, path_lens) -> np.ndarray:
+    """accept (kernels.metal:1630-1636) moves each verify run's accepted path to the front of
+    its head rows: out[head0 + j] = draw at row path[j]."""
+    out = draws.copy()
+    if paths is None:
+        return out
+    for h0, path, n in zip(head0s, paths, path_lens):
+        for j in range(int(n)):
+            out[h0 + j] = draws[h0 + int(path[j])]
+    return out
+
+
+def check_sampled(got_ids, got_logits, want_ids, want_logits, rows, what, head0s=(), got_path=None,
+                  got_path_len=(), want_path=None, want_path_len=()) -> np.ndarray:
     """Sampled ids against the oracle. The GPU's draws must equal the oracle sampler's on the
     GPU's own logits, and the oracle step's draws the oracle sampler's on its logits (both bit
-    for bit); the logits agree within the tolerance. Rows where the two sides' draws still
-    differ are draws that the logits' rounding difference moved across an edge of the ordered
-    CDF; they are returned (the caller bounds and reports them)."""
+    for bit, after accept's compaction of each side's own accepted path); the logits agree
+    within the tolerance. Rows where the two sides' draws still differ are draws that the
+    logits' rounding difference moved across an edge of the ordered CDF; they are returned
+    (the caller bounds and reports them)."""
     close(got_logits, want_logits, LOGIT_ATOL, LOGIT_RTOL, f"{what} logits")
-    assert np.array_equal(oracle.sample(L, got_logits, rows), got_ids), f"{what}: GPU draws != sampler on GPU logits"
-    assert np.array_equal(oracle.sample(L, want_logits, rows), want_ids), f"{what}: oracle step draws != sampler"
-    return np.flatnonzero(got_ids != want_ids)
+    got_raw = oracle.sample(L, got_logits, rows)
+    want_raw = oracle.sample(L, want_logits, rows)
+    assert np.array_equal(compacted(got_raw, head0s, got_path, got_path_len), got_ids), \
+        f"{what}: GPU draws != sampler on GPU logits"
+    assert np.array_equal(compacted(want_raw, head0s, want_path, want_path_len), want_ids), \
+        f"{what}: oracle step draws != sampler"
+    return np.flatnonzero(got_raw != want_raw)
 
 
 def read_head(eng, n_head):
@@ -329,6 +347,7 @@ def test_sampled_graph_replay_multi_stream(gpu, top_p):
         if after:
             after()
         got_ids, got_logits = read_head(eng, len(ids_r))
+        # linear chains: accept's compaction leaves the head rows in place
         e = check_sampled(got_ids, got_logits, ids_r, logits_r, sample_rows_of(ref, extra), what)
         draws += len(ids_r)
         if e.size:
@@ -442,7 +461,9 @@ def test_sampled_tree_step_accepts_planted_path(gpu):
     put_u32(eng, "d_tree", ref.tree)
     res = eng.step(runs, logits=True)
     ids_r, logits_r, em_r, extra = ref.step(runs)
-    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "tree step")
+    gp, gl = dev_u32(eng, "d_path", (S, 16))[: len(runs)], dev_u32(eng, "d_path_len", (S,))[: len(runs)]
+    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "tree step",
+                      [16 * j for j in range(len(runs))], gp, gl, extra["path"], extra["path_len"])
     print(f"  {len(ids_r)} draws, {e.size} across a CDF edge; emitted {list(em_r)}", flush=True)
     assert e.size == 0, f"draws {e} moved across a CDF edge (rerun with another seed)"
     assert (em_r >= 4).all(), "the planted path root -> 2 -> 7 -> 15 is accepted"
@@ -484,7 +505,9 @@ def test_trees_32_streams_full_layer(gpu):
     res = eng.step(runs, logits=True)
     assert res.info.n_tokens == 512
     ids_r, logits_r, em_r, extra = ref.step(runs)
-    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "trees32")
+    gp, gl = dev_u32(eng, "d_path", (S, 16)), dev_u32(eng, "d_path_len", (S,))
+    e = check_sampled(res.ids, res.logits, ids_r, logits_r, sample_rows_of(ref, extra), "trees32",
+                      [16 * j for j in range(S)], gp, gl, extra["path"], extra["path_len"])
     print(f"  {len(ids_r)} draws, {e.size} across a CDF edge; emitted {int(em_r.sum())}", flush=True)
     assert e.size <= 1
     ok = np.ones(S, bool)
