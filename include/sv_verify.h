@@ -222,6 +222,20 @@ sv_status sv_attn_verify(void* stream, const sv_shape* shape, const float* d_qkv
                          const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
                          float* d_out, void* d_workspace, size_t workspace_bytes);
 
+/* No counterpart in the reference: sv_attn_verify for callers that cannot allocate (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The same kernels and
+ * results, with the split partials in a static array of the library, one per GPU, of
+ * sv_attn_noalloc_max_bytes() bytes (32 MiB), held until the process ends; no allocation and no
+ * library routine that allocates. A call whose partials (sv_attn_workspace_bytes) exceed it
+ * returns SV_ERR_CAPACITY before anything runs. Calls on one GPU share the array: calls that
+ * overlap on one GPU (different streams, or host threads) race and must be serialised. */
+size_t sv_attn_noalloc_max_bytes(void);
+sv_status sv_attn_verify_noalloc(void* stream, const sv_shape* shape, const float* d_qkv, const uint32_t* d_meta,
+                                 uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
+                                 const float* d_rope, const sv_kv_args* kv, const sv_attn_args* args,
+                                 const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
+                                 float* d_out);
+
 /* sample (kernels.metal:1503-1576, with argmax_partial 1430-1451 folded in): one token
  * per row of d_logits [rows][vocab]: the argmax at temperature 0 (ties to the lowest id),
  * else the Philox-keyed inverse-CDF draw with top-p rounds. Bit-exact with the oracle. */

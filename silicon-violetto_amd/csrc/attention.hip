@@ -27,6 +27,8 @@
 //     coherent 16-byte loads.
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "attn_device.h"
 #include "sv_internal.h"
@@ -446,7 +448,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts, const uint32_t* host_runs) {
+                      uint32_t parts, const uint32_t* host_runs, bool may_fuse) {
   if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
     return fail(SV_ERR_ARG, "attn_verify: null pointer");
   if (n_runs == 0) return SV_OK;
@@ -465,7 +467,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   // The merge runs as its own launch over (run, kv head, column) workgroups (measured
   // faster at 9-65 splits); with g_attn_fused_merge set the last split of each (run, kv head)
   // to arrive merges instead.
-  const bool fused_merge = g_attn_fused_merge;
+  const bool fused_merge = may_fuse && g_attn_fused_merge;
   const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
   if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
   AttnParams p;
@@ -559,6 +561,53 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     else launch(attn_merge_kernel<128, false>, mg, dim3(256), 0, stream, p, P);
   }
   return check_launch("attn_merge");
+}
+
+// ------------------------------------------------- the entry point that allocates nothing
+// Split partials of sv_attn_verify_noalloc live in this array: one copy per GPU, held until the
+// process ends. Its name is a host-side stand-in; host code uses the device address that
+// hipGetSymbolAddress returns for the current device. The partials need no clearing: every
+// partial the merge reads is written by the same call (the counted merge, which needs counters
+// at zero, is not used here).
+constexpr size_t ATTN_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[ATTN_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static std::vector<void*> g_scratch_ptr;  // per device
+
+static sv_status scratch_address(void** out) {
+  int dev = 0;
+  const hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return check_hip(de, "attn_verify_noalloc: device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if ((size_t)dev >= g_scratch_ptr.size()) g_scratch_ptr.resize(dev + 1, nullptr);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(SV_ERR_HIP, "attn_verify_noalloc: scratch address: %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SV_OK;
+}
+
+size_t attn_scratch_bytes() { return ATTN_SCRATCH_BYTES; }
+
+sv_status attn_launch_noalloc(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
+                              uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
+                              const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
+                              uint32_t max_run, const uint32_t* vis, float* out) {
+  if (!sh || !args) return fail(SV_ERR_ARG, "attn_verify_noalloc: null pointer");
+  if (max_run == 0 || max_run > SV_MAX_RUN) return fail(SV_ERR_ARG, "attn_verify_noalloc: max_run %u", max_run);
+  const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
+  if (need > ATTN_SCRATCH_BYTES)
+    return fail(SV_ERR_CAPACITY, "attn_verify_noalloc: %zu bytes of split partials exceed the %zu-byte scratch", need,
+                ATTN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const sv_status st = scratch_address(&ws);
+  if (st != SV_OK) return st;
+  return attn_launch(stream, sh, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, n_runs, max_run, vis,
+                     out, ws, ATTN_SCRATCH_BYTES, 3, nullptr, false);
 }
 
 }  // namespace sv

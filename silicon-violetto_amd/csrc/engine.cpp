@@ -93,6 +93,17 @@ extern "C" sv_status sv_attn_verify(void* stream, const sv_shape* shape, const f
                      d_runs, n_runs, max_run, d_vis, d_out, d_workspace, workspace_bytes);
 }
 
+extern "C" size_t sv_attn_noalloc_max_bytes(void) { return attn_scratch_bytes(); }
+
+extern "C" sv_status sv_attn_verify_noalloc(void* stream, const sv_shape* shape, const float* d_qkv,
+                                            const uint32_t* d_meta, uint16_t* d_k_cache, uint16_t* d_v_cache,
+                                            const uint32_t* d_page_table, const float* d_rope, const sv_kv_args* kv,
+                                            const sv_attn_args* args, const uint32_t* d_runs, uint32_t n_runs,
+                                            uint32_t max_run, const uint32_t* d_vis, float* d_out) {
+  return attn_launch_noalloc((hipStream_t)stream, shape, d_qkv, d_meta, d_k_cache, d_v_cache, d_page_table, d_rope, kv,
+                             args, d_runs, n_runs, max_run, d_vis, d_out);
+}
+
 extern "C" sv_status sv_sample(void* stream, const float* d_logits, const sv_sample_row* d_rows, uint32_t* d_out,
                                const uint32_t* d_meta, uint32_t n_rows, uint32_t vocab) {
   return sample_launch((hipStream_t)stream, d_logits, d_rows, d_out, d_meta, n_rows, vocab);

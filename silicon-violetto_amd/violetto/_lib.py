@@ -116,6 +116,9 @@ PROTOS = {
     "sv_attn_workspace_bytes": (C.c_size_t, [P(Shape), u32, u32, u32]),
     "sv_attn_verify": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, P(KvArgs), P(AttnArgs), vp, u32, u32, vp, vp,
                                  vp, C.c_size_t]),
+    "sv_attn_noalloc_max_bytes": (C.c_size_t, []),
+    "sv_attn_verify_noalloc": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, P(KvArgs), P(AttnArgs), vp, u32, u32,
+                                         vp, vp]),
     "sv_sample": (C.c_int, [vp, vp, vp, vp, vp, u32, u32]),
     "sv_accept": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, u32, vp, vp, vp, vp]),
     "sv_kv_compact": (C.c_int, [vp, P(Shape), vp, u32, vp, vp, vp, vp, vp, vp, P(KvArgs)]),

@@ -98,6 +98,17 @@ def attn_verify(shape: ModelShape, qkv: torch.Tensor, meta: torch.Tensor, k_cach
                                    _p(vis), _p(out), _p(ws.t), ws.nbytes))
 
 
+def attn_verify_noalloc(shape: ModelShape, qkv: torch.Tensor, meta: torch.Tensor, k_cache: torch.Tensor,
+                        v_cache: torch.Tensor, page_table: torch.Tensor, rope: torch.Tensor, kv: L.KvArgs,
+                        args: L.AttnArgs, runs: torch.Tensor, n_runs: int, max_run: int, vis: torch.Tensor,
+                        out: torch.Tensor, stream: int | None = None) -> None:
+    """sv_attn_verify_noalloc: attn_verify with the library's static scratch (no allocation)."""
+    sh = shape.c()
+    L.check(L.lib().sv_attn_verify_noalloc(_stream(stream), C.byref(sh), _p(qkv), _p(meta), _p(k_cache), _p(v_cache),
+                                           _p(page_table), _p(rope), C.byref(kv), C.byref(args), _p(runs), n_runs,
+                                           max_run, _p(vis), _p(out)))
+
+
 def embed(shape: ModelShape, table, tokens, out, tin, meta, lens, feed, tree, vis, n: int, stream=None) -> None:
     sh = shape.c()
     L.check(L.lib().sv_embed(_stream(stream), C.byref(sh), _p(table), _p(tokens), _p(out), _p(tin), _p(meta), _p(lens),
