@@ -48,6 +48,7 @@ extern "C" {
 #define SV_SAMPLE_ROUNDS 8u     /* top-p rejection rounds (kernels.metal:1413) */
 #define SV_RMS_EPS 1.1920928955078125e-07f /* 2^-23 (kernels.metal:13) */
 #define SV_ROPE_PAIRS 32u       /* RoPE pairs per head: dims 0..63 (kernels.metal:727-736) */
+#define SV_DRAFT_CANDS 4u       /* drafter candidates per block row, at most (kernels.metal:1845) */
 
 /* Matmul epilogues and flags (kernels.metal:151-152, kernels.rs:4-10). */
 enum {
@@ -253,6 +254,21 @@ sv_status sv_kv_compact(void* stream, const sv_shape* shape, const sv_run_in* d_
                         const uint32_t* d_path, const uint32_t* d_path_len, const uint32_t* d_lens,
                         uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
                         const sv_kv_args* kv);
+
+/* draft_top (kernels.metal:1845-1891, dispatched by drafter.rs:427-436): for each drafted
+ * block row r (d_tin[r] = (slot, row in block); rows with row 0, the bonus token's, are
+ * skipped) the ncand (1..SV_DRAFT_CANDS) best drafter logits of d_logits [n_rows][nv], ties to
+ * the lowest id, as target ids through d_vocab[nv] and their probabilities at temperature
+ * 1 / inv_t, into d_cand / d_cand_q [n_rows][SV_DRAFT_CANDS]. A row without a candidate's
+ * value (NaN or -inf logits) gets SV_NO_TOK and probability 0. */
+sv_status sv_draft_top(void* stream, const float* d_logits, const uint32_t* d_vocab, const uint32_t* d_tin,
+                       uint32_t* d_cand, float* d_cand_q, uint32_t n_rows, uint32_t nv, float inv_t, uint32_t ncand);
+/* draft_tree (kernels.metal:1893-1934, drafter.rs:437-446): each block (d_blocks: uint2 (first
+ * row, rows <= SV_FEED_W)) builds its DDTree best-first from its rows' candidates and writes
+ * the nodes to d_feed / d_tree [slots][SV_FEED_W] entries 1.. of its slot, dead nodes after. */
+sv_status sv_draft_tree(void* stream, const uint32_t* d_blocks, uint32_t nblocks, const uint32_t* d_tin,
+                        const uint32_t* d_cand, const float* d_cand_q, uint32_t* d_feed, uint32_t* d_tree,
+                        uint32_t ncand);
 
 /* replay_draft (kernels.metal:1705-1724): the test drafter. */
 sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,

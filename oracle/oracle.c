@@ -38,6 +38,11 @@
  *                               closed form.
  *   orc_replay_draft            rate 0 replays the trace, rate 1 shifts every id by one, runs
  *                               without head rows untouched, chain node encoding.
+ *   orc_draft_top               numpy: the candidates are the top ids of a float64 sort
+ *                               (value descending, id ascending); probabilities within 1e-6 of
+ *                               the float64 softmax.
+ *   orc_draft_tree              brute force over every candidate path of the block: the nodes
+ *                               are the paths with the highest fp32 path products, in order.
  */
 #include "oracle.h"
 
@@ -412,6 +417,95 @@ static void tg_scan(const float* v, float* ex) {
   }
   ex[SV_SAMPLE_THREADS] = acc;
   for (uint32_t t = 0; t < SV_SAMPLE_THREADS; t++) ex[t] += base[t / 32];
+}
+
+/* kernels.metal:1845-1891 draft_top(): for each drafted block row (tin[r].y > 0; the
+ * block's row 0 is the bonus token's and is skipped) the `ncand` best drafter logits, taken
+ * one at a time as the best id not yet taken (ties to the lowest id), their target ids
+ * through `vocab`, and their probabilities at temperature 1 / inv_t: exp((v_c - v_0) inv_t)
+ * / z, z = the sum over the whole row. exp(y) is exp2(y log2 e) with this file's exp2; the
+ * sum runs in the sampler's order (thread t of 1024 owns ids t, t + 1024, ...; tg_scan). */
+void orc_draft_top(const float* logits, const uint32_t* vocab, const uint32_t* tin, uint32_t* cand, float* cand_q,
+                   uint32_t n_rows, uint32_t nv, float inv_t, uint32_t ncand) {
+  float* s = (float*)malloc(sizeof(float) * SV_SAMPLE_THREADS);
+  float* ex = (float*)malloc(sizeof(float) * (SV_SAMPLE_THREADS + 1));
+  const float c = inv_t * LOG2E_F;
+  for (uint32_t r = 0; r < n_rows; r++) {
+    if (tin[2 * r + 1] == 0) continue;
+    const float* x = logits + (size_t)r * nv;
+    float top_v[SV_DRAFT_CANDS];
+    uint32_t top_i[SV_DRAFT_CANDS];
+    for (uint32_t k = 0; k < ncand; k++) {
+      float bv = -FLT_MAX;
+      uint32_t bi = 0xffffffffu;
+      for (uint32_t j = 0; j < nv; j++) {
+        int taken = 0;
+        for (uint32_t m = 0; m < k; m++) taken |= top_i[m] == j;
+        if (!taken) better(&bv, &bi, x[j], j);
+      }
+      top_v[k] = bv;
+      top_i[k] = bi;
+    }
+    for (uint32_t t = 0; t < SV_SAMPLE_THREADS; t++) {
+      float a = 0.0f;
+      for (uint32_t j = t; j < nv; j += SV_SAMPLE_THREADS) a += orc_exp2((x[j] - top_v[0]) * c);
+      s[t] = a;
+    }
+    tg_scan(s, ex);
+    const float z = ex[SV_SAMPLE_THREADS];
+    for (uint32_t k = 0; k < ncand; k++) {  /* a row without k + 1 ordered values: no candidate */
+      const int ok = top_i[k] < nv && top_i[0] < nv;
+      cand[r * SV_DRAFT_CANDS + k] = ok ? vocab[top_i[k]] : SV_NO_TOK;
+      cand_q[r * SV_DRAFT_CANDS + k] = ok ? orc_exp2((top_v[k] - top_v[0]) * c) / z : 0.0f;
+    }
+  }
+  free(s);
+  free(ex);
+}
+
+/* kernels.metal:1893-1934 draft_tree(): each block's draft tree, best-first (DDTree): the next
+ * node is the best not-yet-taken candidate of any node so far, scored by the fp32 product of
+ * q along its path; a node at depth d takes its children from block row d + 1's candidates
+ * (rows are marginals); depth stays below the block's rows. Nodes go to feed/tree[slot][1..]
+ * in the order taken (parents first, encoded depth | parent << 8 | sees << 16); the rest of
+ * the slot's 16 entries become dead nodes (depth 1, no parent, seeing the root and itself).
+ * A candidate draft_top could not fill (SV_NO_TOK) is never taken (the reference would read
+ * its vocabulary out of range there). */
+void orc_draft_tree(const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin, const uint32_t* cand,
+                    const float* cand_q, uint32_t* feed, uint32_t* tree, uint32_t ncand) {
+  for (uint32_t b = 0; b < nblocks; b++) {
+    const uint32_t first = blocks[2 * b], rows = blocks[2 * b + 1] < SV_FEED_W ? blocks[2 * b + 1] : SV_FEED_W;
+    const uint32_t slot = tin[2 * first];
+    float score[SV_FEED_W];
+    uint32_t depth[SV_FEED_W], taken[SV_FEED_W], sees[SV_FEED_W];
+    score[0] = 1.0f;
+    depth[0] = taken[0] = 0;
+    sees[0] = 1;
+    uint32_t n = 1;
+    for (; n < rows; n++) {
+      float best = -1.0f;
+      uint32_t p = 0;
+      for (uint32_t i = 0; i < n; i++) {
+        const uint32_t cc = (first + depth[i] + 1) * SV_DRAFT_CANDS + taken[i];
+        if (depth[i] + 1 == rows || taken[i] == ncand || cand[cc] == SV_NO_TOK) continue;
+        const float sc = score[i] * cand_q[cc];
+        if (sc > best) {
+          best = sc;
+          p = i;
+        }
+      }
+      if (best < 0.0f) break;
+      const uint32_t d = depth[p] + 1;
+      feed[slot * SV_FEED_W + n] = cand[(first + d) * SV_DRAFT_CANDS + taken[p]];
+      taken[p]++;
+      score[n] = best;
+      depth[n] = d;
+      taken[n] = 0;
+      sees[n] = sees[p] | 1u << n;
+      tree[slot * SV_FEED_W + n] = d | p << 8 | sees[n] << 16;
+    }
+    for (; n < SV_FEED_W; n++) tree[slot * SV_FEED_W + n] = 1u | SV_NO_PARENT << 8 | (1u | 1u << n) << 16;
+  }
 }
 
 /* kernels.metal:1503-1576 sample() (with argmax_partial :1430-1451), thread by thread in

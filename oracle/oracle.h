@@ -32,6 +32,10 @@ float orc_round_bf16(float x);
 void orc_philox(uint32_t ctr[4], const uint32_t key[2]);
 float orc_uniform01(uint32_t seed_lo, uint32_t seed_hi, uint32_t pos, uint32_t round);
 float orc_exp2(float x);
+void orc_draft_top(const float* logits, const uint32_t* vocab, const uint32_t* tin, uint32_t* cand, float* cand_q,
+                   uint32_t n_rows, uint32_t nv, float inv_t, uint32_t ncand);
+void orc_draft_tree(const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin, const uint32_t* cand,
+                    const float* cand_q, uint32_t* feed, uint32_t* tree, uint32_t ncand);
 void orc_to_bf_array(const float* x, uint16_t* out, size_t n);
 void orc_exp2_array(const float* x, float* out, size_t n);
 

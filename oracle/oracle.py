@@ -158,6 +158,26 @@ def replay_draft(L, runs, lens, feed, trace, trace_len, ra, tree):
                            ptr(tree))
 
 
+def draft_top(logits: np.ndarray, vocab: np.ndarray, tin: np.ndarray, inv_t: float, ncand: int):
+    """kernels.metal:1845-1891 draft_top: (cand [rows][4] target ids, cand_q [rows][4])."""
+    logits = np.ascontiguousarray(logits, np.float32)
+    n, nv = logits.shape
+    cand = np.zeros((n, 4), np.uint32)
+    cand_q = np.zeros((n, 4), np.float32)
+    lib().orc_draft_top(ptr(logits), ptr(np.ascontiguousarray(vocab, np.uint32)), ptr(np.ascontiguousarray(tin, np.uint32)),
+                        ptr(cand), ptr(cand_q), u32(n), u32(nv), f32(inv_t), u32(ncand))
+    return cand, cand_q
+
+
+def draft_tree(blocks: np.ndarray, tin: np.ndarray, cand: np.ndarray, cand_q: np.ndarray, feed: np.ndarray,
+               tree: np.ndarray, ncand: int) -> None:
+    """kernels.metal:1893-1934 draft_tree, writing feed/tree [slots * 16] in place."""
+    b = np.ascontiguousarray(blocks, np.uint32)
+    lib().orc_draft_tree(ptr(b), u32(b.size // 2), ptr(np.ascontiguousarray(tin, np.uint32)),
+                         ptr(np.ascontiguousarray(cand, np.uint32)), ptr(np.ascontiguousarray(cand_q, np.float32)),
+                         ptr(feed), ptr(tree), u32(ncand))
+
+
 def embed(L, shape, table, tokens, tin, lens, feed, tree, vis):
     sh = shape.c()
     n = len(tokens)

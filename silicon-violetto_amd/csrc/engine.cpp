@@ -125,6 +125,18 @@ extern "C" sv_status sv_kv_compact(void* stream, const sv_shape* shape, const sv
                            d_page_table, kv);
 }
 
+extern "C" sv_status sv_draft_top(void* stream, const float* d_logits, const uint32_t* d_vocab, const uint32_t* d_tin,
+                                  uint32_t* d_cand, float* d_cand_q, uint32_t n_rows, uint32_t nv, float inv_t,
+                                  uint32_t ncand) {
+  return draft_top_launch((hipStream_t)stream, d_logits, d_vocab, d_tin, d_cand, d_cand_q, n_rows, nv, inv_t, ncand);
+}
+
+extern "C" sv_status sv_draft_tree(void* stream, const uint32_t* d_blocks, uint32_t nblocks, const uint32_t* d_tin,
+                                   const uint32_t* d_cand, const float* d_cand_q, uint32_t* d_feed, uint32_t* d_tree,
+                                   uint32_t ncand) {
+  return draft_tree_launch((hipStream_t)stream, d_blocks, nblocks, d_tin, d_cand, d_cand_q, d_feed, d_tree, ncand);
+}
+
 extern "C" sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,
                                      uint32_t* d_feed, const uint32_t* d_trace, const uint32_t* d_trace_len,
                                      const sv_replay_args* ra, uint32_t* d_tree) {

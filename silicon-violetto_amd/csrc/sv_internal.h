@@ -87,6 +87,10 @@ sv_status accept_launch(hipStream_t stream, const sv_run_in* runs, const uint32_
 sv_status kv_compact_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
                             const uint32_t* path, const uint32_t* path_len, const uint32_t* lens, uint16_t* k_cache,
                             uint16_t* v_cache, const uint32_t* page_table, const sv_kv_args* kv);
+sv_status draft_top_launch(hipStream_t stream, const float* logits, const uint32_t* vocab, const uint32_t* tin,
+                           uint32_t* cand, float* cand_q, uint32_t n_rows, uint32_t nv, float inv_t, uint32_t ncand);
+sv_status draft_tree_launch(hipStream_t stream, const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin,
+                            const uint32_t* cand, const float* cand_q, uint32_t* feed, uint32_t* tree, uint32_t ncand);
 sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nruns, const uint32_t* lens,
                         uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
                         uint32_t* tree);

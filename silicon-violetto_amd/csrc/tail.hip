@@ -444,6 +444,124 @@ sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_
   return check_launch("rmsnorm_rows");
 }
 
+// ---------------------------------------------------------------- draft builder
+// draft_top (kernels.metal:1845-1891): one workgroup of 1024 per drafted block row (the
+// block's row 0, the bonus token's, is skipped). ncand rounds of a workgroup argmax over the
+// ids not yet taken (ties to the lowest id, an order-independent maximum), then the row's sum
+// of exp((x - x_top) inv_t) in the sampler's order (thread t owns ids t, t + 1024, ...; the
+// same exp2 and scan as the sampler), and each candidate's target id and probability.
+__global__ __launch_bounds__(1024) void draft_top_kernel(const float* logits, const uint32_t* vocab, const uint32_t* tin,
+                                                         uint32_t* cand, float* cand_q, uint32_t nv, float c,
+                                                         uint32_t ncand) {
+  __shared__ float ex[SV_SAMPLE_THREADS + 1];
+  __shared__ float base[32];
+  __shared__ float bvs[16];
+  __shared__ uint32_t bis[16];
+  __shared__ float top_v[SV_DRAFT_CANDS];
+  __shared__ uint32_t top_i[SV_DRAFT_CANDS];
+  const uint32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  if (tin[2 * r + 1] == 0) return;
+  const float* x = logits + (size_t)r * nv;
+  for (uint32_t k = 0; k < ncand; k++) {
+    float bv = -3.402823466e+38f;
+    uint32_t bi = 0xffffffffu;
+    for (uint32_t j = tid; j < nv; j += SV_SAMPLE_THREADS) {
+      bool taken = false;
+      for (uint32_t m = 0; m < k; m++) taken = taken || top_i[m] == j;
+      if (!taken) better(bv, bi, x[j], j);
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float v = __shfl_xor(bv, o, WAVE);
+      const uint32_t i = __shfl_xor(bi, o, WAVE);
+      better(bv, bi, v, i);
+    }
+    if (lane == 0) {
+      bvs[wv] = bv;
+      bis[wv] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      for (int w = 1; w < 16; w++) better(bv, bi, bvs[w], bis[w]);
+      top_v[k] = bv;
+      top_i[k] = bi;
+    }
+    __syncthreads();
+  }
+  float s = 0.0f;
+  for (uint32_t j = tid; j < nv; j += SV_SAMPLE_THREADS) s += sv_exp2((x[j] - top_v[0]) * c);
+  scan1024(s, ex, base, tid);
+  if (tid < ncand) {
+    const bool ok = top_i[tid] < nv && top_i[0] < nv;  // a row without tid + 1 ordered values
+    cand[r * SV_DRAFT_CANDS + tid] = ok ? vocab[top_i[tid]] : SV_NO_TOK;
+    cand_q[r * SV_DRAFT_CANDS + tid] = ok ? sv_exp2((top_v[tid] - top_v[0]) * c) / ex[SV_SAMPLE_THREADS] : 0.0f;
+  }
+}
+
+// draft_tree (kernels.metal:1893-1934): one thread per block builds its DDTree best-first: the
+// next node is the not-yet-taken candidate of any node so far with the highest path product
+// (first such node on ties), a node at depth d drawing children from block row d + 1's
+// candidates; nodes go to feed/tree[slot][1..] parents first, the rest become dead nodes. A
+// candidate draft_top could not fill (SV_NO_TOK) is never taken.
+__global__ __launch_bounds__(64) void draft_tree_kernel(const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin,
+                                                        const uint32_t* cand, const float* cand_q, uint32_t* feed,
+                                                        uint32_t* tree, uint32_t ncand) {
+  const uint32_t b = blockIdx.x * 64 + threadIdx.x;
+  if (b >= nblocks) return;
+  const uint32_t first = blocks[2 * b], rows = min(blocks[2 * b + 1], SV_FEED_W), slot = tin[2 * first];
+  float score[SV_FEED_W];
+  uint32_t depth[SV_FEED_W], taken[SV_FEED_W], sees[SV_FEED_W];
+  score[0] = 1.0f;
+  depth[0] = taken[0] = 0;
+  sees[0] = 1;
+  uint32_t n = 1;
+  for (; n < rows; n++) {
+    float best = -1.0f;
+    uint32_t p = 0;
+    for (uint32_t i = 0; i < n; i++) {
+      const uint32_t cc = (first + depth[i] + 1) * SV_DRAFT_CANDS + taken[i];
+      if (depth[i] + 1 == rows || taken[i] == ncand || cand[cc] == SV_NO_TOK) continue;
+      const float sc = score[i] * cand_q[cc];
+      if (sc > best) {
+        best = sc;
+        p = i;
+      }
+    }
+    if (best < 0.0f) break;
+    const uint32_t d = depth[p] + 1;
+    feed[slot * SV_FEED_W + n] = cand[(first + d) * SV_DRAFT_CANDS + taken[p]];
+    taken[p]++;
+    score[n] = best;
+    depth[n] = d;
+    taken[n] = 0;
+    sees[n] = sees[p] | 1u << n;
+    tree[slot * SV_FEED_W + n] = d | p << 8 | sees[n] << 16;
+  }
+  for (; n < SV_FEED_W; n++) tree[slot * SV_FEED_W + n] = 1u | SV_NO_PARENT << 8 | (1u | 1u << n) << 16;
+}
+
+sv_status draft_top_launch(hipStream_t stream, const float* logits, const uint32_t* vocab, const uint32_t* tin,
+                           uint32_t* cand, float* cand_q, uint32_t n_rows, uint32_t nv, float inv_t, uint32_t ncand) {
+  if (!logits || !vocab || !tin || !cand || !cand_q) return fail(SV_ERR_ARG, "draft_top: null pointer");
+  if (ncand == 0 || ncand > SV_DRAFT_CANDS) return fail(SV_ERR_ARG, "draft_top: %u candidates (1..%u)", ncand, SV_DRAFT_CANDS);
+  if (nv < ncand) return fail(SV_ERR_ARG, "draft_top: %u ids for %u candidates", nv, ncand);
+  if (!(inv_t > 0.0f) || !__builtin_isfinite(inv_t)) return fail(SV_ERR_ARG, "draft_top: inverse temperature %g", inv_t);
+  if (n_rows == 0) return SV_OK;
+  launch(draft_top_kernel, dim3(n_rows), dim3(SV_SAMPLE_THREADS), 0, stream, logits, vocab, tin, cand, cand_q, nv,
+         inv_t * LOG2E_F, ncand);
+  return check_launch("draft_top");
+}
+
+sv_status draft_tree_launch(hipStream_t stream, const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin,
+                            const uint32_t* cand, const float* cand_q, uint32_t* feed, uint32_t* tree, uint32_t ncand) {
+  if (!blocks || !tin || !cand || !cand_q || !feed || !tree) return fail(SV_ERR_ARG, "draft_tree: null pointer");
+  if (ncand == 0 || ncand > SV_DRAFT_CANDS) return fail(SV_ERR_ARG, "draft_tree: %u candidates (1..%u)", ncand, SV_DRAFT_CANDS);
+  if (nblocks == 0) return SV_OK;
+  launch(draft_tree_kernel, dim3((nblocks + 63) / 64), dim3(64), 0, stream, blocks, nblocks, tin, cand, cand_q, feed,
+         tree, ncand);
+  return check_launch("draft_tree");
+}
+
 sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,
                         const uint32_t* meta, uint32_t n_rows, uint32_t vocab) {
   if (!logits || !rows || !out) return fail(SV_ERR_ARG, "sample: null pointer");

@@ -122,6 +122,8 @@ PROTOS = {
     "sv_sample": (C.c_int, [vp, vp, vp, vp, vp, u32, u32]),
     "sv_accept": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, u32, vp, vp, vp, vp]),
     "sv_kv_compact": (C.c_int, [vp, P(Shape), vp, u32, vp, vp, vp, vp, vp, vp, P(KvArgs)]),
+    "sv_draft_top": (C.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, f32, u32]),
+    "sv_draft_tree": (C.c_int, [vp, vp, u32, vp, vp, vp, vp, vp, u32]),
     "sv_replay_draft": (C.c_int, [vp, vp, u32, vp, vp, vp, vp, P(ReplayArgs), vp]),
     "sv_engine_create": (C.c_int, [P(EngineConfig), P(f32), P(vp)]),
     "sv_engine_destroy": (None, [vp]),

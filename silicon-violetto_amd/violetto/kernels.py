@@ -109,6 +109,18 @@ def attn_verify_noalloc(shape: ModelShape, qkv: torch.Tensor, meta: torch.Tensor
                                            max_run, _p(vis), _p(out)))
 
 
+def draft_top(logits, vocab, tin, cand, cand_q, n_rows: int, nv: int, inv_t: float, ncand: int, stream=None) -> None:
+    """sv_draft_top: each drafted block row's ncand best candidates and their probabilities."""
+    L.check(L.lib().sv_draft_top(_stream(stream), _p(logits), _p(vocab), _p(tin), _p(cand), _p(cand_q), n_rows, nv,
+                                 inv_t, ncand))
+
+
+def draft_tree(blocks, nblocks: int, tin, cand, cand_q, feed, tree, ncand: int, stream=None) -> None:
+    """sv_draft_tree: each block's DDTree into its slot's feed / tree entries."""
+    L.check(L.lib().sv_draft_tree(_stream(stream), _p(blocks), nblocks, _p(tin), _p(cand), _p(cand_q), _p(feed),
+                                  _p(tree), ncand))
+
+
 def embed(shape: ModelShape, table, tokens, out, tin, meta, lens, feed, tree, vis, n: int, stream=None) -> None:
     sh = shape.c()
     L.check(L.lib().sv_embed(_stream(stream), C.byref(sh), _p(table), _p(tokens), _p(out), _p(tin), _p(meta), _p(lens),

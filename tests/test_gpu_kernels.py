@@ -677,3 +677,52 @@ def test_matmul_skinny_groups_of_256(gpu):
     K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_RAW)
     torch.cuda.synchronize()
     close(y.cpu().numpy(), ref, atol=5e-5 * float(np.abs(ref).max()), rtol=1e-4, what="skinny grouped")
+
+
+# ------------------------------------------------------------------- DDTree draft builder
+def _draft_case(seed, block_rows, nv=16384):
+    rng = np.random.default_rng(seed)
+    slots = rng.permutation(16)[: len(block_rows)]
+    blocks, tin = [], []
+    for slot, rows in zip(slots, block_rows):
+        blocks.append((len(tin), rows))
+        tin += [(int(slot), i) for i in range(rows)]
+    n = len(tin)
+    logits = rng.normal(0, 3, (n, nv)).astype(np.float32)
+    logits[1, rng.integers(0, nv, 3)] = logits[1].max() + 0.25  # tied maxima
+    if n > 3:
+        logits[3, :] = -np.inf                                    # no candidate at all
+        logits[3, 7] = 2.0                                        # ... but one
+    vocab = np.sort(rng.choice(151680, nv, replace=False)).astype(np.uint32)
+    return (np.array(blocks, np.uint32), np.array(tin, np.uint32), logits, vocab,
+            rng.integers(0, 1 << 30, 16 * 16).astype(np.uint32), rng.integers(0, 1 << 30, 16 * 16).astype(np.uint32))
+
+
+@pytest.mark.parametrize("ncand", [1, 2, 3, 4])
+@pytest.mark.parametrize("seed,block_rows", [(1, [5, 8, 1, 16]), (2, [8] * 12), (3, [2, 3, 4, 16, 7])])
+def test_draft_builder_bit_exact(gpu, ncand, seed, block_rows):
+    """draft_top then draft_tree (kernels.metal:1845-1934) on drafter logits over a 16384-id
+    draft vocabulary: candidate ids, their probabilities (bit for bit: the same exp2 and
+    summation order), and every slot's feed and tree entries equal the oracle's."""
+    banner(f"draft builder ncand={ncand} blocks={block_rows}")
+    blocks, tin, logits, vocab, feed0, tree0 = _draft_case(seed * 10 + ncand, block_rows)
+    n, nv = logits.shape
+    inv_t = 1.0 / 0.6
+    cand_r, q_r = oracle.draft_top(logits, vocab, tin, inv_t, ncand)
+    feed_r, tree_r = feed0.copy(), tree0.copy()
+    oracle.draft_tree(blocks, tin, cand_r, q_r, feed_r, tree_r, ncand)
+    cand = torch.zeros(n * 4, dtype=torch.int32, device="cuda")
+    q = torch.zeros(n * 4, dtype=torch.float32, device="cuda")
+    d_tin, d_blocks = to_dev(tin), to_dev(blocks)
+    K.draft_top(to_dev(logits), to_dev(vocab), d_tin, cand, q, n, nv, inv_t, ncand)
+    feed, tree = to_dev(feed0.view(np.int32)), to_dev(tree0.view(np.int32))
+    K.draft_tree(d_blocks, len(blocks), d_tin, cand, q, feed, tree, ncand)
+    torch.cuda.synchronize()
+    drafted = tin[:, 1] > 0
+    got_c = cand.cpu().numpy().view(np.uint32).reshape(n, 4)
+    got_q = q.cpu().numpy().reshape(n, 4)
+    assert np.array_equal(got_c[drafted, :ncand], cand_r[drafted, :ncand])
+    assert np.array_equal(got_q[drafted, :ncand].view(np.uint32), q_r[drafted, :ncand].view(np.uint32))
+    assert np.array_equal(feed.cpu().numpy().view(np.uint32), feed_r)
+    assert np.array_equal(tree.cpu().numpy().view(np.uint32), tree_r)
+    assert not (feed_r[feed_r != feed0] == L.NO_TOK).any(), "an unfilled candidate became a node"

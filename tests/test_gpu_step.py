@@ -518,3 +518,51 @@ def test_trees_32_streams_full_layer(gpu):
         if ok[j]:
             assert eng.seq_len(s) == ref.seq_len[s] and eng.seq_pages(s) == ref.pool.pages(s)
     eng.close()
+
+
+def test_ddtree_feeds_verify_step(gpu):
+    """The draft builder feeding the verify step: drafter logits (random, over a 2048-id draft
+    vocabulary mapped into the target's) go through draft_top and draft_tree straight into the
+    engine's feed and tree; three streams then verify their trees (8, 5 and 16 rows: best-first
+    DDTrees of up to four candidates per row) in one greedy step. Trees, logits, ids, emitted
+    counts, lengths and page tables against the oracle engine given the oracle's trees."""
+    banner("DDTree -> verify step")
+    from violetto import kernels as K
+
+    shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4096)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[300, 77, 650], n_seqs=3, seed=23, max_seq_len=1024,
+                                                 shuffle=True, max_head_rows=48)
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ref.seq_len[s], t)
+        ref.set_feed(s, ref.seq_len[s], t)
+    block_rows = [8, 5, 16]
+    blocks, tin = [], []
+    for s, rows in zip(slots, block_rows):
+        blocks.append((len(tin), rows))
+        tin += [(s, i) for i in range(rows)]
+    blocks, tin = np.array(blocks, np.uint32), np.array(tin, np.uint32)
+    nv = 2048
+    logits = rng.normal(0, 2, (len(tin), nv)).astype(np.float32)
+    vocab = np.sort(rng.choice(shape.vocab_real, nv, replace=False)).astype(np.uint32)
+    cand_r, q_r = oracle.draft_top(logits, vocab, tin, 1.0, 4)
+    oracle.draft_tree(blocks, tin, cand_r, q_r, ref.feed, ref.tree, 4)
+    cand = torch.zeros(len(tin) * 4, dtype=torch.int32, device="cuda")
+    q = torch.zeros(len(tin) * 4, dtype=torch.float32, device="cuda")
+    d_tin = torch.from_numpy(tin.view(np.int32)).cuda()
+    d_logits, d_vocab = torch.from_numpy(logits).cuda(), torch.from_numpy(vocab.view(np.int32)).cuda()
+    d_blocks = torch.from_numpy(blocks.view(np.int32)).cuda()
+    torch.cuda.synchronize()  # torch's copies land before the engine's stream reads them
+    K.draft_top(d_logits, d_vocab, d_tin, cand, q, len(tin), nv, 1.0, 4, stream=eng.stream)
+    K.draft_tree(d_blocks, len(blocks), d_tin, cand, q,
+                 eng.view("d_feed", (3 * 16,)), eng.view("d_tree", (3 * 16,)), 4, stream=eng.stream)
+    eng.sync()
+    assert np.array_equal(dev_u32(eng, "d_feed", (3 * 16,)), ref.feed), "trees' tokens"
+    assert np.array_equal(dev_u32(eng, "d_tree", (3 * 16,)), ref.tree), "trees' nodes"
+    assert any((ref.tree[s * 16 + i] >> 8) & 0xFF not in (0xFF, i - 1) for s in slots for i in range(1, 16)), \
+        "some tree branches (a node whose parent is not the row before)"
+    runs = [(s, [L.FEED_ROW + i for i in range(rows)], True) for s, rows in zip(slots, block_rows)]
+    res = eng.step(runs, logits=True)
+    ids_r, logits_r, em_r, extra_r = ref.step(runs)
+    compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
+    eng.close()

@@ -609,3 +609,106 @@ def test_replay_draft_rules():
     fb, _ = run(0.5, seed=3)
     assert np.array_equal(fa, fb)
     assert set(np.nonzero(fa[0, 1:] != want)[0]) == set(np.nonzero(fa[0, 1:] == (want + 1) % vocab)[0])
+
+
+# ------------------------------------------------------------------- DDTree draft builder
+@pytest.mark.parametrize("ncand", [1, 2, 4])
+def test_draft_top_against_sort(ncand):
+    """draft_top: each drafted row's candidates are its top ids by a float64 sort (value
+    descending, ties to the lower id), mapped through the draft vocabulary; their
+    probabilities the float64 softmax at temperature 1 / inv_t; the block's row 0 untouched."""
+    rng = np.random.default_rng(ncand)
+    nv, n, inv_t = 3000, 6, 1.0 / 0.7
+    logits = rng.normal(0, 2, (n, nv)).astype(np.float32)
+    logits[2, [17, 900, 2999]] = logits[2].max() + 1.0  # tied maxima: lowest ids first
+    logits[3, 5:] = logits[3, :5].min() - 50.0          # a peaked row
+    vocab = np.sort(rng.choice(100000, nv, replace=False)).astype(np.uint32)
+    tin = np.array([[0, i] for i in range(n)], np.uint32)  # one block: row 0 is the bonus token's
+    cand, cand_q = O.draft_top(logits, vocab, tin, inv_t, ncand)
+    assert (cand[0] == 0).all() and (cand_q[0] == 0).all()
+    for r in range(1, n):
+        x = logits[r].astype(np.float64)
+        order = np.lexsort((np.arange(nv), -x))[:ncand]
+        assert np.array_equal(cand[r, :ncand], vocab[order]), f"row {r}"
+        p = np.exp((x - x.max()) * inv_t)
+        p /= p.sum()
+        np.testing.assert_allclose(cand_q[r, :ncand], p[order], rtol=2e-5)
+
+
+def _tree_brute_force(q, ids, first, rows, ncand):
+    """Every candidate path of the block (block row d gives the choices at depth d), scored by
+    the fp32 product of q along it, highest first: the first rows - 1 are the tree's nodes."""
+    paths = [()]
+    frontier = [()]
+    for d in range(1, rows):
+        frontier = [p + (c,) for p in frontier for c in range(ncand)]
+        paths += frontier
+    scored = []
+    for p in paths[1:]:
+        s = np.float32(1.0)
+        for d, c in enumerate(p, start=1):
+            s = np.float32(s * np.float32(q[first + d, c]))
+        scored.append((float(s), p))
+    scored.sort(key=lambda e: -e[0])
+    top = scored[: rows - 1]
+    if len(scored) > rows - 1:
+        assert top[-1][0] != scored[rows - 1][0], "tie at the cut (pick another seed)"
+    index = {(): 0}
+    nodes = []
+    sees = {0: 1}
+    for n, (_, p) in enumerate(top, start=1):
+        parent = index[p[:-1]]
+        index[p] = n
+        sees[n] = sees[parent] | 1 << n
+        nodes.append((int(ids[first + len(p), p[-1]]), len(p) | parent << 8 | sees[n] << 16))
+    return nodes
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_draft_tree_brute_force(seed):
+    """draft_tree against a brute force over every candidate path: the nodes, in order, are the
+    highest path products (a child never outscores its parent, so best-first order is score
+    order); tokens from their block row's candidates; parents, depths and ancestry masks from
+    the paths; the rest of each slot's entries dead nodes; slot 0 entries other blocks do not
+    own untouched."""
+    rng = np.random.default_rng(100 + seed)
+    ncand = [1, 2, 3, 4, 2, 2][seed]  # the enumeration has ncand^(rows - 1) leaves
+    block_rows = [[1, 2, 5], [8, 3], [6, 8, 2, 4], [5, 8], [16], [12, 1, 9]][seed]
+    blocks, tin = [], []
+    slots = rng.permutation(8)[: len(block_rows)]
+    for slot, rows in zip(slots, block_rows):
+        blocks.append((len(tin), rows))
+        tin += [(int(slot), i) for i in range(rows)]
+    n = len(tin)
+    q = np.sort(rng.dirichlet(np.ones(6), n)[:, :4], axis=1)[:, ::-1].astype(np.float32)  # descending, < 1
+    ids = rng.integers(0, 50000, (n, 4)).astype(np.uint32)
+    feed = rng.integers(0, 50000, 8 * 16).astype(np.uint32)
+    tree = rng.integers(0, 1 << 30, 8 * 16).astype(np.uint32)
+    feed0, tree0 = feed.copy(), tree.copy()
+    O.draft_tree(np.array(blocks, np.uint32), np.array(tin, np.uint32), ids, q, feed, tree, ncand)
+    for slot, (first, rows) in zip(slots, blocks):
+        nodes = _tree_brute_force(q, ids, first, rows, ncand) if rows > 1 else []
+        got_feed = feed[slot * 16: slot * 16 + 16]
+        got_tree = tree[slot * 16: slot * 16 + 16]
+        assert got_feed[0] == feed0[slot * 16] and got_tree[0] == tree0[slot * 16], "the root entry is the caller's"
+        for i, (tok, node) in enumerate(nodes, start=1):
+            assert got_feed[i] == tok and got_tree[i] == node, f"slot {slot} node {i}"
+        for i in range(len(nodes) + 1, 16):
+            assert got_tree[i] == 1 | 0xFF << 8 | (1 | 1 << i) << 16, f"slot {slot} dead node {i}"
+            assert got_feed[i] == feed0[slot * 16 + i]
+    for s in set(range(8)) - set(int(x) for x in slots):
+        assert np.array_equal(feed[s * 16: s * 16 + 16], feed0[s * 16: s * 16 + 16])
+        assert np.array_equal(tree[s * 16: s * 16 + 16], tree0[s * 16: s * 16 + 16])
+
+
+def test_draft_tree_skips_unfilled_candidates():
+    """A block row with fewer candidates than ncand (draft_top's SV_NO_TOK: no ordered value
+    left) offers only the ones it has: a chain of 4 rows where row 2 has one candidate."""
+    q = np.array([[0, 0, 0, 0], [0.6, 0.3, 0, 0], [0.9, 0, 0, 0], [0.5, 0.4, 0, 0]], np.float32)
+    ids = np.array([[0, 0, 0, 0], [11, 12, 0, 0], [21, L.NO_TOK, 0, 0], [31, 32, 0, 0]], np.uint32)
+    feed = np.zeros(16, np.uint32)
+    tree = np.zeros(16, np.uint32)
+    O.draft_tree(np.array([0, 4], np.uint32), np.array([[0, i] for i in range(4)], np.uint32), ids, q, feed, tree, 2)
+    # best-first: 11 (0.6), 21 under it (0.54), 12 (0.3)... : three nodes, none of them NO_TOK
+    assert list(feed[1:4]) == [11, 21, 12]
+    assert L.NO_TOK not in feed
