@@ -82,8 +82,9 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     eng.set_model(model)
     rng = np.random.default_rng(seed)
     slots = [eng.new_seq() for _ in range(streams)]
-    for s in slots:
-        eng.set_sampling(s, temperature, 1.0, seed * 1000 + s + 1)
+    seeds = [seed * 1000 + s + 1 for s in slots]
+    for s, sd in zip(slots, seeds):
+        eng.set_sampling(s, temperature, 1.0, sd)
     if shuffle:  # pages taken one at a time by randomly ordered sequences: shuffled tables
         left = {s: c for s, c in zip(slots, ctxs)}
         while left:
@@ -227,7 +228,8 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
     step_bytes = shape.weight_bytes(int8=int8) + shape.n_layers * attn_bytes + n_rows * H * 2
     mat_elems = {"qkv": shape.qkv_width * H, "o": H * H, "gate_up": 2 * F * H, "down": H * F}
     flops = 2 * n_rows * (shape.n_layers * sum(mat_elems.values()) + V * H)
-    res = dict(eng=eng, kd=kd, vd=vd, traces=traces, ctxs=ctxs, slots=slots, steps=steps, warmup=warmup,
+    res = dict(eng=eng, kd=kd, vd=vd, traces=traces, ctxs=ctxs, slots=slots, seeds=seeds, replay_seed=seed + 7,
+               steps=steps, warmup=warmup,
                emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless,
                lossless_streams=None if tree else sum(same), divergences=divergences, prof=prof,
                per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
@@ -293,7 +295,9 @@ def main() -> int:
     ap.add_argument("--draft", type=int, default=4, help="drafts per step (k)")
     ap.add_argument("--mistake-rate", type=float, default=0.35)
     ap.add_argument("--profile-reps", type=int, default=5, help="steps timed per kernel with hipEvents")
-    ap.add_argument("--cpu-steps", type=int, default=2, help="oracle steps for the CPU baseline (0: skip)")
+    ap.add_argument("--cpu-steps", type=int, default=2, help="oracle steps for the CPU baselines (0: skip)")
+    ap.add_argument("--cpu-streams", type=int, default=4,
+                    help="streams of configs[2] in its CPU baseline's sample (0: skip that baseline)")
     ap.add_argument("--streams32-steps", type=int, default=30, help="timed steps of configs[2] (0: skip)")
     ap.add_argument("--long-steps", type=int, default=20,
                     help="timed steps of configs[3] (bf16 weights, 65536 ctx, 1 and 8 streams; 0: skip)")
@@ -324,7 +328,7 @@ def main() -> int:
     r1 = run_workload(args, model, shape, streams=1, ctxs=[args.ctx], temperature=0.0, shuffle=False,
                       steps=args.steps, warmup=args.warmup, profile_reps=args.profile_reps, seed=args.seed)
     log("per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r1["per_step_ms"].items()))
-    cpu = cpu_baseline(args, shape, model, r1) if args.cpu_steps > 0 else None
+    cpu = cpu_baseline(args, shape, model, r1, [0], "configs[1]", 0.0) if args.cpu_steps > 0 else None
     r1["eng"].close()
 
     s32 = None
@@ -336,6 +340,8 @@ def main() -> int:
         r2 = run_workload(args, model, shape, streams=32, ctxs=ctxs, temperature=0.7, shuffle=True,
                           steps=args.streams32_steps, warmup=8, profile_reps=2, seed=args.seed + 1)
         log("32 streams, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r2["per_step_ms"].items()))
+        cpu2 = (cpu_baseline(args, shape, model, r2, list(range(args.cpu_streams)), "configs[2]", 0.7)
+                if args.cpu_steps > 0 and args.cpu_streams > 0 else None)
         s32 = {"value": round(r2["value"], 2), "unit": "verified tok/s", "ms_per_step": round(r2["ms_step"], 5),
                "steps": r2["steps"], "emitted_per_step": round(r2["emitted"] / r2["steps"], 3),
                "lossless_trace_check": r2["lossless"], "lossless_streams": r2["lossless_streams"],
@@ -344,6 +350,7 @@ def main() -> int:
                                       "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
                           "rows_per_step": 32 * r2["rows"]},
                "roofline": roofline_of(r2, 2, "configs[2]"), "step_roofline": step_roofline(r2),
+               "cpu_baseline": cpu2,
                "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r2["per_step_ms"].items()}}
         r2["eng"].close()
 
@@ -412,9 +419,12 @@ def main() -> int:
     return 0
 
 
-def cpu_baseline(args, shape, model, r1):
-    """The oracle's verify step (C, OpenMP over output rows and heads) on this host's cores, on
-    the configs[1] workload: args.cpu_steps steps of the 16-layer model at its context."""
+def cpu_baseline(args, shape, model, res, picks, workload, temperature):
+    """The oracle's verify step (C, OpenMP over output rows and heads) on this host's cores, on a
+    bounded sample of a measured workload: args.cpu_steps verify steps of the 16-layer model for
+    the streams `picks` (indices into the workload's streams), each at its context with the same
+    cached K/V (copied by position from the GPU), sampling seeds and replayed drafts. Returns the
+    cpu_baseline object; matches_gpu: the oracle emitted the GPU's recorded continuation."""
     import numpy as np
     import torch
 
@@ -423,44 +433,53 @@ def cpu_baseline(args, shape, model, r1):
     from violetto import _lib as L
     from violetto.model import rope_freq
 
-    eng, kd, vd, trace, ctx, rows = r1["eng"], r1["kd"], r1["vd"], r1["traces"][0], r1["ctxs"][0], r1["rows"]
-    log(f"CPU baseline: copying the model to host, {args.cpu_steps} oracle steps")
+    eng, kd, vd, rows = res["eng"], res["kd"], res["vd"], res["rows"]
+    log(f"CPU baseline ({workload}): copying the model to host, {len(picks)} stream(s), {args.cpu_steps} oracle steps")
     emb, lay, sc = oracle.host_weights(model)
-    max_len = ctx + 16 * (args.cpu_steps + 2)
-    ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=1, max_seq_len=max_len, kv_tokens=max_len,
-                              attn_scale=0.125, freq=rope_freq(500000.0, shape.head_dim))
-    s = ref.new_seq()
-    ref.bench_fill(s, ctx)
-    ref_pages = ref.pool.pages(s)
-    assert eng.seq_pages(0)[: len(ref_pages)] == ref_pages, "page order differs"
-    n = min(ref.n_pages, kd.shape[1])
-    ref.k[:, :n] = kd[:, :n].view(torch.int16).cpu().numpy().view(np.uint16)
-    ref.v[:, :n] = vd[:, :n].view(torch.int16).cpu().numpy().view(np.uint16)
-    ref.set_feed(s, ctx, trace[0])
-    tr = np.zeros((1, max_len), np.uint32)
-    m = min(len(trace), max_len - ctx)
-    tr[0, ctx:ctx + m] = trace[:m]
-    tr_len = np.array([ctx + m], np.uint32)
-    ra = L.ReplayArgs(max_len, args.seed + 7, args.mistake_rate, shape.vocab_real)
-    run_in = [L.RunIn(s, 0, rows, 0, rows, 1)]
+    ctxs = [res["ctxs"][i] for i in picks]
+    traces = [res["traces"][i] for i in picks]
+    max_len = max(ctxs) + 16 * (args.cpu_steps + 2)
+    ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=len(picks), max_seq_len=max_len,
+                              kv_tokens=len(picks) * max_len, attn_scale=0.125, freq=rope_freq(500000.0, shape.head_dim))
+    tr = np.zeros((len(picks), max_len), np.uint32)
+    tr_len = np.zeros(len(picks), np.uint32)
+    run_in, runs = [], []
+    for j, (i, ctx, trace) in enumerate(zip(picks, ctxs, traces)):
+        s = ref.new_seq()
+        ref.bench_fill(s, ctx)
+        gpu_pages = eng.seq_pages(res["slots"][i])[: len(ref.pool.pages(s))]
+        idx = torch.tensor(gpu_pages, device=kd.device)
+        ref.k[:, ref.pool.pages(s)] = kd[:, idx].view(torch.int16).cpu().numpy().view(np.uint16)
+        ref.v[:, ref.pool.pages(s)] = vd[:, idx].view(torch.int16).cpu().numpy().view(np.uint16)
+        ref.set_sampling(s, temperature, 1.0, res["seeds"][i])
+        ref.set_feed(s, ctx, trace[0])
+        m = min(len(trace), max_len - ctx)
+        tr[s, ctx:ctx + m] = trace[:m]
+        tr_len[s] = ctx + m
+        run_in.append(L.RunIn(s, rows * j, rows, rows * j, rows, 1))
+        runs.append((s, [L.FEED_ROW + r for r in range(rows)], True))
+    ra = L.ReplayArgs(max_len, res["replay_seed"], args.mistake_rate, shape.vocab_real)
     oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tr_len, ra, ref.tree)
     emitted, secs, agree = 0, 0.0, True
     for _ in range(args.cpu_steps):
-        pos = int(ref.lens[s])
+        pos = [int(ref.lens[s]) for s, _, _ in runs]
         t_a = time.perf_counter()
-        ids, _, em, _ = ref.step([(s, [L.FEED_ROW + i for i in range(rows)], True)])
+        ids, _, em, _ = ref.step(runs)
         secs += time.perf_counter() - t_a
-        emitted += int(em[0])
-        agree = agree and [int(x) for x in ids[: em[0]]] == trace[pos - ctx + 1: pos - ctx + 1 + int(em[0])]
+        emitted += int(em.sum())
+        for j, (s, _, _) in enumerate(runs):
+            got = [int(x) for x in ids[rows * j: rows * j + int(em[j])]]
+            want = traces[j][pos[j] - ctxs[j] + 1: pos[j] - ctxs[j] + 1 + int(em[j])]
+            agree = agree and got == want
         oracle.replay_draft(L, run_in, ref.lens, ref.feed, tr, tr_len, ra, ref.tree)
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    log(f"CPU: {emitted} tokens in {secs:.2f} s over {args.cpu_steps} steps, {threads} threads; "
+    log(f"CPU ({workload}): {emitted} tokens in {secs:.2f} s over {args.cpu_steps} steps, {threads} threads; "
         f"oracle tokens = GPU trace: {agree}")
     return {"value": round(emitted / secs, 3), "unit": "verified tok/s", "cores": threads, "kind": "port",
             "matches_gpu": agree,
-            "sample": f"{args.cpu_steps} verify steps of the configs[1] workload (16 layers, 1 stream, {ctx} ctx, "
-                      f"k={rows - 1}) by the C oracle, OpenMP over output rows and attention heads; "
-                      f"{secs / args.cpu_steps:.2f} s/step; emitted tokens equal the GPU's: {agree}"}
+            "sample": f"{args.cpu_steps} verify steps of {len(picks)} of the workload's streams ({workload}: 16 "
+                      f"layers, contexts {ctxs}, k={rows - 1}) by the C oracle, OpenMP over output rows and "
+                      f"attention heads; {secs / args.cpu_steps:.2f} s/step; emitted tokens equal the GPU's: {agree}"}
 
 
 if __name__ == "__main__":

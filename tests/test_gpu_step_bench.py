@@ -19,7 +19,7 @@ ROOT = Path(__file__).resolve().parent.parent
 def test_bench_json_contract(gpu):
     banner("bench.py contract (configs[1], 3 steps)")
     cmd = [sys.executable, str(ROOT / "bench.py"), "--steps", "3", "--warmup", "1", "--streams32-steps", "3",
-           "--long-steps", "0", "--tree-steps", "0", "--cpu-steps", "1", "--profile-reps", "1"]
+           "--long-steps", "0", "--tree-steps", "0", "--cpu-steps", "1", "--cpu-streams", "1", "--profile-reps", "1"]
     out = subprocess.run(cmd, capture_output=True, text=True, timeout=115, cwd=ROOT)
     assert out.returncode == 0, out.stderr[-2000:]
     lines = [ln for ln in out.stdout.splitlines() if ln.startswith("{")]
@@ -51,3 +51,4 @@ def test_bench_json_contract(gpu):
     div = s32["warmup_divergences"]
     assert all(x["order_distance"] == 1 for x in div), div
     assert s32["lossless_streams"] >= 32 - len(div) - 1, s32
+    assert s32["cpu_baseline"]["value"] > 0 and s32["cpu_baseline"]["kind"] == "port"
