@@ -243,11 +243,11 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
 TREE_PARENTS = [None, 0, 0, 0, 0, 1, 1, 2, 2, 3, 3, 4, 4, 5, 6, 7]
 
 
-def extra_object(res, workload, rows, reps):
+def extra_object(res, workload, rows, reps, key=None):
     return {"value": round(res["value"], 2), "unit": "verified tok/s", "ms_per_step": round(res["ms_step"], 5),
             "steps": res["steps"], "emitted_per_step": round(res["emitted"] / res["steps"], 3),
             "lossless_trace_check": res["lossless"], "config": {"workload": workload, "rows_per_step": rows},
-            "roofline": roofline_of(res, reps), "step_roofline": step_roofline(res),
+            "roofline": roofline_of(res, reps, key), "step_roofline": step_roofline(res),
             "kernel_ms_per_step": {kk: round(v, 4) for kk, v in res["per_step_ms"].items()}}
 
 
@@ -360,7 +360,7 @@ def main() -> int:
                           steps=args.tree_steps, warmup=3, profile_reps=2, seed=args.seed + 4, tree=True)
         log("trees, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r4["per_step_ms"].items()))
         s64 = extra_object(r4, "configs[4]: 32 streams x 16-node draft tree (random node ids), 4096 ctx, T=0.7 "
-                               "Philox-seeded sample-and-match, accepted path compacted", 32 * 16, 2)
+                               "Philox-seeded sample-and-match, accepted path compacted", 32 * 16, 2, "configs[4]")
         r4["eng"].close()
     del model
     torch.cuda.empty_cache()
@@ -376,7 +376,7 @@ def main() -> int:
             log(f"65536 ctx x {streams}, per step (ms): " + ", ".join(f"{kk} {v:.4f}" for kk, v in r3["per_step_ms"].items()))
             long_ctx[f"streams{streams}"] = extra_object(
                 r3, f"configs[3]: bf16 weights, {streams} stream(s) x 65536 ctx, k=4 chain, greedy, KV rollback",
-                streams * r3["rows"], 2)
+                streams * r3["rows"], 2, f"configs[3]x{streams}")
             r3["eng"].close()
             torch.cuda.empty_cache()
         del model16
