@@ -270,6 +270,30 @@ sv_status sv_draft_tree(void* stream, const uint32_t* d_blocks, uint32_t nblocks
                         const uint32_t* d_cand, const float* d_cand_q, uint32_t* d_feed, uint32_t* d_tree,
                         uint32_t ncand);
 
+/* The weight file (engine/src/weights.rs:38-74; format tools/convert.py:117-150): header
+ * "VIOLETTO", version 1, 128-byte records, 16 KiB-aligned data region. sv_weights_open reads and
+ * checks the records on the host; sv_weights_upload copies every tensor into one device buffer;
+ * sv_weights_matrix resolves a matrix as model.rs:80-103 does (bf16, or int8 with `<name>.scale`,
+ * groups of 8..256 k, or one per row). Error strings follow the reference's. */
+typedef struct sv_tensor_info {
+  char name[64];
+  uint32_t dtype; /* 0 f32, 1 bf16, 2 int8 */
+  uint32_t ndim;
+  uint32_t shape[4];
+  uint64_t offset; /* bytes from the data region (device buffer) start */
+  uint64_t nbytes;
+} sv_tensor_info;
+typedef struct sv_weights sv_weights;
+sv_status sv_weights_open(const char* path, sv_weights** out);
+uint32_t sv_weights_count(const sv_weights* w);
+sv_status sv_weights_info(const sv_weights* w, uint32_t i, sv_tensor_info* out);
+sv_status sv_weights_find(const sv_weights* w, const char* name, sv_tensor_info* out);
+sv_status sv_weights_read(const sv_weights* w, const char* name, void* host, size_t bytes);
+sv_status sv_weights_upload(sv_weights* w, void* stream);
+sv_status sv_weights_device(const sv_weights* w, const char* name, void** d_ptr);
+sv_status sv_weights_matrix(const sv_weights* w, const char* name, uint32_t m, uint32_t k, sv_matrix* out);
+void sv_weights_close(sv_weights* w);
+
 /* replay_draft (kernels.metal:1705-1724): the test drafter. */
 sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,
                           uint32_t* d_feed, const uint32_t* d_trace, const uint32_t* d_trace_len,

@@ -273,8 +273,9 @@ class OracleEngine:
                     scl = np.ascontiguousarray(scl, np.uint16)
                     self._keep.append(scl)
                 m, k = w.shape
+                gshift = 0 if scl is None else (31 if scl.shape[1] == 1 else int(k // scl.shape[1]).bit_length() - 1)
                 mats.append(L.Matrix(w.ctypes.data, scl.ctypes.data if scl is not None else None, m, k,
-                                     1 if w.dtype == np.int8 else 0, 31 if scl is not None else 0))
+                                     1 if w.dtype == np.int8 else 0, gshift))
             layers[i] = L.Layer(*mats, *sc[:6], int(sc[6]), 0)
         self.layers = layers
 

@@ -326,11 +326,16 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 
 // X chunks a wave keeps in flight: all NCH if NCH NT <= 24 (<= 96 registers), else fewer.
 constexpr int x_depth(int nch, int nt) { return nch * nt <= 24 ? nch : (2 * nt <= 24 ? 2 : 1); }
+// The one-shot kernel's int8 variant with scale groups of 64 or 128 k (the reference's default
+// layer format, tools/convert.py:20): each group's products are summed on their own and scaled.
+constexpr int FMT_I8_G64 = 16;
 
 template <int FMT, int RT, int W, int NCH, int NT>
 __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
-  constexpr int WV = FMT == SV_FMT_I8 ? 1 : 2;
-  constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
+  constexpr bool I8 = FMT != SV_FMT_BF16;
+  constexpr bool SG = FMT == FMT_I8_G64;  // scale groups of 64 or 128 k
+  constexpr int WV = I8 ? 1 : 2;
+  constexpr int ESZ = I8 ? 1 : 2;
   constexpr int XD = x_depth(NCH, NT);
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_all[];  // [W][n][hi, lo][XROW]
   __shared__ f32x4 red[W][RT][64];
@@ -343,7 +348,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   const uint32_t xg = item / S, sp = item % S;  // row group, k split (the splits of a group share an XCD)
   uint16_t* xs = xs_all + (size_t)wv * n * 2 * XROW;
   const uint32_t c0 = (sp * W + wv) * NCH;
-  const bool grouped = FMT == SV_FMT_I8 && !p.per_row;
+  const bool grouped = I8 && !SG && !p.per_row;
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
   // Loads go through buffer resources: one per-lane offset, a uniform offset per load.
   const __amdgpu_buffer_rsrc_t xrs = coherent_rsrc(p.x), wrs = coherent_rsrc(p.w);
@@ -387,12 +392,30 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
       const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
-      if (FMT == SV_FMT_I8 && p.per_row) rsc[rt] = *(const uint2*)(p.scales + row0);
+      if (I8 && p.per_row) rsc[rt] = *(const uint2*)(p.scales + row0);
       if (p.epi == SV_EPI_RESID && (uint32_t)t < n) base_pre[rt] = *(const f32x4*)(p.base + (size_t)t * p.m + row0);
     }
   }
   float gsc[RT][4];
   if (grouped) load_gscale(gsc, c0);
+  // Groups of 64 (four per chunk) or 128 (two): each lane's four rows' scales of every chunk
+  // it multiplies, requested with the weights (8 bytes per row and chunk).
+  u32x2 sgw[SG ? NCH : 1][SG ? RT : 1][SG ? 4 : 1];
+  if (SG) {
+    const uint32_t gpc = KC >> p.gshift;
+#pragma unroll
+    for (int j = 0; j < NCH; j++)
+#pragma unroll
+      for (int rt = 0; rt < RT; rt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint16_t* sp_ = p.scales + ((size_t)(xg * RT + rt) * 16 + 4 * q + i) * ng + min(c0 + j, p.chunks - 1) * gpc;
+          u32x2 v;
+          v[0] = ldg_u32(sp_);
+          v[1] = gpc == 4 ? ldg_u32(sp_ + 2) : 0u;
+          sgw[SG ? j : 0][SG ? rt : 0][SG ? i : 0] = v;
+        }
+  }
   __builtin_amdgcn_s_barrier();
   u32x4 wr[NCH][RT][NBLK * WV];
 #pragma unroll
@@ -445,9 +468,9 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    f32x4 part[RT];
+    f32x4 part[RT], gpart[RT];
 #pragma unroll
-    for (int rt = 0; rt < RT; rt++) part[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rt = 0; rt < RT; rt++) part[rt] = gpart[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int b = 0; b < NBLK; b++) {
       bf16x8 xh0 = zero, xh1 = zero, xl0 = zero, xl1 = zero;
@@ -461,7 +484,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
       for (int rt = 0; rt < RT; rt++) {
         bf16x8 a0, a1;
-        if (FMT == SV_FMT_I8) {
+        if (I8) {
           const u32x4 w = wr[j][rt][b];
           a0 = i8x8_to_bf(w[0], w[1]);
           a1 = i8x8_to_bf(w[2], w[3]);
@@ -469,10 +492,24 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
           a0 = __builtin_bit_cast(bf16x8, wr[j][rt][2 * b]);
           a1 = __builtin_bit_cast(bf16x8, wr[j][rt][2 * b + 1]);
         }
-        part[rt] = mfma16(a0, xh0, part[rt]);
-        part[rt] = mfma16(a0, xl0, part[rt]);
-        part[rt] = mfma16(a1, xh1, part[rt]);
-        part[rt] = mfma16(a1, xl1, part[rt]);
+        f32x4& pa = SG ? gpart[rt] : part[rt];
+        pa = mfma16(a0, xh0, pa);
+        pa = mfma16(a0, xl0, pa);
+        pa = mfma16(a1, xh1, pa);
+        pa = mfma16(a1, xl1, pa);
+      }
+      // a group of 64 ends with every block, one of 128 with every second: its sum, scaled
+      if (SG && (p.gshift == 6 || (b & 1))) {
+        const int g = p.gshift == 6 ? b : b >> 1;
+#pragma unroll
+        for (int rt = 0; rt < RT; rt++) {
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const uint32_t w2 = sgw[SG ? j : 0][SG ? rt : 0][SG ? i : 0][g >> 1];
+            part[rt][i] = __builtin_fmaf(bf(g & 1 ? w2 >> 16 : w2 & 0xffffu), gpart[rt][i], part[rt][i]);
+          }
+          gpart[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
       }
     }
     // the next chunk's LDS writes stay behind these reads
@@ -554,7 +591,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     for (int rt = 0; rt < RT; rt++) acc[rt] = tot[rt];
     ss = sst;
   }
-  if (FMT == SV_FMT_I8 && p.per_row) {
+  if (I8 && p.per_row) {
 #pragma unroll
     for (int rt = 0; rt < RT; rt++) {
       acc[rt][0] *= bf(rsc[rt].x & 0xffffu);
@@ -1201,7 +1238,7 @@ static void stream_launch_one(hipStream_t stream, const MMParams& p, uint32_t gr
 #define SV_STREAM_SHAPES(FMT, NT, CALL)                                        \
   SV_ST(FMT, NT, 1, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 1, CALL) SV_ST(FMT, NT, 1, 8, 2, CALL) \
   SV_ST(FMT, NT, 1, 4, 1, CALL) SV_ST(FMT, NT, 1, 4, 2, CALL)                                \
-  if (FMT == SV_FMT_I8) { SV_ST(FMT, NT, 4, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 2, CALL) SV_ST(FMT, NT, 1, 8, 4, CALL) }
+  if (FMT != SV_FMT_BF16) { SV_ST(FMT, NT, 4, 8, 1, CALL) SV_ST(FMT, NT, 2, 8, 2, CALL) SV_ST(FMT, NT, 1, 8, 4, CALL) }
 
 template <int FMT, int NT>
 static bool stream_dispatch(hipStream_t stream, const MMParams& p, const StreamCfg& c, uint32_t grid) {
@@ -1237,6 +1274,10 @@ void matmul_init() {
   SV_STREAM_SHAPES(SV_FMT_BF16, 5, 0)
   SV_STREAM_SHAPES(SV_FMT_BF16, 8, 0)
   SV_STREAM_SHAPES(SV_FMT_BF16, 16, 0)
+  SV_STREAM_SHAPES(FMT_I8_G64, 4, 0)
+  SV_STREAM_SHAPES(FMT_I8_G64, 5, 0)
+  SV_STREAM_SHAPES(FMT_I8_G64, 8, 0)
+  SV_STREAM_SHAPES(FMT_I8_G64, 16, 0)
 #undef SV_ST
   (void)hipGetLastError();  // an attribute the device refused is found by the launch check
 }
@@ -1257,8 +1298,13 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   } else if (fmt != SV_FMT_BF16) {
     return fail(SV_ERR_ARG, "matmul: format %u", w->format);
   }
-  // The skinny kernel takes int8 scales per row or per group of >= 256 (one per k chunk).
-  const bool skinny = use_skinny(a->n, a->m, a->k) && (per_row || a->gshift >= 8);
+  // The skinny kernels take int8 scales per row or per group of >= 256 (one per k chunk); the
+  // one-shot kernel also groups of 64 and 128 (FMT_I8_G64).
+  const bool small_groups = fmt == SV_FMT_I8 && !per_row && (a->gshift == 6 || a->gshift == 7);
+  StreamCfg sc{};
+  const bool stream_ok = a->n <= 16 && a->m % 16 == 0 && a->k % KC == 0 && g_skinny_tune.path != 1 &&
+                         (per_row || a->gshift >= 6) && pick_stream(fmt, a->n, a->m, a->k, &sc);
+  const bool skinny = use_skinny(a->n, a->m, a->k) && (per_row || a->gshift >= 8 || (small_groups && stream_ok));
   if (!skinny && (a->k % GKC != 0 || a->m % 64 != 0))
     return fail(SV_ERR_ARG, "matmul: k %u and m %u must be multiples of %d and 16 (or of %d and 64)", a->k, a->m, KC,
                 GKC);
@@ -1267,7 +1313,7 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
   if (a->epi == SV_EPI_RESID && !base) return fail(SV_ERR_ARG, "matmul: resid needs base");
   if ((a->flags & (SV_FLAG_WRITE_INV | SV_FLAG_WRITE_RAW)) && !aux) return fail(SV_ERR_ARG, "matmul: flags need aux");
   if (!per_row) {
-    const uint32_t min_shift = skinny ? 8 : 6;
+    const uint32_t min_shift = skinny && !stream_ok ? 8 : 6;
     if (a->gshift < min_shift || a->k % (1u << a->gshift) != 0)
       return fail(SV_ERR_UNSUPPORTED, "matmul: int8 group 2^%u: groups of at least %u (or one per row) are built",
                   a->gshift, 1u << min_shift);
@@ -1299,9 +1345,6 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
     g_mm_variant = 2;
     return gemm_launch(stream, fmt, p, ws, ws_bytes);
   }
-  StreamCfg sc;
-  const bool stream_ok = a->n <= 16 && g_skinny_tune.path != 1 && (per_row || a->gshift >= 8) &&
-                         pick_stream(fmt, a->n, a->m, a->k, &sc);
   if (g_skinny_tune.path == 3 && !stream_ok) return fail(SV_ERR_ARG, "matmul: forced one-shot shape does not fit");
   if (stream_ok) {
     const uint32_t grid = a->m / 16 / sc.rt * sc.s;
@@ -1317,8 +1360,9 @@ sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, 
       p.ssp = (float*)((char*)ws + ss_off);
       p.part = (float*)((char*)ws + part_off);
     }
-    const bool ok = fmt == SV_FMT_I8 ? stream_dispatch_n<SV_FMT_I8>(stream, p, sc, grid)
-                                     : stream_dispatch_n<SV_FMT_BF16>(stream, p, sc, grid);
+    const bool ok = fmt == SV_FMT_BF16 ? stream_dispatch_n<SV_FMT_BF16>(stream, p, sc, grid)
+                    : small_groups     ? stream_dispatch_n<FMT_I8_G64>(stream, p, sc, grid)
+                                       : stream_dispatch_n<SV_FMT_I8>(stream, p, sc, grid);
     if (!ok) return fail(SV_ERR_ARG, "matmul: launch shape rt %d, waves %d, chunks %d", sc.rt, sc.w, sc.nch);
     g_mm_variant = 3;
     return check_launch("matmul");

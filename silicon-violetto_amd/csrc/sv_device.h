@@ -89,6 +89,8 @@ typedef __attribute__((address_space(1))) const u32x4 g_u32x4;
 typedef __attribute__((address_space(1))) const uint16_t g_u16;
 __device__ __forceinline__ u32x4 ldg_nt(const void* p) { return __builtin_nontemporal_load((g_u32x4*)p); }
 __device__ __forceinline__ uint16_t ldg_u16(const uint16_t* p) { return *(g_u16*)p; }
+typedef __attribute__((address_space(1))) const uint32_t g_u32;
+__device__ __forceinline__ uint32_t ldg_u32(const void* p) { return *(g_u32*)p; }
 
 // Address of lane `lane`'s 16-byte weight word v (bf16: two per block) of 64-k block kb of
 // row tile `tile` (16 rows): lane (t, q) = (lane % 16, lane / 16) takes row 16 tile + t, k

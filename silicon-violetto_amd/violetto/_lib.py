@@ -100,6 +100,11 @@ class Run(C.Structure):
     _fields_ = [("slot", u32), ("count", u32), ("tokens", C.POINTER(u32)), ("verify", u32), ("head", u32)]
 
 
+class TensorInfo(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("dtype", u32), ("ndim", u32), ("shape", u32 * 4), ("offset", C.c_uint64),
+                ("nbytes", C.c_uint64)]
+
+
 class PlanInfo(C.Structure):
     _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits")]
 
@@ -124,6 +129,15 @@ PROTOS = {
     "sv_kv_compact": (C.c_int, [vp, P(Shape), vp, u32, vp, vp, vp, vp, vp, vp, P(KvArgs)]),
     "sv_draft_top": (C.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, f32, u32]),
     "sv_draft_tree": (C.c_int, [vp, vp, u32, vp, vp, vp, vp, vp, u32]),
+    "sv_weights_open": (C.c_int, [C.c_char_p, P(vp)]),
+    "sv_weights_count": (u32, [vp]),
+    "sv_weights_info": (C.c_int, [vp, u32, P(TensorInfo)]),
+    "sv_weights_find": (C.c_int, [vp, C.c_char_p, P(TensorInfo)]),
+    "sv_weights_read": (C.c_int, [vp, C.c_char_p, vp, C.c_size_t]),
+    "sv_weights_upload": (C.c_int, [vp, vp]),
+    "sv_weights_device": (C.c_int, [vp, C.c_char_p, P(vp)]),
+    "sv_weights_matrix": (C.c_int, [vp, C.c_char_p, u32, u32, P(Matrix)]),
+    "sv_weights_close": (None, [vp]),
     "sv_replay_draft": (C.c_int, [vp, vp, u32, vp, vp, vp, vp, P(ReplayArgs), vp]),
     "sv_engine_create": (C.c_int, [P(EngineConfig), P(f32), P(vp)]),
     "sv_engine_destroy": (None, [vp]),

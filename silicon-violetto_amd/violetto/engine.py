@@ -66,10 +66,12 @@ class Engine:
             pass
 
     # -- model
-    def set_model(self, model: SyntheticModel) -> None:
-        assert model.device.type == "cuda", "the engine reads weights from device memory"
+    def set_model(self, model) -> None:
+        """A SyntheticModel on the GPU or a weights.VltModel (anything with embed_ptr() and
+        c_layer(i) over device memory)."""
+        assert getattr(model, "device", torch.device("cuda")).type == "cuda", "the engine reads weights from device memory"
         self.model = model
-        L.check(self.lib.sv_engine_set_embed(self.h, model.embed.data_ptr()))
+        L.check(self.lib.sv_engine_set_embed(self.h, model.embed_ptr()))
         for i in range(model.shape.n_layers):
             lay = model.c_layer(i)
             L.check(self.lib.sv_engine_set_layer(self.h, i, C.byref(lay)))

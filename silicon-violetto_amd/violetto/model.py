@@ -65,6 +65,24 @@ def quantize_rows(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return q, s
 
 
+def quantize_groups(w: torch.Tensor, group: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """int8 over groups of `group` consecutive k (tools/convert.py:41-50): per group s =
+    bf16(absmax / 127), q = clamp(round_half_even(w / s), -127, 127). Returns (q int8 [m][k],
+    s bf16 [m][k / group])."""
+    m, k = w.shape
+    g = w.float().reshape(m, k // group, group)
+    s = (g.abs().amax(-1) / 127).to(torch.bfloat16)
+    sf = s.float().unsqueeze(-1)
+    q = torch.where(sf > 0, g / sf, torch.zeros((), device=w.device)).round().clamp(-127, 127).to(torch.int8)
+    return q.reshape(m, k), s
+
+
+def gshift_of(k: int, scales: torch.Tensor) -> int:
+    """sv_matrix.gshift of int8 scales [m][groups]: 31 for one per row, else log2(k / groups)."""
+    groups = scales.shape[1]
+    return 31 if groups == 1 else int(k // groups).bit_length() - 1
+
+
 @dataclass
 class LayerScalars:
     qkv_scale: float = 1.0
@@ -87,7 +105,9 @@ class SyntheticModel:
 
     @staticmethod
     def generate(shape: ModelShape, *, int8: bool = True, seed: int = 0, device: str | torch.device = "cpu",
-                 scalars: LayerScalars | list[LayerScalars] | None = None, std: float = 0.02) -> "SyntheticModel":
+                 scalars: LayerScalars | list[LayerScalars] | None = None, std: float = 0.02,
+                 group: int | None = None) -> "SyntheticModel":
+        """group: int8 scale groups of `group` k (the reference's default is 64); None: one per row."""
         dev = torch.device(device)
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
@@ -103,7 +123,10 @@ class SyntheticModel:
             for name, (m, k) in (("qkv", (shape.qkv_width, H)), ("o", (H, shape.n_heads * shape.head_dim)),
                                  ("gate_up", (2 * F, H)), ("down", (H, F))):
                 w = normal(m, k)
-                lay[name] = quantize_rows(w) if int8 else (w.to(torch.bfloat16), None)
+                if not int8:
+                    lay[name] = (w.to(torch.bfloat16), None)
+                else:
+                    lay[name] = quantize_rows(w) if group is None else quantize_groups(w, group)
                 del w
             layers.append(lay)
         if scalars is None:
@@ -119,6 +142,9 @@ class SyntheticModel:
         layers = [{k: (w.to(dev), None if s is None else s.to(dev)) for k, (w, s) in lay.items()} for lay in self.layers]
         return SyntheticModel(self.shape, self.int8, dev, self.embed.to(dev), layers, self.scalars)
 
+    def embed_ptr(self) -> int:
+        return self.embed.data_ptr()
+
     def c_layer(self, i: int) -> L.Layer:
         """The sv_layer of layer i (device pointers: the model must live on the GPU)."""
         lay, s = self.layers[i], self.scalars[i]
@@ -128,7 +154,7 @@ class SyntheticModel:
             m, k = w.shape
             if sc is None:
                 return L.Matrix(w.data_ptr(), None, m, k, L.FMT_BF16, 0)
-            return L.Matrix(w.data_ptr(), sc.data_ptr(), m, k, L.FMT_I8, 31)
+            return L.Matrix(w.data_ptr(), sc.data_ptr(), m, k, L.FMT_I8, gshift_of(k, sc))
 
         return L.Layer(mat("qkv"), mat("o"), mat("gate_up"), mat("down"), s.qkv_scale, s.o_scale, s.resid_attn,
                        s.post_attn, s.resid_mlp, s.post_mlp, s.rope, 0)

@@ -726,3 +726,44 @@ def test_draft_builder_bit_exact(gpu, ncand, seed, block_rows):
     assert np.array_equal(feed.cpu().numpy().view(np.uint32), feed_r)
     assert np.array_equal(tree.cpu().numpy().view(np.uint32), tree_r)
     assert not (feed_r[feed_r != feed0] == L.NO_TOK).any(), "an unfilled candidate became a node"
+
+
+# --------------------------------------------- int8 scale groups of 64 / 128 (1-16 rows)
+@pytest.mark.parametrize("m,k,group", [(3072, 2048, 64), (2048, 8192, 64), (16384, 2048, 128), (2048, 2048, 64),
+                                       (512, 1280, 128)])
+@pytest.mark.parametrize("n", [1, 5, 16])
+@pytest.mark.parametrize("epi", [L.EPI_NORM, L.EPI_RESID, L.EPI_SWIGLU])
+@pytest.mark.parametrize("tiled", [False, True])
+def test_matmul_int8_groups_one_shot(gpu, m, k, group, n, epi, tiled):
+    """The reference's default int8 layer format (tools/convert.py:20: groups of 64 k; 128 as
+    well) on the one-shot kernel at 1-16 rows: each group's products summed on their own and
+    scaled, against the oracle's dequantised float64 matmul."""
+    if k % 256:
+        pytest.skip("the one-shot kernel takes k in chunks of 256")
+    banner(f"int8 groups m={m} k={k} group={group} n={n} epi={epi} tiled={tiled}")
+    rng = np.random.default_rng(m + k + group + 10 * n + epi)
+    w = rng.normal(0, 0.02, (m, k)).astype(np.float32)
+    w[:, :group] *= 40.0  # the first group of every row 40x larger: scales that differ a lot
+    wq, sc = oracle.quantize(w, group)
+    gs = int(np.log2(group))
+    mat = K.matrix(torch.from_numpy(wq).cuda(), torch.from_numpy(sc.view(np.int16)).cuda().view(torch.bfloat16), gs)
+    if tiled:
+        mat = mat.tiled()
+    x = (rng.normal(0, 1, (n, k)) * rng.uniform(0.5, 4, (n, 1))).astype(np.float32)
+    base = rng.normal(0, 1, (n, m)).astype(np.float32)
+    flags = {L.EPI_NORM: L.FLAG_WRITE_INV, L.EPI_RESID: L.FLAG_WRITE_RAW}.get(epi, 0)
+    a = L.MatArgs(n, k, m, epi, flags, m, 0.8, 1.1, 0.7, 1, k, gs)
+    out_m = m // 2 if epi == L.EPI_SWIGLU else m
+    aux_n = n if epi == L.EPI_NORM else n * m
+    aux_ref = np.zeros(aux_n, np.float32)
+    ref = oracle.matmul(L, wq, sc, gs, x, a, base=base if epi == L.EPI_RESID else None, aux=aux_ref)
+    y = torch.zeros(n, out_m, device="cuda")
+    aux = torch.zeros(aux_n, device="cuda")
+    K.matmul(mat, to_dev(x), y, n=n, epi=epi, flags=flags, scale=0.8, ra=1.1, rb=0.7,
+             base=to_dev(base) if epi == L.EPI_RESID else None, aux=aux)
+    torch.cuda.synchronize()
+    assert C.c_int.in_dll(L.lib(), "_ZN2sv12g_mm_variantE").value == 3, "1-16 rows run the one-shot kernel"
+    mag = float(np.abs(ref[np.isfinite(ref)]).max())
+    close(y.cpu().numpy(), ref, atol=5e-5 * max(mag, 1.0), rtol=1e-4, what=f"grouped epi {epi}")
+    if epi in (L.EPI_NORM, L.EPI_RESID):
+        close(aux.cpu().numpy(), aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")

@@ -566,3 +566,61 @@ def test_ddtree_feeds_verify_step(gpu):
     ids_r, logits_r, em_r, extra_r = ref.step(runs)
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
     eng.close()
+
+
+@pytest.mark.parametrize("group", [64, None])
+def test_step_from_weight_file(gpu, tmp_path, group):
+    """A model served from the reference's weight-file layout (engine/src/weights.rs): a
+    two-layer model written as `embed`, `Lnn.{qkv,o,gate_up,down}` (int8 with `.scale`: groups
+    of 64 k, the reference's default, or one per row) and `Lnn.scalars`, uploaded and resolved by
+    sv_weights_*, verifies three streams' drafts in one step against the oracle engine."""
+    banner(f"step from a weight file, group={group}")
+    from violetto.weights import VltModel, WeightFile, write_vlt
+
+    shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
+    scal = [LayerScalars(0.9, 1.1, 1.0, 0.8, 1.0, 1.2, 1), LayerScalars(1.0, 0.95, 1.1, 1.0, 0.9, 1.0, 1)]
+    model = SyntheticModel.generate(shape, seed=29, device="cpu", scalars=scal, group=group)
+    tensors = {"embed": model.embed}
+    for i, (lay, s) in enumerate(zip(model.layers, model.scalars)):
+        for name, (w, sc) in lay.items():
+            tensors[f"L{i:02d}.{name}"] = w
+            tensors[f"L{i:02d}.{name}.scale"] = sc
+        tensors[f"L{i:02d}.scalars"] = torch.tensor([s.qkv_scale, s.o_scale, s.resid_attn, s.post_attn, s.resid_mlp,
+                                                     s.post_mlp, 0.0, 0.0])
+    path = tmp_path / "model.vlt"
+    write_vlt(path, tensors)
+    wf = WeightFile(path)
+    wf.upload()
+    vm = VltModel(wf, shape)
+    freq = rope_freq(500000.0, shape.head_dim)
+    eng = Engine(shape, max_seqs=3, max_step_tokens=48, max_seq_len=1024, max_head_rows=48, kv_tokens=3 * 1024,
+                 attn_scale=0.125, freq=freq)
+    eng.set_model(vm)
+    emb, lay, sc = oracle.host_weights(model)
+    ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=3, max_seq_len=1024, kv_tokens=3 * 1024, attn_scale=0.125,
+                              freq=freq)
+    rng = np.random.default_rng(31)
+    slots = []
+    for c in (200, 513, 64):
+        s = eng.new_seq()
+        assert s == ref.new_seq()
+        eng.bench_fill(s, c)
+        ref.bench_fill(s, c)
+        slots.append(s)
+    kd, vd = eng.kv_cache()
+    bits = rng.integers(0x3C00, 0x4000, (2,) + tuple(kd.shape), dtype=np.uint16) | \
+        (rng.integers(0, 2, (2,) + tuple(kd.shape), dtype=np.uint16) << np.uint16(15))
+    ref.k[...], ref.v[...] = bits[0], bits[1]
+    kd.copy_(torch.from_numpy(bits[0].view(np.int16)).cuda().view(torch.bfloat16))
+    vd.copy_(torch.from_numpy(bits[1].view(np.int16)).cuda().view(torch.bfloat16))
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ref.seq_len[s], t)
+        ref.set_feed(s, ref.seq_len[s], t)
+    runs = [(s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, k)], True)
+            for s, k in zip(slots, (4, 2, 4))]
+    res = eng.step(runs, logits=True)
+    ids_r, logits_r, em_r, extra_r = ref.step(runs)
+    compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
+    eng.close()
+    wf.close()

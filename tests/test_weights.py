@@ -1,0 +1,132 @@
+"""The weight file (engine/src/weights.rs:38-74, layout tools/convert.py:117-150) on the host:
+the writer's bytes against the documented layout packed by hand, the reader's records and
+contents, and the checks that refuse malformed files and matrices (no GPU needed)."""
+from __future__ import annotations
+
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from violetto import _lib as L
+from violetto.model import quantize_groups, quantize_rows
+from violetto.weights import WeightFile, write_vlt
+
+
+def _tensors():
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(64, 512, generator=g) * 0.02
+    q64, s64 = quantize_groups(w, 64)
+    qr, sr = quantize_rows(w)
+    return {
+        "embed": (torch.randn(100, 512, generator=g) * 0.02).to(torch.bfloat16),
+        "L00.scalars": torch.tensor([1.0, 0.9, 1.1, 1.0, 0.8, 1.2, 0.0, 0.0]),
+        "L00.qkv": q64, "L00.qkv.scale": s64,
+        "L00.o": qr, "L00.o.scale": sr,
+        "L00.down": w.to(torch.bfloat16),
+        "empty": torch.zeros(0, dtype=torch.float32),
+    }
+
+
+def test_layout_is_the_documented_one(tmp_path):
+    """Header, first record and first tensor at the offsets the format documents."""
+    path = tmp_path / "m.vlt"
+    t = _tensors()
+    write_vlt(path, t)
+    b = path.read_bytes()
+    magic, version, n, data_offset, r0, r1 = struct.unpack_from("<8sIIQII", b, 0)
+    assert (magic, version, n, r0, r1) == (b"VIOLETTO", 1, len(t), 0, 0)
+    assert data_offset == 16384 and len(b) % 16384 == 0
+    name, dtype, ndim, s0, s1, s2, s3, off, nbytes = struct.unpack_from("<64sII4IQQ", b, 32)
+    assert name.rstrip(b"\0") == b"embed" and dtype == 1 and ndim == 2 and (s0, s1, s2, s3) == (100, 512, 0, 0)
+    assert off == 0 and nbytes == 100 * 512 * 2
+    assert b[data_offset:data_offset + nbytes] == t["embed"].view(torch.uint8).numpy().tobytes()
+    # the second tensor starts at the next 256-byte boundary
+    off1 = struct.unpack_from("<Q", b, 32 + 128 + 88)[0]
+    assert off1 == -(-nbytes // 256) * 256
+
+
+def test_reader_records_and_contents(tmp_path):
+    path = tmp_path / "m.vlt"
+    t = _tensors()
+    write_vlt(path, t)
+    wf = WeightFile(path)
+    assert len(wf) == len(t)
+    names = [wf.info(i).name.decode() for i in range(len(wf))]
+    assert names == list(t)
+    for name, x in t.items():
+        info = wf.find(name)
+        assert tuple(info.shape[: info.ndim]) == tuple(x.shape)
+        got = wf.read(name)
+        want = x.view(torch.int16).numpy().view(np.uint16) if x.dtype == torch.bfloat16 else x.numpy()
+        assert np.array_equal(got, want), name
+    with pytest.raises(L.SvError, match="weight file has no tensor missing"):
+        wf.find("missing")
+    # matrices are checked before any device memory is needed
+    with pytest.raises(L.SvError, match="expected I8 \\[64, 256\\], found I8 \\[64, 512\\]"):
+        wf.matrix("L00.qkv", 64, 256)
+    with pytest.raises(L.SvError, match="not uploaded"):
+        wf.matrix("L00.qkv", 64, 512)
+    wf.close()
+
+
+def _write_raw(path, records, data=b"", n=None, version=1, magic=b"VIOLETTO"):
+    head = struct.pack("<8sIIQII", magic, version, len(records) if n is None else n, 16384, 0, 0)
+    body = head + b"".join(records)
+    body += b"\0" * (16384 - len(body)) + data
+    path.write_bytes(body)
+
+
+def _rec(name, dtype, shape, off, nbytes):
+    sh = list(shape) + [0] * (4 - len(shape))
+    return struct.pack("<64sII4IQQ24x", name.encode(), dtype, len(shape), *sh, off, nbytes)
+
+
+@pytest.mark.parametrize("case,msg", [
+    ("magic", "not a version-1 violetto weight file"),
+    ("version", "not a version-1 violetto weight file"),
+    ("dtype", "x: unknown dtype 5"),
+    ("bytes", "x: 12 bytes for 4 elements of F32"),
+    ("past_end", "x: bytes past the end of the file"),
+    ("twice", "x: two tensors of this name"),
+    ("records", "records do not fit the file"),
+])
+def test_malformed_files_refused(tmp_path, case, msg):
+    p = tmp_path / "bad.vlt"
+    data = b"\0" * 256
+    if case == "magic":
+        _write_raw(p, [_rec("x", 0, [4], 0, 16)], data, magic=b"VIOLETTA")
+    elif case == "version":
+        _write_raw(p, [_rec("x", 0, [4], 0, 16)], data, version=2)
+    elif case == "dtype":
+        _write_raw(p, [_rec("x", 5, [4], 0, 16)], data)
+    elif case == "bytes":
+        _write_raw(p, [_rec("x", 0, [4], 0, 12)], data)
+    elif case == "past_end":
+        _write_raw(p, [_rec("x", 0, [4], 250, 16)], data)
+    elif case == "twice":
+        _write_raw(p, [_rec("x", 0, [4], 0, 16), _rec("x", 0, [4], 16, 16)], data)
+    else:
+        _write_raw(p, [_rec("x", 0, [4], 0, 16)], data, n=200)
+    with pytest.raises(L.SvError, match=msg):
+        WeightFile(p)
+
+
+def test_matrix_groups_checked(tmp_path):
+    """model.rs:94-99: int8 groups must be a power of two from 8 to 256 that divides k (one
+    group per row, the configurations' format, also accepted); the scale must exist."""
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(16, 96, generator=g)
+    q, _ = quantize_rows(w)
+    path = tmp_path / "g.vlt"
+    write_vlt(path, {"a": q, "a.scale": torch.ones(16, 5, dtype=torch.bfloat16),  # 96 / 5 is no group
+                     "b": q, "b.scale": torch.ones(16, 24, dtype=torch.bfloat16),  # groups of 4
+                     "c": q})
+    wf = WeightFile(path)
+    with pytest.raises(L.SvError, match="a.scale: 5 groups per row of 96"):
+        wf.matrix("a", 16, 96)
+    with pytest.raises(L.SvError, match="b.scale: 24 groups per row of 96"):
+        wf.matrix("b", 16, 96)
+    with pytest.raises(L.SvError, match="weight file has no tensor c.scale"):
+        wf.matrix("c", 16, 96)
