@@ -440,7 +440,8 @@ enum {
   SV_KIND_COMPACT = 9,
   SV_KIND_REPLAY = 10,
   SV_KIND_ATTN_MERGE = 11, /* the attention split merge (its own launch) */
-  SV_KIND_COUNT = 12
+  SV_KIND_KV_WRITE = 12,   /* prompt chunks: the new K/V rows, before the attention */
+  SV_KIND_COUNT = 13
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

@@ -720,7 +720,8 @@ int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const uint32_t slot = in_runs[4 * ri], count = in_runs[4 * ri + 1], verify = in_runs[4 * ri + 2],
                    head = in_runs[4 * ri + 3];
-    if (count == 0 || count > SV_MAX_RUN) return -1;
+    /* a verify run holds at most SV_MAX_RUN rows (its tree); other runs (prompt chunks) any */
+    if (count == 0 || (verify && count > SV_MAX_RUN)) return -1;
     for (uint32_t j = 0; j < ri; j++)
       if (in_runs[4 * j] == slot) return -1;
     const uint32_t first_row = n;
@@ -728,7 +729,7 @@ int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens
       tokens[n] = in_tokens[n];
       tin[2 * n] = slot;
       tin[2 * n + 1] = row;
-      vis[n] = 0xffffffffu >> (31 - row);
+      vis[n] = 0xffffffffu >> (31 - row % SV_MAX_RUN); /* causal within its attention run of 16 */
       n++;
     }
     const uint32_t first_head = n_head;
@@ -794,7 +795,7 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     sv_kv_args kv = io->kv;
     kv.kv_layer = li;
     orc_attn_verify(sh, qkv, io->meta, io->k_cache, io->v_cache, io->page_table, io->rope, &kv, &aa,
-                    io->attn_runs, io->n_runs, io->vis, attn);
+                    io->attn_runs, io->n_attn ? io->n_attn : io->n_runs, io->vis, attn);
     /* o: Resid (encode.rs:172-175) */
     a.k = NQ * D;
     a.m = H;

@@ -97,7 +97,7 @@ typedef struct orc_step_io {
   const uint32_t* head_rows; /* [n_head]                         */
   const sv_sample_row* samples;
   const sv_run_in* runs;
-  const uint32_t* attn_runs; /* [n_runs][2] (first, count)      */
+  const uint32_t* attn_runs; /* [n_attn][2] (first, count <= 16) */
   uint32_t compact;          /* run kv_compact                   */
   /* device-resident state in the reference */
   uint32_t* lens, *feed, *tree;
@@ -112,6 +112,7 @@ typedef struct orc_step_io {
   uint32_t* out;   /* [n_head]        */
   uint32_t* emitted, *path, *path_len, *on_path;
   float* hidden;   /* [n][H] final residual, may be NULL */
+  uint32_t n_attn; /* attention runs: each run's rows in runs of 16 (0: n_runs) */
 } orc_step_io;
 
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,

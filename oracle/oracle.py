@@ -221,7 +221,8 @@ class StepIO(C.Structure):
                 ("head_rows", vp), ("samples", vp), ("runs", vp), ("attn_runs", vp), ("compact", u32),
                 ("lens", vp), ("feed", vp), ("tree", vp), ("gen", vp), ("k_cache", vp), ("v_cache", vp),
                 ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
-                ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp)]
+                ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp),
+                ("n_attn", u32)]
 
 
 def _chain(row: int) -> int:
@@ -333,7 +334,10 @@ class OracleEngine:
         n_head = lib().orc_plan(ptr(in_runs), u32(n_runs), ptr(in_tokens), ptr(seq_len), samp, ptr(tokens), ptr(tin),
                                 ptr(vis), ptr(head_rows), samples, run_in)
         assert n_head >= 0, "plan rejected"
-        attn_runs = np.array([[ri.first, ri.count] for ri in run_in], np.uint32).reshape(-1)
+        # attention runs of at most 16 rows: a prompt chunk's later rows see its earlier ones as
+        # cached keys (written by the earlier runs)
+        attn_runs = np.array([[ri.first + j, min(16, ri.count - j)] for ri in run_in for j in range(0, ri.count, 16)],
+                             np.uint32).reshape(-1)
         branches = any(r[2] and len(r[1]) > 2 for r in runs)
         meta = np.zeros(2 * n, np.uint32)
         logits = np.zeros((max(1, n_head), self.shape.vocab), np.float32)
@@ -350,6 +354,7 @@ class OracleEngine:
         io.runs = C.cast(run_in, vp)
         io.attn_runs = ptr(attn_runs)
         io.compact = int(branches if compact is None else compact)
+        io.n_attn = attn_runs.size // 2
         io.lens, io.feed, io.tree = ptr(self.lens), ptr(self.feed), ptr(self.tree)
         io.gen = C.cast(self.gen, vp)
         io.k_cache, io.v_cache, io.page_table = ptr(self.k), ptr(self.v), ptr(self.pool.table)

@@ -389,6 +389,19 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t 
   *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
 }
 
+// Prompt chunks (qkv_post, kernels.metal:749-801, for the chunk path of encode.rs:300-355):
+// every attention run's new K/V rows (norm, RoPE, bf16) to the cache before any run reads
+// them, so a chunk's later runs of 16 rows find its earlier rows as cached keys. The same
+// new_keys code as the attention's own pass, so both write the same bits. Grid (runs, kv
+// heads).
+template <int D, bool INL>
+__global__ __launch_bounds__(256) void kv_write_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
+  uint32_t t0, T, seq;
+  run_header<INL>(p, blockIdx.x, t0, T, seq);
+  new_keys<D, false>(p, seq, blockIdx.y, t0, T, p.meta[2 * t0 + 1], nk, nv, threadIdx.x, 256);
+}
+
 // Dynamic LDS of up to 4 x 64 x 128 floats (+ l): allow it once per instantiation, outside
 // any graph capture (sv_engine_create calls this; attn_launch does on its first use).
 void attn_init() {
@@ -515,6 +528,17 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW;
   const bool allin = fits && (g_attn_allin == 1 || (g_attn_allin < 0 && (size_t)args->max_splits * NKV * n_runs <= attn_cus()));
   p.newest_own = attn_newest_own((int)nct, allin ? SV_ATTN_NBW : 0) ? 1u : 0u;
+  if (parts & 4) {
+    const dim3 g4(n_runs, NKV);
+    if (D == 64) {
+      if (p.n_inline) launch(kv_write_kernel<64, true>, g4, dim3(256), 0, stream, p);
+      else launch(kv_write_kernel<64, false>, g4, dim3(256), 0, stream, p);
+    } else {
+      if (p.n_inline) launch(kv_write_kernel<128, true>, g4, dim3(256), 0, stream, p);
+      else launch(kv_write_kernel<128, false>, g4, dim3(256), 0, stream, p);
+    }
+    SV_TRY_LAUNCH("kv_write");
+  }
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);
     const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;

@@ -1,7 +1,6 @@
-// attn_device.h — device pieces of the verify attention shared by attn_verify_kernel and the
-// persistent step kernel: paged K/V addressing, the 32-key batch (load + MFMA products), the
-// query build and the new-key pass (the reference's attn_verify, engine/src/kernels.metal:
-// 891-1148).
+// attn_device.h — device pieces of the verify attention (attn_verify_kernel, kv_write_kernel):
+// paged K/V addressing, the 32-key batch (load + MFMA products), the query build and the
+// new-key pass (the reference's attn_verify, engine/src/kernels.metal:891-1148).
 #pragma once
 #include "sv_device.h"
 
@@ -58,16 +57,6 @@ __device__ __forceinline__ void run_header(const AttnParams& p, uint32_t r, uint
     seq = p.meta[2 * t0];
   }
 }
-
-// Step constants of one run, cached in LDS by the persistent step for all layers: positions
-// and visibility of its T new rows, the layer-0 cache element offset of each new key (for
-// kv head g), and the rope (cos, sin) of each row's position.
-struct RunConsts {
-  uint32_t pos[SV_MAX_RUN], vis[SV_MAX_RUN];
-  size_t row0[SV_MAX_RUN];
-  float2 rope[SV_MAX_RUN][SV_ROPE_PAIRS];
-  size_t kvt[8][2];  // per wave: layer-0 offsets of its first cached batch's two 16-key tiles
-};
 
 // Element offset of kv head g's row at cache position pos (kernels.metal:704-711, global).
 template <int D>
@@ -391,7 +380,7 @@ struct QRaw {
 
 template <int D, int NCT, bool COH>
 __device__ __forceinline__ void qload(const AttnParams& p, uint32_t t0, uint32_t g, uint32_t ncols, QRaw<D, NCT>& r,
-                                      int lane, const RunConsts* rc = nullptr) {
+                                      int lane) {
   constexpr int KST = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -400,8 +389,7 @@ __device__ __forceinline__ void qload(const AttnParams& p, uint32_t t0, uint32_t
     r.pos[ct] = 0;
     if (c < ncols) {
       const uint32_t i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
-      // with rc: the row index into its tables
-      r.pos[ct] = rc ? i : p.meta[2 * t + 1];
+      r.pos[ct] = p.meta[2 * t + 1];
       const size_t qo = (size_t)t * p.W + h * D + 8 * q;
 #pragma unroll
       for (int ks = 0; ks < KST; ks++) {
@@ -424,7 +412,7 @@ __device__ __forceinline__ void qload(const AttnParams& p, uint32_t t0, uint32_t
 // The rope words of a lane's columns (all columns requested together).
 template <int D, int NCT>
 __device__ __forceinline__ void qrope_load(const AttnParams& p, uint32_t ncols, const QRaw<D, NCT>& r,
-                                           float2 (&cs)[NCT][D / 32][4], int lane, const RunConsts* rc = nullptr) {
+                                           float2 (&cs)[NCT][D / 32][4], int lane) {
   constexpr int KST = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -435,9 +423,7 @@ __device__ __forceinline__ void qrope_load(const AttnParams& p, uint32_t ncols, 
       for (int jj = 0; jj < 4; jj++) {
         const uint32_t j = 16 * ks + 4 * q + jj;
         const bool on = p.rope_on && 16 * ct + c16 < ncols && 32 * ks + 8 * q < 64;
-        cs[ct][ks][jj] = !on ? float2{1.0f, 0.0f}
-                         : rc ? rc->rope[r.pos[ct]][j]
-                              : *(const float2*)(p.rope + ((size_t)r.pos[ct] * SV_ROPE_PAIRS + j) * 2);
+        cs[ct][ks][jj] = !on ? float2{1.0f, 0.0f} : *(const float2*)(p.rope + ((size_t)r.pos[ct] * SV_ROPE_PAIRS + j) * 2);
       }
 }
 
@@ -481,9 +467,9 @@ __device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, 
 
 template <int D, int NCT>
 __device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r, bf16x8 (&qh)[NCT][D / 32],
-                                        bf16x8 (&ql)[NCT][D / 32], int lane, const RunConsts* rc = nullptr) {
+                                        bf16x8 (&ql)[NCT][D / 32], int lane) {
   float2 cs[NCT][D / 32][4];
-  qrope_load<D, NCT>(p, ncols, r, cs, lane, rc);
+  qrope_load<D, NCT>(p, ncols, r, cs, lane);
   qfinish_cs<D, NCT>(p, ncols, r, cs, qh, ql, lane);
 }
 
@@ -493,11 +479,10 @@ __device__ __forceinline__ void qfinish(const AttnParams& p, uint32_t ncols, QRa
 // loads (written earlier in the same launch by other workgroups).
 template <int D, int NCT, bool COH>
 __device__ __forceinline__ void build_queries(const AttnParams& p, uint32_t t0, uint32_t g, uint32_t ncols,
-                                              bf16x8 (&qh)[NCT][D / 32], bf16x8 (&ql)[NCT][D / 32], int lane,
-                                              const RunConsts* rc = nullptr) {
+                                              bf16x8 (&qh)[NCT][D / 32], bf16x8 (&ql)[NCT][D / 32], int lane) {
   QRaw<D, NCT> r;
-  qload<D, NCT, COH>(p, t0, g, ncols, r, lane, rc);
-  qfinish<D, NCT>(p, ncols, r, qh, ql, lane, rc);
+  qload<D, NCT, COH>(p, t0, g, ncols, r, lane);
+  qfinish<D, NCT>(p, ncols, r, qh, ql, lane);
 }
 
 // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
@@ -505,13 +490,12 @@ __device__ __forceinline__ void build_queries(const AttnParams& p, uint32_t t0, 
 // within a thread); threads tid < nthreads of the caller take keys tid / 16, + nthreads / 16...
 template <int D, bool COH>
 __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t t0, uint32_t T,
-                                         uint32_t p0, uint16_t* nk, uint16_t* nv, uint32_t tid, uint32_t nthreads,
-                                         const RunConsts* rc = nullptr) {
+                                         uint32_t p0, uint16_t* nk, uint16_t* nv, uint32_t tid, uint32_t nthreads) {
   constexpr int DL = D / 16;
   const uint32_t l16 = tid & 15;
   for (uint32_t i = tid >> 4; i < T; i += nthreads >> 4) {
     {
-      const uint32_t t = t0 + i, pos = rc ? 0u : p.meta[2 * t + 1];
+      const uint32_t t = t0 + i, pos = p.meta[2 * t + 1];
       const size_t ko = (size_t)t * p.W + p.KOFF + g * D + DL * l16;
       const size_t vo = (size_t)t * p.W + p.VOFF + g * D + DL * l16;
       float kv[DL], vv[DL];
@@ -524,8 +508,7 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
           vv[e + j] = b[j];
         }
       }
-      const size_t row = rc ? rc->row0[i] + (size_t)p.layer * p.n_pages * p.NKV * ((size_t)D << p.page_shift)
-                            : kv_off<D>(p, seq, g, p0 + i);
+      const size_t row = kv_off<D>(p, seq, g, p0 + i);
       float ss = 0.0f;
 #pragma unroll
       for (int e = 0; e < DL; e++) ss = __builtin_fmaf(kv[e], kv[e], ss);
@@ -538,8 +521,7 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
         const uint32_t d = DL * l16 + e;
         float k0 = kv[e] * inv, k1 = kv[e + 1] * inv;
         if (p.rope_on && d < 64) {
-          const float2 cs = rc ? rc->rope[i][d / 2]
-                               : *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
+          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
           const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
           k0 = r0;
           k1 = r1;

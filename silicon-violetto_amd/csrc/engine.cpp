@@ -190,10 +190,12 @@ uint32_t choose_split(const std::vector<uint32_t>& cached, uint32_t extra, uint3
 
 struct Plan {
   uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
+  uint32_t n_attn = 0;  // attention runs: each run's rows in runs of at most SV_MAX_RUN
+  bool chunk = false;   // some run has more rows (a prompt chunk): new K/V are written first
   std::vector<uint32_t> slots;   // per run
   std::vector<uint32_t> counts;  // per run
   std::vector<uint32_t> verify;  // per run
-  std::vector<uint32_t> inl;     // per run: first token, rows, slot (the attention's inline runs)
+  std::vector<uint32_t> inl;     // per attention run: first token, rows, slot (inline in the launch)
   // Steps this plan may run (encodes, graph replays, profiled steps): each advances a run by at
   // most its row count, and every position it can reach has a reserved page.
   uint64_t budget = 0, issued = 0;
@@ -413,10 +415,14 @@ struct sv_engine {
                matmul(L.qkv, n, h, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
       aa.rope = L.rope;
       const sv_kv_args kv = kv_args(li);
+      if (P.chunk)
+        SV_TIMED(SV_KIND_KV_WRITE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
+                                               attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 4,
+                                               P.inl.data()));
       SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                         attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data()));
+                                         attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data()));
       SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                               attn_runs, P.n_runs, P.max_run, vis, attn, ws, ws_bytes, 2,
+                                               attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 2,
                                                P.inl.data()));
       SV_TIMED(SV_KIND_O,
                matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn, h, nullptr));
@@ -501,7 +507,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   ALLOC(tin, 2 * (size_t)n);
   ALLOC(vis, n);
   ALLOC(head_rows, n);
-  ALLOC(attn_runs, 2 * (size_t)S);
+  ALLOC(attn_runs, 2 * ((size_t)n / SV_MAX_RUN + S));
   ALLOC(sample_rows, std::max(n, R));
   ALLOC(runs, S);
   ALLOC(out_ids, std::max(n, R));
@@ -801,8 +807,8 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const sv_run& r = runs_in[ri];
     SV_TRY(check_slot(e, r.slot));
-    if (r.count == 0 || r.count > SV_MAX_RUN)
-      return fail(SV_ERR_CAPACITY, "%u tokens for one sequence in a step (max %u)", r.count, SV_MAX_RUN);
+    if (r.count == 0 || (r.verify && r.count > SV_MAX_RUN))
+      return fail(SV_ERR_CAPACITY, "%u tokens for one sequence in a verify step (max %u)", r.count, SV_MAX_RUN);
     if (!r.tokens) return fail(SV_ERR_ARG, "plan: run %u has no tokens", ri);
     for (uint32_t j = 0; j < ri; j++)
       if (runs_in[j].slot == r.slot) return fail(SV_ERR_ARG, "a sequence appears twice in one step");
@@ -836,7 +842,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
       tokens.push_back(r.tokens[row]);
       tin.push_back(slot);
       tin.push_back(row);
-      vis.push_back(0xffffffffu >> (31 - row));  // causal within the run (plan.rs:81)
+      vis.push_back(0xffffffffu >> (31 - row % SV_MAX_RUN));  // causal within its attention run (plan.rs:81)
     }
     const uint32_t first_head = (uint32_t)head_rows.size();
     if (r.verify)
@@ -851,21 +857,28 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     }
     run_in.push_back(sv_run_in{slot, first_row, count, first_head, (uint32_t)head_rows.size() - first_head,
                                r.verify ? 1u : 0u});
-    attn_runs.push_back(first_row);
-    attn_runs.push_back(count);
-    max_cached = std::max(max_cached, e->seq_len[slot]);
-    run_cached.push_back(e->seq_len[slot]);
-    P.max_run = std::max(P.max_run, count);
+    // Attention runs of at most SV_MAX_RUN rows: a prompt chunk's later ones see its earlier
+    // rows as cached keys (plan.rs:99-104 tiles the chunk path the same way, in 8s).
+    for (uint32_t j = 0; j < count; j += SV_MAX_RUN) {
+      const uint32_t c = std::min(SV_MAX_RUN, count - j);
+      attn_runs.push_back(first_row + j);
+      attn_runs.push_back(c);
+      P.inl.insert(P.inl.end(), {first_row + j, c, slot});
+      max_cached = std::max(max_cached, e->seq_len[slot] + j);
+      run_cached.push_back(e->seq_len[slot] + j);
+    }
+    P.max_run = std::max(P.max_run, std::min(count, SV_MAX_RUN));
+    P.chunk = P.chunk || count > SV_MAX_RUN;
     P.branches |= (r.verify && count > 2) ? 1u : 0u;
     P.slots.push_back(slot);
     P.counts.push_back(count);
-    P.inl.insert(P.inl.end(), {first_row, count, slot});
     P.verify.push_back(r.verify ? 1u : 0u);
     e->seq_len[slot] += count;
   }
   if (head_rows.size() > e->cfg.max_head_rows)
     return fail(SV_ERR_CAPACITY, "%zu head rows (max %u)", head_rows.size(), e->cfg.max_head_rows);
   P.n = n;
+  P.n_attn = (uint32_t)attn_runs.size() / 2;
   P.budget = budget;
   P.n_head = (uint32_t)head_rows.size();
   P.n_runs = n_runs;
@@ -876,7 +889,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     split = choose_split(run_cached, extra_keys, e->sh.n_kv_heads, P.max_run, e->sh.n_heads / e->sh.n_kv_heads);
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
-  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, n_runs, P.max_splits, P.max_run)));
+  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, P.n_attn, P.max_splits, P.max_run)));
   SV_TRY(e->upload(e->tokens, tokens.data(), tokens.size() * 4));
   SV_TRY(e->upload(e->tin, tin.data(), tin.size() * 4));
   SV_TRY(e->upload(e->vis, vis.data(), vis.size() * 4));

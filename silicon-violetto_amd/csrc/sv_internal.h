@@ -63,7 +63,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts = 3,  // bit 0: attention, bit 1: the split merge
+                      uint32_t parts = 3,  // bit 0: attention, bit 1: the split merge, bit 2: runs' new K/V first
                       const uint32_t* host_runs = nullptr,  // (first token, rows, slot) per run, if known
                       bool may_fuse = true);  // the counted last-split merge may be used (tests select it)
 // attn_launch with the split partials in the library's per-device static scratch array.

@@ -31,7 +31,7 @@ FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
 FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
-KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge")
+KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "kv_write")
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 

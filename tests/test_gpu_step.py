@@ -624,3 +624,63 @@ def test_step_from_weight_file(gpu, tmp_path, group):
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
     eng.close()
     wf.close()
+
+
+def test_prompt_chunks_then_verify(gpu):
+    """The chunk path (encode.rs:300-355): three streams on shuffled pages with 100, 37 and 500
+    cached tokens each take a prompt chunk of 40, 100 and 23 tokens in one step (attention in
+    runs of 16 rows after every new K/V row is written), then a verify step of drafts. Last-row
+    logits and greedy ids, lengths, page tables and both caches (within one bf16 step) against
+    the oracle engine."""
+    banner("prompt chunks, then verify")
+    shape = ModelShape(n_layers=2, vocab=4096, vocab_real=4000)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=[100, 37, 500], n_seqs=3, seed=41, max_seq_len=1024,
+                                                 shuffle=True, max_head_rows=48)
+    eng.close()
+    freq = rope_freq(500000.0, shape.head_dim)
+    eng = Engine(shape, max_seqs=3, max_step_tokens=256, max_seq_len=1024, max_head_rows=48, kv_tokens=3 * 1024,
+                 attn_scale=0.125, freq=freq)
+    eng.set_model(gm)
+    ref2 = oracle.OracleEngine(L, shape, *oracle.host_weights(model), max_seqs=3, max_seq_len=1024,
+                               kv_tokens=3 * 1024, attn_scale=0.125, freq=freq)
+    for s, c in zip(slots, [100, 37, 500]):
+        assert eng.new_seq() == ref2.new_seq() == s
+    left = dict(zip(slots, [100, 37, 500]))
+    while left:  # shuffled page tables, the same on both sides
+        s = int(rng.choice(list(left)))
+        k = min(16, left[s])
+        eng.bench_fill(s, k)
+        ref2.bench_fill(s, k)
+        left[s] -= k
+        if not left[s]:
+            del left[s]
+    kd, vd = eng.kv_cache()
+    bits = rng.integers(0x3C00, 0x4000, (2,) + tuple(kd.shape), dtype=np.uint16) | \
+        (rng.integers(0, 2, (2,) + tuple(kd.shape), dtype=np.uint16) << np.uint16(15))
+    ref2.k[...], ref2.v[...] = bits[0], bits[1]
+    kd.copy_(torch.from_numpy(bits[0].view(np.int16)).cuda().view(torch.bfloat16))
+    vd.copy_(torch.from_numpy(bits[1].view(np.int16)).cuda().view(torch.bfloat16))
+    torch.cuda.synchronize()
+    ref = ref2
+    chunks = [(s, [int(x) for x in rng.integers(0, shape.vocab_real, k)], False, 1) for s, k in zip(slots, [40, 100, 23])]
+    res = eng.step(chunks, logits=True)
+    ids_r, logits_r, em_r, extra_r = ref.step(chunks)
+    assert res.info.n_tokens == 163 and res.info.n_head == 3
+    compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
+    assert np.array_equal(res.ids, ids_r)
+    for s, c in zip(slots, [140, 137, 523]):
+        assert eng.seq_len(s) == ref.seq_len[s] == c
+    got_k = oracle.bf16_to_f32(kd.view(torch.int16).cpu().numpy().view(np.uint16))
+    got_v = oracle.bf16_to_f32(vd.view(torch.int16).cpu().numpy().view(np.uint16))
+    for got, want, what in ((got_k, oracle.bf16_to_f32(ref.k), "K"), (got_v, oracle.bf16_to_f32(ref.v), "V")):
+        bad = np.abs(got - want) > 2 ** -7 * np.abs(want) + 1e-4
+        assert not bad.any(), f"{what} cache differs at {int(bad.sum())} elements"
+    # the fed tokens, then a verify step of four drafts per stream on top of the chunks
+    for s in slots:
+        t = int(ids_r[slots.index(s)])
+        assert int(dev_u32(eng, "d_feed", (3 * 16,))[s * 16]) == t
+    runs = [(s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, 4)], True) for s in slots]
+    res = eng.step(runs, logits=True)
+    ids_r, logits_r, em_r, extra_r = ref.step(runs)
+    compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots)
+    eng.close()

@@ -712,3 +712,39 @@ def test_draft_tree_skips_unfilled_candidates():
     # best-first: 11 (0.6), 21 under it (0.54), 12 (0.3)... : three nodes, none of them NO_TOK
     assert list(feed[1:4]) == [11, 21, 12]
     assert L.NO_TOK not in feed
+
+
+# ------------------------------------------------------------------- prompt chunks
+def test_chunk_prefill_equals_token_by_token():
+    """A prompt chunk (one non-verify run of 40 rows: attention runs of 16, each later one seeing
+    the earlier ones' keys as cached) leaves the same KV cache and the same last-row logits as
+    feeding the prompt one token per step, bit for bit (the oracle's sums run in position
+    order either way), on top of 23 cached tokens."""
+    from violetto.model import ModelShape, SyntheticModel
+
+    shape = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=512, vocab_real=500,
+                       n_layers=2)
+    model = SyntheticModel.generate(shape, seed=5, device="cpu")
+    emb, lay, sc = O.host_weights(model)
+    freq = (500000.0 ** (-2.0 * np.arange(32) / 64)).astype(np.float32)
+    engines = [O.OracleEngine(L, shape, emb, lay, sc, max_seqs=1, max_seq_len=128, kv_tokens=128, freq=freq)
+               for _ in range(2)]
+    rng = np.random.default_rng(6)
+    kv0 = rng.integers(0x3C00, 0x4000, engines[0].k.shape, dtype=np.uint16)
+    prompt = [int(x) for x in rng.integers(0, 500, 40)]
+    for e in engines:
+        s = e.new_seq()
+        e.bench_fill(s, 23)
+        e.k[...] = kv0
+        e.v[...] = kv0 ^ np.uint16(0x8000)
+    ids_a, logits_a, _, _ = engines[0].step([(0, prompt, False, 1)])
+    for i, t in enumerate(prompt):
+        ids_b, logits_b, _, _ = engines[1].step([(0, [t], False, 1)])
+    assert engines[0].seq_len[0] == engines[1].seq_len[0] == 63
+    assert engines[0].lens[0] == engines[1].lens[0] == 63
+    assert np.array_equal(logits_a[-1], logits_b[-1]) and ids_a[-1] == ids_b[-1]
+    pages = engines[0].pool.pages(0)
+    assert pages == engines[1].pool.pages(0)
+    for arr in ("k", "v"):
+        a, b = getattr(engines[0], arr), getattr(engines[1], arr)
+        assert np.array_equal(a[:, pages], b[:, pages]), f"{arr} cache"
