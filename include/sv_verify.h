@@ -49,6 +49,12 @@ extern "C" {
 #define SV_RMS_EPS 1.1920928955078125e-07f /* 2^-23 (kernels.metal:13) */
 #define SV_ROPE_PAIRS 32u       /* RoPE pairs per head: dims 0..63 (kernels.metal:727-736) */
 #define SV_DRAFT_CANDS 4u       /* drafter candidates per block row, at most (kernels.metal:1845) */
+#define SV_VE_GATE_W 12u        /* value-embedding gate inputs: rms_norm(x)[:12] (kernels.metal:738-747) */
+#define SV_MUDD_INNER 32u       /* MUDD inner width (kernels.metal:1367-1372, model.rs:97) */
+#define SV_MUDD_SITES 2u        /* MUDD sites, at most (model.rs:21) */
+/* Attention columns per kv head: a run's rows x (n_heads / n_kv_heads) stay within this. With
+ * n_heads / n_kv_heads = g, attention runs hold min(SV_MAX_RUN, SV_MAX_COLS / g) rows. */
+#define SV_MAX_COLS 64u
 
 /* Matmul epilogues and flags (kernels.metal:151-152, kernels.rs:4-10). */
 enum {
@@ -124,9 +130,13 @@ typedef struct sv_mat_args {
   uint32_t gshift;
 } sv_mat_args;
 
-/* KvArgs (kernels.rs:53-63, kernels.metal:692-700). Only paged ("global") layers are built:
- * is_global must be 1; ring and window are unused. Cache layout per tensor (K and V):
- * bf16 [layers][n_pages][NKV][page][D], page = 1 << page_shift. */
+/* KvArgs (kernels.rs:53-63, kernels.metal:692-700). Cache layout per tensor (K and V):
+ * bf16 [layers][n_pages][NKV][page][D], page = 1 << page_shift, through the page table
+ * [max_seqs][max_pages]. is_global 0 is a sliding-window layer (kernels.metal:808-811): a
+ * query at position pos sees the cached keys from pos - window on (window > 0). Its ring
+ * (kv.rs:26-32, [layer][seq][NKV][ring][D] in the reference) is laid out here as pages too: a
+ * sequence's ring of R pages is pages seq R .. seq R + R - 1 and its page-table row is
+ * cyclic (entry p = seq R + p % R), so one addressing serves both kinds; `ring` is unused. */
 typedef struct sv_kv_args {
   uint32_t is_global, kv_layer;
   uint32_t ring, max_seqs;
@@ -210,18 +220,48 @@ sv_status sv_matmul(void* stream, const sv_matrix* w, const float* d_x, const ui
  * weights are used as loaded, model.rs:22-47); done once at model load. */
 sv_status sv_pack_matrix(void* stream, const sv_matrix* src, void* d_dst, sv_matrix* out);
 
+/* The Limite layer extras of the attention (kernels.metal:738-747 add_ve, 910-942 new_key,
+ * 1316-1362 attn_dec_reduce; model.rs:49-67): any pointer may be NULL, which turns its part
+ * off. With d_ve_gate, each new V row gets 2 sigmoid(rms_norm(x)[:12] . ve_gate[g]) *
+ * value_embed[token][g D ..] before it is rounded and cached (needs d_x, d_inv, d_tokens,
+ * d_value_embed). With d_attn_gate, output o of head h is scaled by 2 sigmoid(rms_norm(x)[:D] .
+ * attn_gate[h]) (needs d_x, d_inv). With d_xsa (needs d_vdir), o - xsa[h] (o . v) v with v the
+ * token's new value row of kv head h / g, normalised (|v| floored at 1e-4), before the gate. */
+typedef struct sv_attn_extras {
+  const float* d_x;              /* [n][hidden] the attention input before its norm    */
+  const float* d_inv;            /* [n] 1 / rms(x) (the qkv matmul's SV_FLAG_WRITE_INV) */
+  const uint32_t* d_tokens;      /* [n] the tokens' ids (resolved)                      */
+  const uint16_t* d_value_embed; /* bf16 [vocab][NKV D]                                 */
+  const float* d_ve_gate;        /* [NKV][SV_VE_GATE_W]                                 */
+  const float* d_attn_gate;      /* [NQ][D]                                             */
+  const float* d_xsa;            /* [NQ]                                                */
+  float* d_vdir;                 /* [n][NKV][D] scratch the attention writes for XSA    */
+  uint32_t hidden;               /* row stride of d_x                                   */
+  uint32_t pad;
+} sv_attn_extras;
+
 /* Fused verify attention (kernels.metal:1008-1148 attn_verify + 1316-1362 attn_dec_reduce;
- * encode.rs:233-297): for each run (d_runs: uint2 (first token, count <= SV_MAX_RUN)),
- * q/k rms-norm + RoPE, the run's new K/V written bf16 to the paged cache at p0 + row,
- * attention over the cached keys [0, p0) and the new keys in each token's vis mask, with
- * split-KV partials merged by plain sums. d_qkv is [n][(NQ + 2 NKV) D] fp32; d_out is
- * [n][NQ D] fp32. XSA and the attention gate are not built (xsa = 0, gate = 1). */
+ * encode.rs:233-297): for each run (d_runs: uint2 (first token, count <= SV_MAX_RUN and
+ * count x NQ / NKV <= SV_MAX_COLS)), q/k rms-norm + RoPE, the run's new K/V written bf16 to
+ * the paged cache at p0 + row, attention over the cached keys [0, p0) (sliding-window layers:
+ * from each query's pos - window) and the new keys in each token's vis mask, with split-KV
+ * partials merged by plain sums. d_qkv is [n][(NQ + 2 NKV) D] fp32; d_out is [n][NQ D] fp32.
+ * extras: NULL, or the layer's extras (sv_attn_extras). */
 size_t sv_attn_workspace_bytes(const sv_shape* shape, uint32_t n_runs, uint32_t max_splits, uint32_t max_run);
 sv_status sv_attn_verify(void* stream, const sv_shape* shape, const float* d_qkv, const uint32_t* d_meta,
                          uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
                          const float* d_rope, const sv_kv_args* kv, const sv_attn_args* args,
                          const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
-                         float* d_out, void* d_workspace, size_t workspace_bytes);
+                         float* d_out, void* d_workspace, size_t workspace_bytes, const sv_attn_extras* extras);
+
+/* mudd (kernels.metal:1364-1407, encode.rs:145-160): per token, one inner projection of
+ * rms_norm(cur) (inner = gelu(dense1 . x), dense1 [SV_MUDD_INNER][hidden]) feeds six mixes
+ * w = mix[i][:32] . inner + mix[i][32] (mix [2][3][33]: attention input, residual base) of the
+ * taps: out_attn = w0 tap0 + w1 tap1 + w2 cur, out_base = w3 tap0 + w4 tap1 + w5 cur. All
+ * [n][hidden] fp32. gelu is the erf form, erf by Abramowitz & Stegun 7.1.26 as the
+ * reference's (kernels.metal:30-37). */
+sv_status sv_mudd(void* stream, const float* d_cur, const float* d_tap0, const float* d_tap1, const float* d_dense1,
+                  const float* d_mix, float* d_out_attn, float* d_out_base, uint32_t n, uint32_t hidden);
 
 /* No counterpart in the reference: sv_attn_verify for callers that cannot allocate (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc). The same kernels and
@@ -317,10 +357,19 @@ typedef struct sv_engine_config {
   float attn_scale;         /* softmax scale (reference ATTN_SCALE, model.rs:19) */
   uint32_t split_keys;      /* cached keys per attention split, multiple of 32; 0: auto */
   uint32_t options;         /* reserved: 0                                      */
+  /* Sliding-window layers (model.rs:16-17,116; kv.rs:26-32): keys a local query sees
+   * besides itself, and which layers are local ([n_layers], 1 local; NULL: all global).
+   * Local layers keep a ring of ceil((window + max_step_tokens) / page) pages per slot. */
+  uint32_t window;
+  uint32_t pad;
+  const uint8_t* local;
 } sv_engine_config;
 
-/* One decoder layer (model.rs:49-67): matrices and scalars. rope: whether the layer's
- * q/k get RoPE (the reference ropes its local layers only, encode.rs:237). */
+/* One decoder layer (model.rs:49-67): matrices, scalars and the extras. rope: whether the
+ * layer's q/k get RoPE (the reference ropes its local layers only, encode.rs:237). Device
+ * pointers, NULL for a part the layer does not have: attn_gate [n_heads][head_dim] (NULL: gate
+ * 1), ve_gate [n_kv_heads][SV_VE_GATE_W] (value embeddings; needs the model's table, set by
+ * sv_engine_set_extras), xsa [n_heads] (NULL: 0). */
 typedef struct sv_layer {
   sv_matrix qkv, o, gate_up, down;
   float qkv_scale, o_scale;
@@ -328,7 +377,25 @@ typedef struct sv_layer {
   float resid_mlp, post_mlp;
   uint32_t rope;
   uint32_t pad;
+  const float* attn_gate;
+  const float* ve_gate;
+  const float* xsa;
 } sv_layer;
+
+/* The model's extras (model.rs:73-83, encode.rs:107-160). value_embed: bf16 [vocab][n_kv_heads
+ * head_dim] for the layers with a ve_gate. MUDD: site s runs before layer mudd_layer[s] on its
+ * input (cur), with taps the embedding's rows and the output of layer mudd_tap[s] <
+ * mudd_layer[s] (the reference: sites 24 and 47, taps 11 and 22); dense1 [SV_MUDD_INNER][hidden],
+ * mix [n_mudd][2][3][33]. */
+typedef struct sv_model_extras {
+  const uint16_t* value_embed;
+  const float* mudd_dense1;
+  const float* mudd_mix;
+  uint32_t n_mudd;
+  uint32_t mudd_layer[SV_MUDD_SITES];
+  uint32_t mudd_tap[SV_MUDD_SITES];
+  uint32_t pad;
+} sv_model_extras;
 
 /* rope_freq: host [SV_ROPE_PAIRS] frequencies (model.rs:81, tools/convert.py:59-61). */
 sv_status sv_engine_create(const sv_engine_config* cfg, const float* rope_freq, sv_engine** out);
@@ -336,6 +403,7 @@ void sv_engine_destroy(sv_engine* e);
 /* Tied bf16 embedding / head [vocab][hidden] (device), and the layers. */
 sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed);
 sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_layer* l);
+sv_status sv_engine_set_extras(sv_engine* e, const sv_model_extras* x);
 /* The HIP stream the engine runs on (a hipStream_t), created by the engine. */
 void* sv_engine_stream(sv_engine* e);
 
@@ -358,6 +426,13 @@ typedef struct sv_engine_buffers {
   uint32_t* d_path_len;     /* [max_seqs]                           */
   uint32_t n_pages, max_pages;
   size_t kv_bytes;          /* bytes of each of K and V             */
+  /* sliding-window layers (NULL without): [n_local][n_local_pages][NKV][page][D] bf16
+   * with the cyclic page table [max_seqs][max_pages] (sv_kv_args) */
+  uint16_t* d_k_local;
+  uint16_t* d_v_local;
+  uint32_t* d_local_table;
+  uint32_t n_local_pages, ring_pages;
+  size_t local_bytes;       /* bytes of each of K and V (local)     */
 } sv_engine_buffers;
 sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* out);
 
@@ -441,7 +516,8 @@ enum {
   SV_KIND_REPLAY = 10,
   SV_KIND_ATTN_MERGE = 11, /* the attention split merge (its own launch) */
   SV_KIND_KV_WRITE = 12,   /* prompt chunks: the new K/V rows, before the attention */
-  SV_KIND_COUNT = 13
+  SV_KIND_MUDD = 13,
+  SV_KIND_COUNT = 14
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

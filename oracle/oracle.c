@@ -317,39 +317,73 @@ static void norm_rope_d(const float* v, double* o, uint32_t D, int rope, const f
     }
 }
 
+/* kernels.metal:808-811 key_lo(): the first cached key a query at pos sees; a
+ * sliding-window layer (is_global 0) sees `window` keys besides itself. */
+static inline uint32_t key_lo(const sv_kv_args* kv, uint32_t pos) {
+  return !kv->is_global && pos > kv->window ? pos - kv->window : 0u;
+}
+
+static inline double sigmoid2_d(double x) { return 2.0 / (1.0 + exp(-x)); }
+
+/* sum over d < n of x[d] inv w[d]: a gate's input, rms_norm(x)[:n] . w (kernels.metal:738-747,
+ * 936-941) */
+static double gate_dot(const float* x, float inv, const float* w, uint32_t n) {
+  double s = 0.0;
+  for (uint32_t d = 0; d < n; d++) s += (double)x[d] * inv * w[d];
+  return s;
+}
+
 /* kernels.metal:891-1148 attn_verify (new_key :910-942, verify_batches :963-1006) and
  * :1316-1362 attn_dec_reduce, as exact math: per run, the new keys are normed, roped,
- * rounded to bf16 and written at p0 + row; each token's query (normed, roped, times
- * scale_log2) attends to the cached keys [0, p0) and the run's new keys in its vis mask,
- * with p = 2^s and out = sum p v / sum p (no running max: scores are bounded,
- * :804-806). XSA and the gate are off (xsa = 0, gate = 1). */
+ * rounded to bf16 and written at p0 + row (values first get their value embedding,
+ * add_ve :738-747); each token's query (normed, roped, times scale_log2) attends to the cached
+ * keys [key_lo(pos), p0) and the run's new keys in its vis mask, with p = 2^s and out =
+ * sum p v / sum p (no running max: scores are bounded, :804-806); then XSA, out - xsa[h]
+ * (out . v) v with v the token's value row of its kv head over max(|v|, 1e-4), and the gate
+ * 2 sigmoid(rms_norm(x)[:D] . attn_gate[h]) (:1355-1361). ex NULL, or a NULL member: that part
+ * off (xsa 0, gate 1). */
 void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
                      uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
                      const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
-                     float* out) {
+                     float* out, const sv_attn_extras* ex) {
   const uint32_t D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads, G = NQ / NKV;
   const uint32_t W = (NQ + 2 * NKV) * D, KOFF = NQ * D, VOFF = (NQ + NKV) * D;
   const uint32_t L = kv->kv_layer;
+  const float* ve_gate = ex ? ex->d_ve_gate : NULL;
+  const float* attn_gate = ex ? ex->d_attn_gate : NULL;
+  const float* xsa = ex ? ex->d_xsa : NULL;
   for (uint32_t r = 0; r < n_runs; r++) {
     const uint32_t t0 = runs[2 * r], T = runs[2 * r + 1];
     const uint32_t seq = meta[2 * t0], p0 = meta[2 * t0 + 1];
-    /* the new keys and values, bf16 */
+    /* the new keys and values, bf16, and the values' directions */
     uint16_t* nk = (uint16_t*)malloc(sizeof(uint16_t) * T * NKV * D);
     uint16_t* nv = (uint16_t*)malloc(sizeof(uint16_t) * T * NKV * D);
+    double* vdir = (double*)malloc(sizeof(double) * T * NKV * D);
     double* tmp = (double*)malloc(sizeof(double) * D);
     for (uint32_t i = 0; i < T; i++) {
       const uint32_t t = t0 + i, pos = meta[2 * t + 1];
       for (uint32_t g = 0; g < NKV; g++) {
         norm_rope_d(qkv + (size_t)t * W + KOFF + g * D, tmp, D, (int)args->rope, rope + (size_t)pos * 64);
         const size_t row = kv_row(kv, page_table, L, seq, g, p0 + i, NKV, D);
+        double ve_g = 0.0;
+        if (ve_gate)
+          ve_g = sigmoid2_d(gate_dot(ex->d_x + (size_t)t * ex->hidden, ex->d_inv[t], ve_gate + g * SV_VE_GATE_W,
+                                     SV_VE_GATE_W));
+        double vs = 0.0;
         for (uint32_t d = 0; d < D; d++) {
+          double v = qkv[(size_t)t * W + VOFF + g * D + d];
+          if (ve_gate) v += ve_g * orc_bf(ex->d_value_embed[((size_t)ex->d_tokens[t] * NKV + g) * D + d]);
+          vdir[((size_t)i * NKV + g) * D + d] = v;
+          vs += v * v;
           const uint16_t kb = orc_to_bf((float)tmp[d]);
-          const uint16_t vb = orc_to_bf(qkv[(size_t)t * W + VOFF + g * D + d]);
+          const uint16_t vb = orc_to_bf((float)v);
           nk[((size_t)i * NKV + g) * D + d] = kb;
           nv[((size_t)i * NKV + g) * D + d] = vb;
           k_cache[row + d] = kb;
           v_cache[row + d] = vb;
         }
+        const double den = fmax(sqrt(vs), 1e-4);
+        for (uint32_t d = 0; d < D; d++) vdir[((size_t)i * NKV + g) * D + d] /= den;
       }
     }
     free(tmp);
@@ -364,7 +398,7 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
           o[d] = 0.0;
         }
         double l = 0.0;
-        for (uint32_t j = 0; j < p0; j++) {
+        for (uint32_t j = key_lo(kv, pos); j < p0; j++) {
           const size_t row = kv_row(kv, page_table, L, seq, g, j, NKV, D);
           double s = 0.0;
           for (uint32_t d = 0; d < D; d++) s += orc_bf(k_cache[row + d]) * q[d];
@@ -380,11 +414,53 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
           l += p;
           for (uint32_t d = 0; d < D; d++) o[d] += p * orc_bf(nv[((size_t)j * NKV + g) * D + d]);
         }
-        for (uint32_t d = 0; d < D; d++) out[(size_t)t * NQ * D + h * D + d] = (float)(o[d] / l);
+        for (uint32_t d = 0; d < D; d++) o[d] /= l;
+        if (xsa) {
+          const double* vd = vdir + ((size_t)i * NKV + g) * D;
+          double dp = 0.0;
+          for (uint32_t d = 0; d < D; d++) dp += o[d] * vd[d];
+          for (uint32_t d = 0; d < D; d++) o[d] -= (double)xsa[h] * dp * vd[d];
+        }
+        const double gate =
+            attn_gate ? sigmoid2_d(gate_dot(ex->d_x + (size_t)t * ex->hidden, ex->d_inv[t], attn_gate + (size_t)h * D, D))
+                      : 1.0;
+        for (uint32_t d = 0; d < D; d++) out[(size_t)t * NQ * D + h * D + d] = (float)(o[d] * gate);
       }
     }
     free(nk);
     free(nv);
+    free(vdir);
+  }
+}
+
+/* kernels.metal:1364-1407 mudd(), exact math: inner = gelu(dense1 . rms_norm(cur)) with the
+ * erf form of gelu (C's erf: the reference's Abramowitz & Stegun 7.1.26 is within 1.5e-7 of it,
+ * kernels.metal:30-37), w = mix . inner + bias, then the two mixes of (tap0, tap1, cur). */
+void orc_mudd(const float* cur, const float* tap0, const float* tap1, const float* dense1, const float* mix,
+              float* out_attn, float* out_base, uint32_t n, uint32_t hidden) {
+#pragma omp parallel for schedule(static)
+  for (uint32_t t = 0; t < n; t++) {
+    const float* c = cur + (size_t)t * hidden;
+    double ss = 0.0;
+    for (uint32_t i = 0; i < hidden; i++) ss += (double)c[i] * c[i];
+    const double inv = 1.0 / sqrt(ss / hidden + (double)SV_RMS_EPS);
+    double inner[SV_MUDD_INNER], w[6];
+    for (uint32_t j = 0; j < SV_MUDD_INNER; j++) {
+      double s = 0.0;
+      for (uint32_t i = 0; i < hidden; i++) s += (double)c[i] * inv * dense1[(size_t)j * hidden + i];
+      inner[j] = 0.5 * s * (1.0 + erf(s * 0.70710678118654752440));
+    }
+    for (uint32_t k = 0; k < 6; k++) {
+      const float* row = mix + k * (SV_MUDD_INNER + 1);
+      double s = 0.0;
+      for (uint32_t j = 0; j < SV_MUDD_INNER; j++) s += inner[j] * row[j];
+      w[k] = s + row[SV_MUDD_INNER];
+    }
+    for (uint32_t i = 0; i < hidden; i++) {
+      const size_t o = (size_t)t * hidden + i;
+      out_attn[o] = (float)(w[0] * tap0[o] + w[1] * tap1[o] + w[2] * c[i]);
+      out_base[o] = (float)(w[3] * tap0[o] + w[4] * tap1[o] + w[5] * c[i]);
+    }
   }
 }
 
@@ -710,18 +786,19 @@ void orc_pool_release(orc_pool* p, uint32_t slot) {
 
 /* -------------------------------------------------------------- the plan */
 
-/* plan.rs:47-151 Engine::plan(), the buffer layout part. Runs of up to SV_MAX_RUN rows see
- * the rows before them in their run (vis bits 0..row); the reference's bits restart every 8
- * rows (plan.rs:81), which only differs past row 7. */
+/* plan.rs:47-151 Engine::plan(), the buffer layout part. Attention runs of up to arun rows
+ * (0: SV_MAX_RUN) see the rows before them in their run (vis bits 0..row % arun); the
+ * reference's bits restart every 8 rows (plan.rs:81), which only differs past row 7. */
 int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens, uint32_t* seq_len,
              const sv_sample_row* sampling_per_slot, uint32_t* tokens, uint32_t* tin, uint32_t* vis,
-             uint32_t* head_rows, sv_sample_row* samples, sv_run_in* run_in) {
+             uint32_t* head_rows, sv_sample_row* samples, sv_run_in* run_in, uint32_t arun) {
+  if (arun == 0 || arun > SV_MAX_RUN) arun = SV_MAX_RUN;
   uint32_t n = 0, n_head = 0;
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const uint32_t slot = in_runs[4 * ri], count = in_runs[4 * ri + 1], verify = in_runs[4 * ri + 2],
                    head = in_runs[4 * ri + 3];
-    /* a verify run holds at most SV_MAX_RUN rows (its tree); other runs (prompt chunks) any */
-    if (count == 0 || (verify && count > SV_MAX_RUN)) return -1;
+    /* a verify run holds at most arun rows (its tree); other runs (prompt chunks) any */
+    if (count == 0 || (verify && count > arun)) return -1;
     for (uint32_t j = 0; j < ri; j++)
       if (in_runs[4 * j] == slot) return -1;
     const uint32_t first_row = n;
@@ -729,7 +806,7 @@ int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens
       tokens[n] = in_tokens[n];
       tin[2 * n] = slot;
       tin[2 * n + 1] = row;
-      vis[n] = 0xffffffffu >> (31 - row % SV_MAX_RUN); /* causal within its attention run of 16 */
+      vis[n] = 0xffffffffu >> (31 - row % arun); /* causal within its attention run */
       n++;
     }
     const uint32_t first_head = n_head;
@@ -755,12 +832,16 @@ int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens
 
 /* ------------------------------------------------------------- the step */
 
-/* encode.rs:99-126 encode_forward, encode_layer :142-190 (no MUDD, no taps),
- * encode_verify_attention :193-231 and encode_tail :383-412. */
+/* encode.rs:99-126 encode_forward, encode_layer :142-190 (MUDD at its sites with the taps
+ * of resid_in / resid_out :107-122), encode_verify_attention :193-231 and encode_tail
+ * :383-412. Sliding-window layers (io->local) use the local cache and io->kv_local; each
+ * layer's KV index counts its own kind (model.rs:112-120). */
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,
              orc_step_io* io) {
   const uint32_t n = io->n, H = sh->hidden, D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads;
   const uint32_t W = (NQ + 2 * NKV) * D, F = sh->ffn;
+  const sv_model_extras* mx = io->extras;
+  const uint32_t n_mudd = mx ? mx->n_mudd : 0;
   float* h = (float*)malloc(sizeof(float) * n * H);
   float* qkv = (float*)malloc(sizeof(float) * n * W);
   float* attn = (float*)malloc(sizeof(float) * n * NQ * D);
@@ -768,11 +849,28 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
   float* act = (float*)malloc(sizeof(float) * n * F);
   float* inv = (float*)malloc(sizeof(float) * n);
   float* hfin = (float*)malloc(sizeof(float) * (io->n_head ? io->n_head : 1) * H);
-  if (!h || !qkv || !attn || !mixed || !act || !inv || !hfin) return -1;
+  float* h0 = (float*)malloc(sizeof(float) * n * H);
+  float* taps = (float*)malloc(sizeof(float) * SV_MUDD_SITES * n * H);
+  float* xattn = (float*)malloc(sizeof(float) * n * H);
+  float* rbase = (float*)malloc(sizeof(float) * n * H);
+  if (!h || !qkv || !attn || !mixed || !act || !inv || !hfin || !h0 || !taps || !xattn || !rbase) return -1;
 
   orc_embed(sh, embed, io->tokens, h, io->tin, io->meta, io->lens, io->feed, io->tree, io->vis, n);
+  memcpy(h0, h, sizeof(float) * n * H);
+  uint32_t n_global = 0, n_local = 0;
   for (uint32_t li = 0; li < sh->n_layers; li++) {
     const sv_layer* l = &layers[li];
+    const int local = io->local && io->local[li];
+    const uint32_t kv_index = local ? n_local++ : n_global++;
+    const float* x = h;
+    const float* resid = h;
+    for (uint32_t site = 0; site < n_mudd; site++)
+      if (mx->mudd_layer[site] == li) {
+        orc_mudd(h, h0, taps + (size_t)site * n * H, mx->mudd_dense1,
+                 mx->mudd_mix + (size_t)site * 6 * (SV_MUDD_INNER + 1), xattn, rbase, n, H);
+        x = xattn;
+        resid = rbase;
+      }
     sv_mat_args a;
     memset(&a, 0, sizeof a);
     a.n = n;
@@ -786,16 +884,18 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     a.flags = SV_FLAG_WRITE_INV;
     a.scale = l->qkv_scale;
     a.gshift = l->qkv.gshift;
-    orc_matmul(&l->qkv, h, NULL, qkv, NULL, inv, &a);
+    orc_matmul(&l->qkv, x, NULL, qkv, NULL, inv, &a);
     /* attention (encode.rs:166-170) */
     sv_attn_args aa;
     memset(&aa, 0, sizeof aa);
     aa.scale_log2 = attn_scale * LOG2E_F;
     aa.rope = l->rope;
-    sv_kv_args kv = io->kv;
-    kv.kv_layer = li;
-    orc_attn_verify(sh, qkv, io->meta, io->k_cache, io->v_cache, io->page_table, io->rope, &kv, &aa,
-                    io->attn_runs, io->n_attn ? io->n_attn : io->n_runs, io->vis, attn);
+    sv_kv_args kv = local ? io->kv_local : io->kv;
+    kv.kv_layer = kv_index;
+    sv_attn_extras ex = {x, inv, io->tokens, mx ? mx->value_embed : NULL, l->ve_gate, l->attn_gate, l->xsa, NULL, H, 0};
+    orc_attn_verify(sh, qkv, io->meta, local ? io->k_local : io->k_cache, local ? io->v_local : io->v_cache,
+                    local ? io->local_table : io->page_table, io->rope, &kv, &aa, io->attn_runs,
+                    io->n_attn ? io->n_attn : io->n_runs, io->vis, attn, &ex);
     /* o: Resid (encode.rs:172-175) */
     a.k = NQ * D;
     a.m = H;
@@ -805,7 +905,7 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     a.ra = l->resid_attn;
     a.rb = l->post_attn;
     a.gshift = l->o.gshift;
-    orc_matmul(&l->o, attn, NULL, mixed, h, NULL, &a);
+    orc_matmul(&l->o, attn, NULL, mixed, resid, NULL, &a);
     /* gate_up: SwiGlu (encode.rs:179-181) */
     a.k = H;
     a.m = 2 * F;
@@ -823,6 +923,8 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     a.rb = l->post_mlp;
     a.gshift = l->down.gshift;
     orc_matmul(&l->down, act, NULL, h, mixed, NULL, &a);
+    for (uint32_t site = 0; site < n_mudd; site++)
+      if (mx->mudd_tap[site] == li) memcpy(taps + (size_t)site * n * H, h, sizeof(float) * n * H);
   }
   if (io->hidden) memcpy(io->hidden, h, sizeof(float) * n * H);
   /* tail (encode.rs:383-412): final norm of the head rows, the tied head, the sampler,
@@ -843,9 +945,20 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
   }
   orc_accept(io->runs, io->tokens, io->out, io->lens, io->feed, io->gen, io->emitted, io->n_runs, io->tree,
              io->path, io->path_len, io->on_path);
-  if (io->compact)
-    orc_kv_compact(sh, io->runs, io->n_runs, io->path, io->path_len, io->lens, io->k_cache, io->v_cache,
+  if (io->compact) {
+    sv_shape part = *sh;
+    part.n_layers = n_global;
+    orc_kv_compact(&part, io->runs, io->n_runs, io->path, io->path_len, io->lens, io->k_cache, io->v_cache,
                    io->page_table, &io->kv);
+    part.n_layers = n_local;
+    if (n_local)
+      orc_kv_compact(&part, io->runs, io->n_runs, io->path, io->path_len, io->lens, io->k_local, io->v_local,
+                     io->local_table, &io->kv_local);
+  }
+  free(h0);
+  free(taps);
+  free(xattn);
+  free(rbase);
   free(h);
   free(qkv);
   free(attn);

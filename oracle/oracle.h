@@ -53,7 +53,9 @@ void orc_matmul(const sv_matrix* w, const float* x, const uint32_t* x_rows, floa
 void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
                      uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
                      const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
-                     float* out);
+                     float* out, const sv_attn_extras* ex);
+void orc_mudd(const float* cur, const float* tap0, const float* tap1, const float* dense1, const float* mix,
+              float* out_attn, float* out_base, uint32_t n, uint32_t hidden);
 void orc_sample(const float* logits, const sv_sample_row* rows, uint32_t* out, const uint32_t* meta,
                 uint32_t n_rows, uint32_t vocab);
 void orc_accept(const sv_run_in* runs, const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed,
@@ -84,7 +86,7 @@ void orc_pool_release(orc_pool* p, uint32_t slot);
  * Returns n_head, or -1 on a rejected plan. */
 int orc_plan(const uint32_t* in_runs, uint32_t n_runs, const uint32_t* in_tokens, uint32_t* seq_len,
              const sv_sample_row* sampling_per_slot, uint32_t* tokens, uint32_t* tin, uint32_t* vis,
-             uint32_t* head_rows, sv_sample_row* samples, sv_run_in* run_in);
+             uint32_t* head_rows, sv_sample_row* samples, sv_run_in* run_in, uint32_t arun);
 
 /* The whole verify step on host memory (encode.rs:99-126 encode_forward + encode_tail
  * 383-412). Weights in `layers` and `embed` are host pointers. */
@@ -113,6 +115,13 @@ typedef struct orc_step_io {
   uint32_t* emitted, *path, *path_len, *on_path;
   float* hidden;   /* [n][H] final residual, may be NULL */
   uint32_t n_attn; /* attention runs: each run's rows in runs of 16 (0: n_runs) */
+  /* the Limite extras: value-embedding table and MUDD (host pointers; NULL: none), the
+   * sliding-window layers ([n_layers], NULL: all global) and their cache */
+  const sv_model_extras* extras;
+  const uint8_t* local;
+  uint16_t* k_local, *v_local;
+  const uint32_t* local_table;
+  sv_kv_args kv_local;
 } orc_step_io;
 
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,

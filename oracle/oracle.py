@@ -109,13 +109,36 @@ def matmul(L, mat_w: np.ndarray, scales: np.ndarray | None, gshift: int, x: np.n
     return y
 
 
-def attn_verify(L, shape, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, vis) -> np.ndarray:
+def attn_extras(L, shape, extras: dict | None):
+    """sv_attn_extras over host arrays (x, inv, tokens, value_embed, ve_gate, attn_gate, xsa), or None."""
+    if not extras:
+        return None, []
+    keep = {k: np.ascontiguousarray(v) for k, v in extras.items() if v is not None}
+    g = lambda k: ptr(keep.get(k))  # noqa: E731
+    return L.AttnExtras(g("x"), g("inv"), g("tokens"), g("value_embed"), g("ve_gate"), g("attn_gate"), g("xsa"),
+                        None, shape.hidden, 0), keep
+
+
+def attn_verify(L, shape, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, vis,
+                extras: dict | None = None) -> np.ndarray:
     sh = shape.c()
     n = qkv.shape[0]
     out = np.zeros((n, shape.n_heads * shape.head_dim), np.float32)
+    ex, keep = attn_extras(L, shape, extras)
     lib().orc_attn_verify(C.byref(sh), ptr(qkv), ptr(meta), ptr(k_cache), ptr(v_cache), ptr(page_table), ptr(rope),
-                          C.byref(kv), C.byref(args), ptr(runs), u32(len(runs) // 2), ptr(vis), ptr(out))
+                          C.byref(kv), C.byref(args), ptr(runs), u32(len(runs) // 2), ptr(vis), ptr(out),
+                          C.byref(ex) if ex is not None else None)
     return out
+
+
+def mudd(cur, tap0, tap1, dense1, mix) -> tuple[np.ndarray, np.ndarray]:
+    """orc_mudd over [n][hidden] rows; mix is one site's [2][3][33]."""
+    c = [np.ascontiguousarray(a, np.float32) for a in (cur, tap0, tap1, dense1, mix)]
+    n, hidden = c[0].shape
+    oa = np.zeros((n, hidden), np.float32)
+    ob = np.zeros((n, hidden), np.float32)
+    lib().orc_mudd(*[ptr(a) for a in c], ptr(oa), ptr(ob), u32(n), u32(hidden))
+    return oa, ob
 
 
 def sample(L, logits: np.ndarray, rows, meta: np.ndarray | None = None) -> np.ndarray:
@@ -222,7 +245,8 @@ class StepIO(C.Structure):
                 ("lens", vp), ("feed", vp), ("tree", vp), ("gen", vp), ("k_cache", vp), ("v_cache", vp),
                 ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
                 ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp),
-                ("n_attn", u32)]
+                ("n_attn", u32), ("extras", vp), ("local", vp), ("k_local", vp), ("v_local", vp), ("local_table", vp),
+                ("kv_local", C.c_uint32 * 8)]
 
 
 def _chain(row: int) -> int:
@@ -238,8 +262,11 @@ class OracleEngine:
     """
 
     def __init__(self, L, shape, embed, weights, scalars, *, max_seqs=8, max_seq_len=8192, kv_tokens=None,
-                 page_shift=4, attn_scale=0.125, freq=None):
+                 page_shift=4, attn_scale=0.125, freq=None, extras=None, max_step_tokens=64):
+        """extras: host_extras() of a model with the Limite extras (sliding-window layers with
+        rings laid out as the engine's, for max_step_tokens rows per step)."""
         self.L, self.shape = L, shape
+        self.arun = min(16, 64 // (shape.n_heads // shape.n_kv_heads))
         self.page_shift = page_shift
         page = 1 << page_shift
         kv_tokens = kv_tokens if kv_tokens is not None else max_seqs * max_seq_len
@@ -247,8 +274,24 @@ class OracleEngine:
         self.max_pages = -(-max_seq_len // page)
         self.max_seqs, self.max_seq_len = max_seqs, max_seq_len
         s = shape
-        self.k = np.zeros((s.n_layers, self.n_pages, s.n_kv_heads, page, s.head_dim), np.uint16)
+        self.hx = extras
+        self.local = np.array(extras["local"] if extras else [0] * s.n_layers, np.uint8)
+        n_local = int(self.local.sum())
+        self.window = extras["window"] if extras else 0
+        self.ring_pages = -(-(self.window + max_step_tokens) // page) if n_local else 0
+        self.n_lpages = max_seqs * self.ring_pages
+        self.k = np.zeros((s.n_layers - n_local, self.n_pages, s.n_kv_heads, page, s.head_dim), np.uint16)
         self.v = np.zeros_like(self.k)
+        self.k_local = np.zeros((n_local, max(1, self.n_lpages), s.n_kv_heads, page, s.head_dim), np.uint16)
+        self.v_local = np.zeros_like(self.k_local)
+        self.local_table = np.array([[slot * self.ring_pages + p % max(1, self.ring_pages) for p in range(self.max_pages)]
+                                     for slot in range(max_seqs)], np.uint32)
+        self._mx = None
+        if extras:
+            n = len(extras["mudd_layer"])
+            self._mx = L.ModelExtras(ptr(extras["value_embed"]), ptr(extras["mudd_dense1"]), ptr(extras["mudd_mix"]), n,
+                                     (u32 * 2)(*(list(extras["mudd_layer"]) + [0] * (2 - n))),
+                                     (u32 * 2)(*(list(extras["mudd_tap"]) + [0] * (2 - n))), 0)
         self.pool = Pool(self.n_pages, max_seqs, self.max_pages, page_shift)
         self.lens = np.zeros(max_seqs, np.uint32)
         self.feed = np.zeros(max_seqs * 16, np.uint32)
@@ -277,7 +320,9 @@ class OracleEngine:
                 gshift = 0 if scl is None else (31 if scl.shape[1] == 1 else int(k // scl.shape[1]).bit_length() - 1)
                 mats.append(L.Matrix(w.ctypes.data, scl.ctypes.data if scl is not None else None, m, k,
                                      1 if w.dtype == np.int8 else 0, gshift))
-            layers[i] = L.Layer(*mats, *sc[:6], int(sc[6]), 0)
+            ex = [ptr(extras[k][i]) if extras and extras[k][i] is not None else None
+                  for k in ("attn_gate", "ve_gate", "xsa")]
+            layers[i] = L.Layer(*mats, *sc[:6], int(sc[6]), 0, *ex)
         self.layers = layers
 
     # sequences
@@ -332,11 +377,12 @@ class OracleEngine:
         seq_len = np.array(self.seq_len, np.uint32)
         samp = (L.SampleRow * self.max_seqs)(*self.sampling)
         n_head = lib().orc_plan(ptr(in_runs), u32(n_runs), ptr(in_tokens), ptr(seq_len), samp, ptr(tokens), ptr(tin),
-                                ptr(vis), ptr(head_rows), samples, run_in)
+                                ptr(vis), ptr(head_rows), samples, run_in, u32(self.arun))
         assert n_head >= 0, "plan rejected"
-        # attention runs of at most 16 rows: a prompt chunk's later rows see its earlier ones as
+        # attention runs of at most arun rows: a prompt chunk's later rows see its earlier ones as
         # cached keys (written by the earlier runs)
-        attn_runs = np.array([[ri.first + j, min(16, ri.count - j)] for ri in run_in for j in range(0, ri.count, 16)],
+        a = self.arun
+        attn_runs = np.array([[ri.first + j, min(a, ri.count - j)] for ri in run_in for j in range(0, ri.count, a)],
                              np.uint32).reshape(-1)
         branches = any(r[2] and len(r[1]) > 2 for r in runs)
         meta = np.zeros(2 * n, np.uint32)
@@ -363,6 +409,11 @@ class OracleEngine:
         io.meta, io.logits, io.out = ptr(meta), ptr(logits), ptr(out)
         io.emitted, io.path, io.path_len, io.on_path = ptr(emitted), ptr(path), ptr(path_len), ptr(on_path)
         io.hidden = ptr(hidden)
+        io.extras = C.cast(C.pointer(self._mx), vp) if self._mx is not None else None
+        io.local = ptr(self.local)
+        io.k_local, io.v_local, io.local_table = ptr(self.k_local), ptr(self.v_local), ptr(self.local_table)
+        io.kv_local[:] = [0, 0, self.ring_pages * page_of(self.page_shift), self.max_seqs, self.page_shift,
+                          max(1, self.n_lpages), self.max_pages, self.window]
         sh = self.shape.c()
         rc = lib().orc_step(C.byref(sh), ptr(self.embed), self.layers, f32(self.attn_scale), C.byref(io))
         assert rc == 0
@@ -373,6 +424,29 @@ class OracleEngine:
         extra = dict(tokens=tokens, meta=meta.reshape(n, 2), vis=vis, path=path.reshape(n_runs, 16),
                      path_len=path_len, on_path=on_path, hidden=hidden, head_rows=head_rows[:n_head])
         return out[:n_head].copy(), logits[:n_head].copy(), emitted, extra
+
+
+def page_of(shift: int) -> int:
+    return 1 << shift
+
+
+def host_extras(model) -> dict | None:
+    """The model's Limite extras as host arrays (OracleEngine's `extras`), or None."""
+    import torch
+
+    x = getattr(model, "extras", None)
+    if x is None:
+        return None
+
+    def f32(t):
+        return None if t is None else np.ascontiguousarray(t.detach().float().cpu().numpy())
+
+    return dict(local=list(x.local), window=x.window, attn_gate=[f32(t) for t in x.attn_gate],
+                ve_gate=[f32(t) for t in x.ve_gate], xsa=[f32(t) for t in x.xsa],
+                value_embed=None if x.value_embed is None else
+                np.ascontiguousarray(x.value_embed.detach().cpu().view(torch.int16).numpy().view(np.uint16)),
+                mudd_dense1=f32(x.mudd_dense1), mudd_mix=f32(x.mudd_mix), mudd_layer=tuple(x.mudd_layer),
+                mudd_tap=tuple(x.mudd_tap))
 
 
 def host_weights(model) -> tuple[np.ndarray, list, list]:

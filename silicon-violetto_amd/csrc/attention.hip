@@ -82,7 +82,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   const uint32_t visw = p.vis[t0 + min((uint32_t)tid, T - 1)];
   constexpr int R = attn_ring(NCT);
   KvBatchT<D> ring[NBW == 0 ? R : 1];
-  const uint32_t kbeg = s * p.split;
+  // A sliding-window layer's splits start at its first query's window (its position first).
+  uint32_t p0 = p.local ? p.meta[2 * t0 + 1] : 0u;
+  const uint32_t kbeg = (p.local ? key_base(p, p0) : 0u) + s * p.split;
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
   uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
@@ -97,7 +99,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   size_t tile_off = 0;
   const uint32_t ncols = T * p.G;
   bf16x8 qh[NCT][KST], ql[NCT][KST];
-  uint32_t p0;
   KvBatchT<D> bt[NBW > 0 ? NBW : 1];
   if constexpr (NBW == 0) {
     if ((uint32_t)lane < 2 * nbw_full)
@@ -198,6 +199,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     return;
   }
   if (s >= nsplit) return;
+  // Each lane column's first visible cached key, and the highest of any column of the run (its
+  // positions are at most p0 + T - 1): batches at or above it need no window mask.
+  uint32_t clo[NCT];
+#pragma unroll
+  for (int ct = 0; ct < NCT; ct++) {
+    const uint32_t c = 16 * ct + c16;
+    clo[ct] = p.local && c < ncols ? key_lo(p, p.meta[2 * (t0 + c / p.G) + 1]) : 0u;
+  }
+  const uint32_t lo_hi = key_lo(p, p0 + T - 1);
   // newest: a split of the new keys alone; takes_new: the last cached split also takes them
   // (attn_newest_own; the launch sets p.newest_own to match).
   const bool newest = attn_newest_own(NCT, NBW) && s == nsplit - 1, takes_new = !attn_newest_own(NCT, NBW) && s == nsplit - 1;
@@ -220,15 +230,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     if (wv == 0) {
       KvBatchT<D> nb0;
       load_batch_new_t<D>(nk, nv, p0, p0 + T, p0, nb0, lane);
-      compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, svis);
+      compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo, svis);
     }
   } else if constexpr (NBW > 0) {
 #pragma unroll
     for (int i = 0; i < NBW; i++) {
       const uint32_t b = wv + 4 * i, kb = kbeg + 32 * b;
       if (b < nb) {
-        if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
-        else compute_batch_t<D, NCT, false>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+        if (kb + 32 <= kend && kb >= lo_hi) compute_batch_t<D, NCT, false, true>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo);
+        else compute_batch_t<D, NCT, false>(p, bt[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo);
       }
     }
   } else {
@@ -245,8 +255,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
         __builtin_amdgcn_sched_barrier(0);  // the loads go out before this batch's work
         if (j < nbw) {
           const uint32_t kb = kbeg + 32 * (wv + 4 * j);
-          if (kb + 32 <= kend) compute_batch_t<D, NCT, false, true>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
-          else compute_batch_t<D, NCT, false>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage);
+          if (kb + 32 <= kend && kb >= lo_hi) compute_batch_t<D, NCT, false, true>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo);
+          else compute_batch_t<D, NCT, false>(p, ring[i], kb, kend, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo);
         }
       }
     }
@@ -259,7 +269,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
       if (wv == 0) {
         KvBatchT<D> nb0;
         load_batch_new_t<D>(nk, nv, p0, p0 + T, p0, nb0, lane);
-        compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, svis);
+        compute_batch_t<D, NCT, true>(p, nb0, p0, p0 + T, p0, ncols, t0, qh, ql, O, lsum, lane, stage, clo, svis);
       }
     }
   }
@@ -337,7 +347,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
 // part j adds splits j, j + P, ... (at most eight, all requested at once, before the context
 // length in meta says how many count), then the parts are added in part order through LDS.
 // P grows with the grid's splits (long contexts at one stream), so no thread waits for more
-// than one round of loads. XSA and the gate are off (xsa = 0, gate = 1).
+// than one round of loads. With the extras, XSA then the gate (kernels.metal:1355-1361): o -=
+// xsa[h] (o . v) v, o *= 2 sigmoid(rms_norm(x)[:D] . attn_gate[h]); a column's D / 4 threads
+// are consecutive lanes of part 0 (the launch keeps 256 / P >= D / 4) and add the dot products
+// by lane exchange.
 template <int D, bool INL>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t P) {
   __shared__ f32x4 so[256];
@@ -385,8 +398,27 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t 
     }
   }
   if (!live || attn_nsplit(p, p0) > p.max_splits) return;  // NaN written by the attention
-  const uint32_t i = col / p.G, h = g * p.G + col % p.G;
-  *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
+  const uint32_t i = col / p.G, h = g * p.G + col % p.G, t = t0 + i;
+  f32x4 res = o / l;
+  if (p.xsa) {
+    const f32x4 vd = *(const f32x4*)(p.vdir + ((size_t)t * p.NKV + g) * D + d);
+    float dp = ((res[0] * vd[0] + res[1] * vd[1]) + res[2] * vd[2]) + res[3] * vd[3];
+#pragma unroll
+    for (int m = 1; m < D / 4; m <<= 1) dp += __shfl_xor(dp, m, WAVE);
+    const float c = p.xsa[h] * dp;
+#pragma unroll
+    for (int e = 0; e < 4; e++) res[e] = __builtin_fmaf(-c, vd[e], res[e]);
+  }
+  if (p.attn_gate) {
+    const f32x4 xv = *(const f32x4*)(p.x + (size_t)t * p.H + d);
+    const f32x4 gv = *(const f32x4*)(p.attn_gate + (size_t)h * D + d);
+    const float iv = p.inv[t];
+    float gs = (((xv[0] * iv) * gv[0] + (xv[1] * iv) * gv[1]) + (xv[2] * iv) * gv[2]) + (xv[3] * iv) * gv[3];
+#pragma unroll
+    for (int m = 1; m < D / 4; m <<= 1) gs += __shfl_xor(gs, m, WAVE);
+    res *= 2.0f * sigmoid_f(gs);
+  }
+  *(f32x4*)(p.out + (size_t)t * p.NQ * D + h * D + d) = res;
 }
 
 // Prompt chunks (qkv_post, kernels.metal:749-801, for the chunk path of encode.rs:300-355):
@@ -461,14 +493,22 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts, const uint32_t* host_runs, bool may_fuse) {
+                      uint32_t parts, const uint32_t* host_runs, bool may_fuse, const sv_attn_extras* ex) {
   if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
     return fail(SV_ERR_ARG, "attn_verify: null pointer");
   if (n_runs == 0) return SV_OK;
   const uint32_t D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads;
   if (D != 64 && D != 128) return fail(SV_ERR_UNSUPPORTED, "attn_verify: head_dim %u (64 or 128 are built)", D);
   if (NKV == 0 || NQ % NKV) return fail(SV_ERR_ARG, "attn_verify: %u heads over %u kv heads", NQ, NKV);
-  if (!kv->is_global) return fail(SV_ERR_UNSUPPORTED, "attn_verify: local (ring) layers are not built");
+  if (!kv->is_global && kv->window == 0) return fail(SV_ERR_ARG, "attn_verify: a sliding-window layer with window 0");
+  if (ex) {
+    if ((ex->d_ve_gate && (!ex->d_value_embed || !ex->d_tokens)) || ((ex->d_ve_gate || ex->d_attn_gate) && (!ex->d_x || !ex->d_inv)) ||
+        (ex->d_xsa && !ex->d_vdir))
+      return fail(SV_ERR_ARG, "attn_verify: an extra without its inputs (ve_gate needs x, inv, tokens, value_embed; "
+                              "attn_gate x, inv; xsa vdir)");
+    if ((ex->d_ve_gate || ex->d_attn_gate) && ex->hidden < D)
+      return fail(SV_ERR_ARG, "attn_verify: hidden %u below head_dim %u", ex->hidden, D);
+  }
   if (kv->page_shift < 4 || kv->page_shift > 16)
     return fail(SV_ERR_UNSUPPORTED, "attn_verify: pages of 2^%u tokens (16..65536 are built)", kv->page_shift);
   if (args->split == 0 || args->split % 32 || args->split > 3968)
@@ -476,11 +516,13 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   if (max_run == 0 || max_run > SV_MAX_RUN) return fail(SV_ERR_ARG, "attn_verify: max_run %u", max_run);
   if (!rope && args->rope) return fail(SV_ERR_ARG, "attn_verify: rope table missing");
   const uint32_t maxcols = cols_pad(sh, max_run), nct = maxcols / 16;
-  if (nct > 4) return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (64 are built)", max_run * NQ / NKV);
+  if (nct > SV_MAX_COLS / 16)
+    return fail(SV_ERR_UNSUPPORTED, "attn_verify: %u columns per kv head (%u are built)", max_run * NQ / NKV, SV_MAX_COLS);
   // The merge runs as its own launch over (run, kv head, column) workgroups (measured
   // faster at 9-65 splits); with g_attn_fused_merge set the last split of each (run, kv head)
   // to arrive merges instead.
-  const bool fused_merge = may_fuse && g_attn_fused_merge;
+  const bool merge_extras = ex && (ex->d_xsa || ex->d_attn_gate);
+  const bool fused_merge = may_fuse && g_attn_fused_merge && !merge_extras;
   const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
   if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
   AttnParams p;
@@ -517,6 +559,17 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.maxcols = maxcols;
   p.n_inline = 0;
   p.newest_own = 1;
+  p.local = kv->is_global ? 0u : 1u;
+  p.window = kv->window;
+  p.x = ex ? ex->d_x : nullptr;
+  p.inv = ex ? ex->d_inv : nullptr;
+  p.tokens = ex ? ex->d_tokens : nullptr;
+  p.vemb = ex ? ex->d_value_embed : nullptr;
+  p.ve_gate = ex ? ex->d_ve_gate : nullptr;
+  p.attn_gate = ex ? ex->d_attn_gate : nullptr;
+  p.xsa = ex ? ex->d_xsa : nullptr;
+  p.vdir = ex && ex->d_xsa ? ex->d_vdir : nullptr;
+  p.H = ex ? ex->hidden : 0u;
   if (host_runs && n_runs <= SV_INLINE_RUNS) {
     p.n_inline = n_runs;
     for (uint32_t i = 0; i < 3 * n_runs; i++) p.inl[i] = host_runs[i];
@@ -525,7 +578,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   // All of a wave's batches in flight where the grid is about one workgroup per CU (latency,
   // not throughput, bounds it) and a wave has at most SV_ATTN_NBW batches. The new keys' split
   // follows attn_newest_own for the variant launched.
-  const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW;
+  const bool fits = D == 64 && nct <= 2 && args->split <= 128u * SV_ATTN_NBW && !p.local;
   const bool allin = fits && (g_attn_allin == 1 || (g_attn_allin < 0 && (size_t)args->max_splits * NKV * n_runs <= attn_cus()));
   p.newest_own = attn_newest_own((int)nct, allin ? SV_ATTN_NBW : 0) ? 1u : 0u;
   if (parts & 4) {
@@ -573,8 +626,10 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
   // parts: enough that a thread adds at most eight splits (a power of two, up to 64)
+  // (with XSA or the gate, a column's D / 4 threads stay in part 0: P <= 1024 / D)
+  const uint32_t P_max = merge_extras ? 1024u / D : 64u;
   uint32_t P = 1;
-  while (P < 64 && 8 * P < args->max_splits) P *= 2;
+  while (P < P_max && 8 * P < args->max_splits) P *= 2;
   const uint32_t G4 = 256 / P, mz = (maxcols * D / 4 + G4 - 1) / G4;
   const dim3 mg(n_runs, NKV, mz);
   if (D == 64) {
@@ -631,7 +686,7 @@ sv_status attn_launch_noalloc(hipStream_t stream, const sv_shape* sh, const floa
   const sv_status st = scratch_address(&ws);
   if (st != SV_OK) return st;
   return attn_launch(stream, sh, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, n_runs, max_run, vis,
-                     out, ws, ATTN_SCRATCH_BYTES, 3, nullptr, false);
+                     out, ws, ATTN_SCRATCH_BYTES, 3, nullptr, false, nullptr);
 }
 
 }  // namespace sv

@@ -34,12 +34,38 @@ struct AttnParams {
   // 1: a run's new keys have a split of their own (after its cached splits); 0: its last cached
   // split (or the only split, without cached keys) takes them too.
   uint32_t newest_own;
+  // Sliding-window layer (kernels.metal:808-811): a query at pos sees cached keys from
+  // pos - window on; 0: every cached key.
+  uint32_t local, window;
+  // The layer extras (null: off): value embeddings in the new V rows, the XSA directions they
+  // leave in vdir, and the merge's XSA and gate.
+  const float* x;
+  const float* inv;
+  const uint32_t* tokens;
+  const uint16_t* vemb;
+  const float* ve_gate;
+  const float* attn_gate;
+  const float* xsa;
+  float* vdir;
+  uint32_t H;
 };
 
-// Splits of a run with p0 cached keys.
+// The first cached key the query at pos sees (kernels.metal:808-811 key_lo).
+__device__ __forceinline__ uint32_t key_lo(const AttnParams& p, uint32_t pos) {
+  return p.local && pos > p.window ? pos - p.window : 0u;
+}
+// A run's cached keys start at its first query's key_lo rounded down to a batch (32 keys):
+// batches stay aligned to the tiles of 16 keys; keys below a column's key_lo are masked.
+__device__ __forceinline__ uint32_t key_base(const AttnParams& p, uint32_t p0) { return key_lo(p, p0) & ~31u; }
+
+// Splits of a run whose first position is p0.
 __device__ __forceinline__ uint32_t attn_nsplit(const AttnParams& p, uint32_t p0) {
-  const uint32_t c = (p0 + p.split - 1) / p.split;
+  const uint32_t c = (p0 - key_base(p, p0) + p.split - 1) / p.split;
   return p.newest_own ? c + 1 : (c ? c : 1u);
+}
+
+__device__ __forceinline__ float sigmoid_f(float x) {
+  return 1.0f / (1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504088896340736f));
 }
 
 // Run r's first token, rows and sequence slot: from the kernel arguments (INL: the launch
@@ -285,12 +311,14 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 // compute_batch's semantics with V through the wave's LDS stage (2 tiles x 16 x D bf16).
 // Keys at or past kend that a partial batch read from their page get V rows of zero, so
 // whatever the cache holds there cannot reach the sums (p is 0 for them).
+// clo: each lane column's first visible cached key (key_lo; 0 on global layers); a FULL batch
+// lies at or above every column's.
 template <int D, int NCT, bool NEW, bool FULL = false>
 __device__ __forceinline__ void compute_batch_t(const AttnParams& p, const KvBatchT<D>& b, uint32_t kb, uint32_t kend,
                                                 uint32_t p0, uint32_t ncols, uint32_t t0,
                                                 const bf16x8 (&qh)[NCT][D / 32], const bf16x8 (&ql)[NCT][D / 32],
                                                 f32x4 (&O)[D / 16][NCT], float (&lsum)[NCT], int lane, uint16_t* stage,
-                                                const uint32_t* vis_cached = nullptr) {
+                                                const uint32_t (&clo)[NCT], const uint32_t* vis_cached = nullptr) {
   constexpr int KST = D / 32, VE = D / 16, NV = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
   // V into the stage first (its LDS writes overlap the score products).
@@ -337,6 +365,7 @@ __device__ __forceinline__ void compute_batch_t(const AttnParams& p, const KvBat
         if (!FULL) {
           bool ok = col_ok && key < kend;
           if (NEW) ok = ok && ((vbits >> (key - p0)) & 1u);
+          else ok = ok && key >= clo[ct];
           e = ok ? e : 0.0f;
         }
         pv[4 * mt + i] = e;
@@ -488,6 +517,8 @@ __device__ __forceinline__ void build_queries(const AttnParams& p, uint32_t t0, 
 // The run's new keys (kernels.metal:910-942 new_key): norm, RoPE, bf16, to the cache at
 // p0 + row and to LDS (nk / nv: [T][D]). 16 threads per key (D / 16 dims each, rope pairs
 // within a thread); threads tid < nthreads of the caller take keys tid / 16, + nthreads / 16...
+// With the extras: the value embedding added to V first (add_ve, kernels.metal:738-747) and
+// V's direction V / max(|V|, 1e-4) to vdir for XSA (fp32, before rounding).
 template <int D, bool COH>
 __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t t0, uint32_t T,
                                          uint32_t p0, uint16_t* nk, uint16_t* nv, uint32_t tid, uint32_t nthreads) {
@@ -507,6 +538,34 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
           kv[e + j] = a[j];
           vv[e + j] = b[j];
         }
+      }
+      if (p.ve_gate) {
+        // 2 sigmoid(rms_norm(x)[:12] . ve_gate[g]) * value_embed[token][g D ..]
+        float s = 0.0f;
+        if (l16 < SV_VE_GATE_W / 4) {
+          const f32x4 xv = *(const f32x4*)(p.x + (size_t)t * p.H + 4 * l16);
+          const f32x4 gv = *(const f32x4*)(p.ve_gate + g * SV_VE_GATE_W + 4 * l16);
+          const float iv = p.inv[t];
+#pragma unroll
+          for (int j = 0; j < 4; j++) s = __builtin_fmaf(xv[j] * iv, gv[j], s);
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) s += __shfl_xor(s, o, WAVE);
+        const float gate = 2.0f * sigmoid_f(s);
+        const uint16_t* ve = p.vemb + ((size_t)p.tokens[t] * p.NKV + g) * D + DL * l16;
+#pragma unroll
+        for (int e = 0; e < DL; e++) vv[e] = __builtin_fmaf(gate, bf(ve[e]), vv[e]);
+      }
+      if (p.vdir) {
+        float vs = 0.0f;
+#pragma unroll
+        for (int e = 0; e < DL; e++) vs = __builtin_fmaf(vv[e], vv[e], vs);
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) vs += __shfl_xor(vs, o, WAVE);
+        const float den = __builtin_fmaxf(__builtin_sqrtf(vs), 1e-4f);
+        float* vd = p.vdir + ((size_t)t * p.NKV + g) * D + DL * l16;
+#pragma unroll
+        for (int e = 0; e < DL; e += 4) *(f32x4*)(vd + e) = f32x4{vv[e] / den, vv[e + 1] / den, vv[e + 2] / den, vv[e + 3] / den};
       }
       const size_t row = kv_off<D>(p, seq, g, p0 + i);
       float ss = 0.0f;

@@ -88,9 +88,16 @@ extern "C" sv_status sv_attn_verify(void* stream, const sv_shape* shape, const f
                                     uint16_t* d_k_cache, uint16_t* d_v_cache, const uint32_t* d_page_table,
                                     const float* d_rope, const sv_kv_args* kv, const sv_attn_args* args,
                                     const uint32_t* d_runs, uint32_t n_runs, uint32_t max_run, const uint32_t* d_vis,
-                                    float* d_out, void* d_workspace, size_t workspace_bytes) {
+                                    float* d_out, void* d_workspace, size_t workspace_bytes,
+                                    const sv_attn_extras* extras) {
   return attn_launch((hipStream_t)stream, shape, d_qkv, d_meta, d_k_cache, d_v_cache, d_page_table, d_rope, kv, args,
-                     d_runs, n_runs, max_run, d_vis, d_out, d_workspace, workspace_bytes);
+                     d_runs, n_runs, max_run, d_vis, d_out, d_workspace, workspace_bytes, 3, nullptr, true, extras);
+}
+
+extern "C" sv_status sv_mudd(void* stream, const float* d_cur, const float* d_tap0, const float* d_tap1,
+                             const float* d_dense1, const float* d_mix, float* d_out_attn, float* d_out_base, uint32_t n,
+                             uint32_t hidden) {
+  return mudd_launch((hipStream_t)stream, d_cur, d_tap0, d_tap1, d_dense1, d_mix, d_out_attn, d_out_base, n, hidden);
 }
 
 extern "C" size_t sv_attn_noalloc_max_bytes(void) { return attn_scratch_bytes(); }
@@ -190,6 +197,7 @@ uint32_t choose_split(const std::vector<uint32_t>& cached, uint32_t extra, uint3
 
 struct Plan {
   uint32_t n = 0, n_head = 0, n_runs = 0, branches = 0, max_run = 0, split = 0, max_splits = 0;
+  uint32_t split_local = 0, max_splits_local = 0;  // sliding-window layers' splits
   uint32_t n_attn = 0;  // attention runs: each run's rows in runs of at most SV_MAX_RUN
   bool chunk = false;   // some run has more rows (a prompt chunk): new K/V are written first
   std::vector<uint32_t> slots;   // per run
@@ -223,6 +231,24 @@ struct sv_engine {
   std::vector<void*> packed;     // engine-owned tiled copies [layer * 4 + matrix]
   void* head_tiled = nullptr;    // tiled copy of the tied embedding for the head matmul
   uint32_t n_pages = 0, max_pages = 0, qkv_w = 0;
+  // Rows per attention run: SV_MAX_COLS columns per kv head at most (16 rows up to 4 query
+  // heads per kv head).
+  uint32_t arun = SV_MAX_RUN;
+  // Layer kinds (model.rs:116): each layer's index among the global or among the local layers.
+  std::vector<uint8_t> is_local;
+  std::vector<uint32_t> kv_index;
+  uint32_t n_global = 0, n_local = 0, ring_pages = 0, n_lpages = 0;
+  uint16_t* k_local = nullptr;
+  uint16_t* v_local = nullptr;
+  uint32_t* local_table = nullptr;  // cyclic: [slot][p] = slot ring_pages + p % ring_pages
+  size_t local_elems = 0;
+  // Model extras (value embeddings, MUDD) and the buffers MUDD routes the residual through.
+  sv_model_extras extras{};
+  float* h0 = nullptr;              // the embedding's rows (MUDD's first tap)
+  float* tap[SV_MUDD_SITES] = {};   // outputs of the tap layers
+  float* xattn = nullptr;           // MUDD's attention input
+  float* rbase = nullptr;           // MUDD's residual base
+  float* vdir = nullptr;            // XSA directions [n][NKV][D]
 
   // device: KV and sequence state
   uint16_t* k_cache = nullptr;
@@ -300,27 +326,51 @@ struct sv_engine {
     if (graph) (void)hipGraphExecDestroy(graph);
     void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
                     head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
-                    attn, mixed, act, inv, logits, ws, mm_ws};
+                    attn, mixed, act, inv, logits, ws, mm_ws, k_local, v_local, local_table, h0, xattn, rbase, vdir};
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     for (void* b : packed)
       if (b) (void)hipFree(b);
     if (head_tiled) (void)hipFree(head_tiled);
+    if (tap[0]) (void)hipFree(tap[0]);
+    if (tap[1] && tap[1] != tap[0]) (void)hipFree(tap[1]);
     if (stream) (void)hipStreamDestroy(stream);
   }
 
   size_t kv_offset_layer() const { return (size_t)n_pages * sh.n_kv_heads * (1u << cfg.page_shift) * sh.head_dim; }
 
-  sv_kv_args kv_args(uint32_t layer) const {
+  // KvArgs of layer li (kv.rs:70-80 args): global layers page through the pool, local ones
+  // through their cyclic rings.
+  sv_kv_args kv_args(uint32_t li) const {
     sv_kv_args kv{};
-    kv.is_global = 1;
-    kv.kv_layer = layer;
+    const bool local = is_local[li] != 0;
+    kv.is_global = local ? 0u : 1u;
+    kv.kv_layer = kv_index[li];
+    kv.ring = local ? ring_pages << cfg.page_shift : 0u;
     kv.max_seqs = cfg.max_seqs;
     kv.page_shift = cfg.page_shift;
-    kv.n_pages = n_pages;
+    kv.n_pages = local ? n_lpages : n_pages;
     kv.max_pages = max_pages;
+    kv.window = local ? cfg.window : 0u;
     return kv;
   }
+  uint16_t* kc_of(uint32_t li) const { return is_local[li] ? k_local : k_cache; }
+  uint16_t* vc_of(uint32_t li) const { return is_local[li] ? v_local : v_cache; }
+  const uint32_t* table_of(uint32_t li) const { return is_local[li] ? local_table : page_table; }
+  // MUDD routing (encode.rs:107-122 resid_in / resid_out): the site of layer li, and the tap
+  // buffer layer li writes (or -1).
+  int mudd_site(uint32_t li) const {
+    for (uint32_t s = 0; s < extras.n_mudd; s++)
+      if (extras.mudd_layer[s] == li) return (int)s;
+    return -1;
+  }
+  float* out_of(uint32_t li) const {
+    for (uint32_t s = 0; s < extras.n_mudd; s++)
+      if (extras.mudd_tap[s] == li) return tap[s];
+    return h;
+  }
+  float* emb_out() const { return extras.n_mudd ? h0 : h; }
+  float* in_of(uint32_t li) const { return li == 0 ? emb_out() : out_of(li - 1); }
 
   // kv.rs:49-56 reserve(): pages until the slot holds `len` positions; the page table
   // entry goes to the device at once.
@@ -365,6 +415,9 @@ struct sv_engine {
     if (!embed) return fail(SV_ERR_STATE, "no embedding set");
     for (uint32_t l = 0; l < sh.n_layers; l++)
       if (!layer_set[l]) return fail(SV_ERR_STATE, "layer %u not set", l);
+    for (uint32_t l = 0; l < sh.n_layers; l++)
+      if (layers[l].ve_gate && !extras.value_embed)
+        return fail(SV_ERR_STATE, "layer %u has value embeddings but no table is set (sv_engine_set_extras)", l);
     return SV_OK;
   }
 
@@ -404,39 +457,53 @@ struct sv_engine {
     const Plan& P = plan;
     const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
     SV_TIMED(SV_KIND_EMBED,
-             embed_launch(stream, &sh, embed, tokens, tok_res, h, tin, meta, lens, feed, tree, vis, n));
+             embed_launch(stream, &sh, embed, tokens, tok_res, emb_out(), tin, meta, lens, feed, tree, vis, n));
     sv_attn_args aa{};
-    aa.split = P.split;
-    aa.max_splits = P.max_splits;
     aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
     for (uint32_t li = 0; li < sh.n_layers; li++) {
       const sv_layer& L = layers[li];
+      float* hin = in_of(li);
+      float* hout = out_of(li);
+      // MUDD (encode.rs:145-160): the attention input and residual base mixed from the taps.
+      const float* x = hin;
+      const float* resid = hin;
+      const int site = mudd_site(li);
+      if (site >= 0) {
+        SV_TIMED(SV_KIND_MUDD, mudd_launch(stream, hin, h0, tap[site], extras.mudd_dense1,
+                                           extras.mudd_mix + (size_t)site * 6 * (SV_MUDD_INNER + 1), xattn, rbase, n, H));
+        x = xattn;
+        resid = rbase;
+      }
       SV_TIMED(SV_KIND_QKV,
-               matmul(L.qkv, n, h, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
+               matmul(L.qkv, n, x, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
       aa.rope = L.rope;
+      const bool local = is_local[li] != 0;
+      aa.split = local ? P.split_local : P.split;
+      aa.max_splits = local ? P.max_splits_local : P.max_splits;
       const sv_kv_args kv = kv_args(li);
+      sv_attn_extras ex{x, inv, tok_res, extras.value_embed, L.ve_gate, L.attn_gate, L.xsa, vdir, H, 0};
+      const sv_attn_extras* exp_ = (L.ve_gate || L.attn_gate || L.xsa) ? &ex : nullptr;
+      uint16_t *kc = kc_of(li), *vc = vc_of(li);
+      const uint32_t* tab = table_of(li);
       if (P.chunk)
-        SV_TIMED(SV_KIND_KV_WRITE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                               attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 4,
-                                               P.inl.data()));
-      SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                         attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data()));
-      SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, k_cache, v_cache, page_table, rope, &kv, &aa,
-                                               attn_runs, P.n_attn, P.max_run, vis, attn, ws, ws_bytes, 2,
-                                               P.inl.data()));
-      SV_TIMED(SV_KIND_O,
-               matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn, h, nullptr));
+        SV_TIMED(SV_KIND_KV_WRITE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
+                                               P.max_run, vis, attn, ws, ws_bytes, 4, P.inl.data(), true, exp_));
+      SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
+                                         P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data(), true, exp_));
+      SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
+                                               P.max_run, vis, attn, ws, ws_bytes, 2, P.inl.data(), true, exp_));
+      SV_TIMED(SV_KIND_O, matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn,
+                                 resid, nullptr));
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
       SV_TIMED(SV_KIND_DOWN,
-               matmul(L.down, n, act, nullptr, h, SV_EPI_RESID, 0, 1.0f, L.resid_mlp, L.post_mlp, mixed, nullptr));
+               matmul(L.down, n, act, nullptr, hout, SV_EPI_RESID, 0, 1.0f, L.resid_mlp, L.post_mlp, mixed, nullptr));
     }
-    (void)H;
     (void)F;
     (void)NQD;
     if (P.n_head > 0) {
       // rmsnorm_rows + the tied head (encode.rs:390-393), the norm folded into the matmul.
-      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, h, head_rows, logits, SV_EPI_HEAD, SV_FLAG_NORM_IN, 1.0f, 0, 0,
-                                    nullptr, nullptr));
+      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, out_of(sh.n_layers - 1), head_rows, logits, SV_EPI_HEAD,
+                                    SV_FLAG_NORM_IN, 1.0f, 0, 0, nullptr, nullptr));
       SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
     }
     // accept + kv_compact + replay drafter (encode.rs:394-435, 439-451) as one launch.
@@ -444,10 +511,12 @@ struct sv_engine {
     sv_replay_args ra = replay;
     ra.stride = cfg.max_seq_len;
     ra.vocab = sh.vocab_real;
-    const sv_kv_args kv0 = kv_args(0);
+    const KvCacheRef caches[2] = {{k_cache, v_cache, page_table, n_global, n_pages},
+                                  {k_local, v_local, local_table, n_local, n_lpages ? n_lpages : 1u}};
     SV_TIMED(SV_KIND_ACCEPT, step_tail_launch(stream, &sh, runs, P.n_runs, tok_res, out_ids, lens, feed, gen, emitted,
-                                              tree, path, path_len, on_path, compact, k_cache, v_cache, page_table,
-                                              &kv0, (flags & SV_STEP_REPLAY) ? &ra : nullptr, trace, trace_len));
+                                              tree, path, path_len, on_path, compact, caches, n_local ? 2u : 1u,
+                                              cfg.page_shift, max_pages, (flags & SV_STEP_REPLAY) ? &ra : nullptr,
+                                              trace, trace_len));
     return SV_OK;
   }
 };
@@ -467,6 +536,12 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
       cfg->kv_tokens == 0)
     return fail(SV_ERR_ARG, "engine_create: zero capacity");
   if (cfg->options != 0) return fail(SV_ERR_ARG, "engine_create: options %u (none are defined)", cfg->options);
+  if (cfg->local) {
+    bool any = false;
+    for (uint32_t li = 0; li < s.n_layers; li++) any = any || cfg->local[li];
+    if (any && (cfg->window == 0 || cfg->window > cfg->max_seq_len))
+      return fail(SV_ERR_ARG, "engine_create: sliding-window layers need 0 < window <= max_seq_len (window %u)", cfg->window);
+  }
   if (cfg->page_shift < 4 || cfg->page_shift > 16) return fail(SV_ERR_ARG, "engine_create: page_shift %u", cfg->page_shift);
   if (cfg->split_keys % 32 || cfg->split_keys > 3968)
     return fail(SV_ERR_ARG, "engine_create: split_keys %u (a multiple of 32, at most 3968)", cfg->split_keys);
@@ -482,19 +557,39 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   e->n_pages = (cfg->kv_tokens + page - 1) / page;
   e->max_pages = (cfg->max_seq_len + page - 1) / page;
   e->qkv_w = (s.n_heads + 2 * s.n_kv_heads) * s.head_dim;
+  e->arun = std::min(SV_MAX_RUN, SV_MAX_COLS / (s.n_heads / s.n_kv_heads));
+  e->is_local.assign(s.n_layers, 0);
+  e->kv_index.assign(s.n_layers, 0);
+  for (uint32_t li = 0; li < s.n_layers; li++) {
+    e->is_local[li] = cfg->local && cfg->local[li] ? 1 : 0;
+    e->kv_index[li] = e->is_local[li] ? e->n_local++ : e->n_global++;
+  }
+  if (e->n_local) {
+    // A ring holds the window plus a whole step (kv.rs:26-28): a step's earlier queries still
+    // need the keys its later rows overwrite.
+    e->ring_pages = (cfg->window + cfg->max_step_tokens + page - 1) / page;
+    e->n_lpages = cfg->max_seqs * e->ring_pages;
+  }
   auto bad = [&](sv_status st) {
     delete e;
     return st;
   };
   if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess) return bad(fail(SV_ERR_HIP, "stream"));
   const uint32_t n = cfg->max_step_tokens, S = cfg->max_seqs, R = cfg->max_head_rows;
-  e->kv_elems = (size_t)s.n_layers * e->kv_offset_layer();
+  e->kv_elems = (size_t)e->n_global * e->kv_offset_layer();
+  e->local_elems = (size_t)e->n_local * e->n_lpages * s.n_kv_heads * page * s.head_dim;
   sv_status st = SV_OK;
 #define ALLOC(ptr, count)                                 \
   if ((st = dalloc(&e->ptr, (count), #ptr)) != SV_OK) return bad(st)
   ALLOC(k_cache, e->kv_elems);
   ALLOC(v_cache, e->kv_elems);
   ALLOC(page_table, (size_t)S * e->max_pages);
+  if (e->n_local) {
+    ALLOC(k_local, e->local_elems);
+    ALLOC(v_local, e->local_elems);
+    ALLOC(local_table, (size_t)S * e->max_pages);
+  }
+  ALLOC(vdir, (size_t)n * s.n_kv_heads * s.head_dim);
   ALLOC(rope, (size_t)(cfg->max_seq_len + SV_FEED_W) * SV_ROPE_PAIRS * 2);
   ALLOC(lens, S);
   ALLOC(feed, (size_t)S * SV_FEED_W);
@@ -507,7 +602,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   ALLOC(tin, 2 * (size_t)n);
   ALLOC(vis, n);
   ALLOC(head_rows, n);
-  ALLOC(attn_runs, 2 * ((size_t)n / SV_MAX_RUN + S));
+  ALLOC(attn_runs, 2 * ((size_t)n / e->arun + S));
   ALLOC(sample_rows, std::max(n, R));
   ALLOC(runs, S);
   ALLOC(out_ids, std::max(n, R));
@@ -562,6 +657,13 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
     }
     if (hipMemcpy(e->gen, g.data(), g.size() * sizeof(sv_gen_state), hipMemcpyHostToDevice) != hipSuccess)
       return bad(fail(SV_ERR_HIP, "gen"));
+  }
+  if (e->n_local) {
+    std::vector<uint32_t> lt((size_t)S * e->max_pages);
+    for (uint32_t slot = 0; slot < S; slot++)
+      for (uint32_t pg = 0; pg < e->max_pages; pg++) lt[(size_t)slot * e->max_pages + pg] = slot * e->ring_pages + pg % e->ring_pages;
+    if (hipMemcpy(e->local_table, lt.data(), lt.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+      return bad(fail(SV_ERR_HIP, "local page table"));
   }
   // kv.rs:40: free pages (0..n).rev(), popped 0, 1, 2, ...
   e->free_pages.resize(e->n_pages);
@@ -649,6 +751,40 @@ extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_
   return SV_OK;
 }
 
+extern "C" sv_status sv_engine_set_extras(sv_engine* e, const sv_model_extras* x) {
+  if (!e || !x) return fail(SV_ERR_ARG, "set_extras: null pointer");
+  if (e->graph) return fail(SV_ERR_STATE, "set_extras: after a graph was captured");
+  const sv_shape& s = e->sh;
+  if (x->n_mudd > SV_MUDD_SITES) return fail(SV_ERR_ARG, "set_extras: %u MUDD sites (at most %u)", x->n_mudd, SV_MUDD_SITES);
+  if (x->n_mudd && (!x->mudd_dense1 || !x->mudd_mix)) return fail(SV_ERR_ARG, "set_extras: MUDD without dense1 / mix");
+  for (uint32_t i = 0; i < x->n_mudd; i++) {
+    if (x->mudd_layer[i] >= s.n_layers || x->mudd_tap[i] >= x->mudd_layer[i])
+      return fail(SV_ERR_ARG, "set_extras: MUDD site %u at layer %u with tap %u (needs tap < layer < %u)", i,
+                  x->mudd_layer[i], x->mudd_tap[i], s.n_layers);
+    for (uint32_t j = 0; j < i; j++)
+      if (x->mudd_layer[j] == x->mudd_layer[i]) return fail(SV_ERR_ARG, "set_extras: two MUDD sites at layer %u", x->mudd_layer[i]);
+  }
+  SV_HIP(hipStreamSynchronize(e->stream), "set_extras");
+  const size_t rows = (size_t)e->cfg.max_step_tokens * s.hidden;
+  if (x->n_mudd) {
+    float** bufs[] = {&e->h0, &e->xattn, &e->rbase};
+    for (float** b : bufs)
+      if (!*b) SV_TRY(dalloc(b, rows, "mudd buffers"));
+    for (uint32_t i = 0; i < SV_MUDD_SITES; i++) {
+      // one buffer per distinct tap layer
+      if (i < x->n_mudd && i > 0 && x->mudd_tap[i] == x->mudd_tap[0]) {
+        if (e->tap[i] && e->tap[i] != e->tap[0]) SV_HIP(hipFree(e->tap[i]), "mudd buffers");
+        e->tap[i] = e->tap[0];
+      } else if (i < x->n_mudd && (!e->tap[i] || (i > 0 && e->tap[i] == e->tap[0]))) {
+        e->tap[i] = nullptr;
+        SV_TRY(dalloc(&e->tap[i], rows, "mudd buffers"));
+      }
+    }
+  }
+  e->extras = *x;
+  return SV_OK;
+}
+
 extern "C" sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* o) {
   if (!e || !o) return fail(SV_ERR_ARG, "get_buffers: null pointer");
   o->d_k_cache = e->k_cache;
@@ -669,6 +805,12 @@ extern "C" sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* o) {
   o->n_pages = e->n_pages;
   o->max_pages = e->max_pages;
   o->kv_bytes = e->kv_elems * 2;
+  o->d_k_local = e->k_local;
+  o->d_v_local = e->v_local;
+  o->d_local_table = e->local_table;
+  o->n_local_pages = e->n_lpages;
+  o->ring_pages = e->ring_pages;
+  o->local_bytes = e->local_elems * 2;
   return SV_OK;
 }
 
@@ -807,8 +949,8 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   for (uint32_t ri = 0; ri < n_runs; ri++) {
     const sv_run& r = runs_in[ri];
     SV_TRY(check_slot(e, r.slot));
-    if (r.count == 0 || (r.verify && r.count > SV_MAX_RUN))
-      return fail(SV_ERR_CAPACITY, "%u tokens for one sequence in a verify step (max %u)", r.count, SV_MAX_RUN);
+    if (r.count == 0 || (r.verify && r.count > e->arun))
+      return fail(SV_ERR_CAPACITY, "%u tokens for one sequence in a verify step (max %u)", r.count, e->arun);
     if (!r.tokens) return fail(SV_ERR_ARG, "plan: run %u has no tokens", ri);
     for (uint32_t j = 0; j < ri; j++)
       if (runs_in[j].slot == r.slot) return fail(SV_ERR_ARG, "a sequence appears twice in one step");
@@ -842,7 +984,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
       tokens.push_back(r.tokens[row]);
       tin.push_back(slot);
       tin.push_back(row);
-      vis.push_back(0xffffffffu >> (31 - row % SV_MAX_RUN));  // causal within its attention run (plan.rs:81)
+      vis.push_back(0xffffffffu >> (31 - row % e->arun));  // causal within its attention run (plan.rs:81)
     }
     const uint32_t first_head = (uint32_t)head_rows.size();
     if (r.verify)
@@ -857,18 +999,18 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     }
     run_in.push_back(sv_run_in{slot, first_row, count, first_head, (uint32_t)head_rows.size() - first_head,
                                r.verify ? 1u : 0u});
-    // Attention runs of at most SV_MAX_RUN rows: a prompt chunk's later ones see its earlier
-    // rows as cached keys (plan.rs:99-104 tiles the chunk path the same way, in 8s).
-    for (uint32_t j = 0; j < count; j += SV_MAX_RUN) {
-      const uint32_t c = std::min(SV_MAX_RUN, count - j);
+    // Attention runs of at most arun rows: a prompt chunk's later ones see its earlier rows as
+    // cached keys (plan.rs:99-104 tiles the chunk path the same way, in 8s).
+    for (uint32_t j = 0; j < count; j += e->arun) {
+      const uint32_t c = std::min(e->arun, count - j);
       attn_runs.push_back(first_row + j);
       attn_runs.push_back(c);
       P.inl.insert(P.inl.end(), {first_row + j, c, slot});
       max_cached = std::max(max_cached, e->seq_len[slot] + j);
       run_cached.push_back(e->seq_len[slot] + j);
     }
-    P.max_run = std::max(P.max_run, std::min(count, SV_MAX_RUN));
-    P.chunk = P.chunk || count > SV_MAX_RUN;
+    P.max_run = std::max(P.max_run, std::min(count, e->arun));
+    P.chunk = P.chunk || count > e->arun;
     P.branches |= (r.verify && count > 2) ? 1u : 0u;
     P.slots.push_back(slot);
     P.counts.push_back(count);
@@ -889,7 +1031,23 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
     split = choose_split(run_cached, extra_keys, e->sh.n_kv_heads, P.max_run, e->sh.n_heads / e->sh.n_kv_heads);
   P.split = split;
   P.max_splits = (max_cached + extra_keys + split - 1) / split + 1;
-  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, P.n_attn, P.max_splits, P.max_run)));
+  // Sliding-window layers: a run's cached keys start at its window (rounded down to 32 keys),
+  // so at most window + 31 of them at any replay.
+  P.split_local = split;
+  P.max_splits_local = P.max_splits;
+  if (e->n_local) {
+    const uint32_t span = e->cfg.window + 31;
+    std::vector<uint32_t> lc;
+    uint32_t max_lc = 0;
+    for (uint32_t c : run_cached) {
+      lc.push_back((uint32_t)std::min<uint64_t>((uint64_t)c + extra_keys, span));
+      max_lc = std::max(max_lc, lc.back());
+    }
+    P.split_local = e->cfg.split_keys ? e->cfg.split_keys
+                                      : choose_split(lc, 0, e->sh.n_kv_heads, P.max_run, e->sh.n_heads / e->sh.n_kv_heads);
+    P.max_splits_local = (max_lc + P.split_local - 1) / P.split_local + 1;
+  }
+  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, P.n_attn, std::max(P.max_splits, P.max_splits_local), P.max_run)));
   SV_TRY(e->upload(e->tokens, tokens.data(), tokens.size() * 4));
   SV_TRY(e->upload(e->tin, tin.data(), tin.size() * 4));
   SV_TRY(e->upload(e->vis, vis.data(), vis.size() * 4));

@@ -65,7 +65,8 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
                       uint32_t parts = 3,  // bit 0: attention, bit 1: the split merge, bit 2: runs' new K/V first
                       const uint32_t* host_runs = nullptr,  // (first token, rows, slot) per run, if known
-                      bool may_fuse = true);  // the counted last-split merge may be used (tests select it)
+                      bool may_fuse = true,  // the counted last-split merge may be used (tests select it)
+                      const sv_attn_extras* ex = nullptr);  // the layer's extras (null: none)
 // attn_launch with the split partials in the library's per-device static scratch array.
 sv_status attn_launch_noalloc(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
                               uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
@@ -95,12 +96,23 @@ sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nrun
                         uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
                         uint32_t* tree);
 
-// accept, then (optionally) kv_compact and the replay drafter, one workgroup per run.
+sv_status mudd_launch(hipStream_t stream, const float* cur, const float* tap0, const float* tap1, const float* dense1,
+                      const float* mix, float* out_attn, float* out_base, uint32_t n, uint32_t hidden);
+
+// A paged K/V cache kv_compact moves rows in: n_layers layers of n_pages pages through `table`.
+struct KvCacheRef {
+  uint16_t* kc;
+  uint16_t* vc;
+  const uint32_t* table;
+  uint32_t n_layers, n_pages;
+};
+// accept, then (optionally) kv_compact over caches[0..n_caches) and the replay drafter, one
+// workgroup per run.
 sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
                            const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed, sv_gen_state* gen,
                            uint32_t* emitted, uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path,
-                           bool compact, uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table,
-                           const sv_kv_args* kv, const sv_replay_args* ra, const uint32_t* trace,
+                           bool compact, const KvCacheRef* caches, uint32_t n_caches, uint32_t page_shift,
+                           uint32_t max_pages, const sv_replay_args* ra, const uint32_t* trace,
                            const uint32_t* trace_len);
 
 

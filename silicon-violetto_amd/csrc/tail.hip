@@ -327,11 +327,9 @@ struct TailParams {
   uint32_t* path;
   uint32_t* path_len;
   uint32_t* on_path;
-  uint16_t* kc;
-  uint16_t* vc;
-  const uint32_t* page_table;
+  KvCacheRef cache[2];  // global (paged) layers, then sliding-window layers (cyclic table)
   uint32_t nruns, compact, replay;
-  uint32_t n_layers, NKV, D, page_shift, n_pages, max_pages;
+  uint32_t NKV, D, page_shift, max_pages;
   sv_replay_args ra;
 };
 
@@ -394,19 +392,22 @@ __global__ __launch_bounds__(256) void step_tail_kernel(TailParams p) {
   if (p.compact && k > 1) {
     const uint32_t chunks = p.D / 4, per_layer = p.NKV * chunks, p0 = len - k;
     const uint32_t pmask = (1u << p.page_shift) - 1u;
-    for (uint32_t e = tid; e < p.n_layers * per_layer; e += 256) {
-      const uint32_t l = e / per_layer, g = (e % per_layer) / chunks, d0 = (e % chunks) * 4;
+    const uint32_t n0 = p.cache[0].n_layers;
+    for (uint32_t e = tid; e < (n0 + p.cache[1].n_layers) * per_layer; e += 256) {
+      const uint32_t lx = e / per_layer, g = (e % per_layer) / chunks, d0 = (e % chunks) * 4;
+      const KvCacheRef& c = lx < n0 ? p.cache[0] : p.cache[1];
+      const uint32_t l = lx < n0 ? lx : lx - n0;
       for (uint32_t j = 1; j < k; j++) {
         const uint32_t from = s_path[j];
         if (from == j) continue;
-        const uint32_t ps = min(p.page_table[(size_t)slot * p.max_pages + ((p0 + from) >> p.page_shift)], p.n_pages - 1);
-        const uint32_t pd = min(p.page_table[(size_t)slot * p.max_pages + ((p0 + j) >> p.page_shift)], p.n_pages - 1);
-        const size_t src = ((((size_t)l * p.n_pages + ps) * p.NKV + g) << p.page_shift) * p.D +
+        const uint32_t ps = min(c.table[(size_t)slot * p.max_pages + ((p0 + from) >> p.page_shift)], c.n_pages - 1);
+        const uint32_t pd = min(c.table[(size_t)slot * p.max_pages + ((p0 + j) >> p.page_shift)], c.n_pages - 1);
+        const size_t src = ((((size_t)l * c.n_pages + ps) * p.NKV + g) << p.page_shift) * p.D +
                            (size_t)((p0 + from) & pmask) * p.D + d0;
-        const size_t dst = ((((size_t)l * p.n_pages + pd) * p.NKV + g) << p.page_shift) * p.D +
+        const size_t dst = ((((size_t)l * c.n_pages + pd) * p.NKV + g) << p.page_shift) * p.D +
                            (size_t)((p0 + j) & pmask) * p.D + d0;
-        *(u32x2*)(p.kc + dst) = *(const u32x2*)(p.kc + src);
-        *(u32x2*)(p.vc + dst) = *(const u32x2*)(p.vc + src);
+        *(u32x2*)(c.kc + dst) = *(const u32x2*)(c.kc + src);
+        *(u32x2*)(c.vc + dst) = *(const u32x2*)(c.vc + src);
       }
     }
   }
@@ -614,10 +615,11 @@ namespace sv {
 sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_in* runs, uint32_t nruns,
                            const uint32_t* tokens, uint32_t* out, uint32_t* lens, uint32_t* feed, sv_gen_state* gen,
                            uint32_t* emitted, uint32_t* tree, uint32_t* path, uint32_t* path_len, uint32_t* on_path,
-                           bool compact, uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table,
-                           const sv_kv_args* kv, const sv_replay_args* ra, const uint32_t* trace,
+                           bool compact, const KvCacheRef* caches, uint32_t n_caches, uint32_t page_shift,
+                           uint32_t max_pages, const sv_replay_args* ra, const uint32_t* trace,
                            const uint32_t* trace_len) {
   if (nruns == 0) return SV_OK;
+  if (n_caches == 0 || n_caches > 2) return fail(SV_ERR_ARG, "step tail: %u caches", n_caches);
   TailParams p;
   p.runs = runs;
   p.tokens = tokens;
@@ -632,18 +634,15 @@ sv_status step_tail_launch(hipStream_t stream, const sv_shape* sh, const sv_run_
   p.path = path;
   p.path_len = path_len;
   p.on_path = on_path;
-  p.kc = k_cache;
-  p.vc = v_cache;
-  p.page_table = page_table;
+  p.cache[0] = caches[0];
+  p.cache[1] = n_caches > 1 ? caches[1] : KvCacheRef{nullptr, nullptr, nullptr, 0u, 1u};
   p.nruns = nruns;
   p.compact = compact ? 1u : 0u;
   p.replay = ra ? 1u : 0u;
-  p.n_layers = sh->n_layers;
   p.NKV = sh->n_kv_heads;
   p.D = sh->head_dim;
-  p.page_shift = kv->page_shift;
-  p.n_pages = kv->n_pages;
-  p.max_pages = kv->max_pages;
+  p.page_shift = page_shift;
+  p.max_pages = max_pages;
   if (ra) {
     if (ra->vocab == 0) return fail(SV_ERR_ARG, "step tail: replay vocab 0");
     p.ra = *ra;

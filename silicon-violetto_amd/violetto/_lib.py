@@ -25,13 +25,18 @@ MAX_RUN = 16
 SAMPLE_THREADS = 1024
 RMS_EPS = 1.1920928955078125e-07
 ROPE_PAIRS = 32
+VE_GATE_W = 12
+MUDD_INNER = 32
+MUDD_SITES = 2
+MAX_COLS = 64
 
 EPI_NORM, EPI_RESID, EPI_SWIGLU, EPI_HEAD, EPI_RAW = 1, 2, 3, 4, 5
 FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
 FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
-KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "kv_write")
+KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "kv_write",
+         "mudd")
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 
@@ -81,19 +86,32 @@ class ReplayArgs(C.Structure):
 class EngineConfig(C.Structure):
     _fields_ = [("shape", Shape), ("max_seqs", u32), ("max_step_tokens", u32), ("max_seq_len", u32),
                 ("max_head_rows", u32), ("kv_tokens", u32), ("page_shift", u32), ("attn_scale", f32),
-                ("split_keys", u32), ("options", u32)]
+                ("split_keys", u32), ("options", u32), ("window", u32), ("pad", u32), ("local", vp)]
 
 
 class Layer(C.Structure):
     _fields_ = [("qkv", Matrix), ("o", Matrix), ("gate_up", Matrix), ("down", Matrix), ("qkv_scale", f32),
                 ("o_scale", f32), ("resid_attn", f32), ("post_attn", f32), ("resid_mlp", f32), ("post_mlp", f32),
-                ("rope", u32), ("pad", u32)]
+                ("rope", u32), ("pad", u32), ("attn_gate", vp), ("ve_gate", vp), ("xsa", vp)]
+
+
+class ModelExtras(C.Structure):
+    _fields_ = [("value_embed", vp), ("mudd_dense1", vp), ("mudd_mix", vp), ("n_mudd", u32),
+                ("mudd_layer", u32 * MUDD_SITES), ("mudd_tap", u32 * MUDD_SITES), ("pad", u32)]
+
+
+class AttnExtras(C.Structure):
+    _fields_ = [(n, vp) for n in ("d_x", "d_inv", "d_tokens", "d_value_embed", "d_ve_gate", "d_attn_gate", "d_xsa",
+                                  "d_vdir")] + [("hidden", u32), ("pad", u32)]
 
 
 class EngineBuffers(C.Structure):
     _fields_ = [(n, vp) for n in ("d_k_cache", "d_v_cache", "d_page_table", "d_lens", "d_feed", "d_tree", "d_gen",
                                   "d_trace", "d_trace_len", "d_logits", "d_rope", "d_out_ids", "d_emitted", "d_path",
-                                  "d_path_len")] + [("n_pages", u32), ("max_pages", u32), ("kv_bytes", C.c_size_t)]
+                                  "d_path_len")] + [("n_pages", u32), ("max_pages", u32), ("kv_bytes", C.c_size_t),
+                                                    ("d_k_local", vp), ("d_v_local", vp), ("d_local_table", vp),
+                                                    ("n_local_pages", u32), ("ring_pages", u32),
+                                                    ("local_bytes", C.c_size_t)]
 
 
 class Run(C.Structure):
@@ -120,7 +138,8 @@ PROTOS = {
     "sv_pack_matrix": (C.c_int, [vp, P(Matrix), vp, P(Matrix)]),
     "sv_attn_workspace_bytes": (C.c_size_t, [P(Shape), u32, u32, u32]),
     "sv_attn_verify": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, P(KvArgs), P(AttnArgs), vp, u32, u32, vp, vp,
-                                 vp, C.c_size_t]),
+                                 vp, C.c_size_t, P(AttnExtras)]),
+    "sv_mudd": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, u32, u32]),
     "sv_attn_noalloc_max_bytes": (C.c_size_t, []),
     "sv_attn_verify_noalloc": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, P(KvArgs), P(AttnArgs), vp, u32, u32,
                                          vp, vp]),
@@ -143,6 +162,7 @@ PROTOS = {
     "sv_engine_destroy": (None, [vp]),
     "sv_engine_set_embed": (C.c_int, [vp, vp]),
     "sv_engine_set_layer": (C.c_int, [vp, u32, P(Layer)]),
+    "sv_engine_set_extras": (C.c_int, [vp, P(ModelExtras)]),
     "sv_engine_stream": (vp, [vp]),
     "sv_engine_get_buffers": (C.c_int, [vp, P(EngineBuffers)]),
     "sv_new_seq": (C.c_int, [vp, P(u32)]),

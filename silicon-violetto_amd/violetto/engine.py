@@ -37,12 +37,16 @@ class StepResult:
 class Engine:
     def __init__(self, shape: ModelShape, *, max_seqs: int = 8, max_step_tokens: int = 64, max_seq_len: int = 8192,
                  max_head_rows: int = 16, kv_tokens: int | None = None, page_shift: int = 4, attn_scale: float = 0.125,
-                 split_keys: int = 0, freq: np.ndarray | None = None):
+                 split_keys: int = 0, freq: np.ndarray | None = None, local: list[int] | None = None,
+                 window: int = 0):
+        """local: per layer 1 for a sliding-window layer of `window` keys (model.rs:16-17,116)."""
         self.shape = shape
         self.lib = L.lib()
+        self._local = None if local is None else (C.c_uint8 * shape.n_layers)(*[int(x) for x in local])
         cfg = L.EngineConfig(shape.c(), max_seqs, max_step_tokens, max_seq_len, max_head_rows,
                              kv_tokens if kv_tokens is not None else max_seqs * max_seq_len, page_shift, attn_scale,
-                             split_keys, 0)
+                             split_keys, 0, window, 0,
+                             C.cast(self._local, C.c_void_p) if self._local is not None else None)
         self.cfg = cfg
         f = np.ascontiguousarray(freq if freq is not None else rope_freq(500000.0, shape.head_dim), dtype=np.float32)
         self.freq = f
@@ -75,12 +79,29 @@ class Engine:
         for i in range(model.shape.n_layers):
             lay = model.c_layer(i)
             L.check(self.lib.sv_engine_set_layer(self.h, i, C.byref(lay)))
+        if getattr(model, "extras", None) is not None:
+            ex = model.extras.c()
+            L.check(self.lib.sv_engine_set_extras(self.h, C.byref(ex)))
 
     # -- views of engine-owned device memory
+    @property
+    def n_local(self) -> int:
+        return 0 if self._local is None else sum(self._local)
+
     def kv_cache(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The global (paged) layers' K and V: [n_global][n_pages][NKV][page][D]."""
         s = self.shape
-        shape = (s.n_layers, self.buf.n_pages, s.n_kv_heads, 1 << self.cfg.page_shift, s.head_dim)
+        shape = (s.n_layers - self.n_local, self.buf.n_pages, s.n_kv_heads, 1 << self.cfg.page_shift, s.head_dim)
         return (device_view(self.buf.d_k_cache, shape, torch.bfloat16), device_view(self.buf.d_v_cache, shape, torch.bfloat16))
+
+    def local_cache(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """The sliding-window layers' K, V [n_local][max_seqs * ring_pages][NKV][page][D] and
+        their cyclic page table [max_seqs][max_pages]."""
+        s = self.shape
+        shape = (self.n_local, self.buf.n_local_pages, s.n_kv_heads, 1 << self.cfg.page_shift, s.head_dim)
+        tab = device_view(self.buf.d_local_table, (self.cfg.max_seqs, self.buf.max_pages), torch.int32)
+        return (device_view(self.buf.d_k_local, shape, torch.bfloat16), device_view(self.buf.d_v_local, shape, torch.bfloat16),
+                tab)
 
     def view(self, name: str, shape: tuple, dtype=torch.int32) -> torch.Tensor:
         return device_view(getattr(self.buf, name), shape, dtype)

@@ -89,13 +89,28 @@ def matmul(mat: Mat, x: torch.Tensor, y: torch.Tensor, *, n: int, epi: int, flag
 def attn_verify(shape: ModelShape, qkv: torch.Tensor, meta: torch.Tensor, k_cache: torch.Tensor,
                 v_cache: torch.Tensor, page_table: torch.Tensor, rope: torch.Tensor, kv: L.KvArgs, args: L.AttnArgs,
                 runs: torch.Tensor, n_runs: int, max_run: int, vis: torch.Tensor, out: torch.Tensor,
-                ws: Workspace | None = None, stream: int | None = None) -> None:
+                ws: Workspace | None = None, stream: int | None = None, extras: dict | None = None) -> None:
+    """extras: the layer's extras (sv_attn_extras) as tensors: x, inv, tokens, value_embed, ve_gate,
+    attn_gate, xsa, vdir (absent: off)."""
     sh = shape.c()
     need = L.lib().sv_attn_workspace_bytes(C.byref(sh), n_runs, args.max_splits, max_run)
     ws = ws.grow(need) if ws is not None else Workspace(need)
+    ex = None
+    if extras:
+        g = lambda k: _p(extras.get(k))  # noqa: E731
+        ex = L.AttnExtras(g("x"), g("inv"), g("tokens"), g("value_embed"), g("ve_gate"), g("attn_gate"), g("xsa"),
+                          g("vdir"), shape.hidden, 0)
     L.check(L.lib().sv_attn_verify(_stream(stream), C.byref(sh), _p(qkv), _p(meta), _p(k_cache), _p(v_cache),
                                    _p(page_table), _p(rope), C.byref(kv), C.byref(args), _p(runs), n_runs, max_run,
-                                   _p(vis), _p(out), _p(ws.t), ws.nbytes))
+                                   _p(vis), _p(out), _p(ws.t), ws.nbytes, C.byref(ex) if ex is not None else None))
+
+
+def mudd(cur: torch.Tensor, tap0: torch.Tensor, tap1: torch.Tensor, dense1: torch.Tensor, mix: torch.Tensor,
+         out_attn: torch.Tensor, out_base: torch.Tensor, stream: int | None = None) -> None:
+    """sv_mudd: the MUDD mixes of [n][hidden] rows (mix: one site's [2][3][33])."""
+    n, hidden = cur.shape
+    L.check(L.lib().sv_mudd(_stream(stream), _p(cur), _p(tap0), _p(tap1), _p(dense1), _p(mix), _p(out_attn),
+                            _p(out_base), n, hidden))
 
 
 def attn_verify_noalloc(shape: ModelShape, qkv: torch.Tensor, meta: torch.Tensor, k_cache: torch.Tensor,

@@ -95,6 +95,76 @@ class LayerScalars:
 
 
 @dataclass
+class Extras:
+    """The Limite model's extras (engine/src/model.rs:49-99, kernels.metal:738-747,1316-1407):
+    sliding-window layers, attention gates, value embeddings, XSA and the MUDD mixes. Per-layer
+    lists hold None where a layer lacks the part."""
+    local: list[int]                           # 1: sliding-window layer
+    window: int
+    attn_gate: list                            # f32 [n_heads][head_dim] or None
+    ve_gate: list                              # f32 [n_kv_heads][12] or None
+    xsa: list                                  # f32 [n_heads] or None
+    value_embed: torch.Tensor | None = None    # bf16 [vocab][n_kv_heads * head_dim]
+    mudd_dense1: torch.Tensor | None = None    # f32 [32][hidden]
+    mudd_mix: torch.Tensor | None = None       # f32 [sites][2][3][33]
+    mudd_layer: tuple = ()
+    mudd_tap: tuple = ()
+
+    def to(self, dev) -> "Extras":
+        mv = lambda t: None if t is None else t.to(dev)  # noqa: E731
+        return Extras(list(self.local), self.window, [mv(t) for t in self.attn_gate], [mv(t) for t in self.ve_gate],
+                      [mv(t) for t in self.xsa], mv(self.value_embed), mv(self.mudd_dense1), mv(self.mudd_mix),
+                      tuple(self.mudd_layer), tuple(self.mudd_tap))
+
+    def c(self) -> L.ModelExtras:
+        n = len(self.mudd_layer)
+        ml = (L.u32 * L.MUDD_SITES)(*(list(self.mudd_layer) + [0] * (L.MUDD_SITES - n)))
+        mt = (L.u32 * L.MUDD_SITES)(*(list(self.mudd_tap) + [0] * (L.MUDD_SITES - n)))
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+        return L.ModelExtras(ptr(self.value_embed), ptr(self.mudd_dense1), ptr(self.mudd_mix), n, ml, mt, 0)
+
+
+def limite_layout(n_layers: int) -> tuple[list[int], list[int], tuple, tuple]:
+    """(local, has value embeddings, MUDD sites, their taps) of the reference's layer pattern
+    (model.rs:21,116-127; encode.rs:107-122): global every fourth layer (i % 4 == 3), value
+    embeddings on i % 3 == 1, MUDD before layers 24 and 47 with taps after 11 and 22; for
+    other depths the sites sit at the middle and the last layer, the taps a quarter and half way."""
+    local = [0 if i % 4 == 3 else 1 for i in range(n_layers)]
+    ve = [1 if i % 3 == 1 else 0 for i in range(n_layers)]
+    if n_layers == 48:
+        return local, ve, (24, 47), (11, 22)
+    if n_layers < 4:
+        return local, ve, (), ()
+    return local, ve, (n_layers // 2, n_layers - 1), (n_layers // 4, n_layers // 2 - 1)
+
+
+def generate_extras(shape: ModelShape, *, seed: int = 1, device="cpu", window: int = 1024,
+                    mudd: bool = True) -> Extras:
+    """Random extras of the reference's layout (limite_layout): gates N(0, 0.05) (gates near 1),
+    value embeddings N(0, 1) bf16, xsa U[0, 1), MUDD dense1 N(0, 0.05) and mixes around
+    (attention input, residual base) = (0.1 tap0 + 0.1 tap1 + cur)."""
+    dev = torch.device(device)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    rn = lambda *sz: torch.randn(*sz, generator=g, device=dev, dtype=torch.float32)  # noqa: E731
+    local, ve, sites, taps = limite_layout(shape.n_layers)
+    if not mudd:
+        sites, taps = (), ()
+    NQ, NKV, D = shape.n_heads, shape.n_kv_heads, shape.head_dim
+    attn_gate = [rn(NQ, D) * 0.05 for _ in range(shape.n_layers)]
+    ve_gate = [rn(NKV, L.VE_GATE_W) * 0.3 if v else None for v in ve]
+    xsa = [torch.rand(NQ, generator=g, device=dev) for _ in range(shape.n_layers)]
+    value_embed = rn(shape.vocab, NKV * D).to(torch.bfloat16) if any(ve) else None
+    dense1 = mix = None
+    if sites:
+        dense1 = rn(L.MUDD_INNER, shape.hidden) * 0.05
+        mix = rn(len(sites), 2, 3, L.MUDD_INNER + 1) * 0.02
+        base = torch.tensor([0.1, 0.1, 1.0], device=dev)
+        mix[:, :, :, L.MUDD_INNER] += base
+    return Extras(local, window, attn_gate, ve_gate, xsa, value_embed, dense1, mix, tuple(sites), tuple(taps))
+
+
+@dataclass
 class SyntheticModel:
     shape: ModelShape
     int8: bool
@@ -102,6 +172,7 @@ class SyntheticModel:
     embed: torch.Tensor                       # bf16 [vocab][hidden]
     layers: list[dict] = field(default_factory=list)  # name -> (w, scales or None)
     scalars: list[LayerScalars] = field(default_factory=list)
+    extras: Extras | None = None
 
     @staticmethod
     def generate(shape: ModelShape, *, int8: bool = True, seed: int = 0, device: str | torch.device = "cpu",
@@ -140,7 +211,15 @@ class SyntheticModel:
     def to(self, device: str | torch.device) -> "SyntheticModel":
         dev = torch.device(device)
         layers = [{k: (w.to(dev), None if s is None else s.to(dev)) for k, (w, s) in lay.items()} for lay in self.layers]
-        return SyntheticModel(self.shape, self.int8, dev, self.embed.to(dev), layers, self.scalars)
+        return SyntheticModel(self.shape, self.int8, dev, self.embed.to(dev), layers, self.scalars,
+                              None if self.extras is None else self.extras.to(dev))
+
+    def with_extras(self, extras: Extras) -> "SyntheticModel":
+        """This model with the Limite extras; RoPE on the sliding-window layers only
+        (encode.rs:237 rope = !global)."""
+        sc = [LayerScalars(s.qkv_scale, s.o_scale, s.resid_attn, s.post_attn, s.resid_mlp, s.post_mlp, int(loc))
+              for s, loc in zip(self.scalars, extras.local)]
+        return SyntheticModel(self.shape, self.int8, self.device, self.embed, self.layers, sc, extras.to(self.device))
 
     def embed_ptr(self) -> int:
         return self.embed.data_ptr()
@@ -156,5 +235,8 @@ class SyntheticModel:
                 return L.Matrix(w.data_ptr(), None, m, k, L.FMT_BF16, 0)
             return L.Matrix(w.data_ptr(), sc.data_ptr(), m, k, L.FMT_I8, gshift_of(k, sc))
 
+        x = self.extras
+        ptr = lambda t: None if t is None else t.data_ptr()  # noqa: E731
         return L.Layer(mat("qkv"), mat("o"), mat("gate_up"), mat("down"), s.qkv_scale, s.o_scale, s.resid_attn,
-                       s.post_attn, s.resid_mlp, s.post_mlp, s.rope, 0)
+                       s.post_attn, s.resid_mlp, s.post_mlp, s.rope, 0, ptr(x.attn_gate[i]) if x else None,
+                       ptr(x.ve_gate[i]) if x else None, ptr(x.xsa[i]) if x else None)

@@ -37,12 +37,12 @@ def test_library_exports_every_declared_symbol():
 
 STRUCTS = ["sv_shape", "sv_matrix", "sv_mat_args", "sv_kv_args", "sv_attn_args", "sv_sample_row", "sv_run_in",
            "sv_gen_state", "sv_replay_args", "sv_engine_config", "sv_layer", "sv_engine_buffers", "sv_run",
-           "sv_plan_info", "sv_tensor_info"]
+           "sv_plan_info", "sv_tensor_info", "sv_model_extras", "sv_attn_extras"]
 PY = {"sv_shape": L.Shape, "sv_matrix": L.Matrix, "sv_mat_args": L.MatArgs, "sv_kv_args": L.KvArgs,
       "sv_attn_args": L.AttnArgs, "sv_sample_row": L.SampleRow, "sv_run_in": L.RunIn, "sv_gen_state": L.GenState,
       "sv_replay_args": L.ReplayArgs, "sv_engine_config": L.EngineConfig, "sv_layer": L.Layer,
       "sv_engine_buffers": L.EngineBuffers, "sv_run": L.Run, "sv_plan_info": L.PlanInfo,
-      "sv_tensor_info": L.TensorInfo}
+      "sv_tensor_info": L.TensorInfo, "sv_model_extras": L.ModelExtras, "sv_attn_extras": L.AttnExtras}
 
 
 def test_struct_layouts_match_c(tmp_path):
@@ -73,7 +73,7 @@ def test_argument_checks_without_gpu():
     args = L.AttnArgs(128, 2, 0.18, 1, 0, 0, 0, 0, 0)
     one = C.c_void_p(16)
     rc = lib.sv_attn_verify(None, C.byref(sh), one, one, one, one, one, one, C.byref(kv), C.byref(args), one, 1, 5,
-                            one, one, one, 1 << 20)
+                            one, one, one, 1 << 20, None)
     assert rc == 4 and b"head_dim 96" in lib.sv_last_error()
     cfg = L.EngineConfig(L.Shape(2048, 32, 8, 64, 8192, 32000, 32000, 16), 1, 16, 1024, 16, 1024, 3, 0.125, 0)
     h = C.c_void_p()
