@@ -927,11 +927,12 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
       if (mx->mudd_tap[site] == li) memcpy(taps + (size_t)site * n * H, h, sizeof(float) * n * H);
   }
   if (io->hidden) memcpy(io->hidden, h, sizeof(float) * n * H);
-  /* tail (encode.rs:383-412): final norm of the head rows, the tied head, the sampler,
+  /* tail (encode.rs:383-412): final norm of the head rows, the head (tied, or its own), the sampler,
    * accept, kv_compact */
   if (io->n_head > 0) {
     orc_rmsnorm_rows(h, io->head_rows, hfin, io->n_head, H);
     sv_matrix head = {embed, NULL, sh->vocab, H, SV_FMT_BF16, 0};
+    if (io->head) head = *io->head;
     sv_mat_args a;
     memset(&a, 0, sizeof a);
     a.n = io->n_head;
@@ -940,6 +941,7 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     a.epi = SV_EPI_HEAD;
     a.vocab_real = sh->vocab_real;
     a.scale = 1.0f;
+    a.gshift = head.gshift;
     orc_matmul(&head, hfin, NULL, io->logits, NULL, NULL, &a);
     orc_sample(io->logits, io->samples, io->out, io->meta, io->n_head, sh->vocab);
   }

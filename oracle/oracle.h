@@ -122,6 +122,7 @@ typedef struct orc_step_io {
   uint16_t* k_local, *v_local;
   const uint32_t* local_table;
   sv_kv_args kv_local;
+  const sv_matrix* head; /* its own head (model.rs:93-95, host), NULL: the tied embedding */
 } orc_step_io;
 
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,

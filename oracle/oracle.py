@@ -246,7 +246,7 @@ class StepIO(C.Structure):
                 ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
                 ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp),
                 ("n_attn", u32), ("extras", vp), ("local", vp), ("k_local", vp), ("v_local", vp), ("local_table", vp),
-                ("kv_local", C.c_uint32 * 8)]
+                ("kv_local", C.c_uint32 * 8), ("head", vp)]
 
 
 def _chain(row: int) -> int:
@@ -262,7 +262,7 @@ class OracleEngine:
     """
 
     def __init__(self, L, shape, embed, weights, scalars, *, max_seqs=8, max_seq_len=8192, kv_tokens=None,
-                 page_shift=4, attn_scale=0.125, freq=None, extras=None, max_step_tokens=64):
+                 page_shift=4, attn_scale=0.125, freq=None, extras=None, max_step_tokens=64, head=None):
         """extras: host_extras() of a model with the Limite extras (sliding-window layers with
         rings laid out as the engine's, for max_step_tokens rows per step)."""
         self.L, self.shape = L, shape
@@ -324,6 +324,13 @@ class OracleEngine:
                   for k in ("attn_gate", "ve_gate", "xsa")]
             layers[i] = L.Layer(*mats, *sc[:6], int(sc[6]), 0, *ex)
         self.layers = layers
+        self._head = None  # its own head: (int8 q [vocab][hidden], bf16 scales bits) as host_head gives
+        if head is not None:
+            q, scl = (np.ascontiguousarray(head[0]), np.ascontiguousarray(head[1], np.uint16))
+            self._keep += [q, scl]
+            m, k = q.shape
+            gshift = 31 if scl.shape[1] == 1 else int(k // scl.shape[1]).bit_length() - 1
+            self._head = L.Matrix(q.ctypes.data, scl.ctypes.data, m, k, 1, gshift)
 
     # sequences
     def new_seq(self) -> int:
@@ -410,6 +417,7 @@ class OracleEngine:
         io.emitted, io.path, io.path_len, io.on_path = ptr(emitted), ptr(path), ptr(path_len), ptr(on_path)
         io.hidden = ptr(hidden)
         io.extras = C.cast(C.pointer(self._mx), vp) if self._mx is not None else None
+        io.head = C.cast(C.pointer(self._head), vp) if self._head is not None else None
         io.local = ptr(self.local)
         io.k_local, io.v_local, io.local_table = ptr(self.k_local), ptr(self.v_local), ptr(self.local_table)
         io.kv_local[:] = [0, 0, self.ring_pages * page_of(self.page_shift), self.max_seqs, self.page_shift,
@@ -447,6 +455,16 @@ def host_extras(model) -> dict | None:
                 np.ascontiguousarray(x.value_embed.detach().cpu().view(torch.int16).numpy().view(np.uint16)),
                 mudd_dense1=f32(x.mudd_dense1), mudd_mix=f32(x.mudd_mix), mudd_layer=tuple(x.mudd_layer),
                 mudd_tap=tuple(x.mudd_tap))
+
+
+def host_head(model):
+    """The model's own head as (int8 q, bf16 scale bits) host arrays, or None (tied)."""
+    import torch
+
+    if getattr(model, "head", None) is None:
+        return None
+    q, s = model.head
+    return (q.detach().cpu().numpy(), s.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16))
 
 
 def host_weights(model) -> tuple[np.ndarray, list, list]:

@@ -225,7 +225,8 @@ struct sv_engine {
   sv_shape sh{};
   hipStream_t stream = nullptr;
   const uint16_t* embed = nullptr;
-  sv_matrix head_mat{};  // the tied head (tiled when the shape allows)
+  sv_matrix head_mat{};  // the head: the tied embedding or its own (tiled when the shape allows)
+  bool own_head = false;
   std::vector<sv_layer> layers;  // as used: matrices repacked into the tiled layout where they fit it
   std::vector<bool> layer_set;
   std::vector<void*> packed;     // engine-owned tiled copies [layer * 4 + matrix]
@@ -717,6 +718,7 @@ static sv_status pack_into(sv_engine* e, const sv_matrix& in, void** slot, sv_ma
 extern "C" sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed) {
   if (!e || !d_embed) return fail(SV_ERR_ARG, "set_embed: null pointer");
   e->embed = d_embed;
+  if (e->own_head) return SV_OK;
   const sv_matrix head{d_embed, nullptr, e->sh.vocab, e->sh.hidden, SV_FMT_BF16, 0};
   SV_TRY(pack_into(e, head, &e->head_tiled, &e->head_mat));
   return SV_OK;
@@ -748,6 +750,26 @@ extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_
   SV_TRY(pack_into(e, l->down, &slots[3], &used.down));
   e->layers[layer] = used;
   e->layer_set[layer] = true;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_engine_set_head(sv_engine* e, const sv_matrix* head) {
+  if (!e) return fail(SV_ERR_ARG, "set_head: null engine");
+  if (e->graph) return fail(SV_ERR_STATE, "set_head: after a graph was captured");
+  if (!head) {
+    e->own_head = false;
+    if (!e->embed) return SV_OK;
+    const sv_matrix tied{e->embed, nullptr, e->sh.vocab, e->sh.hidden, SV_FMT_BF16, 0};
+    return pack_into(e, tied, &e->head_tiled, &e->head_mat);
+  }
+  SV_TRY(check_matrix(*head, e->sh.vocab, e->sh.hidden, "head"));
+  const uint32_t fmt = head->format & ~(uint32_t)SV_FMT_TILED;
+  const bool per_row = head->gshift >= 32 || (1ull << head->gshift) >= head->k;
+  if (fmt == SV_FMT_I8 && !per_row && head->gshift < 6)
+    return fail(SV_ERR_UNSUPPORTED, "set_head: int8 groups of %u (64 or more, or one per row, are built)",
+                1u << head->gshift);
+  SV_TRY(pack_into(e, *head, &e->head_tiled, &e->head_mat));
+  e->own_head = true;
   return SV_OK;
 }
 

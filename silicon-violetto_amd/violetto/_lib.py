@@ -163,6 +163,7 @@ PROTOS = {
     "sv_engine_set_embed": (C.c_int, [vp, vp]),
     "sv_engine_set_layer": (C.c_int, [vp, u32, P(Layer)]),
     "sv_engine_set_extras": (C.c_int, [vp, P(ModelExtras)]),
+    "sv_engine_set_head": (C.c_int, [vp, P(Matrix)]),
     "sv_engine_stream": (vp, [vp]),
     "sv_engine_get_buffers": (C.c_int, [vp, P(EngineBuffers)]),
     "sv_new_seq": (C.c_int, [vp, P(u32)]),

@@ -79,6 +79,8 @@ class Engine:
         for i in range(model.shape.n_layers):
             lay = model.c_layer(i)
             L.check(self.lib.sv_engine_set_layer(self.h, i, C.byref(lay)))
+        head = model.c_head() if hasattr(model, "c_head") else None
+        L.check(self.lib.sv_engine_set_head(self.h, C.byref(head) if head is not None else None))
         if getattr(model, "extras", None) is not None:
             ex = model.extras.c()
             L.check(self.lib.sv_engine_set_extras(self.h, C.byref(ex)))

@@ -173,6 +173,7 @@ class SyntheticModel:
     layers: list[dict] = field(default_factory=list)  # name -> (w, scales or None)
     scalars: list[LayerScalars] = field(default_factory=list)
     extras: Extras | None = None
+    head: tuple | None = None                 # its own head (int8 q, scales) or None: the tied embedding
 
     @staticmethod
     def generate(shape: ModelShape, *, int8: bool = True, seed: int = 0, device: str | torch.device = "cpu",
@@ -212,14 +213,29 @@ class SyntheticModel:
         dev = torch.device(device)
         layers = [{k: (w.to(dev), None if s is None else s.to(dev)) for k, (w, s) in lay.items()} for lay in self.layers]
         return SyntheticModel(self.shape, self.int8, dev, self.embed.to(dev), layers, self.scalars,
-                              None if self.extras is None else self.extras.to(dev))
+                              None if self.extras is None else self.extras.to(dev),
+                              None if self.head is None else tuple(t.to(dev) for t in self.head))
+
+    def with_head(self, group: int | None) -> "SyntheticModel":
+        """This model with an int8 head quantized from the embedding (tools/convert.py:111-112,
+        `matrix("head", "head", embed)`): groups of `group` k, or one scale per row."""
+        w = self.embed.float()
+        q = quantize_rows(w) if group is None else quantize_groups(w, group)
+        return SyntheticModel(self.shape, self.int8, self.device, self.embed, self.layers, self.scalars, self.extras, q)
+
+    def c_head(self) -> L.Matrix | None:
+        if self.head is None:
+            return None
+        q, s = self.head
+        return L.Matrix(q.data_ptr(), s.data_ptr(), q.shape[0], q.shape[1], L.FMT_I8, gshift_of(q.shape[1], s))
 
     def with_extras(self, extras: Extras) -> "SyntheticModel":
         """This model with the Limite extras; RoPE on the sliding-window layers only
         (encode.rs:237 rope = !global)."""
         sc = [LayerScalars(s.qkv_scale, s.o_scale, s.resid_attn, s.post_attn, s.resid_mlp, s.post_mlp, int(loc))
               for s, loc in zip(self.scalars, extras.local)]
-        return SyntheticModel(self.shape, self.int8, self.device, self.embed, self.layers, sc, extras.to(self.device))
+        return SyntheticModel(self.shape, self.int8, self.device, self.embed, self.layers, sc, extras.to(self.device),
+                              self.head)
 
     def embed_ptr(self) -> int:
         return self.embed.data_ptr()

@@ -307,3 +307,71 @@ def test_limite_reference_shape_step(gpu):
         step_both(eng, ref, [(s, [L.FEED_ROW] + drafts, True)], slots, "verify")
         caches_close(eng, ref)
     eng.close()
+
+
+@pytest.mark.parametrize("head_group", [64, None])
+def test_limite_from_weight_file(gpu, tmp_path, head_group):
+    """A Limite-layout model written under the reference's tensor names (tools/convert.py:76-113:
+    int8 layers in groups of 64, gates, XSA, value embeddings, MUDD, RoPE frequencies and an int8
+    head of its own, groups of 64 or one per row), uploaded and resolved by VltModel (the layer
+    pattern of model.rs:116), verifies two streams past the window against the oracle engine
+    built from the same tensors."""
+    banner(f"limite model from a weight file, head group {head_group}")
+    from violetto.weights import VltModel, WeightFile, reference_tensors, write_vlt
+
+    shape = ModelShape(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024, vocab_real=1000,
+                       n_layers=8)
+    window = 48
+    model = SyntheticModel.generate(shape, seed=41, device="cpu", group=64)
+    model = model.with_extras(generate_extras(shape, seed=42, window=window)).with_head(head_group)
+    freq = rope_freq(500000.0, 64)
+    path = tmp_path / "limite.vlt"
+    write_vlt(path, reference_tensors(model, freq))
+    wf = WeightFile(path)
+    wf.upload()
+    vm = VltModel(wf, shape, window=window)
+    assert vm.limite and vm.extras.local == model.extras.local and vm.extras.mudd_layer == (4, 7)
+    assert np.array_equal(vm.rope_freq(), freq)
+    eng = Engine(shape, max_seqs=2, max_step_tokens=64, max_seq_len=512, max_head_rows=32, kv_tokens=1024,
+                 attn_scale=0.125, freq=vm.rope_freq(), local=vm.extras.local, window=window)
+    eng.set_model(vm)
+    emb, lay, sc = oracle.host_weights(model)
+    ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=2, max_seq_len=512, kv_tokens=1024, attn_scale=0.125,
+                              freq=freq, extras=oracle.host_extras(model), max_step_tokens=64,
+                              head=oracle.host_head(model))
+    rng = np.random.default_rng(43)
+    slots = []
+    for c in (130, 77):
+        s = eng.new_seq()
+        assert s == ref.new_seq()
+        eng.bench_fill(s, c)
+        ref.bench_fill(s, c)
+        slots.append(s)
+    kd, vd = eng.kv_cache()
+    kl, vl, _ = eng.local_cache()
+    for dev_t, host in ((kd, ref.k), (vd, ref.v), (kl, ref.k_local), (vl, ref.v_local)):
+        bits = rand_bits(rng, host.shape)
+        host[...] = bits
+        dev_t.copy_(torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16))
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ref.seq_len[s], t)
+        ref.set_feed(s, ref.seq_len[s], t)
+    for step in range(3):
+        runs = [(s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, 4)], True) for s in slots]
+        same, _, _, _ = step_both(eng, ref, runs, slots, f"step {step}")
+        if not same:
+            break
+    eng.close()
+    wf.close()
+
+
+def test_head_of_small_groups_is_refused(gpu):
+    """An int8 head in groups of 8 (the reference converter's head default) is refused with a
+    clear error; groups of 64 and more, or one per row, are served."""
+    shape = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=512, vocab_real=500, n_layers=1)
+    model = SyntheticModel.generate(shape, seed=1).with_head(8).to("cuda")
+    eng = Engine(shape, max_seqs=1, max_step_tokens=16, max_seq_len=64, freq=rope_freq(500000.0, 64))
+    with pytest.raises(L.SvError, match="groups of 8"):
+        eng.set_model(model)
+    eng.close()

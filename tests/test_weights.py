@@ -130,3 +130,40 @@ def test_matrix_groups_checked(tmp_path):
         wf.matrix("b", 16, 96)
     with pytest.raises(L.SvError, match="weight file has no tensor c.scale"):
         wf.matrix("c", 16, 96)
+
+
+def test_limite_tensors_round_trip(tmp_path):
+    """A Limite-layout model (extras and an int8 head of groups of 64) written under the
+    reference's names (tools/convert.py:76-113) reads back with every name, dtype and shape
+    model.rs:109-141 asks for, contents equal."""
+    from violetto.model import ModelShape, SyntheticModel, generate_extras, rope_freq
+    from violetto.weights import reference_tensors
+
+    shape = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=512, vocab_real=500,
+                       n_layers=8)
+    model = SyntheticModel.generate(shape, seed=2, group=64).with_extras(generate_extras(shape, seed=3, window=48))
+    model = model.with_head(64)
+    t = reference_tensors(model, rope_freq(500000.0, 64))
+    path = tmp_path / "limite.vlt"
+    write_vlt(path, t)
+    wf = WeightFile(path)
+    want = {"embed": (1, (512, 256)), "value_embed": (1, (512, 128)), "rope_freq": (0, (32,)),
+            "mudd.dense1": (0, (32, 256)), "mudd.mix": (0, (2, 2, 3, 33)), "head": (2, (512, 256)),
+            "head.scale": (1, (512, 4))}
+    for i in range(8):
+        want[f"L{i:02d}.attn_gate"] = (0, (4, 64))
+        want[f"L{i:02d}.xsa"] = (0, (4,))
+        want[f"L{i:02d}.qkv"] = (2, (512, 256))
+        want[f"L{i:02d}.qkv.scale"] = (1, (512, 4))
+        if i % 3 == 1:
+            want[f"L{i:02d}.ve_gate"] = (0, (2, 12))
+        else:
+            assert not wf.has(f"L{i:02d}.ve_gate")
+    for name, (dt, shp) in want.items():
+        wf.check(name, dt, shp)
+    np.testing.assert_array_equal(wf.read("L04.xsa"), model.extras.xsa[4].numpy())
+    np.testing.assert_array_equal(wf.read("mudd.mix")[:2], model.extras.mudd_mix.numpy())
+    np.testing.assert_array_equal(wf.read("head"), model.head[0].numpy())
+    with pytest.raises(ValueError, match="expected dtype"):
+        wf.check("L00.xsa", 1, (4,))
+    wf.close()
