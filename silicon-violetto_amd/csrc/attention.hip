@@ -63,7 +63,7 @@ constexpr bool attn_newest_own(int NCT, int NBW) { return NBW > 0 || NCT >= 3; }
 // NBW > 0 (splits of at most 128 NBW keys, grids of about one workgroup per CU): each wave
 // requests all of its batches at once, after the queries, positions and page-table words (one
 // round trip) and the rope words, and builds the queries while they arrive.
-template <int D, int NCT, int NBW, bool INL>
+template <int D, int NCT, int NBW, bool INL, bool LOCAL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(D, NCT, NBW)))) void attn_verify_kernel(AttnParams p) {
   constexpr int KST = D / 32, VE = D / 16, COLS = 16 * NCT;
   extern __shared__ __attribute__((aligned(16))) float lds[];  // [4][COLS][D] partial o, then [4][COLS] partial l
@@ -83,8 +83,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   constexpr int R = attn_ring(NCT);
   KvBatchT<D> ring[NBW == 0 ? R : 1];
   // A sliding-window layer's splits start at its first query's window (its position first).
-  uint32_t p0 = p.local ? p.meta[2 * t0 + 1] : 0u;
-  const uint32_t kbeg = (p.local ? key_base(p, p0) : 0u) + s * p.split;
+  uint32_t p0 = LOCAL ? p.meta[2 * t0 + 1] : 0u;
+  const uint32_t kbeg = (LOCAL ? key_base_t<true>(p, p0) : 0u) + s * p.split;
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
   uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
@@ -187,7 +187,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane);
   }
 
-  const uint32_t nsplit = attn_nsplit(p, p0);
+  const uint32_t nsplit = attn_nsplit_t<LOCAL>(p, p0);
   if (nsplit > p.max_splits) {
     // The grid has too few splits for this run's context: its output is NaN (never a
     // partial sum) and the counter is left alone.
@@ -205,9 +205,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
 #pragma unroll
   for (int ct = 0; ct < NCT; ct++) {
     const uint32_t c = 16 * ct + c16;
-    clo[ct] = p.local && c < ncols ? key_lo(p, p.meta[2 * (t0 + c / p.G) + 1]) : 0u;
+    clo[ct] = LOCAL && c < ncols ? key_lo_t<LOCAL>(p, p.meta[2 * (t0 + c / p.G) + 1]) : 0u;
   }
-  const uint32_t lo_hi = key_lo(p, p0 + T - 1);
+  const uint32_t lo_hi = key_lo_t<LOCAL>(p, p0 + T - 1);
   // newest: a split of the new keys alone; takes_new: the last cached split also takes them
   // (attn_newest_own; the launch sets p.newest_own to match).
   const bool newest = attn_newest_own(NCT, NBW) && s == nsplit - 1, takes_new = !attn_newest_own(NCT, NBW) && s == nsplit - 1;
@@ -440,13 +440,18 @@ void attn_init() {
   static bool done = false;
   if (done) return;
   done = true;
-#define SV_ATTR2(DD, N, B, I)                                                                                      \
-  (void)hipFuncSetAttribute((const void*)attn_verify_kernel<DD, N, B, I>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+#define SV_ATTR3(DD, N, B, I, LC)                                                                   \
+  (void)hipFuncSetAttribute((const void*)attn_verify_kernel<DD, N, B, I, LC>,                    \
+                            hipFuncAttributeMaxDynamicSharedMemorySize,                           \
                             (int)((size_t)4 * 16 * N * DD * 4 + (size_t)4 * 16 * N * 4))
+#define SV_ATTR2(DD, N, B, I) SV_ATTR3(DD, N, B, I, false)
 #define SV_ATTR1(DD, N, B) \
   SV_ATTR2(DD, N, B, true); \
   SV_ATTR2(DD, N, B, false)
-#define SV_ATTR(DD, N) SV_ATTR1(DD, N, 0)
+#define SV_ATTR(DD, N)                 \
+  SV_ATTR1(DD, N, 0);                  \
+  SV_ATTR3(DD, N, 0, true, true);      \
+  SV_ATTR3(DD, N, 0, false, true)
   SV_ATTR1(64, 1, SV_ATTN_NBW);
   SV_ATTR1(64, 2, SV_ATTN_NBW);
   SV_ATTR(64, 1);
@@ -460,6 +465,7 @@ void attn_init() {
 #undef SV_ATTR
 #undef SV_ATTR1
 #undef SV_ATTR2
+#undef SV_ATTR3
 }
 
 // Compute units of the current device (the all-batches-in-flight choice).
@@ -601,7 +607,13 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     if (inl) launch((attn_verify_kernel<DD, N, B, true>), grid, dim3(256), shm, stream, p);  \
     else launch((attn_verify_kernel<DD, N, B, false>), grid, dim3(256), shm, stream, p);     \
   } while (0)
-#define SV_ATTN(DD, N) SV_ATTN3(DD, N, 0)
+  // sliding-window layers: the streaming variant with the window compiled in
+#define SV_ATTN(DD, N)                                                                                   \
+  do {                                                                                                   \
+    if (!p.local) SV_ATTN3(DD, N, 0);                                                                    \
+    else if (inl) launch((attn_verify_kernel<DD, N, 0, true, true>), grid, dim3(256), shm, stream, p);   \
+    else launch((attn_verify_kernel<DD, N, 0, false, true>), grid, dim3(256), shm, stream, p);           \
+  } while (0)
     if (allin) {
       if (nct == 1) SV_ATTN3(64, 1, SV_ATTN_NBW);
       else SV_ATTN3(64, 2, SV_ATTN_NBW);

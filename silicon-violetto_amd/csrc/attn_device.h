@@ -50,18 +50,26 @@ struct AttnParams {
   uint32_t H;
 };
 
-// The first cached key the query at pos sees (kernels.metal:808-811 key_lo).
-__device__ __forceinline__ uint32_t key_lo(const AttnParams& p, uint32_t pos) {
-  return p.local && pos > p.window ? pos - p.window : 0u;
+// The first cached key the query at pos sees (kernels.metal:808-811 key_lo); LOCAL: the layer
+// is a sliding-window one (a compile-time choice in the attention kernel, so global layers
+// carry none of it).
+template <bool LOCAL>
+__device__ __forceinline__ uint32_t key_lo_t(const AttnParams& p, uint32_t pos) {
+  return LOCAL && pos > p.window ? pos - p.window : 0u;
 }
 // A run's cached keys start at its first query's key_lo rounded down to a batch (32 keys):
 // batches stay aligned to the tiles of 16 keys; keys below a column's key_lo are masked.
-__device__ __forceinline__ uint32_t key_base(const AttnParams& p, uint32_t p0) { return key_lo(p, p0) & ~31u; }
+template <bool LOCAL>
+__device__ __forceinline__ uint32_t key_base_t(const AttnParams& p, uint32_t p0) { return key_lo_t<LOCAL>(p, p0) & ~31u; }
 
 // Splits of a run whose first position is p0.
-__device__ __forceinline__ uint32_t attn_nsplit(const AttnParams& p, uint32_t p0) {
-  const uint32_t c = (p0 - key_base(p, p0) + p.split - 1) / p.split;
+template <bool LOCAL>
+__device__ __forceinline__ uint32_t attn_nsplit_t(const AttnParams& p, uint32_t p0) {
+  const uint32_t c = (p0 - key_base_t<LOCAL>(p, p0) + p.split - 1) / p.split;
   return p.newest_own ? c + 1 : (c ? c : 1u);
+}
+__device__ __forceinline__ uint32_t attn_nsplit(const AttnParams& p, uint32_t p0) {
+  return p.local ? attn_nsplit_t<true>(p, p0) : attn_nsplit_t<false>(p, p0);
 }
 
 __device__ __forceinline__ float sigmoid_f(float x) {
