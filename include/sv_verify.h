@@ -310,6 +310,32 @@ sv_status sv_draft_tree(void* stream, const uint32_t* d_blocks, uint32_t nblocks
                         const uint32_t* d_cand, const float* d_cand_q, uint32_t* d_feed, uint32_t* d_tree,
                         uint32_t ncand);
 
+/* The drafter's own pieces (kernels.metal:135-148 tap_rows, 1725-1844 draft_kv, draft_ctx,
+ * draft_embed, draft_conv), over [n][hidden] fp32 rows:
+ *  - tap_rows: out[t] = bf16(rms_norm(in[t])) kept as float (a target layer's output tapped);
+ *  - draft_kv: for the tokens on_path, kvp[t] = [layer][k | v][NKV][D] (the fused context through
+ *    every drafter layer's k/v) is normed and roped (k) and written bf16 to the drafter's ring of
+ *    each layer at the token's position (d_meta: (slot, position)); grid over (tokens, layers);
+ *  - draft_ctx: for the tokens on_path, ring[slot][pos % cr] = ctx[t] * ctx_inv[t];
+ *  - draft_embed: block row r (d_tin[r] = (slot, i)) at position lens[slot] + i: row 0 the slot's
+ *    next input feed[slot][0] as rms_norm(embedding), later rows mask_emb; meta and tokens of
+ *    the rows; with cr > 0, last[r] = ring[slot][(lens[slot] - 1) % cr];
+ *  - draft_conv: out[r] = resid[r] (with resid) + (base[0] + corr[r][d / 16]) x[r] + (base[1] +
+ *    corr[r][hidden / 16 + d / 16]) x[r - 1], the second term only for rows after a block's first
+ *    (corr [n][corr_w]); out must not be x. */
+sv_status sv_tap_rows(void* stream, const float* d_in, float* d_out, uint32_t n, uint32_t hidden);
+sv_status sv_draft_kv(void* stream, const sv_shape* shape, const float* d_kvp, const uint32_t* d_meta,
+                      const uint32_t* d_on_path, const float* d_rope, uint16_t* d_k_ring, uint16_t* d_v_ring,
+                      const uint32_t* d_page_table, const sv_kv_args* kv, uint32_t n, uint32_t n_layers);
+sv_status sv_draft_ctx(void* stream, const float* d_ctx, const float* d_ctx_inv, const uint32_t* d_meta,
+                       const uint32_t* d_on_path, float* d_ring, uint32_t cr, uint32_t n, uint32_t hidden);
+sv_status sv_draft_embed(void* stream, const uint16_t* d_embed, const uint32_t* d_tin, const uint32_t* d_lens,
+                         const uint32_t* d_feed, const float* d_mask_emb, float* d_x, uint32_t* d_meta,
+                         uint32_t* d_tokens, const float* d_ring, float* d_last, uint32_t cr, uint32_t rows,
+                         uint32_t hidden);
+sv_status sv_draft_conv(void* stream, const float* d_x, const float* d_corr, uint32_t corr_w, const float* d_base,
+                        const uint32_t* d_tin, const float* d_resid, float* d_out, uint32_t rows, uint32_t hidden);
+
 /* The weight file (engine/src/weights.rs:38-74; format tools/convert.py:117-150): header
  * "VIOLETTO", version 1, 128-byte records, 16 KiB-aligned data region. sv_weights_open reads and
  * checks the records on the host; sv_weights_upload copies every tensor into one device buffer;
@@ -478,7 +504,8 @@ typedef struct sv_plan_info {
 enum {
   SV_STEP_REPLAY = 1,   /* after accept, the replay drafter writes the next drafts */
   SV_STEP_COMPACT = 2,  /* run kv_compact even if no run branches               */
-  SV_STEP_NO_COMPACT = 4
+  SV_STEP_NO_COMPACT = 4,
+  SV_STEP_DRAFT = 8     /* after accept, the drafter's pass writes the next draft trees */
 };
 
 /* Engine::plan (plan.rs:47-151): lays out a step, reserves pages, advances the host-side
@@ -494,6 +521,52 @@ sv_status sv_graph_replay(sv_engine* e, uint32_t count);
 sv_status sv_sync(sv_engine* e);
 /* Replay-drafter settings (generate.rs:421-430). */
 sv_status sv_set_replay(sv_engine* e, uint32_t seed, float rate);
+
+/* The drafter (engine/src/engine/drafter.rs, its file written by tools/spec/export.py): a small
+ * model of the target's shape that reads the target's tapped layers. Device pointers; matrices
+ * as sv_matrix. conv_base[0] NULL: a layer without the two-tap convolutions; inject.d_w NULL:
+ * none. vocab: the draft vocabulary's target ids [v]. The engine taps `taps` (their outputs,
+ * normed and rounded to bf16) on every step once a drafter is set. */
+#define SV_DRAFT_TAPS 4u
+#define SV_DRAFT_LAYERS 8u
+typedef struct sv_draft_layer {
+  sv_matrix qkv, o, gate_up, down;
+  const float* conv_base[4]; /* [2][hidden] each: before attention, after it, before the MLP, after it */
+  sv_matrix conv_corr[4];    /* [corr_w][hidden] each, corr_w = hidden / 8 padded (export.py: 192) */
+} sv_draft_layer;
+typedef struct sv_drafter {
+  uint32_t n_layers, n_taps, v;
+  uint32_t taps[SV_DRAFT_TAPS];
+  sv_matrix fc[SV_DRAFT_TAPS]; /* [hidden][hidden]: the context, sum over taps */
+  sv_matrix kv_all;            /* [n_layers 2 NKV D][hidden]                  */
+  sv_matrix inject;            /* [hidden][hidden] or d_w NULL                */
+  sv_matrix head;              /* [v][hidden], raw logits                     */
+  const float* mask_emb;       /* [hidden]                                    */
+  const uint32_t* vocab;       /* [v]                                         */
+  const sv_draft_layer* layers;/* host [n_layers]                             */
+  float inv_temperature;       /* draft_top's 1 / T (drafter.rs: 1 / 0.6)      */
+  uint32_t window;             /* the context positions a block row sees      */
+} sv_drafter;
+sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d);
+/* Draft rows per block (1 + drafts, at most the attention run length) of a slot's next steps
+ * with SV_STEP_DRAFT; 0: the slot is not drafted. */
+sv_status sv_set_draft_rows(sv_engine* e, uint32_t slot, uint32_t rows);
+/* The drafter's device buffers (Engine::drafter_debug, drafter.rs:263-275), for tests to read:
+ * the last pass's raw logits [rows][v] and candidates [rows][SV_DRAFT_CANDS], the context
+ * [max_step_tokens][hidden], the taps [n_taps][max_step_tokens][hidden], the rings
+ * [n_layers][n_pages][NKV][page][D] bf16 behind the cyclic table [max_seqs][max_pages]. */
+typedef struct sv_draft_buffers {
+  float* d_logits;
+  uint32_t* d_cand;
+  float* d_cand_q;
+  float* d_ctx;
+  float* d_taps[SV_DRAFT_TAPS];
+  uint16_t* d_k_ring;
+  uint16_t* d_v_ring;
+  uint32_t* d_table;
+  uint32_t ring_pages, n_pages, max_pages, pad;
+} sv_draft_buffers;
+sv_status sv_engine_draft_buffers(sv_engine* e, sv_draft_buffers* out);
 
 /* A synchronous step (Engine::step, engine.rs:310-314): plan, encode, wait; read the head
  * rows' ids (ids[n_head]) and, if logits is non-null, their logits [n_head][vocab], and
@@ -521,7 +594,8 @@ enum {
   SV_KIND_ATTN_MERGE = 11, /* the attention split merge (its own launch) */
   SV_KIND_KV_WRITE = 12,   /* prompt chunks: the new K/V rows, before the attention */
   SV_KIND_MUDD = 13,
-  SV_KIND_COUNT = 14
+  SV_KIND_DRAFT = 14,      /* the drafter's pass (every launch of it) */
+  SV_KIND_COUNT = 15
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

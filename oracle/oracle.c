@@ -925,6 +925,8 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     orc_matmul(&l->down, act, NULL, h, mixed, NULL, &a);
     for (uint32_t site = 0; site < n_mudd; site++)
       if (mx->mudd_tap[site] == li) memcpy(taps + (size_t)site * n * H, h, sizeof(float) * n * H);
+    for (uint32_t k = 0; k < io->n_taps; k++)
+      if (io->tap_layers[k] == li) orc_tap_rows(h, io->tap_out[k], n, H);
   }
   if (io->hidden) memcpy(io->hidden, h, sizeof(float) * n * H);
   /* tail (encode.rs:383-412): final norm of the head rows, the head (tied, or its own), the sampler,
@@ -968,6 +970,213 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
   free(act);
   free(inv);
   free(hfin);
+  return 0;
+}
+
+/* ----------------------------------------------------------------- drafter */
+
+/* kernels.metal:135-148 tap_rows(): out[t] = bf16(rms_norm(in[t])) as float. */
+void orc_tap_rows(const float* in, float* out, uint32_t n, uint32_t hidden) {
+  for (uint32_t t = 0; t < n; t++) {
+    const float* x = in + (size_t)t * hidden;
+    double ss = 0.0;
+    for (uint32_t i = 0; i < hidden; i++) ss += (double)x[i] * x[i];
+    const double inv = 1.0 / sqrt(ss / hidden + (double)SV_RMS_EPS);
+    for (uint32_t i = 0; i < hidden; i++) out[(size_t)t * hidden + i] = orc_round_bf16((float)(x[i] * inv));
+  }
+}
+
+/* kernels.metal:1734-1755 draft_kv(): for the tokens on_path, each drafter layer's k (normed,
+ * roped) and v from kvp[t][layer][k | v][NKV][D], bf16 into the ring at the token's position. */
+void orc_draft_kv(const sv_shape* sh, const float* kvp, const uint32_t* meta, const uint32_t* on_path,
+                  const float* rope, uint16_t* k_ring, uint16_t* v_ring, const uint32_t* table, const sv_kv_args* kv,
+                  uint32_t n, uint32_t n_layers) {
+  const uint32_t D = sh->head_dim, NKV = sh->n_kv_heads;
+  double* tmp = (double*)malloc(sizeof(double) * D);
+  for (uint32_t t = 0; t < n; t++) {
+    if (!on_path[t]) continue;
+    const uint32_t seq = meta[2 * t], pos = meta[2 * t + 1];
+    for (uint32_t l = 0; l < n_layers; l++) {
+      const float* row = kvp + ((size_t)t * n_layers + l) * 2 * NKV * D;
+      for (uint32_t g = 0; g < NKV; g++) {
+        norm_rope_d(row + g * D, tmp, D, 1, rope + (size_t)pos * 64);
+        const size_t at = kv_row(kv, table, l, seq, g, pos, NKV, D);
+        for (uint32_t d = 0; d < D; d++) {
+          k_ring[at + d] = orc_to_bf((float)tmp[d]);
+          v_ring[at + d] = orc_to_bf(row[(NKV + g) * D + d]);
+        }
+      }
+    }
+  }
+  free(tmp);
+}
+
+/* kernels.metal:1760-1772 draft_ctx(): ring[slot][pos % cr] = ctx[t] ctx_inv[t], tokens on_path. */
+void orc_draft_ctx(const float* ctx, const float* ctx_inv, const uint32_t* meta, const uint32_t* on_path, float* ring,
+                   uint32_t cr, uint32_t n, uint32_t hidden) {
+  for (uint32_t t = 0; t < n; t++) {
+    if (!on_path[t]) continue;
+    float* dst = ring + ((size_t)meta[2 * t] * cr + meta[2 * t + 1] % cr) * hidden;
+    for (uint32_t i = 0; i < hidden; i++) dst[i] = ctx[(size_t)t * hidden + i] * ctx_inv[t];
+  }
+}
+
+/* kernels.metal:1778-1813 draft_embed(): block row r = (slot, i) at lens[slot] + i; row 0 the
+ * rms-normed embedding of feed[slot][0], later rows mask_emb; with cr, the context before the block. */
+void orc_draft_embed(const uint16_t* table, const uint32_t* tin, const uint32_t* lens, const uint32_t* feed,
+                     const float* mask_emb, float* x, uint32_t* meta, uint32_t* tokens, const float* ring, float* last,
+                     uint32_t cr, uint32_t rows, uint32_t hidden) {
+  for (uint32_t r = 0; r < rows; r++) {
+    const uint32_t slot = tin[2 * r], i = tin[2 * r + 1], tok = feed[slot * SV_FEED_W], len = lens[slot];
+    meta[2 * r] = slot;
+    meta[2 * r + 1] = len + i;
+    tokens[r] = tok;
+    if (cr) memcpy(last + (size_t)r * hidden, ring + ((size_t)slot * cr + (len - 1u) % cr) * hidden, sizeof(float) * hidden);
+    float* xr = x + (size_t)r * hidden;
+    if (i > 0) {
+      memcpy(xr, mask_emb, sizeof(float) * hidden);
+      continue;
+    }
+    const uint16_t* e = table + (size_t)tok * hidden;
+    double ss = 0.0;
+    for (uint32_t j = 0; j < hidden; j++) ss += (double)orc_bf(e[j]) * orc_bf(e[j]);
+    const double inv = 1.0 / sqrt(ss / hidden + (double)SV_RMS_EPS);
+    for (uint32_t j = 0; j < hidden; j++) xr[j] = (float)(orc_bf(e[j]) * inv);
+  }
+}
+
+/* kernels.metal:1820-1836 draft_conv(): out = resid + (base[0] + corr[r][d/16]) x[r] +
+ * (base[1] + corr[r][H/16 + d/16]) x[r - 1] (not for a block's first row). */
+void orc_draft_conv(const float* x, const float* corr, uint32_t corr_w, const float* base, const uint32_t* tin,
+                    const float* resid, float* out, uint32_t rows, uint32_t hidden) {
+  for (uint32_t r = 0; r < rows; r++) {
+    const float* c = corr + (size_t)r * corr_w;
+    for (uint32_t d = 0; d < hidden; d++) {
+      const size_t at = (size_t)r * hidden + d;
+      double y = ((double)base[d] + c[d / 16]) * x[at];
+      if (tin[2 * r + 1] > 0) y += ((double)base[hidden + d] + c[hidden / 16 + d / 16]) * x[at - hidden];
+      out[at] = (float)(resid ? resid[at] + y : y);
+    }
+  }
+}
+
+static void draft_mm(const sv_matrix* w, uint32_t n, const float* x, float* y, uint32_t epi, uint32_t flags, float ra,
+                     const float* base, float* aux) {
+  sv_mat_args a;
+  memset(&a, 0, sizeof a);
+  a.n = n;
+  a.k = w->k;
+  a.m = w->m;
+  a.epi = epi;
+  a.flags = flags;
+  a.scale = 1.0f;
+  a.ra = ra;
+  a.rb = 1.0f;
+  a.ksplit = 1;
+  a.gshift = w->gshift;
+  orc_matmul(w, x, NULL, y, base, aux, &a);
+}
+
+/* drafter.rs:278-447 encode_drafter(): the step's context (taps -> fc -> kv_all -> the rings,
+ * and the context ring with inject), then the blocks through the drafter's layers, the raw
+ * head over the normed rows, draft_top and draft_tree into feed/tree. Host pointers. */
+int orc_draft(const sv_shape* sh, const uint16_t* embed, const sv_drafter* d, float attn_scale, orc_draft_io* io) {
+  const uint32_t n = io->n, H = sh->hidden, D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads;
+  const uint32_t W = (NQ + 2 * NKV) * D, F = sh->ffn, R = io->rows ? io->rows : 1;
+  const uint32_t KVW = d->n_layers * 2 * NKV * D;
+  float* ctx = (float*)calloc((size_t)(n ? n : 1) * H, sizeof(float));
+  float* tmp = (float*)malloc(sizeof(float) * (n ? n : 1) * H);
+  float* ctx_inv = (float*)malloc(sizeof(float) * (n ? n : 1));
+  float* kvp = (float*)malloc(sizeof(float) * (n ? n : 1) * KVW);
+  float* x = (float*)malloc(sizeof(float) * R * H);
+  float* last = (float*)malloc(sizeof(float) * R * H);
+  float* cx = (float*)malloc(sizeof(float) * R * H);
+  float* co = (float*)malloc(sizeof(float) * R * H);
+  float* mixed = (float*)malloc(sizeof(float) * R * H);
+  float* qkv = (float*)malloc(sizeof(float) * R * W);
+  float* inv = (float*)malloc(sizeof(float) * R);
+  float* attn = (float*)malloc(sizeof(float) * R * NQ * D);
+  float* act = (float*)malloc(sizeof(float) * R * F);
+  uint32_t cw = 1;
+  for (uint32_t li = 0; li < d->n_layers; li++)
+    for (int c = 0; c < 4; c++) cw = d->layers[li].conv_corr[c].m > cw ? d->layers[li].conv_corr[c].m : cw;
+  float* corr = (float*)malloc(sizeof(float) * R * cw);
+  float* corr_inv = (float*)malloc(sizeof(float) * R);
+  float* hfin = (float*)malloc(sizeof(float) * R * H);
+  uint32_t* meta = (uint32_t*)malloc(sizeof(uint32_t) * 2 * R);
+  uint32_t* tokens = (uint32_t*)malloc(sizeof(uint32_t) * R);
+  uint32_t* iota = (uint32_t*)malloc(sizeof(uint32_t) * R);
+  uint32_t* cand = (uint32_t*)malloc(sizeof(uint32_t) * R * SV_DRAFT_CANDS);
+  float* cand_q = (float*)malloc(sizeof(float) * R * SV_DRAFT_CANDS);
+  if (!ctx || !tmp || !ctx_inv || !kvp || !x || !last || !cx || !co || !mixed || !qkv || !inv || !attn || !act ||
+      !corr || !corr_inv || !hfin || !meta || !tokens || !iota || !cand || !cand_q)
+    return -1;
+  /* 1. context */
+  for (uint32_t k = 0; k < d->n_taps; k++) {
+    draft_mm(&d->fc[k], n, io->taps[k], tmp, SV_EPI_RAW, 0, 0.0f, NULL, NULL);
+    for (size_t i = 0; i < (size_t)n * H; i++) ctx[i] += tmp[i];
+  }
+  if (io->ctx) memcpy(io->ctx, ctx, sizeof(float) * n * H);
+  draft_mm(&d->kv_all, n, ctx, kvp, SV_EPI_NORM, SV_FLAG_WRITE_INV, 0.0f, NULL, ctx_inv);
+  sv_kv_args kv = io->kv;
+  orc_draft_kv(sh, kvp, io->meta, io->on_path, io->rope, io->k_ring, io->v_ring, io->table, &kv, n, d->n_layers);
+  const uint32_t cr = d->inject.d_w ? io->cr : 0u;
+  if (cr) orc_draft_ctx(ctx, ctx_inv, io->meta, io->on_path, io->ctx_ring, cr, n, H);
+  const uint32_t rows = io->rows;
+  if (rows) {
+    /* 2. block rows */
+    orc_draft_embed(embed, io->tin, io->lens, io->feed, d->mask_emb, x, meta, tokens, io->ctx_ring, last, cr, rows, H);
+    if (cr) draft_mm(&d->inject, rows, last, x, SV_EPI_RESID, 0, 1.0f, x, NULL);
+    sv_attn_args aa;
+    memset(&aa, 0, sizeof aa);
+    aa.scale_log2 = attn_scale * LOG2E_F;
+    aa.rope = 1;
+    for (uint32_t li = 0; li < d->n_layers; li++) {
+      const sv_draft_layer* L = &d->layers[li];
+      const int convs = L->conv_base[0] != NULL;
+#define CONV(c, in, res, out)                                                                               \
+  do {                                                                                                      \
+    draft_mm(&L->conv_corr[c], rows, in, corr, SV_EPI_NORM, SV_FLAG_WRITE_INV, 0.0f, NULL, corr_inv);      \
+    orc_draft_conv(in, corr, L->conv_corr[c].m, L->conv_base[c], io->tin, res, out, rows, H);              \
+  } while (0)
+      const float* xin = x;
+      if (convs) {
+        CONV(0, x, NULL, cx);
+        xin = cx;
+      }
+      draft_mm(&L->qkv, rows, xin, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, 0.0f, NULL, inv);
+      kv.kv_layer = li;
+      orc_attn_verify(sh, qkv, meta, io->k_ring, io->v_ring, io->table, io->rope, &kv, &aa, io->blocks, io->n_blocks,
+                      io->vis, attn, NULL);
+      if (convs) {
+        draft_mm(&L->o, rows, attn, co, SV_EPI_RAW, 0, 0.0f, NULL, NULL);
+        CONV(1, co, x, mixed);
+        CONV(2, mixed, NULL, cx);
+        draft_mm(&L->gate_up, rows, cx, act, SV_EPI_SWIGLU, 0, 0.0f, NULL, NULL);
+        draft_mm(&L->down, rows, act, co, SV_EPI_RAW, 0, 0.0f, NULL, NULL);
+        CONV(3, co, mixed, x);
+      } else {
+        draft_mm(&L->o, rows, attn, mixed, SV_EPI_RESID, 0, 1.0f, x, NULL);
+        draft_mm(&L->gate_up, rows, mixed, act, SV_EPI_SWIGLU, 0, 0.0f, NULL, NULL);
+        draft_mm(&L->down, rows, act, x, SV_EPI_RESID, 0, 1.0f, mixed, NULL);
+      }
+#undef CONV
+    }
+    /* 3. tree */
+    for (uint32_t r = 0; r < rows; r++) iota[r] = r;
+    orc_rmsnorm_rows(x, iota, hfin, rows, H);
+    draft_mm(&d->head, rows, hfin, io->logits, SV_EPI_RAW, 0, 0.0f, NULL, NULL);
+    uint32_t max_run = 1;
+    for (uint32_t b = 0; b < io->n_blocks; b++) max_run = io->blocks[2 * b + 1] > max_run ? io->blocks[2 * b + 1] : max_run;
+    const uint32_t ncand = max_run - 1 < SV_DRAFT_CANDS ? max_run - 1 : SV_DRAFT_CANDS;
+    if (ncand) {
+      orc_draft_top(io->logits, d->vocab, io->tin, cand, cand_q, rows, d->v, d->inv_temperature, ncand);
+      orc_draft_tree(io->blocks, io->n_blocks, io->tin, cand, cand_q, io->feed, io->tree, ncand);
+    }
+  }
+  free(ctx); free(tmp); free(ctx_inv); free(kvp); free(x); free(last); free(cx); free(co); free(mixed); free(qkv);
+  free(inv); free(attn); free(act); free(corr); free(corr_inv); free(hfin); free(meta); free(tokens); free(iota);
+  free(cand); free(cand_q);
   return 0;
 }
 

@@ -123,10 +123,50 @@ typedef struct orc_step_io {
   const uint32_t* local_table;
   sv_kv_args kv_local;
   const sv_matrix* head; /* its own head (model.rs:93-95, host), NULL: the tied embedding */
+  /* the drafter's taps (encode.rs:186-190): tap_out[k] [n][H] from layer tap_layers[k] */
+  uint32_t n_taps;
+  const uint32_t* tap_layers;
+  float* const* tap_out;
 } orc_step_io;
 
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,
              orc_step_io* io);
+
+/* The drafter (drafter.rs:278-447, kernels.metal:135-148, 1725-1934); host pointers. */
+void orc_tap_rows(const float* in, float* out, uint32_t n, uint32_t hidden);
+void orc_draft_kv(const sv_shape* sh, const float* kvp, const uint32_t* meta, const uint32_t* on_path,
+                  const float* rope, uint16_t* k_ring, uint16_t* v_ring, const uint32_t* table, const sv_kv_args* kv,
+                  uint32_t n, uint32_t n_layers);
+void orc_draft_ctx(const float* ctx, const float* ctx_inv, const uint32_t* meta, const uint32_t* on_path, float* ring,
+                   uint32_t cr, uint32_t n, uint32_t hidden);
+void orc_draft_embed(const uint16_t* table, const uint32_t* tin, const uint32_t* lens, const uint32_t* feed,
+                     const float* mask_emb, float* x, uint32_t* meta, uint32_t* tokens, const float* ring, float* last,
+                     uint32_t cr, uint32_t rows, uint32_t hidden);
+void orc_draft_conv(const float* x, const float* corr, uint32_t corr_w, const float* base, const uint32_t* tin,
+                    const float* resid, float* out, uint32_t rows, uint32_t hidden);
+typedef struct orc_draft_io {
+  /* the step's tokens: their taps [n_taps][n][H], meta (slot, position), on_path */
+  uint32_t n;
+  const float* const* taps;
+  const uint32_t* meta;
+  const uint32_t* on_path;
+  const float* rope;
+  /* rings (cyclic page table, kv: is_global 0, window) and the context ring [slots][cr][H] */
+  uint16_t* k_ring, *v_ring;
+  const uint32_t* table;
+  sv_kv_args kv;
+  float* ctx_ring;
+  uint32_t cr;
+  /* blocks: (first row, rows) each, rows' (slot, i) and visibility; state after accept */
+  uint32_t n_blocks, rows;
+  const uint32_t* blocks, *tin, *vis;
+  const uint32_t* lens;
+  uint32_t* feed, *tree;
+  /* outputs: raw logits [rows][v]; the context [n][H] (may be NULL) */
+  float* logits;
+  float* ctx;
+} orc_draft_io;
+int orc_draft(const sv_shape* sh, const uint16_t* embed, const sv_drafter* d, float attn_scale, orc_draft_io* io);
 
 #ifdef __cplusplus
 }

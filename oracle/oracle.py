@@ -41,6 +41,7 @@ def lib() -> C.CDLL:
         L.orc_pool_reserve.restype = C.c_int
         L.orc_plan.restype = C.c_int
         L.orc_step.restype = C.c_int
+        L.orc_draft.restype = C.c_int
         _lib = L
     return _lib
 
@@ -246,7 +247,32 @@ class StepIO(C.Structure):
                 ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
                 ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp),
                 ("n_attn", u32), ("extras", vp), ("local", vp), ("k_local", vp), ("v_local", vp), ("local_table", vp),
-                ("kv_local", C.c_uint32 * 8), ("head", vp)]
+                ("kv_local", C.c_uint32 * 8), ("head", vp), ("n_taps", u32), ("tap_layers", vp), ("tap_out", vp)]
+
+
+class DraftIO(C.Structure):
+    _fields_ = [("n", u32), ("taps", vp), ("meta", vp), ("on_path", vp), ("rope", vp), ("k_ring", vp), ("v_ring", vp),
+                ("table", vp), ("kv", C.c_uint32 * 8), ("ctx_ring", vp), ("cr", u32), ("n_blocks", u32), ("rows", u32),
+                ("blocks", vp), ("tin", vp), ("vis", vp), ("lens", vp), ("feed", vp), ("tree", vp), ("logits", vp),
+                ("ctx", vp)]
+
+
+def host_drafter(drafter):
+    """(sv_drafter over host copies, the arrays it points into) of a SyntheticDrafter."""
+    import torch
+
+    keep = []
+
+    def hp(t):
+        if t.dtype == torch.bfloat16:
+            a = t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+        else:
+            a = t.detach().cpu().contiguous().numpy()
+        a = np.ascontiguousarray(a)
+        keep.append(a)
+        return a.ctypes.data
+
+    return drafter.c(hp), keep
 
 
 def _chain(row: int) -> int:
@@ -332,6 +358,64 @@ class OracleEngine:
             gshift = 31 if scl.shape[1] == 1 else int(k // scl.shape[1]).bit_length() - 1
             self._head = L.Matrix(q.ctypes.data, scl.ctypes.data, m, k, 1, gshift)
 
+    # the drafter
+    def set_drafter(self, drafter, max_step_tokens=64) -> None:
+        """A SyntheticDrafter: its rings laid out as the engine's (cyclic pages of the window plus
+        a step's or a block's rows), the context ring with inject."""
+        self.dr = drafter
+        self._dc, self._dkeep = host_drafter(drafter)
+        s, page = self.shape, 1 << self.page_shift
+        span = drafter.window + max(max_step_tokens, self.arun)
+        self.d_ring_pages = -(-span // page)
+        self.d_n_pages = self.max_seqs * self.d_ring_pages
+        self.d_max_pages = -(-(self.max_seq_len + self.arun) // page)
+        self.dk = np.zeros((drafter.n_layers, self.d_n_pages, s.n_kv_heads, page, s.head_dim), np.uint16)
+        self.dv = np.zeros_like(self.dk)
+        self.d_table = np.array([[slot * self.d_ring_pages + p % self.d_ring_pages for p in range(self.d_max_pages)]
+                                 for slot in range(self.max_seqs)], np.uint32)
+        self.d_cr = max_step_tokens if drafter.inject else 0
+        self.d_cring = np.zeros((self.max_seqs, max(1, self.d_cr), s.hidden), np.float32)
+        self.draft_rows = [0] * self.max_seqs
+
+    def _draft(self, runs, n, meta, on_path, taps, blocks_on):
+        """drafter.rs:278-447 after orc_step: the context of the step's n tokens; with blocks_on,
+        a block per run that draws and whose slot has draft rows."""
+        d, H = self.dr, self.shape.hidden
+        blocks, tin, vis = [], [], []
+        if blocks_on:
+            for r in runs:
+                rows = self.draft_rows[r[0]]
+                head = r[3] if len(r) > 3 else 1
+                if rows == 0 or not (r[2] or head):
+                    continue
+                blocks += [len(vis), rows]
+                for i in range(rows):
+                    tin += [r[0], i]
+                    vis.append((1 << rows) - 1)
+        rows = len(vis)
+        blocks = np.array(blocks or [0], np.uint32)
+        tin = np.array(tin or [0, 0], np.uint32)
+        vis = np.array(vis or [0], np.uint32)
+        logits = np.zeros((max(1, rows), d.v), np.float32)
+        ctx = np.zeros((max(1, n), H), np.float32)
+        tap_arr = [np.ascontiguousarray(t, np.float32) for t in taps]
+        tap_ptrs = (vp * len(tap_arr))(*[t.ctypes.data for t in tap_arr])
+        io = DraftIO()
+        io.n, io.taps, io.meta, io.on_path, io.rope = n, C.cast(tap_ptrs, vp), ptr(meta), ptr(on_path), ptr(self.rope)
+        io.k_ring, io.v_ring, io.table = ptr(self.dk), ptr(self.dv), ptr(self.d_table)
+        io.kv[:] = [0, 0, self.d_ring_pages << self.page_shift, self.max_seqs, self.page_shift, self.d_n_pages,
+                    self.d_max_pages, d.window]
+        io.ctx_ring, io.cr = ptr(self.d_cring), self.d_cr
+        io.n_blocks, io.rows = len(blocks) // 2 if rows else 0, rows
+        io.blocks, io.tin, io.vis = ptr(blocks), ptr(tin), ptr(vis)
+        io.lens, io.feed, io.tree = ptr(self.lens), ptr(self.feed), ptr(self.tree)
+        io.logits, io.ctx = ptr(logits), ptr(ctx)
+        sh = self.shape.c()
+        rc = lib().orc_draft(C.byref(sh), ptr(self.embed), C.byref(self._dc), f32(self.attn_scale), C.byref(io))
+        assert rc == 0
+        return dict(draft_logits=logits[:rows], ctx=ctx[:n], blocks=blocks[: 2 * io.n_blocks].reshape(-1, 2),
+                    draft_tin=tin[: 2 * rows].reshape(-1, 2))
+
     # sequences
     def new_seq(self) -> int:
         slot = self.used.index(False)
@@ -362,8 +446,10 @@ class OracleEngine:
         assert self.pool.reserve(slot, self.seq_len[slot])
         self.lens[slot] = self.seq_len[slot]
 
-    def step(self, runs, compact=None, want_hidden=False):
-        """runs: (slot, tokens, verify[, head]). Returns (ids, logits, emitted, extra)."""
+    def step(self, runs, compact=None, want_hidden=False, draft=False, taps=None):
+        """runs: (slot, tokens, verify[, head]). Returns (ids, logits, emitted, extra). With a
+        drafter set: its context pass, and with draft=True its blocks; `taps` replaces the
+        oracle's own tapped rows as the drafter's input (to check the drafter alone)."""
         L = self.L
         n_runs = len(runs)
         in_runs = np.zeros((n_runs, 4), np.uint32)
@@ -422,15 +508,25 @@ class OracleEngine:
         io.k_local, io.v_local, io.local_table = ptr(self.k_local), ptr(self.v_local), ptr(self.local_table)
         io.kv_local[:] = [0, 0, self.ring_pages * page_of(self.page_shift), self.max_seqs, self.page_shift,
                           max(1, self.n_lpages), self.max_pages, self.window]
+        dr = getattr(self, "dr", None)
+        tap_out = [np.zeros((n, self.shape.hidden), np.float32) for _ in (dr.taps if dr else ())]
+        if dr is not None:
+            tl = np.array(dr.taps, np.uint32)
+            tp = (vp * len(tap_out))(*[t.ctypes.data for t in tap_out])
+            io.n_taps, io.tap_layers, io.tap_out = len(tap_out), ptr(tl), C.cast(tp, vp)
         sh = self.shape.c()
         rc = lib().orc_step(C.byref(sh), ptr(self.embed), self.layers, f32(self.attn_scale), C.byref(io))
         assert rc == 0
+        dx = {}
+        if dr is not None:
+            dx = self._draft(runs, n, meta, on_path, tap_out if taps is None else taps, draft)
+            dx["taps"] = tap_out
         for i, r in enumerate(runs):
             self.seq_len[r[0]] += len(r[1])
             if r[2]:
                 self.seq_len[r[0]] -= len(r[1]) - min(int(emitted[i]), len(r[1]))
         extra = dict(tokens=tokens, meta=meta.reshape(n, 2), vis=vis, path=path.reshape(n_runs, 16),
-                     path_len=path_len, on_path=on_path, hidden=hidden, head_rows=head_rows[:n_head])
+                     path_len=path_len, on_path=on_path, hidden=hidden, head_rows=head_rows[:n_head], **dx)
         return out[:n_head].copy(), logits[:n_head].copy(), emitted, extra
 
 

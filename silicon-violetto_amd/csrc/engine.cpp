@@ -144,6 +144,36 @@ extern "C" sv_status sv_draft_tree(void* stream, const uint32_t* d_blocks, uint3
   return draft_tree_launch((hipStream_t)stream, d_blocks, nblocks, d_tin, d_cand, d_cand_q, d_feed, d_tree, ncand);
 }
 
+extern "C" sv_status sv_tap_rows(void* stream, const float* d_in, float* d_out, uint32_t n, uint32_t hidden) {
+  return tap_rows_launch((hipStream_t)stream, d_in, d_out, n, hidden);
+}
+
+extern "C" sv_status sv_draft_kv(void* stream, const sv_shape* shape, const float* d_kvp, const uint32_t* d_meta,
+                                 const uint32_t* d_on_path, const float* d_rope, uint16_t* d_k_ring, uint16_t* d_v_ring,
+                                 const uint32_t* d_page_table, const sv_kv_args* kv, uint32_t n, uint32_t n_layers) {
+  return draft_kv_launch((hipStream_t)stream, shape, d_kvp, d_meta, d_on_path, d_rope, d_k_ring, d_v_ring, d_page_table,
+                         kv, n, n_layers);
+}
+
+extern "C" sv_status sv_draft_ctx(void* stream, const float* d_ctx, const float* d_ctx_inv, const uint32_t* d_meta,
+                                  const uint32_t* d_on_path, float* d_ring, uint32_t cr, uint32_t n, uint32_t hidden) {
+  return draft_ctx_launch((hipStream_t)stream, d_ctx, d_ctx_inv, d_meta, d_on_path, d_ring, cr, n, hidden);
+}
+
+extern "C" sv_status sv_draft_embed(void* stream, const uint16_t* d_embed, const uint32_t* d_tin, const uint32_t* d_lens,
+                                    const uint32_t* d_feed, const float* d_mask_emb, float* d_x, uint32_t* d_meta,
+                                    uint32_t* d_tokens, const float* d_ring, float* d_last, uint32_t cr, uint32_t rows,
+                                    uint32_t hidden) {
+  return draft_embed_launch((hipStream_t)stream, d_embed, d_tin, d_lens, d_feed, d_mask_emb, d_x, d_meta, d_tokens, d_ring,
+                            d_last, cr, rows, hidden);
+}
+
+extern "C" sv_status sv_draft_conv(void* stream, const float* d_x, const float* d_corr, uint32_t corr_w,
+                                   const float* d_base, const uint32_t* d_tin, const float* d_resid, float* d_out,
+                                   uint32_t rows, uint32_t hidden) {
+  return draft_conv_launch((hipStream_t)stream, d_x, d_corr, corr_w, d_base, d_tin, d_resid, d_out, rows, hidden);
+}
+
 extern "C" sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns, const uint32_t* d_lens,
                                      uint32_t* d_feed, const uint32_t* d_trace, const uint32_t* d_trace_len,
                                      const sv_replay_args* ra, uint32_t* d_tree) {
@@ -204,6 +234,10 @@ struct Plan {
   std::vector<uint32_t> counts;  // per run
   std::vector<uint32_t> verify;  // per run
   std::vector<uint32_t> inl;     // per attention run: first token, rows, slot (inline in the launch)
+  // The drafter's blocks after the step (drafter.rs DraftRun): count, rows, longest, splits,
+  // and per block (first row, rows, slot).
+  uint32_t n_blocks = 0, d_rows = 0, d_max_run = 0, d_split = 0, d_max_splits = 0;
+  std::vector<uint32_t> dinl;
   // Steps this plan may run (encodes, graph replays, profiled steps): each advances a run by at
   // most its row count, and every position it can reach has a reserved page.
   uint64_t budget = 0, issued = 0;
@@ -250,6 +284,42 @@ struct sv_engine {
   float* xattn = nullptr;           // MUDD's attention input
   float* rbase = nullptr;           // MUDD's residual base
   float* vdir = nullptr;            // XSA directions [n][NKV][D]
+  // The drafter (drafter.rs): its matrices, the target's tapped rows, its rings (as the local
+  // layers': pages behind a cyclic table) and its block rows' buffers.
+  bool has_drafter = false;
+  sv_drafter dr{};
+  std::vector<sv_draft_layer> dlayers;
+  float* tapbuf[SV_DRAFT_TAPS] = {};
+  uint16_t* dk_ring = nullptr;
+  uint16_t* dv_ring = nullptr;
+  uint32_t* d_table = nullptr;
+  uint32_t d_ring_pages = 0, d_n_pages = 0, d_max_pages = 0, d_cr = 0, d_rows_max = 0, d_corr_w = 0;
+  float *d_ctx = nullptr, *d_ctx_inv = nullptr, *d_kvp = nullptr, *d_cring = nullptr, *d_last = nullptr,
+        *d_x = nullptr, *d_qkv = nullptr, *d_inv = nullptr, *d_attn = nullptr, *d_mixed = nullptr, *d_act = nullptr,
+        *d_cx = nullptr, *d_co = nullptr, *d_corr = nullptr, *d_corr_inv = nullptr, *d_logits = nullptr,
+        *d_cand_q = nullptr;
+  uint32_t *d_cand = nullptr, *d_meta = nullptr, *d_tokens = nullptr, *d_tin = nullptr, *d_vis = nullptr,
+           *d_tiles = nullptr;
+  std::vector<uint32_t> draft_rows;  // per slot: rows of its blocks (0: not drafted)
+  std::vector<void*> d_packed;       // engine-owned tiled copies of the drafter's matrices
+  sv_matrix d_head_lo{};             // with a head in small int8 groups: its lo part (d_w NULL: none)
+  void free_drafter() {
+    for (void* b : d_packed)
+      if (b) (void)hipFree(b);
+    d_packed.clear();
+    d_head_lo = sv_matrix{};
+    void* bufs[] = {dk_ring, dv_ring, d_table, d_ctx, d_ctx_inv, d_kvp, d_cring, d_last, d_x, d_qkv, d_inv, d_attn,
+                    d_mixed, d_act, d_cx, d_co, d_corr, d_corr_inv, d_logits, d_cand_q, d_cand, d_meta, d_tokens,
+                    d_tin, d_vis, d_tiles, tapbuf[0], tapbuf[1], tapbuf[2], tapbuf[3]};
+    for (void* b : bufs)
+      if (b) (void)hipFree(b);
+    dk_ring = dv_ring = nullptr;
+    d_table = d_cand = d_meta = d_tokens = d_tin = d_vis = d_tiles = nullptr;
+    d_ctx = d_ctx_inv = d_kvp = d_cring = d_last = d_x = d_qkv = d_inv = d_attn = d_mixed = d_act = d_cx = d_co =
+        d_corr = d_corr_inv = d_logits = d_cand_q = nullptr;
+    for (auto& t : tapbuf) t = nullptr;
+    has_drafter = false;
+  }
 
   // device: KV and sequence state
   uint16_t* k_cache = nullptr;
@@ -335,6 +405,7 @@ struct sv_engine {
     if (head_tiled) (void)hipFree(head_tiled);
     if (tap[0]) (void)hipFree(tap[0]);
     if (tap[1] && tap[1] != tap[0]) (void)hipFree(tap[1]);
+    free_drafter();
     if (stream) (void)hipStreamDestroy(stream);
   }
 
@@ -498,6 +569,9 @@ struct sv_engine {
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
       SV_TIMED(SV_KIND_DOWN,
                matmul(L.down, n, act, nullptr, hout, SV_EPI_RESID, 0, 1.0f, L.resid_mlp, L.post_mlp, mixed, nullptr));
+      // the drafter's taps (encode.rs:186-190): this layer's output, normed, rounded to bf16
+      for (uint32_t k = 0; has_drafter && k < dr.n_taps; k++)
+        if (dr.taps[k] == li) SV_TIMED(SV_KIND_DRAFT, tap_rows_launch(stream, hout, tapbuf[k], n, H));
     }
     (void)F;
     (void)NQD;
@@ -518,6 +592,100 @@ struct sv_engine {
                                               tree, path, path_len, on_path, compact, caches, n_local ? 2u : 1u,
                                               cfg.page_shift, max_pages, (flags & SV_STEP_REPLAY) ? &ra : nullptr,
                                               trace, trace_len));
+    if (has_drafter) SV_TRY(encode_draft((flags & SV_STEP_DRAFT) != 0));
+    return SV_OK;
+  }
+
+  sv_kv_args draft_kv_args(uint32_t layer) const {
+    sv_kv_args kv{};
+    kv.is_global = 0;
+    kv.kv_layer = layer;
+    kv.ring = d_ring_pages << cfg.page_shift;
+    kv.max_seqs = cfg.max_seqs;
+    kv.page_shift = cfg.page_shift;
+    kv.n_pages = d_n_pages;
+    kv.max_pages = d_max_pages;
+    kv.window = dr.window;
+    return kv;
+  }
+
+  // drafter.rs:302-447 encode_drafter: the context of every token of the step, then the plan's
+  // blocks through the drafter's layers, its head, draft_top and draft_tree (which write the
+  // slots' next feed and tree).
+  sv_status encode_draft(bool blocks) {
+    const Plan& P = plan;
+    const uint32_t n = P.n, H = sh.hidden, rows = P.d_rows;
+    // 1. Context: sum over the taps of fc[k] tap_k, then every drafter layer's k | v of its norm.
+    for (uint32_t k = 0; k < dr.n_taps; k++)
+      SV_TIMED(SV_KIND_DRAFT, matmul(dr.fc[k], n, tapbuf[k], nullptr, d_ctx, k ? SV_EPI_RESID : SV_EPI_RAW, 0, 1.0f,
+                                     1.0f, 1.0f, d_ctx, nullptr));
+    SV_TIMED(SV_KIND_DRAFT,
+             matmul(dr.kv_all, n, d_ctx, nullptr, d_kvp, SV_EPI_NORM, SV_FLAG_WRITE_INV, 1.0f, 0, 0, nullptr, d_ctx_inv));
+    const sv_kv_args kv0 = draft_kv_args(0);
+    SV_TIMED(SV_KIND_DRAFT, draft_kv_launch(stream, &sh, d_kvp, meta, on_path, rope, dk_ring, dv_ring, d_table, &kv0, n,
+                                            dr.n_layers));
+    const bool inject = dr.inject.d_w != nullptr;
+    if (inject)
+      SV_TIMED(SV_KIND_DRAFT, draft_ctx_launch(stream, d_ctx, d_ctx_inv, meta, on_path, d_cring, d_cr, n, H));
+    if (!blocks || P.n_blocks == 0) return SV_OK;
+    // 2. Block rows.
+    SV_TIMED(SV_KIND_DRAFT, draft_embed_launch(stream, embed, d_tin, lens, feed, dr.mask_emb, d_x, d_meta, d_tokens,
+                                               d_cring, d_last, inject ? d_cr : 0u, rows, H));
+    if (inject)
+      SV_TIMED(SV_KIND_DRAFT, matmul(dr.inject, rows, d_last, nullptr, d_x, SV_EPI_RESID, 0, 1.0f, 1.0f, 1.0f, d_x, nullptr));
+    auto conv = [&](uint32_t li, int c, const float* x, const float* resid, float* out) -> sv_status {
+      const sv_draft_layer& Ld = dlayers[li];
+      SV_TIMED(SV_KIND_DRAFT, matmul(Ld.conv_corr[c], rows, x, nullptr, d_corr, SV_EPI_NORM, SV_FLAG_WRITE_INV, 1.0f, 0,
+                                     0, nullptr, d_corr_inv));
+      SV_TIMED(SV_KIND_DRAFT, draft_conv_launch(stream, x, d_corr, Ld.conv_corr[c].m, Ld.conv_base[c], d_tin, resid,
+                                                out, rows, H));
+      return SV_OK;
+    };
+    sv_attn_args aa{};
+    aa.split = P.d_split;
+    aa.max_splits = P.d_max_splits;
+    aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
+    aa.rope = 1;
+    for (uint32_t li = 0; li < dr.n_layers; li++) {
+      const sv_draft_layer& Ld = dlayers[li];
+      const bool convs = Ld.conv_base[0] != nullptr;
+      const float* xin = d_x;
+      if (convs) {
+        SV_TRY(conv(li, 0, d_x, nullptr, d_cx));
+        xin = d_cx;
+      }
+      SV_TIMED(SV_KIND_DRAFT,
+               matmul(Ld.qkv, rows, xin, nullptr, d_qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, 1.0f, 0, 0, nullptr, d_inv));
+      const sv_kv_args kv = draft_kv_args(li);
+      SV_TIMED(SV_KIND_DRAFT, attn_launch(stream, &sh, d_qkv, d_meta, dk_ring, dv_ring, d_table, rope, &kv, &aa, d_tiles,
+                                          P.n_blocks, P.d_max_run, d_vis, d_attn, ws, ws_bytes, 1, P.dinl.data()));
+      SV_TIMED(SV_KIND_DRAFT, attn_launch(stream, &sh, d_qkv, d_meta, dk_ring, dv_ring, d_table, rope, &kv, &aa, d_tiles,
+                                          P.n_blocks, P.d_max_run, d_vis, d_attn, ws, ws_bytes, 2, P.dinl.data()));
+      if (convs) {
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.o, rows, d_attn, nullptr, d_co, SV_EPI_RAW, 0, 1.0f, 0, 0, nullptr, nullptr));
+        SV_TRY(conv(li, 1, d_co, d_x, d_mixed));
+        SV_TRY(conv(li, 2, d_mixed, nullptr, d_cx));
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.gate_up, rows, d_cx, nullptr, d_act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.down, rows, d_act, nullptr, d_co, SV_EPI_RAW, 0, 1.0f, 0, 0, nullptr, nullptr));
+        SV_TRY(conv(li, 3, d_co, d_mixed, d_x));
+      } else {
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.o, rows, d_attn, nullptr, d_mixed, SV_EPI_RESID, 0, 1.0f, 1.0f, 1.0f, d_x, nullptr));
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.gate_up, rows, d_mixed, nullptr, d_act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
+        SV_TIMED(SV_KIND_DRAFT, matmul(Ld.down, rows, d_act, nullptr, d_x, SV_EPI_RESID, 0, 1.0f, 1.0f, 1.0f, d_mixed, nullptr));
+      }
+    }
+    // 3. The tree: raw logits of the normed rows (the norm folded into the head), candidates,
+    // best-first trees into the slots' feed and tree.
+    SV_TIMED(SV_KIND_DRAFT,
+             matmul(dr.head, rows, d_x, nullptr, d_logits, SV_EPI_RAW, SV_FLAG_NORM_IN, 1.0f, 0, 0, nullptr, nullptr));
+    if (d_head_lo.d_w)
+      SV_TIMED(SV_KIND_DRAFT, matmul(d_head_lo, rows, d_x, nullptr, d_logits, SV_EPI_RESID, SV_FLAG_NORM_IN, 1.0f, 1.0f,
+                                     1.0f, d_logits, nullptr));
+    const uint32_t ncand = std::min(SV_DRAFT_CANDS, P.d_max_run - 1);
+    if (ncand == 0) return SV_OK;  // blocks of one row: nothing to draft
+    SV_TIMED(SV_KIND_DRAFT, draft_top_launch(stream, d_logits, dr.vocab, d_tin, d_cand, d_cand_q, rows, dr.v,
+                                             dr.inv_temperature, ncand));
+    SV_TIMED(SV_KIND_DRAFT, draft_tree_launch(stream, d_tiles, P.n_blocks, d_tin, d_cand, d_cand_q, feed, tree, ncand));
     return SV_OK;
   }
 };
@@ -836,6 +1004,167 @@ extern "C" sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* o) {
   return SV_OK;
 }
 
+// drafter.rs:145-241 Drafter::load + :250-255 load_drafter: the matrices checked and tiled,
+// the rings (cyclic pages, as the sliding-window layers'), the block rows' buffers.
+extern "C" sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d) {
+  if (!e || !d) return fail(SV_ERR_ARG, "set_drafter: null pointer");
+  if (e->graph) return fail(SV_ERR_STATE, "set_drafter: after a graph was captured");
+  const sv_shape& s = e->sh;
+  const uint32_t H = s.hidden, NKV = s.n_kv_heads, D = s.head_dim;
+  if (d->n_layers == 0 || d->n_layers > SV_DRAFT_LAYERS || !d->layers)
+    return fail(SV_ERR_ARG, "set_drafter: %u layers (1..%u)", d->n_layers, SV_DRAFT_LAYERS);
+  if (d->n_taps == 0 || d->n_taps > SV_DRAFT_TAPS) return fail(SV_ERR_ARG, "set_drafter: %u taps (1..%u)", d->n_taps, SV_DRAFT_TAPS);
+  for (uint32_t k = 0; k < d->n_taps; k++)
+    if (d->taps[k] >= s.n_layers) return fail(SV_ERR_ARG, "set_drafter: tap %u at layer %u of %u", k, d->taps[k], s.n_layers);
+  if (d->v < SV_DRAFT_CANDS || !d->vocab || !d->mask_emb) return fail(SV_ERR_ARG, "set_drafter: vocabulary of %u, or no ids / mask_emb", d->v);
+  if (d->window == 0) return fail(SV_ERR_ARG, "set_drafter: window 0");
+  if (!(d->inv_temperature > 0.0f) || !std::isfinite(d->inv_temperature))
+    return fail(SV_ERR_ARG, "set_drafter: inverse temperature %g", d->inv_temperature);
+  if (!e->embed) return fail(SV_ERR_STATE, "set_drafter: no embedding set (sv_engine_set_embed)");
+  if (NKV * D / 4 > 256 || D % 4) return fail(SV_ERR_UNSUPPORTED, "set_drafter: %u kv heads x %u dims", NKV, D);
+  SV_HIP(hipStreamSynchronize(e->stream), "set_drafter");
+  e->free_drafter();
+  sv_drafter dr = *d;
+  std::vector<sv_draft_layer> dl(d->layers, d->layers + d->n_layers);
+  auto take = [&](sv_matrix& m, uint32_t rows, uint32_t cols, const char* name) -> sv_status {
+    SV_TRY(check_matrix(m, rows, cols, name));
+    const bool per_row = m.gshift >= 32 || (1ull << m.gshift) >= m.k;
+    if ((m.format & ~(uint32_t)SV_FMT_TILED) == SV_FMT_I8 && !per_row && m.gshift < 6)
+      return fail(SV_ERR_UNSUPPORTED, "set_drafter: %s in int8 groups of %u (64 or more, or one per row, are built)", name,
+                  1u << m.gshift);
+    e->d_packed.push_back(nullptr);
+    return pack_into(e, m, &e->d_packed.back(), &m);
+  };
+  sv_status st = SV_OK;
+  auto run = [&]() -> sv_status {
+    for (uint32_t k = 0; k < d->n_taps; k++) SV_TRY(take(dr.fc[k], H, H, "drafter fc"));
+    SV_TRY(take(dr.kv_all, d->n_layers * 2 * NKV * D, H, "drafter kv_all"));
+    if (dr.inject.d_w) SV_TRY(take(dr.inject, H, H, "drafter inject"));
+    // A head in int8 groups under 64 (export.py writes groups of 8) runs as the exact sum of
+    // two bf16 matrices, hi + lo.
+    const bool head_split = (dr.head.format & ~(uint32_t)SV_FMT_TILED) == SV_FMT_I8 && dr.head.gshift < 6 &&
+                            (1ull << dr.head.gshift) < dr.head.k;
+    if (head_split) {
+      SV_TRY(check_matrix(dr.head, d->v, H, "drafter head"));
+      if (dr.head.format & SV_FMT_TILED) return fail(SV_ERR_UNSUPPORTED, "set_drafter: a tiled head in groups under 64");
+      uint16_t *hi = nullptr, *lo = nullptr;
+      SV_TRY(dalloc(&hi, (size_t)d->v * H, "drafter head"));
+      e->d_packed.push_back(hi);
+      SV_TRY(dalloc(&lo, (size_t)d->v * H, "drafter head"));
+      e->d_packed.push_back(lo);
+      SV_TRY(split_i8_launch(e->stream, &dr.head, hi, lo));
+      SV_HIP(hipStreamSynchronize(e->stream), "drafter head");
+      dr.head = sv_matrix{hi, nullptr, d->v, H, SV_FMT_BF16, 0};
+      e->d_head_lo = sv_matrix{lo, nullptr, d->v, H, SV_FMT_BF16, 0};
+      SV_TRY(take(e->d_head_lo, d->v, H, "drafter head"));
+    }
+    SV_TRY(take(dr.head, d->v, H, "drafter head"));
+    uint32_t corr_w = 0;
+    for (uint32_t i = 0; i < d->n_layers; i++) {
+      sv_draft_layer& L = dl[i];
+      SV_TRY(take(L.qkv, e->qkv_w, H, "drafter qkv"));
+      SV_TRY(take(L.o, H, s.n_heads * D, "drafter o"));
+      SV_TRY(take(L.gate_up, 2 * s.ffn, H, "drafter gate_up"));
+      SV_TRY(take(L.down, H, s.ffn, "drafter down"));
+      const bool convs = L.conv_base[0] != nullptr;
+      for (int c = 0; c < 4; c++) {
+        if (!convs) continue;
+        if (!L.conv_base[c]) return fail(SV_ERR_ARG, "set_drafter: layer %u has conv 0 but no conv %d", i, c);
+        const uint32_t w = L.conv_corr[c].m;
+        if (H % 16 || w < H / 8 || (corr_w && w != corr_w))
+          return fail(SV_ERR_ARG, "set_drafter: conv corrections of %u rows for hidden %u", w, H);
+        corr_w = w;
+        SV_TRY(take(L.conv_corr[c], w, H, "drafter conv corr"));
+      }
+    }
+    e->d_corr_w = corr_w;
+    // Rings: every key a block row sees (the window before it) plus a step's or a block's new
+    // positions, in whole pages.
+    const uint32_t page = 1u << e->cfg.page_shift;
+    const uint32_t span = d->window + std::max(e->cfg.max_step_tokens, e->arun);
+    e->d_ring_pages = (span + page - 1) / page;
+    e->d_n_pages = e->cfg.max_seqs * e->d_ring_pages;
+    e->d_max_pages = (e->cfg.max_seq_len + e->arun + page - 1) / page;
+    const size_t ring = (size_t)d->n_layers * e->d_n_pages * NKV * page * D;
+    const size_t T = e->cfg.max_step_tokens, R = (size_t)e->cfg.max_seqs * e->arun, S = e->cfg.max_seqs;
+    e->d_rows_max = (uint32_t)R;
+    e->d_cr = dr.inject.d_w ? e->cfg.max_step_tokens : 0u;
+    SV_TRY(dalloc(&e->dk_ring, ring, "drafter rings"));
+    SV_TRY(dalloc(&e->dv_ring, ring, "drafter rings"));
+    SV_TRY(dalloc(&e->d_table, S * e->d_max_pages, "drafter table"));
+    for (uint32_t k = 0; k < d->n_taps; k++) SV_TRY(dalloc(&e->tapbuf[k], T * H, "drafter taps"));
+    SV_TRY(dalloc(&e->d_ctx, T * H, "drafter context"));
+    SV_TRY(dalloc(&e->d_ctx_inv, T, "drafter context"));
+    SV_TRY(dalloc(&e->d_kvp, T * d->n_layers * 2 * NKV * D, "drafter context"));
+    if (e->d_cr) SV_TRY(dalloc(&e->d_cring, S * e->d_cr * H, "drafter context ring"));
+    SV_TRY(dalloc(&e->d_last, R * H, "drafter rows"));
+    SV_TRY(dalloc(&e->d_x, R * H, "drafter rows"));
+    SV_TRY(dalloc(&e->d_qkv, R * e->qkv_w, "drafter rows"));
+    SV_TRY(dalloc(&e->d_inv, R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_attn, R * s.n_heads * D, "drafter rows"));
+    SV_TRY(dalloc(&e->d_mixed, R * H, "drafter rows"));
+    SV_TRY(dalloc(&e->d_act, R * s.ffn, "drafter rows"));
+    SV_TRY(dalloc(&e->d_cx, R * H, "drafter rows"));
+    SV_TRY(dalloc(&e->d_co, R * H, "drafter rows"));
+    if (corr_w) SV_TRY(dalloc(&e->d_corr, R * corr_w, "drafter rows"));
+    SV_TRY(dalloc(&e->d_corr_inv, R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_logits, R * d->v, "drafter logits"));
+    SV_TRY(dalloc(&e->d_cand, R * SV_DRAFT_CANDS, "drafter candidates"));
+    SV_TRY(dalloc(&e->d_cand_q, R * SV_DRAFT_CANDS, "drafter candidates"));
+    SV_TRY(dalloc(&e->d_meta, 2 * R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_tokens, R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_tin, 2 * R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_vis, R, "drafter rows"));
+    SV_TRY(dalloc(&e->d_tiles, 2 * S, "drafter rows"));
+    std::vector<uint32_t> tab(S * e->d_max_pages);
+    for (size_t slot = 0; slot < S; slot++)
+      for (uint32_t pg = 0; pg < e->d_max_pages; pg++)
+        tab[slot * e->d_max_pages + pg] = (uint32_t)slot * e->d_ring_pages + pg % e->d_ring_pages;
+    SV_HIP(hipMemcpy(e->d_table, tab.data(), tab.size() * 4, hipMemcpyHostToDevice), "drafter table");
+    // the pools start at zero (a ring position no step has written reads as zeros, not NaN)
+    SV_HIP(hipMemset(e->dk_ring, 0, ring * 2), "drafter rings");
+    SV_HIP(hipMemset(e->dv_ring, 0, ring * 2), "drafter rings");
+    return SV_OK;
+  };
+  if ((st = run()) != SV_OK) {
+    e->free_drafter();
+    return st;
+  }
+  dr.layers = nullptr;
+  e->dr = dr;
+  e->dlayers = std::move(dl);
+  e->draft_rows.assign(e->cfg.max_seqs, 0u);
+  e->has_drafter = true;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_set_draft_rows(sv_engine* e, uint32_t slot, uint32_t rows) {
+  if (!e) return fail(SV_ERR_ARG, "set_draft_rows: null engine");
+  if (!e->has_drafter) return fail(SV_ERR_STATE, "set_draft_rows: no drafter set");
+  if (slot >= e->cfg.max_seqs) return fail(SV_ERR_ARG, "set_draft_rows: slot %u", slot);
+  if (rows > e->arun) return fail(SV_ERR_CAPACITY, "set_draft_rows: %u rows (at most %u)", rows, e->arun);
+  e->draft_rows[slot] = rows;
+  return SV_OK;
+}
+
+extern "C" sv_status sv_engine_draft_buffers(sv_engine* e, sv_draft_buffers* o) {
+  if (!e || !o) return fail(SV_ERR_ARG, "draft_buffers: null pointer");
+  if (!e->has_drafter) return fail(SV_ERR_STATE, "draft_buffers: no drafter set");
+  *o = sv_draft_buffers{};
+  o->d_logits = e->d_logits;
+  o->d_cand = e->d_cand;
+  o->d_cand_q = e->d_cand_q;
+  o->d_ctx = e->d_ctx;
+  for (uint32_t k = 0; k < SV_DRAFT_TAPS; k++) o->d_taps[k] = e->tapbuf[k];
+  o->d_k_ring = e->dk_ring;
+  o->d_v_ring = e->dv_ring;
+  o->d_table = e->d_table;
+  o->ring_pages = e->d_ring_pages;
+  o->n_pages = e->d_n_pages;
+  o->max_pages = e->d_max_pages;
+  return SV_OK;
+}
+
 static sv_status check_slot(sv_engine* e, uint32_t slot) {
   if (!e) return fail(SV_ERR_ARG, "null engine");
   if (slot >= e->cfg.max_seqs || !e->used[slot]) return fail(SV_ERR_STATE, "unknown sequence %u", slot);
@@ -871,6 +1200,7 @@ extern "C" sv_status sv_free_seq(sv_engine* e, uint32_t slot) {
   pg.clear();
   e->used[slot] = false;
   e->seq_len[slot] = 0;
+  if (e->has_drafter) e->draft_rows[slot] = 0;
   return SV_OK;
 }
 
@@ -1069,7 +1399,44 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
                                       : choose_split(lc, 0, e->sh.n_kv_heads, P.max_run, e->sh.n_heads / e->sh.n_kv_heads);
     P.max_splits_local = (max_lc + P.split_local - 1) / P.split_local + 1;
   }
-  SV_TRY(e->ensure_ws(attn_ws_bytes(&e->sh, P.n_attn, std::max(P.max_splits, P.max_splits_local), P.max_run)));
+  // The drafter's blocks (generate.rs:406-411 draft_runs): one per run that draws a token this
+  // step and whose slot has draft rows, its rows all seeing each other (drafter.rs:327-334).
+  std::vector<uint32_t> dtin, dvis, dtiles;
+  if (e->has_drafter) {
+    std::vector<uint32_t> bc;
+    uint32_t max_bc = 0;
+    const uint32_t span = e->dr.window + 31;
+    for (uint32_t ri = 0; ri < n_runs; ri++) {
+      const sv_run& r = runs_in[ri];
+      const uint32_t rows = e->draft_rows[r.slot];
+      if (!rows || !(r.verify || r.head)) continue;
+      const uint32_t first = (uint32_t)dvis.size();
+      dtiles.insert(dtiles.end(), {first, rows});
+      P.dinl.insert(P.dinl.end(), {first, rows, r.slot});
+      for (uint32_t i = 0; i < rows; i++) {
+        dtin.insert(dtin.end(), {r.slot, i});
+        dvis.push_back((1u << rows) - 1u);
+      }
+      P.d_max_run = std::max(P.d_max_run, rows);
+      bc.push_back((uint32_t)std::min<uint64_t>((uint64_t)e->seq_len[r.slot] + extra_keys, span));
+      max_bc = std::max(max_bc, bc.back());
+    }
+    P.n_blocks = (uint32_t)bc.size();
+    P.d_rows = (uint32_t)dvis.size();
+    if (P.n_blocks) {
+      P.d_split = e->cfg.split_keys ? e->cfg.split_keys
+                                    : choose_split(bc, 0, e->sh.n_kv_heads, P.d_max_run, e->sh.n_heads / e->sh.n_kv_heads);
+      P.d_max_splits = (max_bc + P.d_split - 1) / P.d_split + 1;
+    }
+  }
+  size_t need = attn_ws_bytes(&e->sh, P.n_attn, std::max(P.max_splits, P.max_splits_local), P.max_run);
+  if (P.n_blocks) need = std::max(need, attn_ws_bytes(&e->sh, P.n_blocks, P.d_max_splits, P.d_max_run));
+  SV_TRY(e->ensure_ws(need));
+  if (P.n_blocks) {
+    SV_TRY(e->upload(e->d_tin, dtin.data(), dtin.size() * 4));
+    SV_TRY(e->upload(e->d_vis, dvis.data(), dvis.size() * 4));
+    SV_TRY(e->upload(e->d_tiles, dtiles.data(), dtiles.size() * 4));
+  }
   SV_TRY(e->upload(e->tokens, tokens.data(), tokens.size() * 4));
   SV_TRY(e->upload(e->tin, tin.data(), tin.size() * 4));
   SV_TRY(e->upload(e->vis, vis.data(), vis.size() * 4));

@@ -96,6 +96,18 @@ sv_status replay_launch(hipStream_t stream, const sv_run_in* runs, uint32_t nrun
                         uint32_t* feed, const uint32_t* trace, const uint32_t* trace_len, const sv_replay_args* ra,
                         uint32_t* tree);
 
+sv_status tap_rows_launch(hipStream_t stream, const float* in, float* out, uint32_t n, uint32_t hidden);
+sv_status draft_kv_launch(hipStream_t stream, const sv_shape* sh, const float* kvp, const uint32_t* meta,
+                          const uint32_t* on_path, const float* rope, uint16_t* kc, uint16_t* vc, const uint32_t* table,
+                          const sv_kv_args* kv, uint32_t n, uint32_t n_layers);
+sv_status draft_ctx_launch(hipStream_t stream, const float* ctx, const float* ctx_inv, const uint32_t* meta,
+                           const uint32_t* on_path, float* ring, uint32_t cr, uint32_t n, uint32_t hidden);
+sv_status draft_embed_launch(hipStream_t stream, const uint16_t* embed, const uint32_t* tin, const uint32_t* lens,
+                             const uint32_t* feed, const float* mask_emb, float* x, uint32_t* meta, uint32_t* tokens,
+                             const float* ring, float* last, uint32_t cr, uint32_t rows, uint32_t hidden);
+sv_status split_i8_launch(hipStream_t stream, const sv_matrix* w, uint16_t* hi, uint16_t* lo);
+sv_status draft_conv_launch(hipStream_t stream, const float* x, const float* corr, uint32_t corr_w, const float* base,
+                            const uint32_t* tin, const float* resid, float* out, uint32_t rows, uint32_t hidden);
 sv_status mudd_launch(hipStream_t stream, const float* cur, const float* tap0, const float* tap1, const float* dense1,
                       const float* mix, float* out_attn, float* out_base, uint32_t n, uint32_t hidden);
 

@@ -29,14 +29,17 @@ VE_GATE_W = 12
 MUDD_INNER = 32
 MUDD_SITES = 2
 MAX_COLS = 64
+DRAFT_TAPS = 4
+DRAFT_LAYERS = 8
+DRAFT_CANDS = 4
 
 EPI_NORM, EPI_RESID, EPI_SWIGLU, EPI_HEAD, EPI_RAW = 1, 2, 3, 4, 5
 FLAG_WRITE_INV, FLAG_WRITE_RAW, FLAG_NORM_IN = 1, 2, 4
 FMT_BF16, FMT_I8 = 0, 1
 FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
-STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT = 1, 2, 4
+STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT, STEP_DRAFT = 1, 2, 4, 8
 KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "kv_write",
-         "mudd")
+         "mudd", "draft")
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 
@@ -114,6 +117,23 @@ class EngineBuffers(C.Structure):
                                                     ("local_bytes", C.c_size_t)]
 
 
+class DraftLayer(C.Structure):
+    _fields_ = [("qkv", Matrix), ("o", Matrix), ("gate_up", Matrix), ("down", Matrix), ("conv_base", vp * 4),
+                ("conv_corr", Matrix * 4)]
+
+
+class Drafter(C.Structure):
+    _fields_ = [("n_layers", u32), ("n_taps", u32), ("v", u32), ("taps", u32 * DRAFT_TAPS), ("fc", Matrix * DRAFT_TAPS),
+                ("kv_all", Matrix), ("inject", Matrix), ("head", Matrix), ("mask_emb", vp), ("vocab", vp),
+                ("layers", C.POINTER(DraftLayer)), ("inv_temperature", f32), ("window", u32)]
+
+
+class DraftBuffers(C.Structure):
+    _fields_ = [("d_logits", vp), ("d_cand", vp), ("d_cand_q", vp), ("d_ctx", vp), ("d_taps", vp * DRAFT_TAPS),
+                ("d_k_ring", vp), ("d_v_ring", vp), ("d_table", vp), ("ring_pages", u32), ("n_pages", u32),
+                ("max_pages", u32), ("pad", u32)]
+
+
 class Run(C.Structure):
     _fields_ = [("slot", u32), ("count", u32), ("tokens", C.POINTER(u32)), ("verify", u32), ("head", u32)]
 
@@ -148,6 +168,11 @@ PROTOS = {
     "sv_kv_compact": (C.c_int, [vp, P(Shape), vp, u32, vp, vp, vp, vp, vp, vp, P(KvArgs)]),
     "sv_draft_top": (C.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, f32, u32]),
     "sv_draft_tree": (C.c_int, [vp, vp, u32, vp, vp, vp, vp, vp, u32]),
+    "sv_tap_rows": (C.c_int, [vp, vp, vp, u32, u32]),
+    "sv_draft_kv": (C.c_int, [vp, P(Shape), vp, vp, vp, vp, vp, vp, vp, P(KvArgs), u32, u32]),
+    "sv_draft_ctx": (C.c_int, [vp, vp, vp, vp, vp, vp, u32, u32, u32]),
+    "sv_draft_embed": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, u32, u32, u32]),
+    "sv_draft_conv": (C.c_int, [vp, vp, vp, u32, vp, vp, vp, vp, u32, u32]),
     "sv_weights_open": (C.c_int, [C.c_char_p, P(vp)]),
     "sv_weights_count": (u32, [vp]),
     "sv_weights_info": (C.c_int, [vp, u32, P(TensorInfo)]),
@@ -164,6 +189,9 @@ PROTOS = {
     "sv_engine_set_layer": (C.c_int, [vp, u32, P(Layer)]),
     "sv_engine_set_extras": (C.c_int, [vp, P(ModelExtras)]),
     "sv_engine_set_head": (C.c_int, [vp, P(Matrix)]),
+    "sv_engine_set_drafter": (C.c_int, [vp, P(Drafter)]),
+    "sv_set_draft_rows": (C.c_int, [vp, u32, u32]),
+    "sv_engine_draft_buffers": (C.c_int, [vp, P(DraftBuffers)]),
     "sv_engine_stream": (vp, [vp]),
     "sv_engine_get_buffers": (C.c_int, [vp, P(EngineBuffers)]),
     "sv_new_seq": (C.c_int, [vp, P(u32)]),

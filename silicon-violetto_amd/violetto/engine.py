@@ -85,6 +85,42 @@ class Engine:
             ex = model.extras.c()
             L.check(self.lib.sv_engine_set_extras(self.h, C.byref(ex)))
 
+    # -- the drafter (drafter.rs)
+    def set_drafter(self, drafter) -> None:
+        """A SyntheticDrafter on the GPU: the engine taps its layers on every step and, with
+        STEP_DRAFT, drafts each slot's next block after the step."""
+        assert drafter.device.type == "cuda", "the engine reads weights from device memory"
+        self.drafter = drafter
+        self._dc = drafter.c()
+        L.check(self.lib.sv_engine_set_drafter(self.h, C.byref(self._dc)))
+        b = L.DraftBuffers()
+        L.check(self.lib.sv_engine_draft_buffers(self.h, C.byref(b)))
+        self.dbuf = b
+
+    def set_draft_rows(self, slot: int, rows: int) -> None:
+        L.check(self.lib.sv_set_draft_rows(self.h, slot, rows))
+
+    def draft_logits(self, rows: int) -> torch.Tensor:
+        return device_view(self.dbuf.d_logits, (rows, self.drafter.v), torch.float32)
+
+    def draft_candidates(self, rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+        return (device_view(self.dbuf.d_cand, (rows, L.DRAFT_CANDS), torch.int32),
+                device_view(self.dbuf.d_cand_q, (rows, L.DRAFT_CANDS), torch.float32))
+
+    def draft_taps(self, n: int) -> list[torch.Tensor]:
+        return [device_view(self.dbuf.d_taps[k], (n, self.shape.hidden), torch.float32)
+                for k in range(len(self.drafter.taps))]
+
+    def draft_context(self, n: int) -> torch.Tensor:
+        return device_view(self.dbuf.d_ctx, (n, self.shape.hidden), torch.float32)
+
+    def draft_rings(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """The drafter's K, V [n_layers][n_pages][NKV][page][D] and their cyclic table."""
+        s, b = self.shape, self.dbuf
+        shape = (self.drafter.n_layers, b.n_pages, s.n_kv_heads, 1 << self.cfg.page_shift, s.head_dim)
+        return (device_view(b.d_k_ring, shape, torch.bfloat16), device_view(b.d_v_ring, shape, torch.bfloat16),
+                device_view(b.d_table, (self.cfg.max_seqs, b.max_pages), torch.int32))
+
     # -- views of engine-owned device memory
     @property
     def n_local(self) -> int:

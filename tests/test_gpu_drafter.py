@@ -1,0 +1,158 @@
+"""GPU parity of the drafter's pass (engine/src/engine/drafter.rs:278-447 with kernels.metal:135-148,
+1725-1934) against the oracle (orc_draft, pinned against a float64 restatement of
+tools/spec/drafter.py in test_oracle_drafter.py).
+
+Each step runs on the GPU first; the oracle then runs the same step on the GPU's tapped rows (so
+the drafter is checked on its own inputs, the target's taps separately), and:
+  - the target's logits and ids, and the taps (bf16 of the normed layer outputs), agree;
+  - the drafter's raw logits agree within the logit tolerance;
+  - the candidates and their probabilities equal draft_top over the GPU's own logits, and the
+    slots' next feed and tree equal draft_tree over those (integer and fp32-compare work:
+    bit-exact);
+  - the drafter's rings (context keys and values of every on-path token, cyclic pages) agree.
+The oracle then takes the GPU's trees, so the next step verifies the same drafts on both sides.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import banner
+from helpers import close, greedy_ids_match
+from test_gpu_limite import LOGIT_ATOL, LOGIT_RTOL, build_limite_pair
+from test_gpu_step import dev_u32, put_u32
+from violetto import _lib as L
+from violetto.drafter import SyntheticDrafter
+from violetto.model import ModelShape
+
+pytestmark = pytest.mark.gpu
+
+
+def ring_close(eng, ref) -> None:
+    kd, vd, tab = eng.draft_rings()
+    assert np.array_equal(tab.cpu().numpy().view(np.uint32), ref.d_table), "drafter tables differ"
+    for name, dev_t, host in (("K", kd, ref.dk), ("V", vd, ref.dv)):
+        got = oracle.bf16_to_f32(dev_t.view(torch.int16).cpu().numpy().view(np.uint16))
+        want = oracle.bf16_to_f32(host)
+        bad = ~(np.abs(got - want) <= 2 ** -7 * np.abs(want) + 2e-3)
+        if bad.any():
+            idx = np.argwhere(bad)
+            raise AssertionError(f"drafter ring {name}: {bad.sum()} values off; first {idx[0].tolist()}: "
+                                 f"{got[tuple(idx[0])]} != {want[tuple(idx[0])]}")
+
+
+def draft_step(eng, ref, d, runs, slots, what, flags=L.STEP_DRAFT):
+    res = eng.step(runs, flags=flags, logits=True)
+    n = res.info.n_tokens
+    gpu_taps = [t.cpu().numpy().copy() for t in eng.draft_taps(n)]
+    ids_r, logits_r, em_r, extra = ref.step(runs, draft=bool(flags & L.STEP_DRAFT), taps=gpu_taps)
+    close(res.logits, logits_r, LOGIT_ATOL, LOGIT_RTOL, f"{what} target logits")
+    greedy_ids_match(res.ids, ids_r, logits_r)
+    same = np.array_equal(res.ids, ids_r)
+    for k, (g, w) in enumerate(zip(gpu_taps, extra["taps"])):
+        bad = ~(np.abs(g - w) <= 2 ** -7 * np.abs(w) + 2e-3)
+        assert not bad.any(), f"{what} tap {k}: {bad.sum()} values off"
+    close(eng.draft_context(n).cpu().numpy(), extra["ctx"], 2e-3, 2e-3, f"{what} context")
+    blocks, tin = extra["blocks"], extra["draft_tin"]
+    rows = len(tin) if len(blocks) else 0
+    if rows:
+        got = eng.draft_logits(rows).cpu().numpy()
+        close(got, extra["draft_logits"], LOGIT_ATOL, LOGIT_RTOL, f"{what} draft logits")
+        err = np.abs(got.astype(np.float64) - extra["draft_logits"]).max()
+        print(f"  {what}: {len(blocks)} blocks, {rows} rows, draft logits max-abs err {err:.3e}", flush=True)
+        ncand = min(L.DRAFT_CANDS, int(blocks[:, 1].max()) - 1)
+        if ncand > 0:
+            cand, cand_q = (t.cpu().numpy() for t in eng.draft_candidates(rows))
+            cand = cand.view(np.uint32)
+            want_c, want_q = oracle.draft_top(got, d.vocab.cpu().numpy().astype(np.uint32), tin.reshape(-1), d.inv_temperature,
+                                              ncand)
+            drafted = tin[:, 1] > 0
+            assert np.array_equal(cand[drafted, :ncand], want_c[drafted, :ncand]), f"{what} candidates"
+            assert np.array_equal(cand_q[drafted, :ncand], want_q[drafted, :ncand]), f"{what} candidate probabilities"
+            feed, tree = ref.feed.copy(), ref.tree.copy()
+            oracle.draft_tree(blocks.reshape(-1), tin.reshape(-1), want_c, want_q, feed, tree, ncand)
+            S = ref.max_seqs
+            gfeed, gtree = dev_u32(eng, "d_feed", (S * 16,)), dev_u32(eng, "d_tree", (S * 16,))
+            for s in {int(x) for x in tin[:, 0]}:
+                r = blocks[[int(tin[int(b[0]), 0]) == s for b in blocks]][0][1]
+                assert gfeed[s * 16] == ref.feed[s * 16], f"{what} slot {s} bonus token"
+                assert np.array_equal(gfeed[s * 16:s * 16 + r], feed[s * 16:s * 16 + r]), f"{what} slot {s} feed"
+                assert np.array_equal(gtree[s * 16:s * 16 + r], tree[s * 16:s * 16 + r]), f"{what} slot {s} tree"
+            # the next step verifies the GPU's drafts on both sides
+            ref.feed[:], ref.tree[:] = gfeed, gtree
+    if same:
+        assert np.array_equal(res.emitted, em_r), f"{what} emitted {res.emitted} != {em_r}"
+        ring_close(eng, ref)
+    return same, res
+
+
+@pytest.mark.parametrize("which", ["cfg", "ref"])
+def test_drafter_steps(gpu, which):
+    """A Limite-layout target of 8 layers, two sequences 150 and 201 tokens in, and a 2-layer
+    drafter (convolutions, inject, a head in int8 groups of 8 as export.py writes it, window
+    48 so its rings of 112 positions wrap) tapping layers 2 and 7: a prompt chunk of 24 rows per
+    sequence that drafts blocks of 4 and 3 rows, then verify steps of those trees that draft
+    again. cfg: hidden 512, 8 query heads of 64 over 2 kv heads (runs of 16 rows); ref: the
+    reference's head layout, 10 query heads of 128 over 2 (runs of 12)."""
+    if which == "cfg":
+        shape = ModelShape(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024, vocab_real=1000,
+                           n_layers=8)
+    else:
+        shape = ModelShape(hidden=1280, n_heads=10, n_kv_heads=2, head_dim=128, ffn=1280, vocab=1024,
+                           vocab_real=1000, n_layers=8)
+    banner(f"drafter steps {which}")
+    model, gm, eng, ref, slots, rng = build_limite_pair(shape, window=48, ctx=[150, 201], n_seqs=2, seed=31,
+                                                        max_seq_len=512, max_head_rows=32)
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(2, 7), v=512, window=48, seed=4, device="cpu")
+    eng.set_drafter(d.to("cuda"))
+    ref.set_drafter(d, max_step_tokens=eng.cfg.max_step_tokens)
+    rows = {slots[0]: 4, slots[1]: 3}
+    for s, r in rows.items():
+        eng.set_draft_rows(s, r)
+        ref.draft_rows[s] = r
+    prompt = [[int(t) for t in rng.integers(0, shape.vocab_real, 24)] for _ in slots]
+    same, _ = draft_step(eng, ref, d, [(s, p, False, 1) for s, p in zip(slots, prompt)], slots, "chunk")
+    assert same, "chunk step ids"
+    compared = 1
+    for step in range(5):
+        runs = [(s, [L.FEED_ROW + i for i in range(rows[s])], True) for s in slots]
+        same, res = draft_step(eng, ref, d, runs, slots, f"verify step {step}")
+        if not same:
+            break
+        compared += 1
+    assert compared >= 3, "too few steps compared"
+    eng.close()
+
+
+def test_drafter_context_without_blocks_and_refusals(gpu):
+    """Without STEP_DRAFT the context still reaches the rings (so a later drafted step sees it);
+    a slot without draft rows gets no block; more rows than an attention run, a tap past the
+    target's layers, and a drafter matrix in int8 groups of 8 are refused."""
+    shape = ModelShape(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024, vocab_real=1000,
+                       n_layers=4)
+    banner("drafter context and refusals")
+    model, gm, eng, ref, slots, rng = build_limite_pair(shape, window=48, ctx=[40, 60], n_seqs=2, seed=8,
+                                                        max_seq_len=256, max_head_rows=32)
+    bad = SyntheticDrafter.generate(shape, n_layers=1, taps=(1, 4), v=256, window=48, seed=1, device="cuda")
+    with pytest.raises(L.SvError):
+        eng.set_drafter(bad)
+    bad = SyntheticDrafter.generate(shape, n_layers=1, taps=(1, 2), v=256, window=48, seed=1, device="cuda", group=8)
+    with pytest.raises(L.SvError):
+        eng.set_drafter(bad)
+    d = SyntheticDrafter.generate(shape, n_layers=1, taps=(1, 2), v=256, window=48, seed=2, device="cpu",
+                                  convs=False, inject=False, head_group=None)
+    eng.set_drafter(d.to("cuda"))
+    ref.set_drafter(d, max_step_tokens=eng.cfg.max_step_tokens)
+    with pytest.raises(L.SvError):
+        eng.set_draft_rows(slots[0], 17)
+    prompt = [[int(t) for t in rng.integers(0, shape.vocab_real, 10)] for _ in slots]
+    same, _ = draft_step(eng, ref, d, [(s, p, False, 1) for s, p in zip(slots, prompt)], slots, "context only", flags=0)
+    assert same
+    eng.set_draft_rows(slots[1], 5)
+    ref.draft_rows[slots[1]] = 5
+    runs = [(s, [L.FEED_ROW], False, 1) for s in slots]
+    same, _ = draft_step(eng, ref, d, runs, slots, "one slot drafted")
+    assert same
+    eng.close()
