@@ -286,6 +286,86 @@ def step_roofline(res):
             "roofline_ms": round(bound_ms, 4), "frac": round(bound_ms / res["ms_step"], 4)}
 
 
+def run_drafter(args, streams: int, ctx: int, steps: int, reps: int = 3):
+    """The drafter's pass (drafter.rs:278-447) after each verify step, at the reference drafter's
+    shape (tools/spec/drafter.py: 2 layers of hidden 1280, 10 x 128 query heads over 2 kv heads,
+    ffn 3328, two-tap convolutions, inject, window 1024; export.py: int8 groups of 64, the head
+    over a 16384-id draft vocabulary in groups of 8) on a 4-layer target of the reference's
+    dimensions (its depth does not enter the drafter's cost): `streams` slots `ctx` tokens in,
+    blocks of 8 rows (the bonus token and 7 drafts, drafter.py BLOCK), each step verifying the
+    tree the drafter wrote the step before. Graph-replayed steps with and without the pass; the
+    pass's own kernels timed by hipEvents (kind "draft")."""
+    import dataclasses
+
+    import torch
+
+    import violetto
+    from violetto import _lib as L
+    from violetto.drafter import SyntheticDrafter
+    from violetto.model import REFERENCE_SHAPE, SyntheticModel, rope_freq
+
+    shape = dataclasses.replace(REFERENCE_SHAPE, n_layers=4)
+    rows = 8
+    n_steps = 2 * (steps + reps) + 16
+    max_seq_len = ctx + rows * n_steps + 64
+    model = SyntheticModel.generate(shape, int8=True, seed=args.seed, device="cuda", group=64)
+    eng = violetto.Engine(shape, max_seqs=streams, max_step_tokens=max(64, streams * rows), max_seq_len=max_seq_len,
+                          max_head_rows=streams * rows, kv_tokens=streams * (max_seq_len + 16), page_shift=4,
+                          attn_scale=0.1, freq=rope_freq(500000.0, shape.head_dim))
+    eng.set_model(model)
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(1, 3), v=16384, window=1024, seed=args.seed + 5,
+                                  device="cuda", group=64, head_group=8)
+    eng.set_drafter(d)
+    slots = [eng.new_seq() for _ in range(streams)]
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 9)
+    for s in slots:
+        eng.bench_fill(s, ctx)
+        eng.set_feed(s, ctx, int(torch.randint(0, shape.vocab_real, (1,), generator=gen, device="cuda")))
+        eng.set_draft_rows(s, rows)
+    kd, vd = eng.kv_cache()
+    kr, vr, _ = eng.draft_rings()
+    for t in (kd, vd, kr, vr):
+        t.copy_(torch.randn(t.shape, generator=gen, device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    # the first step drafts from the bonus token; later steps verify the drafter's trees
+    eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=8)
+    eng.encode(L.STEP_DRAFT)
+    eng.sync()
+    out = {}
+    for flags, key in ((0, "verify_only"), (L.STEP_DRAFT, "verify_and_draft")):
+        eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots], extra_keys=rows * (steps + reps + 4))
+        eng.graph_capture(flags)
+        eng.graph_replay(2)
+        eng.sync()
+        t_a = time.perf_counter()
+        eng.graph_replay(steps)
+        eng.sync()
+        out[key] = (time.perf_counter() - t_a) / steps * 1e3
+    prof = eng.profile_step(L.STEP_DRAFT, reps=reps)
+    per_step = {kk: v[0] / reps for kk, v in prof.items() if v[1]}
+    # the bytes one pass reads: every drafter matrix once in its file format (the head's int8
+    # groups of 8 included, read here as the exact bf16 hi + lo pair: 4 bytes a weight)
+    file_bytes = sum(w.numel() * w.element_size() + (0 if sc is None else sc.numel() * 2) for w, sc in d.mats.values())
+    head_w, head_s = d.mats["head"]
+    read_bytes = file_bytes - head_w.numel() - head_s.numel() * 2 + 4 * head_w.numel()
+    draft_ms = per_step.get("draft", float("nan"))
+    eng.close()
+    del model, d
+    torch.cuda.empty_cache()
+    gbs = file_bytes / (draft_ms * 1e-3) / 1e9
+    return {"config": {"workload": f"drafter pass: {streams} slot(s) x {ctx} ctx, blocks of {rows} rows, reference "
+                                   "drafter shape (2 layers, hidden 1280, v 16384, convs + inject, window 1024)",
+                       "streams": streams, "ctx": ctx, "block_rows": rows},
+            "ms_per_step_verify_only": round(out["verify_only"], 5),
+            "ms_per_step_verify_and_draft": round(out["verify_and_draft"], 5),
+            "draft_pass_ms": round(draft_ms, 5),
+            "draft_weight_bytes": int(file_bytes), "draft_bytes_read": int(read_bytes),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "kernel_ms_per_step": {kk: round(v, 4) for kk, v in per_step.items()}}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -302,6 +382,8 @@ def main() -> int:
     ap.add_argument("--long-steps", type=int, default=20,
                     help="timed steps of configs[3] (bf16 weights, 65536 ctx, 1 and 8 streams; 0: skip)")
     ap.add_argument("--tree-steps", type=int, default=20, help="timed steps of configs[4] (16-node trees x 32; 0: skip)")
+    ap.add_argument("--drafter-steps", type=int, default=20,
+                    help="timed steps of the drafter's pass (1 and 32 slots, reference drafter shape; 0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-keys", type=int, default=0, help="attention keys per split (0: the engine's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -381,6 +463,14 @@ def main() -> int:
             torch.cuda.empty_cache()
         del model16
 
+    drafter = None
+    if args.drafter_steps > 0:
+        drafter = {}
+        for streams in (1, 32):
+            log(f"drafter pass, {streams} slot(s)")
+            drafter[f"streams{streams}"] = run_drafter(args, streams, 4096, args.drafter_steps)
+            log(f"  {drafter[f'streams{streams}']}")
+
     line = {
         "metric": METRIC,
         "value": round(r1["value"], 2),
@@ -406,6 +496,7 @@ def main() -> int:
         "streams32": s32,
         "long_ctx_bf16": long_ctx,
         "trees32": s64,
+        "drafter": drafter,
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy:

@@ -447,30 +447,84 @@ sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_
 
 // ---------------------------------------------------------------- draft builder
 // draft_top (kernels.metal:1845-1891): one workgroup of 1024 per drafted block row (the
-// block's row 0, the bonus token's, is skipped). ncand rounds of a workgroup argmax over the
-// ids not yet taken (ties to the lowest id, an order-independent maximum), then the row's sum
-// of exp((x - x_top) inv_t) in the sampler's order (thread t owns ids t, t + 1024, ...; the
-// same exp2 and scan as the sampler), and each candidate's target id and probability.
+// block's row 0, the bonus token's, is skipped). The ncand best ids in the order (value
+// descending, id ascending) over the ids with a value above -FLT_MAX: every thread keeps its
+// own sorted top ncand over ids t, t + 1024, ... in one pass (loads issued eight at a time),
+// then ncand rounds of a workgroup argmax over the threads' list heads, the winner popping its
+// head (the k-th pick of a strict total order is the same however the ids are dealt out).
+// Then the row's sum of exp((x - x_top) inv_t) in the sampler's order (thread t adds ids t,
+// t + 1024, ... in turn; 32 runs of 32 threads, then their bases) and each candidate's target
+// id and probability.
 __global__ __launch_bounds__(1024) void draft_top_kernel(const float* logits, const uint32_t* vocab, const uint32_t* tin,
                                                          uint32_t* cand, float* cand_q, uint32_t nv, float c,
                                                          uint32_t ncand) {
-  __shared__ float ex[SV_SAMPLE_THREADS + 1];
-  __shared__ float base[32];
+  __shared__ float part[SV_SAMPLE_THREADS];
   __shared__ float bvs[16];
   __shared__ uint32_t bis[16];
   __shared__ float top_v[SV_DRAFT_CANDS];
   __shared__ uint32_t top_i[SV_DRAFT_CANDS];
+  __shared__ float total;
   const uint32_t r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   if (tin[2 * r + 1] == 0) return;
   const float* x = logits + (size_t)r * nv;
+  float lv[SV_DRAFT_CANDS];
+  uint32_t li[SV_DRAFT_CANDS];
+#pragma unroll
+  for (uint32_t m = 0; m < SV_DRAFT_CANDS; m++) {
+    lv[m] = -3.402823466e+38f;
+    li[m] = 0xffffffffu;
+  }
+  // insert (v, j) into the sorted list if it beats the list's last entry
+  auto insert = [&](float v, uint32_t j) {
+    float cv = lv[SV_DRAFT_CANDS - 1];
+    uint32_t ci = li[SV_DRAFT_CANDS - 1];
+    better(cv, ci, v, j);
+    if (ci != j) return;
+#pragma unroll
+    for (int m = SV_DRAFT_CANDS - 1; m >= 0; m--) {
+      const bool above = m > 0 && (v > lv[m - 1] || (v == lv[m - 1] && j < li[m - 1]));
+      if (above) {
+        lv[m] = lv[m - 1];
+        li[m] = li[m - 1];
+      } else {
+        lv[m] = v;
+        li[m] = j;
+        break;
+      }
+    }
+  };
+  // a row of up to 16 x 1024 ids is read once, every load in flight, and kept for the sum below
+  constexpr int KEEP = 16;
+  const bool kept = nv <= KEEP * SV_SAMPLE_THREADS;
+  float keep[KEEP];
+  uint32_t j = tid;
+  if (kept) {
+#pragma unroll
+    for (int u = 0; u < KEEP; u++) keep[u] = j + u * SV_SAMPLE_THREADS < nv ? x[j + u * SV_SAMPLE_THREADS] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < KEEP; u++)
+      if (j + u * SV_SAMPLE_THREADS < nv) insert(keep[u], j + u * SV_SAMPLE_THREADS);
+  } else {
+    for (; j + 7 * SV_SAMPLE_THREADS < nv; j += 8 * SV_SAMPLE_THREADS) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = x[j + u * SV_SAMPLE_THREADS];
+#pragma unroll
+      for (int u = 0; u < 8; u++) insert(v[u], j + u * SV_SAMPLE_THREADS);
+    }
+    for (; j < nv; j += SV_SAMPLE_THREADS) insert(x[j], j);
+  }
+  uint32_t head = 0;
   for (uint32_t k = 0; k < ncand; k++) {
     float bv = -3.402823466e+38f;
     uint32_t bi = 0xffffffffu;
-    for (uint32_t j = tid; j < nv; j += SV_SAMPLE_THREADS) {
-      bool taken = false;
-      for (uint32_t m = 0; m < k; m++) taken = taken || top_i[m] == j;
-      if (!taken) better(bv, bi, x[j], j);
-    }
+#pragma unroll
+    for (uint32_t m = 0; m < SV_DRAFT_CANDS; m++)
+      if (m == head) {
+        bv = lv[m];
+        bi = li[m];
+      }
+    const uint32_t mine = bi;
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
       const float v = __shfl_xor(bv, o, WAVE);
@@ -482,63 +536,112 @@ __global__ __launch_bounds__(1024) void draft_top_kernel(const float* logits, co
       bis[wv] = bi;
     }
     __syncthreads();
+    bv = bvs[0];
+    bi = bis[0];
+    for (int w = 1; w < 16; w++) better(bv, bi, bvs[w], bis[w]);
     if (tid == 0) {
-      for (int w = 1; w < 16; w++) better(bv, bi, bvs[w], bis[w]);
       top_v[k] = bv;
       top_i[k] = bi;
     }
+    if (bi != 0xffffffffu && bi == mine) head++;  // this thread's head was picked
     __syncthreads();
   }
-  float s = 0.0f;
-  for (uint32_t j = tid; j < nv; j += SV_SAMPLE_THREADS) s += sv_exp2((x[j] - top_v[0]) * c);
-  scan1024(s, ex, base, tid);
+  const float t0 = top_v[0];
+  float sum = 0.0f;
+  j = tid;
+  if (kept) {
+#pragma unroll
+    for (int u = 0; u < KEEP; u++)
+      if (j + u * SV_SAMPLE_THREADS < nv) sum += sv_exp2((keep[u] - t0) * c);
+    j = nv;
+  }
+  for (; j + 7 * SV_SAMPLE_THREADS < nv; j += 8 * SV_SAMPLE_THREADS) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = x[j + u * SV_SAMPLE_THREADS];
+#pragma unroll
+    for (int u = 0; u < 8; u++) sum += sv_exp2((v[u] - t0) * c);
+  }
+  for (; j < nv; j += SV_SAMPLE_THREADS) sum += sv_exp2((x[j] - t0) * c);
+  // the sampler's scan order for the total: 32 serial runs of 32 threads, then the runs in order
+  part[tid] = sum;
+  __syncthreads();
+  if (tid < 32) {
+    float acc = 0.0f;
+    for (uint32_t i = 32 * tid; i < 32 * tid + 32; i++) acc += part[i];
+    part[32 * tid] = acc;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float acc = 0.0f;
+    for (uint32_t g = 0; g < 32; g++) acc += part[32 * g];
+    total = acc;
+  }
+  __syncthreads();
   if (tid < ncand) {
     const bool ok = top_i[tid] < nv && top_i[0] < nv;  // a row without tid + 1 ordered values
     cand[r * SV_DRAFT_CANDS + tid] = ok ? vocab[top_i[tid]] : SV_NO_TOK;
-    cand_q[r * SV_DRAFT_CANDS + tid] = ok ? sv_exp2((top_v[tid] - top_v[0]) * c) / ex[SV_SAMPLE_THREADS] : 0.0f;
+    cand_q[r * SV_DRAFT_CANDS + tid] = ok ? sv_exp2((top_v[tid] - t0) * c) / total : 0.0f;
   }
 }
 
-// draft_tree (kernels.metal:1893-1934): one thread per block builds its DDTree best-first: the
-// next node is the not-yet-taken candidate of any node so far with the highest path product
-// (first such node on ties), a node at depth d drawing children from block row d + 1's
-// candidates; nodes go to feed/tree[slot][1..] parents first, the rest become dead nodes. A
-// candidate draft_top could not fill (SV_NO_TOK) is never taken.
+// draft_tree (kernels.metal:1893-1934): a workgroup per block stages the block's candidates in
+// LDS, then one thread builds its DDTree best-first: the next node is the not-yet-taken
+// candidate of any node so far with the highest path product (first such node on ties), a node
+// at depth d drawing children from block row d + 1's candidates; nodes go to feed/tree[slot][1..]
+// parents first, the rest become dead nodes. A candidate draft_top could not fill (SV_NO_TOK) is
+// never taken.
 __global__ __launch_bounds__(64) void draft_tree_kernel(const uint32_t* blocks, uint32_t nblocks, const uint32_t* tin,
                                                         const uint32_t* cand, const float* cand_q, uint32_t* feed,
                                                         uint32_t* tree, uint32_t ncand) {
-  const uint32_t b = blockIdx.x * 64 + threadIdx.x;
-  if (b >= nblocks) return;
+  __shared__ uint32_t sc_id[SV_FEED_W * SV_DRAFT_CANDS];
+  __shared__ float sc_q[SV_FEED_W * SV_DRAFT_CANDS];
+  __shared__ uint32_t out_feed[SV_FEED_W], out_tree[SV_FEED_W];
+  const uint32_t b = blockIdx.x, tid = threadIdx.x;
   const uint32_t first = blocks[2 * b], rows = min(blocks[2 * b + 1], SV_FEED_W), slot = tin[2 * first];
-  float score[SV_FEED_W];
-  uint32_t depth[SV_FEED_W], taken[SV_FEED_W], sees[SV_FEED_W];
-  score[0] = 1.0f;
-  depth[0] = taken[0] = 0;
-  sees[0] = 1;
-  uint32_t n = 1;
-  for (; n < rows; n++) {
-    float best = -1.0f;
-    uint32_t p = 0;
-    for (uint32_t i = 0; i < n; i++) {
-      const uint32_t cc = (first + depth[i] + 1) * SV_DRAFT_CANDS + taken[i];
-      if (depth[i] + 1 == rows || taken[i] == ncand || cand[cc] == SV_NO_TOK) continue;
-      const float sc = score[i] * cand_q[cc];
-      if (sc > best) {
-        best = sc;
-        p = i;
-      }
-    }
-    if (best < 0.0f) break;
-    const uint32_t d = depth[p] + 1;
-    feed[slot * SV_FEED_W + n] = cand[(first + d) * SV_DRAFT_CANDS + taken[p]];
-    taken[p]++;
-    score[n] = best;
-    depth[n] = d;
-    taken[n] = 0;
-    sees[n] = sees[p] | 1u << n;
-    tree[slot * SV_FEED_W + n] = d | p << 8 | sees[n] << 16;
+  if (tid < rows * SV_DRAFT_CANDS) {
+    sc_id[tid] = cand[first * SV_DRAFT_CANDS + tid];
+    sc_q[tid] = cand_q[first * SV_DRAFT_CANDS + tid];
   }
-  for (; n < SV_FEED_W; n++) tree[slot * SV_FEED_W + n] = 1u | SV_NO_PARENT << 8 | (1u | 1u << n) << 16;
+  __syncthreads();
+  if (tid == 0) {
+    float score[SV_FEED_W];
+    uint32_t depth[SV_FEED_W], taken[SV_FEED_W], sees[SV_FEED_W];
+    score[0] = 1.0f;
+    depth[0] = taken[0] = 0;
+    sees[0] = 1;
+    uint32_t n = 1;
+    for (; n < rows; n++) {
+      float best = -1.0f;
+      uint32_t p = 0;
+      for (uint32_t i = 0; i < n; i++) {
+        const uint32_t cc = (depth[i] + 1) * SV_DRAFT_CANDS + taken[i];
+        if (depth[i] + 1 == rows || taken[i] == ncand || sc_id[cc] == SV_NO_TOK) continue;
+        const float s = score[i] * sc_q[cc];
+        if (s > best) {
+          best = s;
+          p = i;
+        }
+      }
+      if (best < 0.0f) break;
+      const uint32_t d = depth[p] + 1;
+      out_feed[n] = sc_id[d * SV_DRAFT_CANDS + taken[p]];
+      taken[p]++;
+      score[n] = best;
+      depth[n] = d;
+      taken[n] = 0;
+      sees[n] = sees[p] | 1u << n;
+      out_tree[n] = d | p << 8 | sees[n] << 16;
+    }
+    for (uint32_t m = n; m < SV_FEED_W; m++) out_tree[m] = 1u | SV_NO_PARENT << 8 | (1u | 1u << m) << 16;
+    out_feed[0] = n;  // the count of fed nodes, for the flush below
+  }
+  __syncthreads();
+  const uint32_t n = out_feed[0];
+  if (tid >= 1 && tid < SV_FEED_W) {
+    if (tid < n) feed[slot * SV_FEED_W + tid] = out_feed[tid];
+    tree[slot * SV_FEED_W + tid] = out_tree[tid];
+  }
 }
 
 sv_status draft_top_launch(hipStream_t stream, const float* logits, const uint32_t* vocab, const uint32_t* tin,
@@ -558,7 +661,7 @@ sv_status draft_tree_launch(hipStream_t stream, const uint32_t* blocks, uint32_t
   if (!blocks || !tin || !cand || !cand_q || !feed || !tree) return fail(SV_ERR_ARG, "draft_tree: null pointer");
   if (ncand == 0 || ncand > SV_DRAFT_CANDS) return fail(SV_ERR_ARG, "draft_tree: %u candidates (1..%u)", ncand, SV_DRAFT_CANDS);
   if (nblocks == 0) return SV_OK;
-  launch(draft_tree_kernel, dim3((nblocks + 63) / 64), dim3(64), 0, stream, blocks, nblocks, tin, cand, cand_q, feed,
+  launch(draft_tree_kernel, dim3(nblocks), dim3(64), 0, stream, blocks, nblocks, tin, cand, cand_q, feed,
          tree, ncand);
   return check_launch("draft_tree");
 }

@@ -156,3 +156,43 @@ def test_drafter_context_without_blocks_and_refusals(gpu):
     same, _ = draft_step(eng, ref, d, runs, slots, "one slot drafted")
     assert same
     eng.close()
+
+
+@pytest.mark.parametrize("hidden,rows", [(512, 7), (1280, 12)])
+def test_draft_conv_and_tap_rows_kernels(gpu, hidden, rows):
+    """sv_draft_conv (kernels.metal:1820-1836, the corrections given) and sv_tap_rows
+    (kernels.metal:135-148) through the C ABI against the oracle: two blocks (rows 0..2 and
+    3..rows-1), with and without the residual."""
+    import ctypes as C
+
+    banner(f"draft_conv / tap_rows kernels hidden {hidden}")
+    rng = np.random.default_rng(hidden + rows)
+    cw = -(-(hidden // 8) // 64) * 64
+    x = rng.normal(0, 1, (rows, hidden)).astype(np.float32)
+    corr = rng.normal(0, 0.1, (rows, cw)).astype(np.float32)
+    base = np.stack([1 + rng.normal(0, 0.1, hidden), rng.normal(0, 0.1, hidden)]).astype(np.float32)
+    resid = rng.normal(0, 1, (rows, hidden)).astype(np.float32)
+    tin = np.array([[0, i] for i in range(3)] + [[1, i] for i in range(rows - 3)], np.uint32)
+    lib = L.lib()
+    dev = {k: torch.from_numpy(v.view(np.int32) if v.dtype == np.uint32 else v).cuda()
+           for k, v in dict(x=x, corr=corr, base=base, resid=resid, tin=tin).items()}
+    for with_resid in (False, True):
+        out = torch.zeros_like(dev["x"])
+        L.check(lib.sv_draft_conv(None, dev["x"].data_ptr(), dev["corr"].data_ptr(), cw, dev["base"].data_ptr(),
+                                  dev["tin"].data_ptr(), dev["resid"].data_ptr() if with_resid else None,
+                                  out.data_ptr(), rows, hidden))
+        torch.cuda.synchronize()
+        want = np.zeros_like(x)
+        O = oracle
+        O.lib().orc_draft_conv(O.ptr(x), O.ptr(corr), C.c_uint32(cw), O.ptr(base), O.ptr(tin),
+                               O.ptr(resid) if with_resid else None, O.ptr(want), C.c_uint32(rows), C.c_uint32(hidden))
+        close(out.cpu().numpy(), want, 1e-5, 1e-5, f"draft_conv resid={with_resid}")
+    taps = torch.zeros_like(dev["x"])
+    L.check(lib.sv_tap_rows(None, dev["x"].data_ptr(), taps.data_ptr(), rows, hidden))
+    torch.cuda.synchronize()
+    want = np.zeros_like(x)
+    oracle.lib().orc_tap_rows(oracle.ptr(x), oracle.ptr(want), C.c_uint32(rows), C.c_uint32(hidden))
+    got = taps.cpu().numpy()
+    # bf16 values: equal, or one bf16 step apart where fp32 and float64 norms round differently
+    assert (np.abs(got - want) <= np.abs(want) * 2.0 ** -8).all()
+    assert (got == want).mean() > 0.99
