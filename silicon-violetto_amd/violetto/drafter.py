@@ -15,6 +15,7 @@ from __future__ import annotations
 import ctypes as C
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import _lib as L
@@ -154,3 +155,96 @@ class SyntheticDrafter:
         m, k = w.shape
         grp = k // s.shape[1]
         return (w.double().reshape(m, s.shape[1], grp) * s.double().unsqueeze(-1)).reshape(m, k)
+
+
+BLOCK = 8  # tools/spec/drafter.py BLOCK: the meta tensor's block size (rows are set per slot here)
+
+
+def drafter_tensors(d: SyntheticDrafter) -> dict[str, torch.Tensor]:
+    """The tensors tools/spec/export.py:28-60 writes, under its names, for a SyntheticDrafter:
+    int8 matrices as `<name>` + `<name>.scale`, convolution bases f32 [2][hidden], `mask_emb`,
+    `vocab` (f32 ids) and `meta` (f32: layers, taps, block, window, vocabulary, the taps)."""
+    out: dict[str, torch.Tensor] = {}
+    for name, (w, s) in d.mats.items():
+        out[name] = w
+        if s is not None:
+            out[name + ".scale"] = s
+    for key, base in d.conv_base.items():
+        out[key + ".base"] = base.float()
+    out["mask_emb"] = d.mask_emb.float()
+    out["vocab"] = d.vocab.float()
+    out["meta"] = torch.tensor([d.n_layers, len(d.taps), BLOCK, d.window, d.v, *d.taps], dtype=torch.float32)
+    return out
+
+
+class VltDrafter:
+    """A drafter served from an uploaded weight file with export.py's tensor names (the reader
+    side of drafter.rs:145-241 `Drafter::load`): `meta`, `fc.k`, `kv_all`, `inject` (optional),
+    `D{i}.qkv/o/gate_up/down`, `D{i}.conv{c}.base/.corr` (optional, all four or none), `head`,
+    `mask_emb`, `vocab`. Shapes are checked as the reference checks them; the window is the
+    file's (the reference also requires it to equal its engine's WINDOW)."""
+
+    def __init__(self, wf, shape: ModelShape, inv_temperature: float = 1.0 / TRAIN_TEMPERATURE):
+        self.wf, self.shape, self.device = wf, shape, torch.device("cuda")
+        meta = wf.read("meta")
+        if meta.size < 5:
+            raise ValueError(f"meta {meta.tolist()}")
+        n_layers, n_taps, window, v = int(meta[0]), int(meta[1]), int(meta[3]), int(meta[4])
+        if meta.size != 5 + n_taps:
+            raise ValueError(f"window {window}, meta {meta.tolist()}")
+        self.n_layers, self.window, self.taps = n_layers, window, tuple(int(t) for t in meta[5:])
+        self.inv_temperature = inv_temperature
+        H, F, NKV, D = shape.hidden, shape.ffn, shape.n_kv_heads, shape.head_dim
+        self.fc = [wf.matrix(f"fc.{k}", H, H) for k in range(n_taps)]
+        self.kv_all = wf.matrix("kv_all", n_layers * 2 * NKV * D, H)
+        self.inject = wf.matrix("inject", H, H) if wf.has("inject") else None
+        self.head = wf.matrix("head", v, H)
+        self.layers = []
+        for i in range(n_layers):
+            p = f"D{i:02d}."
+            lay = dict(qkv=wf.matrix(p + "qkv", shape.qkv_width, H), o=wf.matrix(p + "o", H, shape.n_heads * D),
+                       gate_up=wf.matrix(p + "gate_up", 2 * F, H), down=wf.matrix(p + "down", H, F), convs=None)
+            if wf.has(p + "conv0.base"):
+                convs = []
+                for c in range(4):
+                    wf.check(f"{p}conv{c}.base", 0, (2, H))
+                    corr = wf.find(f"{p}conv{c}.corr")
+                    convs.append((wf.device_ptr(f"{p}conv{c}.base"), wf.matrix(f"{p}conv{c}.corr", corr.shape[0], H)))
+                lay["convs"] = convs
+            self.layers.append(lay)
+        wf.check("mask_emb", 0, (H,))
+        self.mask_emb = wf.device_ptr("mask_emb")
+        wf.check("vocab", 0, (v,))
+        ids = wf.read("vocab")
+        if not np.array_equal(ids, np.round(ids)) or ids.min() < 0 or ids.max() >= shape.vocab_real:
+            raise ValueError("vocab: the draft vocabulary's ids must be target ids")
+        self.vocab = torch.from_numpy(ids.astype(np.int32)).to(self.device)
+        self.v = v
+
+    @property
+    def convs(self) -> bool:
+        return self.layers[0]["convs"] is not None
+
+    def c(self) -> L.Drafter:
+        layers = (L.DraftLayer * self.n_layers)()
+        for i, lay in enumerate(self.layers):
+            dl = layers[i]
+            dl.qkv, dl.o, dl.gate_up, dl.down = lay["qkv"], lay["o"], lay["gate_up"], lay["down"]
+            for c in range(4):
+                if lay["convs"] is not None:
+                    dl.conv_base[c], dl.conv_corr[c] = lay["convs"][c]
+        d = L.Drafter()
+        d.n_layers, d.n_taps, d.v = self.n_layers, len(self.taps), self.v
+        for k, t in enumerate(self.taps):
+            d.taps[k] = t
+            d.fc[k] = self.fc[k]
+        d.kv_all = self.kv_all
+        d.inject = self.inject if self.inject is not None else L.Matrix(None, None, 0, 0, 0, 0)
+        d.head = self.head
+        d.mask_emb = self.mask_emb
+        d.vocab = self.vocab.data_ptr()
+        d.layers = C.cast(layers, C.POINTER(L.DraftLayer))
+        d.inv_temperature = self.inv_temperature
+        d.window = self.window
+        d._layers = layers
+        return d

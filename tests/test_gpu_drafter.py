@@ -196,3 +196,40 @@ def test_draft_conv_and_tap_rows_kernels(gpu, hidden, rows):
     # bf16 values: equal, or one bf16 step apart where fp32 and float64 norms round differently
     assert (np.abs(got - want) <= np.abs(want) * 2.0 ** -8).all()
     assert (got == want).mean() > 0.99
+
+
+def test_drafter_from_weight_file(gpu, tmp_path):
+    """The same drafter served from its weight file (export.py's names, uploaded through
+    sv_weights_*; VltDrafter) and from memory drafts the same blocks: raw logits, candidates and
+    trees bit-identical over a prompt step and two verify steps."""
+    from violetto.drafter import VltDrafter, drafter_tensors
+    from violetto.weights import WeightFile, write_vlt
+
+    shape = ModelShape(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024, vocab_real=1000,
+                       n_layers=4)
+    banner("drafter from weight file")
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(1, 3), v=256, window=48, seed=6, device="cpu")
+    path = tmp_path / "drafter.vlt"
+    write_vlt(path, drafter_tensors(d))
+    wf = WeightFile(path)
+    wf.upload()
+    results = []
+    for source in ("memory", "file"):
+        model, gm, eng, ref, slots, rng = build_limite_pair(shape, window=48, ctx=[40, 60], n_seqs=2, seed=12,
+                                                            max_seq_len=256, max_head_rows=32)
+        eng.set_drafter(d.to("cuda") if source == "memory" else VltDrafter(wf, shape))
+        for s in slots:
+            eng.set_draft_rows(s, 4)
+        out = []
+        prompt = [[int(t) for t in rng.integers(0, shape.vocab_real, 10)] for _ in slots]
+        eng.step([(s, p, False, 1) for s, p in zip(slots, prompt)], flags=L.STEP_DRAFT)
+        out.append(eng.draft_logits(8).cpu().numpy().copy())
+        for _ in range(2):
+            eng.step([(s, [L.FEED_ROW + i for i in range(4)], True) for s in slots], flags=L.STEP_DRAFT)
+            out.append(eng.draft_logits(8).cpu().numpy().copy())
+            out.append(dev_u32(eng, "d_feed", (2 * 16,)))
+            out.append(dev_u32(eng, "d_tree", (2 * 16,)))
+        results.append(out)
+        eng.close()
+    for a, b in zip(*results):
+        np.testing.assert_array_equal(a, b)

@@ -167,3 +167,27 @@ def test_limite_tensors_round_trip(tmp_path):
     with pytest.raises(ValueError, match="expected dtype"):
         wf.check("L00.xsa", 1, (4,))
     wf.close()
+
+
+def test_drafter_tensors_round_trip(tmp_path):
+    """A drafter written under export.py's names (tools/spec/export.py:28-60) reads back with
+    the names, dtypes and shapes drafter.rs:145-241 asks for: meta (layers, taps, block, window,
+    vocabulary, the taps), the head in int8 groups of 8, corrections padded to 64-row tiles."""
+    from violetto.drafter import SyntheticDrafter, drafter_tensors
+    from violetto.model import ModelShape
+
+    shape = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=384, vocab=512, vocab_real=500,
+                       n_layers=6)
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(2, 5), v=128, window=48, seed=1)
+    path = tmp_path / "drafter.vlt"
+    write_vlt(path, drafter_tensors(d))
+    wf = WeightFile(path)
+    np.testing.assert_array_equal(wf.read("meta"), np.array([2, 2, 8, 48, 128, 2, 5], np.float32))
+    want = {"fc.0": (2, (256, 256)), "fc.1": (2, (256, 256)), "kv_all": (2, (512, 256)), "inject": (2, (256, 256)),
+            "head": (2, (128, 256)), "head.scale": (1, (128, 32)), "mask_emb": (0, (256,)), "vocab": (0, (128,)),
+            "D01.qkv": (2, (512, 256)), "D01.gate_up": (2, (768, 256)), "D01.down": (2, (256, 384)),
+            "D00.conv3.base": (0, (2, 256)), "D00.conv3.corr": (2, (64, 256)), "D00.conv3.corr.scale": (1, (64, 4))}
+    for name, (dt, shp) in want.items():
+        wf.check(name, dt, shp)
+    np.testing.assert_array_equal(wf.read("vocab").astype(np.int64), d.vocab.numpy())
+    np.testing.assert_array_equal(wf.read("head"), d.mats["head"][0].numpy())
