@@ -20,7 +20,7 @@ import torch
 
 import oracle
 from conftest import banner
-from helpers import close, greedy_ids_match
+from helpers import bf16_bits, close, greedy_ids_match
 from test_gpu_limite import LOGIT_ATOL, LOGIT_RTOL, build_limite_pair
 from test_gpu_step import dev_u32, put_u32
 from violetto import _lib as L
@@ -233,3 +233,45 @@ def test_drafter_from_weight_file(gpu, tmp_path):
         eng.close()
     for a, b in zip(*results):
         np.testing.assert_array_equal(a, b)
+
+
+def test_drafter_reference_shape(gpu):
+    """The reference drafter's own shape (tools/spec/drafter.py: hidden 1280, 10 x 128 query heads
+    over 2 kv heads, ffn 3328, 2 layers, window 1024, blocks of 8 rows; export.py: int8 groups of
+    64, a 16384-id head in groups of 8) on a 4-layer target of the reference's dimensions
+    (vocabulary 151680), two sequences 1500 and 1100 tokens in with the drafter's rings filled
+    (1088 positions a slot: wrapped) and the window crossing them: a prompt step and three verify
+    steps of the drafter's trees, against the oracle as in test_drafter_steps."""
+    import dataclasses
+
+    from violetto.model import REFERENCE_SHAPE
+
+    shape = dataclasses.replace(REFERENCE_SHAPE, n_layers=4)
+    banner("drafter at the reference shape")
+    model, gm, eng, ref, slots, rng = build_limite_pair(shape, window=1024, ctx=[1500, 1100], n_seqs=2, seed=41,
+                                                        max_seq_len=1700, max_head_rows=32, group=64)
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(1, 3), v=16384, window=1024, seed=9, device="cpu")
+    eng.set_drafter(d.to("cuda"))
+    ref.set_drafter(d, max_step_tokens=eng.cfg.max_step_tokens)
+    kd, vd, _ = eng.draft_rings()
+    assert kd.shape == ref.dk.shape
+    for dev_t, host in ((kd, ref.dk), (vd, ref.dv)):
+        bits = bf16_bits(rng.normal(0, 1, host.shape).astype(np.float32))
+        host[...] = bits
+        dev_t.copy_(torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16))
+    torch.cuda.synchronize()
+    for s in slots:
+        eng.set_draft_rows(s, 8)
+        ref.draft_rows[s] = 8
+    prompt = [[int(t) for t in rng.integers(0, shape.vocab_real, 6)] for _ in slots]
+    same, _ = draft_step(eng, ref, d, [(s, p, False, 1) for s, p in zip(slots, prompt)], slots, "prompt")
+    assert same, "prompt step ids"
+    compared = 1
+    for step in range(3):
+        runs = [(s, [L.FEED_ROW + i for i in range(8)], True) for s in slots]
+        same, _ = draft_step(eng, ref, d, runs, slots, f"verify step {step}")
+        if not same:
+            break
+        compared += 1
+    assert compared >= 3, "too few steps compared"
+    eng.close()
