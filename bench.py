@@ -366,6 +366,91 @@ def run_drafter(args, streams: int, ctx: int, steps: int, reps: int = 3):
             "kernel_ms_per_step": {kk: round(v, 4) for kk, v in per_step.items()}}
 
 
+def run_reference_model(args, streams: int, ctx: int, steps: int):
+    """The reference's own model shape (engine/src/model.rs:6-21: Limite, 48 layers of hidden
+    1280, 10 x 128 query heads over 2 kv heads, ffn 3328, vocabulary 151680; every fourth layer
+    global, the others sliding-window layers of 1024 keys; value embeddings, gates, XSA, MUDD;
+    int8 groups of 64, its own int8 head) with random weights, `streams` sequences `ctx` tokens
+    in. Two graph-replayed steps, each timed over `steps`:
+      - plain decode, one row per sequence (what docs/performance.md's "plain" column measures:
+        one token per sequence per step whatever the weights, so its tok/s is comparable);
+      - a verify step of an 8-row block per sequence plus the drafter's pass (the reference
+        drafter's shape, tapping layers 35 and 47 as tools/spec/drafter.py TAPS), the step the
+        reference's "with the drafter" column runs; random weights accept nothing, so only its
+        time is reported."""
+    import torch
+
+    import violetto
+    from violetto import _lib as L
+    from violetto.drafter import SyntheticDrafter
+    from violetto.model import REFERENCE_SHAPE, SyntheticModel, generate_extras, rope_freq
+
+    shape = REFERENCE_SHAPE
+    rows = 8
+    max_seq_len = ctx + (rows + 1) * (2 * steps + 16) + 64
+    model = SyntheticModel.generate(shape, int8=True, seed=args.seed, device="cuda", group=64)
+    model = model.with_extras(generate_extras(shape, seed=args.seed + 3, device="cuda", window=1024)).with_head(64)
+    eng = violetto.Engine(shape, max_seqs=streams, max_step_tokens=max(64, streams * rows), max_seq_len=max_seq_len,
+                          max_head_rows=streams * rows, kv_tokens=streams * (max_seq_len + 16), page_shift=4,
+                          attn_scale=0.1, freq=rope_freq(500000.0, shape.head_dim), local=model.extras.local,
+                          window=1024)
+    eng.set_model(model)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(args.seed + 11)
+    slots = [eng.new_seq() for _ in range(streams)]
+    for s in slots:
+        eng.bench_fill(s, ctx)
+        eng.set_feed(s, ctx, int(torch.randint(0, shape.vocab_real, (1,), generator=gen, device="cuda")))
+    kd, vd = eng.kv_cache()
+    kl, vl, _ = eng.local_cache()
+    for t in (kd, vd, kl, vl):
+        for l0 in range(0, t.shape[0], 4):
+            t[l0:l0 + 4].copy_(torch.randn(t[l0:l0 + 4].shape, generator=gen, device="cuda").to(torch.bfloat16))
+    torch.cuda.synchronize()
+    out = {}
+    # plain decode
+    eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=steps + 8)
+    eng.graph_capture(0)
+    eng.graph_replay(3)
+    eng.sync()
+    t_a = time.perf_counter()
+    eng.graph_replay(steps)
+    eng.sync()
+    ms = (time.perf_counter() - t_a) / steps * 1e3
+    out["plain_decode"] = {"ms_per_step": round(ms, 4), "tok_per_s": round(streams / ms * 1e3, 1)}
+    prof = eng.profile_step(0, reps=2)
+    out["plain_decode"]["kernel_ms_per_step"] = {kk: round(v[0] / 2, 4) for kk, v in prof.items() if v[1]}
+    # verify an 8-row block per sequence, then the drafter's pass
+    d = SyntheticDrafter.generate(shape, n_layers=2, taps=(35, 47), v=16384, window=1024, seed=args.seed + 5,
+                                  device="cuda", group=64, head_group=8)
+    eng.set_drafter(d)
+    for s in slots:
+        eng.set_draft_rows(s, rows)
+    kr, vr, _ = eng.draft_rings()
+    for t in (kr, vr):
+        t.copy_(torch.randn(t.shape, generator=gen, device="cuda").to(torch.bfloat16))
+    eng.plan([(s, [L.FEED_ROW], False, 1) for s in slots], extra_keys=8)
+    eng.encode(L.STEP_DRAFT)
+    eng.sync()
+    eng.plan([(s, [L.FEED_ROW + i for i in range(rows)], True) for s in slots], extra_keys=rows * (steps + 8))
+    eng.graph_capture(L.STEP_DRAFT)
+    eng.graph_replay(2)
+    eng.sync()
+    t_a = time.perf_counter()
+    eng.graph_replay(steps)
+    eng.sync()
+    ms = (time.perf_counter() - t_a) / steps * 1e3
+    prof = eng.profile_step(L.STEP_DRAFT, reps=2)
+    per = {kk: round(v[0] / 2, 4) for kk, v in prof.items() if v[1]}
+    out["verify_and_draft"] = {"ms_per_step": round(ms, 4), "draft_ms": per.get("draft"), "kernel_ms_per_step": per}
+    eng.close()
+    del model, d
+    torch.cuda.empty_cache()
+    return {"config": {"workload": f"reference model (Limite 48 layers, int8 groups of 64, window 1024, MUDD, value "
+                                   f"embeddings), {streams} sequence(s) x {ctx} ctx, random weights",
+                       "streams": streams, "ctx": ctx}, **out}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -384,6 +469,9 @@ def main() -> int:
     ap.add_argument("--tree-steps", type=int, default=20, help="timed steps of configs[4] (16-node trees x 32; 0: skip)")
     ap.add_argument("--drafter-steps", type=int, default=20,
                     help="timed steps of the drafter's pass (1 and 32 slots, reference drafter shape; 0: skip)")
+    ap.add_argument("--refmodel-steps", type=int, default=20,
+                    help="timed steps of the reference's own model (plain decode and verify + draft, 1 and 32 "
+                         "sequences at 8192 ctx; 0: skip)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--split-keys", type=int, default=0, help="attention keys per split (0: the engine's choice)")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -471,6 +559,14 @@ def main() -> int:
             drafter[f"streams{streams}"] = run_drafter(args, streams, 4096, args.drafter_steps)
             log(f"  {drafter[f'streams{streams}']}")
 
+    refmodel = None
+    if args.refmodel_steps > 0:
+        refmodel = {}
+        for streams in (1, 32):
+            log(f"reference model, {streams} sequence(s)")
+            refmodel[f"streams{streams}"] = run_reference_model(args, streams, 8192, args.refmodel_steps)
+            log(f"  {refmodel[f'streams{streams}']}")
+
     line = {
         "metric": METRIC,
         "value": round(r1["value"], 2),
@@ -497,6 +593,7 @@ def main() -> int:
         "long_ctx_bf16": long_ctx,
         "trees32": s64,
         "drafter": drafter,
+        "reference_model": refmodel,
     }
     print(json.dumps(line), flush=True)
     if args.calibrate_copy:

@@ -547,6 +547,7 @@ typedef struct sv_drafter {
   float inv_temperature;       /* draft_top's 1 / T (drafter.rs: 1 / 0.6)      */
   uint32_t window;             /* the context positions a block row sees      */
 } sv_drafter;
+/* Drops a captured step and the current plan (plan again). */
 sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d);
 /* Draft rows per block (1 + drafts, at most the attention run length) of a slot's next steps
  * with SV_STEP_DRAFT; 0: the slot is not drafted. */

@@ -477,6 +477,19 @@ struct sv_engine {
     return SV_OK;
   }
 
+  // The matmuls' workspace (split-k partials, counters zero at rest), grown to `bytes`.
+  sv_status ensure_mm_ws(size_t bytes) {
+    if (bytes <= mm_ws_bytes) return SV_OK;
+    SV_HIP(hipStreamSynchronize(stream), "matmul workspace");
+    if (mm_ws) SV_HIP(hipFree(mm_ws), "matmul workspace");
+    mm_ws = nullptr;
+    mm_ws_bytes = 0;
+    SV_HIP(hipMalloc(&mm_ws, bytes), "matmul workspace");
+    SV_HIP(hipMemset(mm_ws, 0, bytes), "matmul workspace");
+    mm_ws_bytes = bytes;
+    return SV_OK;
+  }
+
   sv_status upload(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return SV_OK;
     SV_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream), "upload");
@@ -1008,7 +1021,6 @@ extern "C" sv_status sv_engine_get_buffers(sv_engine* e, sv_engine_buffers* o) {
 // the rings (cyclic pages, as the sliding-window layers'), the block rows' buffers.
 extern "C" sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d) {
   if (!e || !d) return fail(SV_ERR_ARG, "set_drafter: null pointer");
-  if (e->graph) return fail(SV_ERR_STATE, "set_drafter: after a graph was captured");
   const sv_shape& s = e->sh;
   const uint32_t H = s.hidden, NKV = s.n_kv_heads, D = s.head_dim;
   if (d->n_layers == 0 || d->n_layers > SV_DRAFT_LAYERS || !d->layers)
@@ -1023,6 +1035,12 @@ extern "C" sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d) {
   if (!e->embed) return fail(SV_ERR_STATE, "set_drafter: no embedding set (sv_engine_set_embed)");
   if (NKV * D / 4 > 256 || D % 4) return fail(SV_ERR_UNSUPPORTED, "set_drafter: %u kv heads x %u dims", NKV, D);
   SV_HIP(hipStreamSynchronize(e->stream), "set_drafter");
+  // a captured step and the plan were laid out without this drafter: both go
+  if (e->graph) {
+    (void)hipGraphExecDestroy(e->graph);
+    e->graph = nullptr;
+  }
+  e->planned = false;
   e->free_drafter();
   sv_drafter dr = *d;
   std::vector<sv_draft_layer> dl(d->layers, d->layers + d->n_layers);
@@ -1116,6 +1134,17 @@ extern "C" sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d) {
     SV_TRY(dalloc(&e->d_tin, 2 * R, "drafter rows"));
     SV_TRY(dalloc(&e->d_vis, R, "drafter rows"));
     SV_TRY(dalloc(&e->d_tiles, 2 * S, "drafter rows"));
+    // the matmul workspace covers the drafter's shapes: the context's at the step's rows, the
+    // blocks' at their rows
+    size_t mws = 0;
+    const uint32_t ctx_mk[][2] = {{H, H}, {d->n_layers * 2 * NKV * D, H}};
+    const uint32_t blk_mk[][2] = {{H, H}, {e->qkv_w, H}, {H, s.n_heads * D}, {2 * s.ffn, H}, {H, s.ffn}, {d->v, H},
+                                  {corr_w ? corr_w : H, H}};
+    for (auto& x : ctx_mk)
+      for (uint32_t r = 1; r <= (uint32_t)T; r++) mws = std::max(mws, matmul_ws_bytes(r, x[0], x[1]));
+    for (auto& x : blk_mk)
+      for (uint32_t r = 1; r <= (uint32_t)R; r++) mws = std::max(mws, matmul_ws_bytes(r, x[0], x[1]));
+    SV_TRY(e->ensure_mm_ws(mws));
     std::vector<uint32_t> tab(S * e->d_max_pages);
     for (size_t slot = 0; slot < S; slot++)
       for (uint32_t pg = 0; pg < e->d_max_pages; pg++)

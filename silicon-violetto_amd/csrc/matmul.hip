@@ -643,7 +643,7 @@ constexpr int GKC = 64;
 // Split-k hand-off counters (skinny and GEMM paths): a region of fixed size at the front of the
 // workspace, so every matmul sharing one workspace finds its counters at zero there, whatever
 // its shape.
-constexpr size_t COUNTER_SLOTS = 16384;
+constexpr size_t COUNTER_SLOTS = 65536;
 
 // Wait for this thread's LDS operations, then the workgroup barrier. Unlike __syncthreads()
 // this leaves global loads in flight (no vmcnt wait).

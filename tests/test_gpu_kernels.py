@@ -605,6 +605,28 @@ def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
         close(got_aux, aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")
 
 
+def test_matmul_head_many_cells(gpu):
+    """The reference model's head at 32 sequences x 8 rows: 151680 rows x 1280 in int8 groups
+    of 64 at n = 256 (the GEMM's k-split cells, rows blocks x token blocks, past 16384),
+    softcapped with the norm folded in; a seeded sample of 8 rows against the oracle."""
+    m, k, n = 151680, 1280, 256
+    banner(f"gemm head m={m} k={k} n={n}")
+    rng = np.random.default_rng(5)
+    w = rng.normal(0, 0.02, (m, k)).astype(np.float32)
+    wq, sc = oracle.quantize(w, 64)
+    mat = K.matrix(torch.from_numpy(wq).cuda(), torch.from_numpy(sc.view(np.int16)).cuda().view(torch.bfloat16), 6)
+    x = rng.normal(0, 1, (n, k)).astype(np.float32)
+    rows = np.sort(rng.choice(n, 8, replace=False)).astype(np.uint32)
+    a_ref = L.MatArgs(len(rows), k, m, L.EPI_HEAD, L.FLAG_NORM_IN, m - 13, 1.0, 0.0, 0.0, 1, k, 6)
+    ref = oracle.matmul(L, wq, sc, 6, x, a_ref, x_rows=rows)
+    y = torch.zeros(n, m, device="cuda")
+    ws = K.Workspace(L.lib().sv_matmul_workspace_bytes(n, m, k))
+    K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_HEAD, flags=L.FLAG_NORM_IN, vocab_real=m - 13, ws=ws)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()[rows]
+    close(got, ref, atol=5e-5 * 23, rtol=1e-4, what="head at 256 rows")
+
+
 @pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
                                                   (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4),
                                                   (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4), (4, 4, 2, 2), (4, 3, 1, 2),
