@@ -444,7 +444,30 @@ def run_reference_model(args, streams: int, ctx: int, steps: int):
     per = {kk: round(v[0] / 2, 4) for kk, v in prof.items() if v[1]}
     out["verify_and_draft"] = {"ms_per_step": round(ms, 4), "draft_ms": per.get("draft"), "kernel_ms_per_step": per}
     eng.close()
-    del model, d
+    del d
+    torch.cuda.empty_cache()
+    if streams == 1:
+        # prefill (docs/performance.md's prefill table): one prompt of `ctx` tokens in chunks of
+        # 512 rows, each a step with its head row only on the last chunk, host planning included
+        chunk = 512
+        eng = violetto.Engine(shape, max_seqs=1, max_step_tokens=chunk, max_seq_len=ctx + 64, max_head_rows=16,
+                              kv_tokens=ctx + 64, page_shift=4, attn_scale=0.1, freq=rope_freq(500000.0, shape.head_dim),
+                              local=model.extras.local, window=1024)
+        eng.set_model(model)
+        prompt = torch.randint(0, shape.vocab_real, (ctx,), generator=gen, device="cuda").cpu().tolist()
+        for rep in range(2):  # the first pass warms the kernels and the allocator
+            s0 = eng.new_seq()
+            torch.cuda.synchronize()
+            t_a = time.perf_counter()
+            for c0 in range(0, ctx, chunk):
+                last = c0 + chunk >= ctx
+                eng.step([(s0, prompt[c0:c0 + chunk], False, 1 if last else 0)])
+            eng.sync()
+            secs = time.perf_counter() - t_a
+            eng.free_seq(s0)
+        out["prefill"] = {"tokens": ctx, "chunk": chunk, "seconds": round(secs, 4), "tok_per_s": round(ctx / secs, 1)}
+        eng.close()
+    del model
     torch.cuda.empty_cache()
     return {"config": {"workload": f"reference model (Limite 48 layers, int8 groups of 64, window 1024, MUDD, value "
                                    f"embeddings), {streams} sequence(s) x {ctx} ctx, random weights",
