@@ -340,6 +340,7 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   extern __shared__ __attribute__((aligned(16))) uint16_t xs_all[];  // [W][n][hi, lo][XROW]
   __shared__ f32x4 red[W][RT][64];
   __shared__ float ssred[W][NT];
+  __shared__ uint32_t last_flag;
   const int lane = threadIdx.x & 63, t = lane & 15, q = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t n = p.n, nwg = gridDim.x, S = p.splits;
@@ -386,15 +387,13 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   f32x4 xr[XD][NT];
 #pragma unroll
   for (int d = 0; d < XD; d++) load_x(xr[d], c0 + d);
-  f32x4 base_pre[RT];
-  uint2 rsc[RT];
-  if (wv == 0) {
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      const uint32_t row0 = (xg * RT + rt) * 16 + 4 * q;
-      if (I8 && p.per_row) rsc[rt] = *(const uint2*)(p.scales + row0);
-      if (p.epi == SV_EPI_RESID && (uint32_t)t < n) base_pre[rt] = *(const f32x4*)(p.base + (size_t)t * p.m + row0);
-    }
+  // wave wv < RT finishes row tile wv: its per-row scales and residual base, requested now
+  f32x4 base_pre[1];
+  uint2 rsc = {0u, 0u};
+  if (wv < RT) {
+    const uint32_t row0 = (xg * RT + wv) * 16 + 4 * q;
+    if (I8 && p.per_row) rsc = *(const uint2*)(p.scales + row0);
+    if (p.epi == SV_EPI_RESID && (uint32_t)t < n) base_pre[0] = *(const f32x4*)(p.base + (size_t)t * p.m + row0);
   }
   float gsc[RT][4];
   if (grouped) load_gscale(gsc, c0);
@@ -532,7 +531,8 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
     }
   }
 
-  // 3. waves' sums in wave order; sums of squares per token.
+  // 3. waves' sums: row tile rt's are added in wave order and finished by wave rt (the tiles'
+  //    epilogues run in parallel); sums of squares per token.
   const bool need_ss = p.epi == SV_EPI_NORM || p.epi == SV_EPI_SWIGLU || (p.flags & SV_FLAG_NORM_IN);
   if (need_ss) {
 #pragma unroll
@@ -544,13 +544,13 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
   for (int rt = 0; rt < RT; rt++) red[wv][rt][lane] = acc[rt];
   __syncthreads();
-  if (wv != 0) return;
+  const bool mine = wv < RT;  // this wave finishes row tile wv
+  const uint32_t rt0 = mine ? (uint32_t)wv : 0u;
+  f32x4 tile = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (mine) {
+    tile = red[0][rt0][lane];
 #pragma unroll
-  for (int rt = 0; rt < RT; rt++) {
-    f32x4 a = red[0][rt][lane];
-#pragma unroll
-    for (int w = 1; w < W; w++) a += red[w][rt][lane];
-    acc[rt] = a;
+    for (int w = 1; w < W; w++) tile += red[w][rt0][lane];
   }
   float ss = 0.0f;
   if (need_ss && (uint32_t)t < NT) {
@@ -558,50 +558,40 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
 #pragma unroll
     for (int w = 1; w < W; w++) ss += ssred[w][t];
   }
+  const uint32_t tg = xg * RT + rt0;  // this wave's row tile (of 16 rows)
   if (S > 1) {
-    // k splits: each split's sums to the workspace (coherent stores), the last split of the
-    // row group to arrive adds them in split order (wave 0 only: it alone wrote).
+    // k splits: each split's tile sums to the workspace (coherent stores), the last split of
+    // the row group to arrive adds them in split order (each wave its own tile).
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part), srs = coherent_rsrc(p.ssp);
     const uint32_t pbase = (xg * S) * RT * 1024, sbase = (xg * S) * 64;
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) store_wt4(prs, pbase + (sp * RT + rt) * 1024 + 16 * lane, acc[rt]);
-    if (lane < 16) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ss), srs, sbase + sp * 64 + 4 * lane, 0, SV_CPOL_SC1);
-    wait_mem();
-    uint32_t old = 0;
-    if (lane == 0) old = __hip_atomic_fetch_add(p.counters + xg, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    old = __builtin_amdgcn_readfirstlane(old);
-    if (old != S - 1) return;
-    if (lane == 0) __hip_atomic_store(p.counters + xg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    f32x4 tot[RT];
+    if (mine) store_wt4(prs, pbase + (sp * RT + rt0) * 1024 + 16 * lane, tile);
+    if (wv == 0 && lane < 16) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ss), srs, sbase + sp * 64 + 4 * lane, 0, SV_CPOL_SC1);
+    if (!arrive_last(p.counters + xg, S, &last_flag)) return;
+    if (!mine) return;
+    f32x4 tot = f32x4{0.f, 0.f, 0.f, 0.f};
     float sst = 0.0f;
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) tot[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t s2 = 0; s2 < S; s2++) {
       if (s2 == sp) {
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) tot[rt] += acc[rt];
+        tot += tile;
         sst += ss;
       } else {
-#pragma unroll
-        for (int rt = 0; rt < RT; rt++) tot[rt] += load_wt4(prs, pbase + (s2 * RT + rt) * 1024 + 16 * lane);
+        tot += load_wt4(prs, pbase + (s2 * RT + rt0) * 1024 + 16 * lane);
         sst += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srs, sbase + s2 * 64 + 4 * t, 0, SV_CPOL_SC1));
       }
     }
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) acc[rt] = tot[rt];
+    tile = tot;
     ss = sst;
   }
+  if (!mine) return;
   if (I8 && p.per_row) {
-#pragma unroll
-    for (int rt = 0; rt < RT; rt++) {
-      acc[rt][0] *= bf(rsc[rt].x & 0xffffu);
-      acc[rt][1] *= bf(rsc[rt].x >> 16);
-      acc[rt][2] *= bf(rsc[rt].y & 0xffffu);
-      acc[rt][3] *= bf(rsc[rt].y >> 16);
-    }
+    tile[0] *= bf(rsc.x & 0xffffu);
+    tile[1] *= bf(rsc.x >> 16);
+    tile[2] *= bf(rsc.y & 0xffffu);
+    tile[3] *= bf(rsc.y >> 16);
   }
   if ((uint32_t)t >= n) return;
-  skinny_epilogue<RT>(p, acc, ss, xg, q, t, base_pre);
+  f32x4 one[1] = {tile};
+  skinny_epilogue<1>(p, one, ss, tg, q, t, base_pre);
 }
 
 // Tiled copy of a row-major matrix (SV_FMT_TILED): one thread per 16-byte word of the
