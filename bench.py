@@ -570,6 +570,11 @@ def main() -> int:
             long_ctx[f"streams{streams}"] = extra_object(
                 r3, f"configs[3]: bf16 weights, {streams} stream(s) x 65536 ctx, k=4 chain, greedy, KV rollback",
                 streams * r3["rows"], 2, f"configs[3]x{streams}")
+            if streams == 1 and args.cpu_steps > 0:
+                # one oracle step (about 2 GB of bf16 weights and 64k keys per layer on the host)
+                steps_saved, args.cpu_steps = args.cpu_steps, 1
+                long_ctx["streams1"]["cpu_baseline"] = cpu_baseline(args, shape, model16, r3, [0], "configs[3]x1", 0.0)
+                args.cpu_steps = steps_saved
             r3["eng"].close()
             torch.cuda.empty_cache()
         del model16
