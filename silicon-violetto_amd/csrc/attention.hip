@@ -88,30 +88,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
   uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
-  // 2 i + mt), requested at once with the split taken as full (kv_off clamps into the table;
-  // tiles past the context are masked later): the batch loop takes its tile offsets with
-  // readlane and never waits for a page-table load (such a wait, vmcnt(0), also waits for every
-  // K/V load in flight). The wave's first batch is requested as soon as they arrive, before
-  // the context length (meta) and while the queries are built; it is read whether or not the
-  // split has keys there (inside its page) and used only if it does.
+  // 2 i + mt) go out with the query words and positions, the split taken as full (indices
+  // clamped into the table; tiles past the context are masked later): the batch loop takes its
+  // tile offsets with readlane and never waits for a page-table load (such a wait, vmcnt(0),
+  // also waits for every K/V load in flight). The rope words follow, then the wave's first
+  // batches (all of them in the all-in-flight variant, R - 1 in the streaming one): s_waitcnt
+  // counts loads in issue order, so the queries, built once the rope words are in, never wait
+  // for a batch, and each batch is read whether or not the split has keys there (inside its
+  // page) and used only if it does.
   // (split <= 3968 keys: at most 31 batches per wave, 62 lanes)
   const uint32_t nbw_full = p.split / 32 > (uint32_t)wv ? (p.split / 32 - wv + 3) / 4 : 0u;
   size_t tile_off = 0;
   const uint32_t ncols = T * p.G;
   bf16x8 qh[NCT][KST], ql[NCT][KST];
   KvBatchT<D> bt[NBW > 0 ? NBW : 1];
-  if constexpr (NBW == 0) {
-    if ((uint32_t)lane < 2 * nbw_full)
-      tile_off = kv_off<D>(p, seq, g, kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1));
-#pragma unroll
-    for (int i = 0; i < R - 1; i++) {
-      const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
-      load_batch_tiles_t<D>(p, toffs, ring[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
-    }
-    p0 = p.meta[2 * t0 + 1];
-    build_queries<D, NCT, false>(p, t0, g, ncols, qh, ql, lane);
-    if (tid < T) svis[tid] = visw;
-  } else {
+  {
     // Queries, positions and page-table words in one round trip; then the rope words, then
     // every batch of the wave (slots past the split's batches read nothing); the queries are
     // built once the rope words are in, while the batches stream.
@@ -136,7 +127,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     }
     const uint32_t tpos = kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1);
     const uint32_t pword = p.page_table[(size_t)seq * p.max_pages + min(tpos >> p.page_shift, p.max_pages - 1)];
-    p0 = p.meta[2 * t0 + 1];
+    if constexpr (!LOCAL) p0 = p.meta[2 * t0 + 1];  // (a window layer read it first: kbeg needs it)
     __builtin_amdgcn_sched_barrier(0);
     // 2. Rope words (they need the positions), then every batch of the wave (they need the
     //    page words; slots past the split's batches read nothing).
@@ -161,10 +152,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
       tile_off = ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
                  (size_t)(tpos & ((1u << p.page_shift) - 1u)) * D;
     }
+    if constexpr (NBW > 0) {
 #pragma unroll
-    for (int i = 0; i < NBW; i++) {
-      const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
-      load_batch_tiles_t<D>(p, toffs, bt[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
+      for (int i = 0; i < NBW; i++) {
+        const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
+        load_batch_tiles_t<D>(p, toffs, bt[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
+      }
+    } else {
+      // the ring's first R - 1 batches (the loop requests each next one R - 1 ahead)
+#pragma unroll
+      for (int i = 0; i < R - 1; i++) {
+        const size_t toffs[2] = {readlane64(tile_off, 2 * i), readlane64(tile_off, 2 * i + 1)};
+        load_batch_tiles_t<D>(p, toffs, ring[i], lane, (uint32_t)i < nbw_full ? 0u : 0x80000000u);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     if (tid < T) svis[tid] = visw;
