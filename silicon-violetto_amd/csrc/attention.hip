@@ -128,25 +128,32 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     const uint32_t tpos = kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1);
     const uint32_t pword = p.page_table[(size_t)seq * p.max_pages + min(tpos >> p.page_shift, p.max_pages - 1)];
     if constexpr (!LOCAL) p0 = p.meta[2 * t0 + 1];  // (a window layer read it first: kbeg needs it)
-    __builtin_amdgcn_sched_barrier(0);
-    // 2. Rope words (they need the positions), then every batch of the wave (they need the
-    //    page words; slots past the split's batches read nothing).
-    //    Rope words through a descriptor whose range is empty without rope (zeros, no
-    //    access), so no branch splits the loads' accounting.
+    // Rope words through a descriptor whose range is empty without rope (zeros, no access), so
+    // no branch splits the loads' accounting. Inline runs: the step's rows by token, in this
+    // same round trip; else the table's rows at the positions, once those are in.
     float2 cs[NCT][KST][4];
-    const __amdgpu_buffer_rsrc_t rrs =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(p.rope), 0, p.rope_on ? 0x7fffffff : 0, 0x00020000);
+    auto load_rope = [&](const float* base, bool by_token) {
+      const __amdgpu_buffer_rsrc_t rrs =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, p.rope_on ? 0x7fffffff : 0, 0x00020000);
 #pragma unroll
-    for (int ct = 0; ct < NCT; ct++)
+      for (int ct = 0; ct < NCT; ct++)
 #pragma unroll
-      for (int ks = 0; ks < KST; ks++)
+        for (int ks = 0; ks < KST; ks++)
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-          const uint32_t j = 16 * ks + 4 * q + jj;
-          const bool on = p.rope_on && 32 * ks + 8 * q < 64;
-          const uint32_t off = (qr.pos[ct] * SV_ROPE_PAIRS + j) * 8 + (on ? 0u : 0x80000000u);
-          cs[ct][ks][jj] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rrs, off, 0, 0));
-        }
+          for (int jj = 0; jj < 4; jj++) {
+            const uint32_t j = 16 * ks + 4 * q + jj;
+            const bool on = p.rope_on && 32 * ks + 8 * q < 64;
+            const uint32_t c = min(16u * ct + c16, ncols - 1);
+            const uint32_t row = by_token ? t0 + c / p.G : qr.pos[ct];
+            const uint32_t off = (row * SV_ROPE_PAIRS + j) * 8 + (on ? 0u : 0x80000000u);
+            cs[ct][ks][jj] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rrs, off, 0, 0));
+          }
+    };
+    if constexpr (INL) load_rope(p.rope_rows, true);
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. (Without inline runs, the rope words: they need the positions.) Then every batch of
+    //    the wave (they need the page words; slots past the split's batches read nothing).
+    if constexpr (!INL) load_rope(p.rope, false);
     if ((uint32_t)lane < 2 * nbw_full) {
       const uint32_t page = min(pword, p.n_pages - 1);
       tile_off = ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
@@ -499,7 +506,8 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts, const uint32_t* host_runs, bool may_fuse, const sv_attn_extras* ex) {
+                      uint32_t parts, const uint32_t* host_runs, bool may_fuse, const sv_attn_extras* ex,
+                      const float* rope_rows) {
   if (!sh || !qkv || !meta || !k_cache || !v_cache || !page_table || !kv || !args || !runs || !vis || !out)
     return fail(SV_ERR_ARG, "attn_verify: null pointer");
   if (n_runs == 0) return SV_OK;
@@ -576,7 +584,9 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.xsa = ex ? ex->d_xsa : nullptr;
   p.vdir = ex && ex->d_xsa ? ex->d_vdir : nullptr;
   p.H = ex ? ex->hidden : 0u;
-  if (host_runs && n_runs <= SV_INLINE_RUNS) {
+  p.rope_rows = rope_rows;
+  // inline runs take the queries' rope words from the step's rows by token
+  if (host_runs && rope_rows && n_runs <= SV_INLINE_RUNS) {
     p.n_inline = n_runs;
     for (uint32_t i = 0; i < 3 * n_runs; i++) p.inl[i] = host_runs[i];
   }

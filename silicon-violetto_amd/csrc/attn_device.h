@@ -15,6 +15,9 @@ struct AttnParams {
   uint16_t* vc;
   const uint32_t* page_table;
   const float* rope;
+  // The step's rope words by token (the table's row at each token's position, written by the
+  // embed kernel): with inline runs the queries' rope words need no position first.
+  const float* rope_rows;
   const uint32_t* runs;
   const uint32_t* vis;
   float* out;
@@ -588,7 +591,8 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
         const uint32_t d = DL * l16 + e;
         float k0 = kv[e] * inv, k1 = kv[e + 1] * inv;
         if (p.rope_on && d < 64) {
-          const float2 cs = *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
+          const float2 cs = p.rope_rows ? *(const float2*)(p.rope_rows + ((size_t)t * SV_ROPE_PAIRS + d / 2) * 2)
+                                        : *(const float2*)(p.rope + ((size_t)pos * SV_ROPE_PAIRS + d / 2) * 2);
           const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
           k0 = r0;
           k1 = r1;

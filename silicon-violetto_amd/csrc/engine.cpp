@@ -327,6 +327,7 @@ struct sv_engine {
   size_t kv_elems = 0;
   uint32_t* page_table = nullptr;
   float* rope = nullptr;
+  float* rope_rows = nullptr;  // [max_step_tokens][32 pairs]: the table's row at each step row's position
   uint32_t *lens = nullptr, *feed = nullptr, *tree = nullptr, *trace = nullptr, *trace_len = nullptr;
   sv_gen_state* gen = nullptr;
   // device: one step set (plan.rs writes these per step)
@@ -395,7 +396,7 @@ struct sv_engine {
 
   ~sv_engine() {
     if (graph) (void)hipGraphExecDestroy(graph);
-    void* bufs[] = {k_cache, v_cache, page_table, rope, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
+    void* bufs[] = {k_cache, v_cache, page_table, rope, rope_rows, lens, feed, tree, trace, trace_len, gen, tokens, tok_res, tin, vis,
                     head_rows, attn_runs, sample_rows, runs, out_ids, emitted, meta, path, path_len, on_path, h, qkv,
                     attn, mixed, act, inv, logits, ws, mm_ws, k_local, v_local, local_table, h0, xattn, rbase, vdir};
     for (void* b : bufs)
@@ -542,7 +543,8 @@ struct sv_engine {
     const Plan& P = plan;
     const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
     SV_TIMED(SV_KIND_EMBED,
-             embed_launch(stream, &sh, embed, tokens, tok_res, emb_out(), tin, meta, lens, feed, tree, vis, n));
+             embed_launch(stream, &sh, embed, tokens, tok_res, emb_out(), tin, meta, lens, feed, tree, vis, n, rope,
+                          rope_rows, cfg.max_seq_len + SV_FEED_W));
     sv_attn_args aa{};
     aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
     for (uint32_t li = 0; li < sh.n_layers; li++) {
@@ -572,11 +574,13 @@ struct sv_engine {
       const uint32_t* tab = table_of(li);
       if (P.chunk)
         SV_TIMED(SV_KIND_KV_WRITE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
-                                               P.max_run, vis, attn, ws, ws_bytes, 4, P.inl.data(), true, exp_));
+                                               P.max_run, vis, attn, ws, ws_bytes, 4, P.inl.data(), true, exp_,
+                                               rope_rows));
       SV_TIMED(SV_KIND_ATTN, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
-                                         P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data(), true, exp_));
+                                         P.max_run, vis, attn, ws, ws_bytes, 1, P.inl.data(), true, exp_, rope_rows));
       SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
-                                               P.max_run, vis, attn, ws, ws_bytes, 2, P.inl.data(), true, exp_));
+                                               P.max_run, vis, attn, ws, ws_bytes, 2, P.inl.data(), true, exp_,
+                                               rope_rows));
       SV_TIMED(SV_KIND_O, matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn,
                                  resid, nullptr));
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
@@ -790,6 +794,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   ALLOC(out_ids, std::max(n, R));
   ALLOC(emitted, S);
   ALLOC(meta, 2 * (size_t)n);
+  ALLOC(rope_rows, (size_t)n * SV_ROPE_PAIRS * 2);
   ALLOC(path, (size_t)S * SV_FEED_W);
   ALLOC(path_len, S);
   ALLOC(on_path, n);

@@ -66,7 +66,9 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint32_t parts = 3,  // bit 0: attention, bit 1: the split merge, bit 2: runs' new K/V first
                       const uint32_t* host_runs = nullptr,  // (first token, rows, slot) per run, if known
                       bool may_fuse = true,  // the counted last-split merge may be used (tests select it)
-                      const sv_attn_extras* ex = nullptr);  // the layer's extras (null: none)
+                      const sv_attn_extras* ex = nullptr,   // the layer's extras (null: none)
+                      // the step's rope words by token (embed_launch writes them); inline runs need them
+                      const float* rope_rows = nullptr);
 // attn_launch with the split partials in the library's per-device static scratch array.
 sv_status attn_launch_noalloc(hipStream_t stream, const sv_shape* sh, const float* qkv, const uint32_t* meta,
                               uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
@@ -77,7 +79,9 @@ size_t attn_scratch_bytes();
 // tokens_out may equal tokens (resolution in place, as the reference's embed).
 sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,
                        uint32_t* tokens_out, float* out, const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
-                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n);
+                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n,
+                       const float* rope = nullptr,  // with rope_rows: the table's row at each token's position
+                       float* rope_rows = nullptr, uint32_t rope_n = 0);  // rope_n: the table's rows
 sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
                               uint32_t hidden);
 sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,

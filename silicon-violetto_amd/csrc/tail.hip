@@ -24,7 +24,8 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, const
                                                     uint32_t* tokens_out, float* out,
                                                     const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
                                                     const uint32_t* feed, const uint32_t* tree, uint32_t* vis,
-                                                    uint32_t H, uint32_t vocab) {
+                                                    uint32_t H, uint32_t vocab, const float* rope, float* rope_rows,
+                                                    uint32_t rope_n) {
   __shared__ float red[4];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   const uint32_t slot = tin[2 * t];
@@ -48,6 +49,9 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, const
     meta[2 * t] = slot;
     meta[2 * t + 1] = lens[slot] + depth;
   }
+  // the rope table's row at this token's position, for the layers' attention (by token)
+  if (rope_rows && tid < 2 * SV_ROPE_PAIRS)
+    rope_rows[(size_t)t * 2 * SV_ROPE_PAIRS + tid] = rope[(size_t)min(lens[slot] + depth, rope_n - 1) * 2 * SV_ROPE_PAIRS + tid];
   for (uint32_t i = tid; i < H; i += 256) out[(size_t)t * H + i] = bf(row[i]) * inv;
 }
 
@@ -428,12 +432,14 @@ __global__ __launch_bounds__(256) void step_tail_kernel(TailParams p) {
 
 sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,
                        uint32_t* tokens_out, float* out, const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
-                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n) {
+                       const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n, const float* rope,
+                       float* rope_rows, uint32_t rope_n) {
   if (!sh || !table || !tokens || !tokens_out || !out || !tin || !meta || !lens || !feed || !tree || !vis)
     return fail(SV_ERR_ARG, "embed: null pointer");
+  if (rope_rows && (!rope || rope_n == 0)) return fail(SV_ERR_ARG, "embed: rope rows without the table");
   if (n == 0) return SV_OK;
   launch(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, tokens_out, out, tin, meta, lens, feed,
-                     tree, vis, sh->hidden, sh->vocab);
+                     tree, vis, sh->hidden, sh->vocab, rope, rope_rows, rope_n);
   return check_launch("embed");
 }
 
