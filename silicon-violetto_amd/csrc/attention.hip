@@ -85,8 +85,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   // A sliding-window layer's splits start at its first query's window (its position first).
   uint32_t p0 = LOCAL ? p.meta[2 * t0 + 1] : 0u;
   const uint32_t kbeg = (LOCAL ? key_base_t<true>(p, p0) : 0u) + s * p.split;
-  // this wave's V stage (2 tiles x 16 keys x D bf16), at the front of the reduction buffer
-  uint16_t* stage = (uint16_t*)lds + (size_t)wv * 32 * D;
+  // this wave's V stage (2 tiles x 16 keys), at the front of the reduction buffer
+  uint16_t* stage = (uint16_t*)((char*)lds + (size_t)wv * stage_bytes<D>());
   // Page-table lookups of this wave's batches wv + 4 i of the split (tile mt of batch i in lane
   // 2 i + mt) go out with the query words and positions, the split taken as full (indices
   // clamped into the table; tiles past the context are masked later): the batch loop takes its
@@ -610,7 +610,8 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   }
   if (parts & 1) {
     dim3 grid(args->max_splits, NKV, n_runs);
-    const size_t shm = (size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4;
+    // the reduction buffer, at least the 4 waves' V stages (2 x 16 rows of 2 D + 32 bytes) it holds
+    const size_t shm = std::max((size_t)4 * maxcols * D * 4 + (size_t)4 * maxcols * 4, (size_t)4 * 32 * (2 * D + 32));
     const bool inl = p.n_inline != 0;
 #define SV_ATTN3(DD, N, B)                                                          \
   do {                                                                              \

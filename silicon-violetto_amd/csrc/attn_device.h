@@ -319,7 +319,17 @@ __device__ __forceinline__ void load_batch_new_t(const uint16_t* nk, const uint1
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
-// compute_batch's semantics with V through the wave's LDS stage (2 tiles x 16 x D bf16).
+// Bytes per key row of the V stage: 2 D plus 32, an odd multiple of 32 bytes, so the 32-byte
+// slabs that a transposing read takes from 8 consecutive rows fall on 8 different bank groups
+// (at 2 D = 128 bytes, rows alternated between two: a 4-way conflict on gfx950's 256-byte
+// banks); the stage's 16-byte writes stay 8 consecutive lanes to one row.
+template <int D>
+constexpr uint32_t stage_row() { return 2 * D + 32; }
+template <int D>
+constexpr uint32_t stage_bytes() { return 32 * stage_row<D>(); }  // 2 tiles x 16 keys
+
+// compute_batch's semantics with V through the wave's LDS stage (2 tiles x 16 keys, rows of
+// stage_row bytes).
 // Keys at or past kend that a partial batch read from their page get V rows of zero, so
 // whatever the cache holds there cannot reach the sums (p is 0 for them).
 // clo: each lane column's first visible cached key (key_lo; 0 on global layers); a FULL batch
@@ -342,7 +352,8 @@ __device__ __forceinline__ void compute_batch_t(const AttnParams& p, const KvBat
         const uint32_t row = (16 * lane + 1024 * v) / (2 * D);
         if (kb + 16 * mt + row >= kend) w = u32x4{0u, 0u, 0u, 0u};
       }
-      *(u32x4*)((char*)stage + mt * 32 * D + 16 * lane + 1024 * v) = w;
+      const uint32_t byte = 16 * lane + 1024 * v;
+      *(u32x4*)((char*)stage + (16 * mt + byte / (2 * D)) * stage_row<D>() + byte % (2 * D)) = w;
     }
   // S^T tiles: lane holds keys kb + 16 mt + 4 q + i, column 16 ct + c16.
   f32x4 S[2][NCT];
@@ -387,11 +398,11 @@ __device__ __forceinline__ void compute_batch_t(const AttnParams& p, const KvBat
   // O^T[dt] (rows: dims 16 dt + 4 q + i) += V^T[dt] P^T; the A operand's k slots 4 mt + t are
   // keys kb + 16 mt + 4 q + t (P's layout), read transposed: lane (i, q) addresses key
   // 4 q + i / 4 of tile mt, dims 16 dt + 4 (i % 4) .. + 3.
-  const uint32_t rd = (uint32_t)(4 * q + c16 / 4) * 2 * D + (uint32_t)(4 * (c16 % 4)) * 2;
+  const uint32_t rd = (uint32_t)(4 * q + c16 / 4) * stage_row<D>() + (uint32_t)(4 * (c16 % 4)) * 2;
 #pragma unroll
   for (int dt = 0; dt < VE; dt++) {
     const i16x4 h0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((char*)stage + rd + 32 * dt));
-    const i16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((char*)stage + 32 * D + rd + 32 * dt));
+    const i16x4 h1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)((char*)stage + 16 * stage_row<D>() + rd + 32 * dt));
     const u32x4 a = u32x4{__builtin_bit_cast(u32x2, h0)[0], __builtin_bit_cast(u32x2, h0)[1],
                           __builtin_bit_cast(u32x2, h1)[0], __builtin_bit_cast(u32x2, h1)[1]};
     const bf16x8 av = __builtin_bit_cast(bf16x8, a);

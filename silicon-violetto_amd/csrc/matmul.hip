@@ -699,16 +699,19 @@ __device__ __forceinline__ void gemm_epilogue(const MMParams& p, const f32x4 (&a
 template <int FMT, int RTW, int NT, bool GROUPED, int GD>
 __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   static_assert(GD % 2 == 0, "chunk parity = slot parity");
+  constexpr int NTH = 256;
   constexpr int BN = 16 * NT;
   constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
   constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;  // dwordx4 per lane per row tile per chunk
   constexpr int PAIRS = BN * 8;                 // (token, 8-k group) pairs per chunk
-  constexpr int PPT = (PAIRS + 255) / 256;      // pairs per thread
-  // LDS: [2 buffers][NT][2 k-steps x (hi, lo)][80 slots] of 16 bytes; lane (t, q) of k-step
-  // ks reads slot t + 16 q + 2 (2 q + ks): each quarter-wave reads 16 consecutive slots, and
-  // the writers (8 lanes per token, k groups g = 2 q + ks) land on 16 different bank groups per
-  // 16 lanes (unpadded, the 8 lanes of a token shared 4 banks: an 8-way conflict).
-  __shared__ u32x4 xs[2][NT][4][80];
+  constexpr int PPT = (PAIRS + NTH - 1) / NTH;  // pairs per thread
+  // LDS: [2 buffers][NT][hi, lo][128 slots] of 16 bytes; lane (t, q) of k-step ks reads slot
+  // 64 ks + 16 q + (t ^ (4 ks + q)). gfx950 serves a 16-byte read conflict-free when every
+  // quarter-wave starts at a multiple of 16 slots and its lanes keep their slot mod 16 up to a
+  // permutation within groups of 8 lanes (the XOR only flips the low three bits); a 16-byte
+  // write, when each 8 consecutive lanes hit 8 different slots mod 8: the writers of one token
+  // (8 lanes, k groups g = 2 q + ks) get t ^ (4 ks + q), 8 different values mod 8.
+  __shared__ u32x4 xs[2][NT][2][128];
   __shared__ float ssp[BN][8];
   __shared__ uint32_t last_flag;
   const int tid = threadIdx.x, lane = tid & 63, t16 = lane & 15, q = lane >> 4;
@@ -722,7 +725,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   const uint32_t item = xcd * xq + min(xcd, nwg % 8) + blockIdx.x / 8;
   const uint32_t tblk = item % n_tblk, sp = (item / n_tblk) % S, rblk = item / (n_tblk * S);
   const uint32_t t0 = tblk * BN;
-  const uint32_t row0 = rblk * 64 * RTW + wv * 16 * RTW;  // this wave's first row
+  const uint32_t row0 = (rblk * 4 + wv) * 16 * RTW;  // this wave's first row
   const uint32_t nc = __builtin_amdgcn_readfirstlane(p.k / GKC / S);
   const uint32_t cb = __builtin_amdgcn_readfirstlane(sp * nc);
 
@@ -738,7 +741,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   uint32_t xoff[PPT];
 #pragma unroll
   for (int j = 0; j < PPT; j++) {
-    const int i = tid + 256 * j;
+    const int i = tid + NTH * j;
     const uint32_t tt = t0 + i / 8;
     const bool v = i < PAIRS && tt < p.n;
     xoff[j] = v ? ((p.x_rows ? p.x_rows[tt] : tt) * p.k + 8 * (i % 8)) * 4 : OOB;
@@ -769,7 +772,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   auto store_x = [&](int buf, const f32x4 (&xr)[PPT][2]) {
 #pragma unroll
     for (int j = 0; j < PPT; j++) {
-      const int i = tid + 256 * j;
+      const int i = tid + NTH * j;
       if (i >= PAIRS) continue;
       float v[8];
 #pragma unroll
@@ -782,9 +785,9 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
       bf16x8 h, l;
       split8(v, h, l);
       const int tok = i / 8, g8 = i % 8, qq = g8 >> 1, ks = g8 & 1;
-      const int slot = (tok & 15) + 16 * qq + 2 * g8;
-      xs[buf][tok >> 4][2 * ks][slot] = __builtin_bit_cast(u32x4, h);
-      xs[buf][tok >> 4][2 * ks + 1][slot] = __builtin_bit_cast(u32x4, l);
+      const int slot = 64 * ks + 16 * qq + ((tok & 15) ^ (4 * ks + qq));
+      xs[buf][tok >> 4][0][slot] = __builtin_bit_cast(u32x4, h);
+      xs[buf][tok >> 4][1][slot] = __builtin_bit_cast(u32x4, l);
     }
   };
   const uint32_t ng = p.per_row ? 1u : p.k >> p.gshift;
@@ -837,9 +840,9 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
         }
 #pragma unroll
         for (int n = 0; n < NT; n++) {
-          const int slot = lane + 2 * (2 * q + ks);
-          const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][2 * ks][slot]);
-          const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][2 * ks + 1][slot]);
+          const int slot = 64 * ks + 16 * q + (t16 ^ (4 * ks + q));
+          const bf16x8 bh = __builtin_bit_cast(bf16x8, xs[buf][n][0][slot]);
+          const bf16x8 bl = __builtin_bit_cast(bf16x8, xs[buf][n][1][slot]);
 #pragma unroll
           for (int r = 0; r < RTW; r++) {
             f32x4& g = GROUPED ? grp[GROUPED ? r : 0][GROUPED ? n : 0] : acc[r][n];
@@ -885,7 +888,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   // Sums of squares per token: the thread's pairs, then the 8 k groups in order.
 #pragma unroll
   for (int j = 0; j < PPT; j++) {
-    const int i = tid + 256 * j;
+    const int i = tid + NTH * j;
     if (i < PAIRS) ssp[i / 8][i % 8] = ssacc[j];
   }
   __syncthreads();
@@ -904,16 +907,16 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
     // [cell][split][BN] sums of squares; the last split of the cell adds them in split order.
     const uint32_t cell = rblk * n_tblk + tblk;
     const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part), srs = coherent_rsrc(p.ssp);
-    constexpr uint32_t PER = 256 * RTW * NT * 16;
+    constexpr uint32_t PER = NTH * RTW * NT * 16;
     const uint32_t pb = (cell * S) * PER;
 #pragma unroll
     for (int r = 0; r < RTW; r++)
 #pragma unroll
-      for (int n = 0; n < NT; n++) store_wt4(prs, pb + sp * PER + ((r * NT + n) * 256 + tid) * 16, acc[r][n]);
-    if (tid < BN)
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ssp[tid][0] + ssp[tid][1] + ssp[tid][2] + ssp[tid][3] +
-                                                            ssp[tid][4] + ssp[tid][5] + ssp[tid][6] + ssp[tid][7]),
-                                            srs, ((cell * S + sp) * BN + tid) * 4, 0, SV_CPOL_SC1);
+      for (int n = 0; n < NT; n++) store_wt4(prs, pb + sp * PER + ((r * NT + n) * NTH + tid) * 16, acc[r][n]);
+    for (int tt = tid; tt < BN; tt += NTH)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ssp[tt][0] + ssp[tt][1] + ssp[tt][2] + ssp[tt][3] +
+                                                            ssp[tt][4] + ssp[tt][5] + ssp[tt][6] + ssp[tt][7]),
+                                            srs, ((cell * S + sp) * BN + tt) * 4, 0, SV_CPOL_SC1);
     if (!arrive_last(p.counters + cell, S, &last_flag)) return;
 #pragma unroll
     for (int r = 0; r < RTW; r++)
@@ -925,7 +928,7 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
 #pragma unroll
       for (int r = 0; r < RTW; r++)
 #pragma unroll
-        for (int n = 0; n < NT; n++) acc[r][n] += load_wt4(prs, pb + s2 * PER + ((r * NT + n) * 256 + tid) * 16);
+        for (int n = 0; n < NT; n++) acc[r][n] += load_wt4(prs, pb + s2 * PER + ((r * NT + n) * NTH + tid) * 16);
 #pragma unroll
       for (int n = 0; n < NT; n++)
         ssn[n] += __uint_as_float(
@@ -945,10 +948,316 @@ __global__ __launch_bounds__(256) void mm_gemm(MMParams p, uint32_t n_tblk) {
   }
 }
 
+// 32 x 32 x 16 GEMM (n > 16 rows). gfx950 runs v_mfma_f32_32x32x16_bf16 (32,768 flops) in
+// about the time v_mfma_f32_16x16x32_bf16 (16,384 flops) takes when both stream back to back
+// (measured: 2.2 vs 1.2 PFLOP/s), so the 32-wide tile halves the matrix-core time of the same
+// product. Same structure as mm_gemm: NW waves (4 or 8), BM = 32 RT NW rows (RT 32-row tiles per wave),
+// BN = 32 NT tokens, 1/S of k, chunks of 64 k in a software pipeline GD deep, X split once per
+// workgroup into LDS, k splits merged by the last split to arrive.
+//   - MFMA lane (c, h) = (lane % 32, lane / 32) supplies A row c and B column c with 8 k per
+//     step; the chunk's k order is permuted (the same way for A and B): step ks, lane half h,
+//     element e is k = 32 h + 8 ks + e. So a lane's weights for a chunk are 32 consecutive k of
+//     its row: two 16-byte words (bf16: four) of the tiled layout, word q = 2 h + qq of the
+//     lane's 16-row block.
+//   - X in LDS as [hi, lo][4 steps][2 halves][32 columns] 16-byte slots, the column XOR-ed
+//     with 4 h + ks (< 8): reads of a quarter-wave start at a multiple of 16 slots and keep the
+//     slot order up to a permutation within 8 lanes, writes of a token's 8 k groups land on 8
+//     different slots mod 8 (both conflict-free on gfx950).
+//   - Lane (c, h) receives rows 8 j + 4 h + i (j, i = 0..3) of token c: f32x4 row groups, so
+//     the epilogue (rms-norm fold, SwiGLU pairs, residual) is the 16-wide one per group.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+template <int FMT, int RT, int NT, int GD, int NW, int CPI>
+__global__ __launch_bounds__(NW * 64) void mm_gemm32(MMParams p, uint32_t n_tblk) {
+  static_assert(GD % (2 * CPI) == 0, "iteration parity = buffer parity");
+  constexpr int BN = 32 * NT;
+  constexpr int ESZ = FMT == SV_FMT_I8 ? 1 : 2;
+  constexpr int WL = FMT == SV_FMT_I8 ? 1 : 2;  // 16-byte words per lane per 16 k
+  constexpr int NTH = NW * 64;
+  constexpr int PAIRS = BN * 8;                 // (token, 8-k group) pairs per chunk
+  constexpr int PPT = (PAIRS + NTH - 1) / NTH;  // pairs per thread
+  __shared__ u32x4 xs[2][CPI][NT][2][256];  // [buffer][chunk of the iteration]
+  __shared__ float ssp[BN][8];
+  __shared__ uint32_t last_flag;
+  const int tid = threadIdx.x, lane = tid & 63, c32 = lane & 31, h = lane >> 5;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // Work items dealt to XCDs as in mm_gemm (token block fastest within an XCD's range).
+  const uint32_t nwg = gridDim.x, S = p.splits;
+  const uint32_t xcd = blockIdx.x % 8, xq = nwg / 8;
+  const uint32_t item = xcd * xq + min(xcd, nwg % 8) + blockIdx.x / 8;
+  const uint32_t tblk = item % n_tblk, sp = (item / n_tblk) % S, rblk = item / (n_tblk * S);
+  const uint32_t t0 = tblk * BN;
+  const uint32_t row0 = (rblk * NW + wv) * 32 * RT;  // this wave's first row
+  const uint32_t nc = __builtin_amdgcn_readfirstlane(p.k / GKC / S);
+  const uint32_t cb = __builtin_amdgcn_readfirstlane(sp * nc);
+
+  const __amdgpu_buffer_rsrc_t xrs = coherent_rsrc(p.x), wrs = coherent_rsrc(p.w);
+  constexpr uint32_t OOB = 0x80000000u;
+  // Weights: lane (c, h) takes row c of the wave's 32-row tile r (16-row block c / 16, row
+  // c % 16), words q = 2 h, 2 h + 1 of each chunk.
+  const uint32_t tile_bytes = 16 * p.k * ESZ;  // one 16-row block over all k
+  const uint32_t wl = p.tiled ? (uint32_t)(c32 >> 4) * tile_bytes + (uint32_t)((c32 & 15) + 32 * h) * 16
+                              : ((uint32_t)c32 * p.k + 32 * h) * ESZ;
+  const uint32_t chunk_bytes = p.tiled ? 1024 * ESZ : 64 * ESZ, qq_bytes = p.tiled ? 256 : 16 * ESZ,
+                 v_bytes = p.tiled ? 1024 : 16;
+  uint32_t xoff[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    const int i = tid + NTH * j;
+    const uint32_t tt = t0 + i / 8;
+    xoff[j] = i < PAIRS && tt < p.n ? ((p.x_rows ? p.x_rows[tt] : tt) * p.k + 8 * (i % 8)) * 4 : OOB;
+  }
+  auto load_x = [&](uint32_t c, f32x4 (&xr)[PPT][2]) {
+    const uint32_t so = __builtin_amdgcn_readfirstlane((cb + min(c, nc - 1)) * GKC * 4);
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      const uint32_t vo = c < nc ? xoff[j] : OOB;
+      xr[j][0] = __builtin_bit_cast(f32x4, buf_ld16(xrs, vo, so));
+      xr[j][1] = __builtin_bit_cast(f32x4, buf_ld16(xrs, vo + 16, so));
+    }
+  };
+  auto load_w = [&](uint32_t c, u32x4 (&wr)[RT][2 * WL]) {
+    const uint32_t cc = c < nc ? cb + c : 0u;
+    const uint32_t vo = c < nc ? wl : OOB;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int qq = 0; qq < 2; qq++)
+#pragma unroll
+        for (int v = 0; v < WL; v++) {
+          const uint32_t rbase = p.tiled ? (row0 / 16 + 2 * r) * tile_bytes : (row0 + 32 * r) * p.k * ESZ;
+          wr[r][qq * WL + v] =
+              buf_ld16(wrs, vo, __builtin_amdgcn_readfirstlane(rbase + cc * chunk_bytes + qq * qq_bytes + v * v_bytes));
+        }
+  };
+  float ssacc[PPT];
+#pragma unroll
+  for (int j = 0; j < PPT; j++) ssacc[j] = 0.0f;
+  auto store_x = [&](int buf, int u, const f32x4 (&xr)[PPT][2]) {
+#pragma unroll
+    for (int j = 0; j < PPT; j++) {
+      const int i = tid + NTH * j;
+      if (PAIRS % NTH != 0 && i >= PAIRS) continue;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[e] = xr[j][0][e];
+        v[4 + e] = xr[j][1][e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) ssacc[j] = __builtin_fmaf(v[e], v[e], ssacc[j]);
+      bf16x8 hv, lv;
+      split8(v, hv, lv);
+      const int tok = i / 8, g8 = i % 8;  // k group g8 = 4 h + ks
+      const int slot = 64 * (g8 & 3) + 32 * (g8 >> 2) + ((tok & 31) ^ g8);
+      xs[buf][u][tok >> 5][0][slot] = __builtin_bit_cast(u32x4, hv);
+      xs[buf][u][tok >> 5][1][slot] = __builtin_bit_cast(u32x4, lv);
+    }
+  };
+
+  // Two accumulator sets (even and odd k-steps) halve the chain of dependent products.
+  f32x16 acc[RT][NT], acc2[RT][NT];
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int n = 0; n < NT; n++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[r][n][e] = acc2[r][n][e] = 0.0f;
+
+  f32x4 xr[GD][PPT][2];
+  u32x4 wr[GD][RT][2 * WL];
+#pragma unroll
+  for (int d = 0; d < GD; d++) {
+    load_w(d, wr[d]);
+    load_x(d, xr[d]);
+  }
+#pragma unroll
+  for (int u = 0; u < CPI; u++) {
+    store_x(0, u, xr[u]);
+    load_x(GD + u, xr[u]);
+  }
+  lds_barrier();
+
+  // CPI chunks per barrier: chunks c .. c + CPI - 1 multiplied from LDS buffer `buf` while
+  // chunks c + CPI .. are split into the other.
+  for (uint32_t c0 = 0; c0 < nc; c0 += GD) {
+#pragma unroll
+    for (int d = 0; d < GD; d += CPI) {
+      const uint32_t c = c0 + d;
+      const int buf = (d / CPI) & 1;
+      u32x4 cur[CPI][RT][2 * WL];
+#pragma unroll
+      for (int u = 0; u < CPI; u++) {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+          for (int v = 0; v < 2 * WL; v++) cur[u][r][v] = wr[d + u][r][v];
+        load_w(c + u + GD, wr[d + u]);
+      }
+      // Every B operand of the iteration is requested before the first product (one LDS
+      // wait per iteration instead of one per k-step).
+      bf16x8 bx[CPI][4][NT][2];
+#pragma unroll
+      for (int u = 0; u < CPI; u++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+          const int slot = 64 * ks + 32 * h + (c32 ^ (4 * h + ks));
+#pragma unroll
+          for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int hl = 0; hl < 2; hl++) bx[u][ks][n][hl] = __builtin_bit_cast(bf16x8, xs[buf][u][n][hl][slot]);
+        }
+      __builtin_amdgcn_sched_barrier(0);
+      // The next iteration's X (requested GD - CPI chunks ago) to the other buffer while this
+      // iteration's operands arrive, then the chunks GD further requested into its registers:
+      // the split's VALU work overlaps the LDS reads' latency, and the products the writes'.
+#pragma unroll
+      for (int u = 0; u < CPI; u++) {
+        const int dn = (d + CPI + u) % GD;
+        store_x(buf ^ 1, u, xr[dn]);
+        load_x(c + CPI + u + GD, xr[dn]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < CPI; u++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+          bf16x8 a[RT];
+#pragma unroll
+          for (int r = 0; r < RT; r++) {
+            if (FMT == SV_FMT_I8) {
+              const u32x4 w = cur[u][r][ks >> 1];
+              a[r] = i8x8_to_bf(w[2 * (ks & 1)], w[2 * (ks & 1) + 1]);
+            } else {
+              a[r] = __builtin_bit_cast(bf16x8, cur[u][r][ks]);
+            }
+          }
+#pragma unroll
+          for (int n = 0; n < NT; n++)
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+              f32x16& g = (ks & 1) ? acc2[r][n] : acc[r][n];
+              g = mfma32(a[r], bx[u][ks][n][0], g);
+              g = mfma32(a[r], bx[u][ks][n][1], g);
+            }
+        }
+      lds_barrier();
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int n = 0; n < NT; n++) acc[r][n] += acc2[r][n];
+  // Per-row int8 scales: lane (c, h) holds rows 8 j + 4 h + i of each tile.
+  if (FMT == SV_FMT_I8) {
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint2 sw = *(const uint2*)(p.scales + row0 + 32 * r + 8 * j + 4 * h);
+        const float s0 = __uint_as_float(sw.x << 16), s1 = __uint_as_float(sw.x & 0xffff0000u),
+                    s2 = __uint_as_float(sw.y << 16), s3 = __uint_as_float(sw.y & 0xffff0000u);
+#pragma unroll
+        for (int n = 0; n < NT; n++) {
+          acc[r][n][4 * j + 0] *= s0;
+          acc[r][n][4 * j + 1] *= s1;
+          acc[r][n][4 * j + 2] *= s2;
+          acc[r][n][4 * j + 3] *= s3;
+        }
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < PPT; j++) {
+    const int i = tid + NTH * j;
+    if (i < PAIRS) ssp[i / 8][i % 8] = ssacc[j];
+  }
+  __syncthreads();
+  float ssn[NT];
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    const uint32_t tl = 32 * n + c32;
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += ssp[tl][e];
+    ssn[n] = ss;
+  }
+
+  if (S > 1) {
+    // [cell][split][NTH threads][RT NT 4] f32x4 and [cell][split][BN] sums of squares; the
+    // last split of the cell adds them in split order.
+    const uint32_t cell = rblk * n_tblk + tblk;
+    const __amdgpu_buffer_rsrc_t prs = coherent_rsrc(p.part), srs = coherent_rsrc(p.ssp);
+    constexpr uint32_t PER = NTH * RT * NT * 64;
+    const uint32_t pb = (cell * S) * PER;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          store_wt4(prs, pb + sp * PER + (((r * NT + n) * 4 + j) * NTH + tid) * 16,
+                    f32x4{acc[r][n][4 * j], acc[r][n][4 * j + 1], acc[r][n][4 * j + 2], acc[r][n][4 * j + 3]});
+    for (int tt = tid; tt < BN; tt += NTH)
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ssp[tt][0] + ssp[tt][1] + ssp[tt][2] + ssp[tt][3] +
+                                                            ssp[tt][4] + ssp[tt][5] + ssp[tt][6] + ssp[tt][7]),
+                                            srs, ((cell * S + sp) * BN + tt) * 4, 0, SV_CPOL_SC1);
+    if (!arrive_last(p.counters + cell, S, &last_flag)) return;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int n = 0; n < NT; n++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[r][n][e] = 0.0f;
+#pragma unroll
+    for (int n = 0; n < NT; n++) ssn[n] = 0.0f;
+    for (uint32_t s2 = 0; s2 < S; s2++) {
+#pragma unroll
+      for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int n = 0; n < NT; n++)
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const f32x4 v = load_wt4(prs, pb + s2 * PER + (((r * NT + n) * 4 + j) * NTH + tid) * 16);
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc[r][n][4 * j + i] += v[i];
+          }
+#pragma unroll
+      for (int n = 0; n < NT; n++)
+        ssn[n] += __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(srs, ((cell * S + s2) * BN + 32 * n + c32) * 4, 0, SV_CPOL_SC1));
+    }
+  }
+
+  // Epilogue: each (tile, token tile, j) is a group of 4 rows for token t0 + 32 n + c.
+#pragma unroll
+  for (int n = 0; n < NT; n++) {
+    const uint32_t t = t0 + 32 * n + c32;
+    if (t >= p.n) continue;
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f32x4 col[1] = {f32x4{acc[r][n][4 * j], acc[r][n][4 * j + 1], acc[r][n][4 * j + 2], acc[r][n][4 * j + 3]}};
+        gemm_epilogue<1>(p, col, row0 + 32 * r + 8 * j + 4 * h, 0, t, ssn[n],
+                         rblk == 0 && wv == 0 && r == 0 && j == 0 && h == 0);
+      }
+  }
+}
+
 // GEMM launch shape: RTW row tiles per wave (BM = 64 RTW), NT token tiles (BN = 16 NT),
 // S k splits.
 struct GemmCfg {
-  int rtw, nt, s, d;  // d: chunks in flight (4 or 8)
+  int rtw, nt, s, d;  // d: chunks in flight (2, 4 or 8)
+  int mf = 16;        // MFMA tile: 16 (mm_gemm, tiles of 16) or 32 (mm_gemm32, tiles of 32)
+  int nw = 4;         // waves per workgroup (mm_gemm32: 4 or 8)
+  int cpi = 1;        // mm_gemm32: chunks per barrier (1, or 2 with 4 chunks in flight)
+  uint32_t bm() const { return (uint32_t)(nw * mf * rtw); }
+  uint32_t bn() const { return (uint32_t)mf * nt; }
+  uint32_t acc_bytes() const { return (uint32_t)(rtw * nt) * mf * mf / 16; }  // per thread
 };
 GemmTune g_gemm_tune;  // all zero: the built-in choice
 
@@ -962,8 +1271,26 @@ GemmTune g_gemm_tune;  // all zero: the built-in choice
 // per wave, two chunks in flight), unsplit.
 static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uint32_t k) {
   if (g_gemm_tune.rtw)
-    return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4};
+    return GemmCfg{g_gemm_tune.rtw, g_gemm_tune.nt, std::max(1, g_gemm_tune.s), g_gemm_tune.d ? g_gemm_tune.d : 4,
+                   g_gemm_tune.mf ? g_gemm_tune.mf : 16, g_gemm_tune.nw ? g_gemm_tune.nw : 4,
+                   g_gemm_tune.cpi ? g_gemm_tune.cpi : 1};
   const uint32_t nch = k / GKC;
+  // int8 at 96 rows and more: 32 x 32 tiles, 8 waves of one 32-row tile (256-row blocks), 32
+  // tokens (64 for the widest matrices), the fewest k splits that give 160 workgroups, four
+  // chunks in flight at 32 tokens. Measured on MI355X against the 16-wide shapes below at 160
+  // and 512 rows: qkv 14.0 -> 13.4 and 23.6 -> 20.1 us, o 13.9 -> 13.1 and 20.5 -> 17.8, down
+  // 26.5 -> 23.9 and 51.6 -> 44.1, gate_up 34.2 -> 31.8 and 73.5 -> 73.0.
+  if (fmt == SV_FMT_I8 && !grouped && n >= 96 && m % 256 == 0) {
+    GemmCfg c{1, m >= 8192 ? 2 : 1, 1, 4, 32, 8, 1};
+    if (c.nt == 2) c.d = 2;
+    const uint32_t cells = m / c.bm() * ((n + c.bn() - 1) / c.bn());
+    for (int s : {1, 2, 4, 8})
+      if (nch % s == 0 && nch / s >= 4) {
+        c.s = s;
+        if (cells * s >= 160) break;
+      }
+    return c;
+  }
   // Wide matrices at many rows: 256-row x 64-token blocks halve the operand traffic through
   // L2 (weights re-read per token block, X per row block) where they still fill the device.
   // Two chunks in flight (not four) keep that shape at two waves per SIMD.
@@ -1021,18 +1348,24 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
 
 static size_t gemm_ws_layout(uint32_t n, uint32_t m, const GemmCfg& c, size_t* ss_off, size_t* part_off) {
   if (c.s <= 1) return 0;
-  const size_t n_tblk = (n + 16 * c.nt - 1) / (16 * c.nt), cells = m / (64 * c.rtw) * n_tblk;
+  const size_t n_tblk = (n + c.bn() - 1) / c.bn(), cells = m / c.bm() * n_tblk;
   size_t off = COUNTER_SLOTS * 4;
   *ss_off = off;
-  off += (cells * c.s * 16 * c.nt * 4 + 255) / 256 * 256;
+  off += (cells * c.s * c.bn() * 4 + 255) / 256 * 256;
   *part_off = off;
-  off += cells * c.s * 256 * c.rtw * c.nt * 16;
+  off += cells * c.s * 64 * c.nw * c.acc_bytes();
   return off;
 }
 
 static bool gemm_shape_ok(uint32_t m, uint32_t k, const GemmCfg& c) {
   const bool nt_ok = c.nt == 2 || c.nt == 3 || c.nt == 4 || c.nt == 5 || c.nt == 8;
-  return nt_ok && (c.rtw == 1 || c.rtw == 2 || (c.rtw == 4 && c.nt <= 5)) && (c.d == 2 || c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
+  // 32-wide tiles: one or two row tiles per wave, one to three token tiles.
+  if (c.mf == 32)
+    return (c.rtw == 1 || c.rtw == 2) && c.nt >= 1 && c.nt <= 3 && (c.d == 2 || c.d == 4) && (c.nw == 4 || c.nw == 8) &&
+           (c.cpi == 1 || (c.cpi == 2 && c.d == 4)) &&
+           c.s >= 1 && c.s <= 64 &&
+           m % c.bm() == 0 && (k / GKC) % c.s == 0;
+  return c.mf == 16 && c.nw == 4 && nt_ok && (c.rtw == 1 || c.rtw == 2 || (c.rtw == 4 && c.nt <= 5)) && (c.d == 2 || c.d == 4 || c.d == 8) && c.s >= 1 && c.s <= 64 && m % (64 * c.rtw) == 0 &&
          (k / GKC) % c.s == 0;
 }
 
@@ -1054,15 +1387,31 @@ static void gemm_dispatch_nt(hipStream_t stream, const MMParams& p, int nt, int 
   }
 }
 
+static void gemm_dispatch32(hipStream_t stream, uint32_t fmt, const GemmCfg& c, const MMParams& p, uint32_t nwg,
+                            uint32_t n_tblk) {
+#define SV_G32W(F, R, N, D, C)                                                                 \
+  (c.nw == 8 ? launch((mm_gemm32<F, R, N, D, 8, C>), dim3(nwg), dim3(512), 0, stream, p, n_tblk) \
+             : launch((mm_gemm32<F, R, N, D, 4, C>), dim3(nwg), dim3(256), 0, stream, p, n_tblk))
+#define SV_G32(F, R, N, D) (D == 4 && c.cpi == 2 ? SV_G32W(F, R, N, 4, 2) : SV_G32W(F, R, N, D, 1))
+#define SV_G32_NT(F, R, D) (c.nt == 1 ? SV_G32(F, R, 1, D) : c.nt == 2 ? SV_G32(F, R, 2, D) : SV_G32(F, R, 3, D))
+#define SV_G32_D(F, R) (c.d == 4 ? SV_G32_NT(F, R, 4) : SV_G32_NT(F, R, 2))
+  if (fmt == SV_FMT_I8) c.rtw == 2 ? SV_G32_D(SV_FMT_I8, 2) : SV_G32_D(SV_FMT_I8, 1);
+  else c.rtw == 2 ? SV_G32_D(SV_FMT_BF16, 2) : SV_G32_D(SV_FMT_BF16, 1);
+#undef SV_G32_D
+#undef SV_G32_NT
+#undef SV_G32
+#undef SV_G32W
+}
+
 static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, MMParams& p, void* ws, size_t ws_bytes) {
   const bool grouped = fmt == SV_FMT_I8 && !p.per_row;
   const GemmCfg c = pick_gemm(fmt, grouped, p.n, p.m, p.k);
-  if (!gemm_shape_ok(p.m, p.k, c) || (grouped && c.rtw != 1))
+  if (!gemm_shape_ok(p.m, p.k, c) || (grouped && (c.rtw != 1 || c.mf != 16)))
     return fail(SV_ERR_ARG, "matmul (gemm): launch shape rtw %d, nt %d, splits %d for m %u, k %u", c.rtw, c.nt, c.s,
                 p.m, p.k);
   if ((size_t)p.m * p.k * (fmt == SV_FMT_I8 ? 1 : 2) >= (1ull << 31) || (size_t)p.n * p.k * 4 >= (1ull << 31))
     return fail(SV_ERR_UNSUPPORTED, "matmul (gemm): operands of 2 GiB or more");
-  const uint32_t n_tblk = (p.n + 16 * c.nt - 1) / (16 * c.nt), rb = p.m / (64 * c.rtw);
+  const uint32_t n_tblk = (p.n + c.bn() - 1) / c.bn(), rb = p.m / c.bm();
   size_t ss_off = 0, part_off = 0;
   const size_t need = gemm_ws_layout(p.n, p.m, c, &ss_off, &part_off);
   if (need) {
@@ -1075,7 +1424,9 @@ static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, MMParams& p, void
   }
   p.splits = c.s;
   const uint32_t nwg = rb * n_tblk * c.s;
-  if (fmt == SV_FMT_I8) {
+  if (c.mf == 32) {
+    gemm_dispatch32(stream, fmt, c, p, nwg, n_tblk);
+  } else if (fmt == SV_FMT_I8) {
     if (grouped) gemm_dispatch_nt<SV_FMT_I8, 1, true>(stream, p, c.nt, c.d, nwg, n_tblk);
     else if (c.rtw == 4) gemm_dispatch_nt<SV_FMT_I8, 4, false>(stream, p, c.nt, c.d, nwg, n_tblk);
     else if (c.rtw == 2) gemm_dispatch_nt<SV_FMT_I8, 2, false>(stream, p, c.nt, c.d, nwg, n_tblk);

@@ -48,7 +48,7 @@ extern int g_mm_variant;
 // GEMM launch-shape override (row tiles per wave, token tiles, k splits, chunks in flight;
 // zero: built-in).
 struct GemmTune {
-  int rtw, nt, s, d;
+  int rtw, nt, s, d, mf, nw, cpi;  // mf: MFMA tile (16 or 32); nw: waves (4); cpi: chunks per barrier (1)
 };
 extern GemmTune g_gemm_tune;
 extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave, splits)

@@ -627,27 +627,38 @@ def test_matmul_head_many_cells(gpu):
     close(got, ref, atol=5e-5 * 23, rtol=1e-4, what="head at 256 rows")
 
 
-@pytest.mark.parametrize("rtw,nt,splits,depth", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
+@pytest.mark.parametrize("shape", [(1, 2, 1, 4), (2, 2, 2, 4), (2, 2, 4, 8), (1, 3, 2, 8), (2, 3, 1, 4),
                                                   (2, 4, 2, 4), (1, 5, 4, 4), (2, 5, 1, 4), (2, 8, 2, 4), (1, 8, 1, 4),
                                                   (4, 4, 1, 4), (4, 2, 2, 4), (4, 5, 4, 4), (4, 4, 2, 2), (4, 3, 1, 2),
                                                   (4, 2, 4, 2), (4, 2, 1, 2), (2, 2, 4, 2), (1, 2, 2, 2), (2, 5, 1, 2),
-                                                  (2, 2, 8, 2), (1, 2, 8, 2), (4, 2, 8, 2)])
-@pytest.mark.parametrize("n", [17, 100])
-def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
+                                                  (2, 2, 8, 2), (1, 2, 8, 2), (4, 2, 8, 2),
+                                                  # 32 x 32 x 16 tiles (the fifth field: tile width)
+                                                  (1, 1, 1, 2, 32), (1, 1, 2, 2, 32), (2, 1, 4, 2, 32), (1, 2, 1, 4, 32),
+                                                  (2, 2, 2, 2, 32), (1, 3, 8, 2, 32), (2, 3, 1, 4, 32), (1, 1, 8, 4, 32),
+                                                  # eight waves (the sixth field)
+                                                  (1, 1, 2, 2, 32, 8), (1, 2, 1, 2, 32, 8), (2, 1, 4, 4, 32, 8),
+                                                  (1, 3, 8, 2, 32, 8),
+                                                  # two chunks per barrier (the seventh field)
+                                                  (1, 1, 2, 4, 32, 8, 2), (2, 1, 1, 4, 32, 4, 2), (1, 2, 8, 4, 32, 8, 2)])
+@pytest.mark.parametrize("n", [17, 100, 170])
+def test_matmul_gemm_launch_shapes(gpu, shape, n):
     """Every GEMM launch shape (row tiles per wave, token tiles, k splits merged by the last
     split to arrive, chunks in flight) gives the oracle's result: int8 with EPI_NORM (sums of
     squares carried across splits, the inverse norm written once) and bf16 with EPI_RESID in
     the tiled layout, with a row gather, ragged token blocks (17, 100 rows) and a k whose chunk
     count leaves a partial round of zero chunks (k = 1280: 20 chunks; 2560 = 40 chunks for eight
     splits, five each); two calls share one workspace. The shape is forced through the
-    library's internal override."""
-    banner(f"gemm launch shape rtw={rtw} nt={nt} splits={splits} depth={depth} n={n}")
-    tune = (C.c_int * 4).in_dll(L.lib(), "_ZN2sv11g_gemm_tuneE")
+    library's internal override: 16-wide tiles (mm_gemm) and 32-wide tiles (mm_gemm32) with 4
+    or 8 waves and one or two chunks per barrier."""
+    rtw, nt, splits, depth, mf, nw, cpi = (tuple(shape) + (16, 4, 1)[len(shape) - 4:])[:7]
+    banner(f"gemm launch shape rtw={rtw} nt={nt} splits={splits} depth={depth} tile={mf} waves={nw} "
+           f"chunks per barrier={cpi} n={n}")
+    tune = (C.c_int * 7).in_dll(L.lib(), "_ZN2sv11g_gemm_tuneE")
     rng = np.random.default_rng(rtw * 1000 + nt * 100 + splits * 10 + depth + n)
-    m, k = {1: 384, 2: 512, 4: 768}[rtw], (2560 if splits == 8 else 1280)
+    m, k = ({1: 384, 2: 512, 4: 768} if nw == 4 else {1: 512, 2: 1024})[rtw], (2560 if splits == 8 else 1280)
     ws = K.Workspace(16 << 20)
     try:
-        tune[0], tune[1], tune[2], tune[3] = rtw, nt, splits, depth
+        tune[0], tune[1], tune[2], tune[3], tune[4], tune[5], tune[6] = rtw, nt, splits, depth, mf, nw, cpi
         w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
         q, s = quantize_rows(w)
         mi8 = K.matrix(q.cuda(), s.cuda(), 31)
@@ -681,7 +692,7 @@ def test_matmul_gemm_launch_shapes(gpu, rtw, nt, splits, depth, n):
             close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4,
                   what=f"bf16 call {call}")
     finally:
-        tune[0] = tune[1] = tune[2] = tune[3] = 0
+        tune[0] = tune[1] = tune[2] = tune[3] = tune[4] = tune[5] = tune[6] = 0
 
 
 def test_matmul_skinny_groups_of_256(gpu):
