@@ -1059,14 +1059,20 @@ __global__ __launch_bounds__(NW * 64) void mm_gemm32(MMParams p, uint32_t n_tblk
     }
   };
 
-  // Two accumulator sets (even and odd k-steps) halve the chain of dependent products.
-  f32x16 acc[RT][NT], acc2[RT][NT];
+  // One tile per wave: two accumulator sets (even and odd k-steps) halve the chain of
+  // dependent products, and every B operand of an iteration is requested before the first
+  // product (one LDS wait per iteration). Wider waves have independent tiles to interleave and
+  // read each k-step's operands as they go (fewer registers).
+  constexpr bool DUAL = RT * NT == 1, UPF = NT == 1;
+  f32x16 acc[RT][NT], acc2[1][1];  // acc2: used when DUAL
 #pragma unroll
   for (int r = 0; r < RT; r++)
 #pragma unroll
     for (int n = 0; n < NT; n++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[r][n][e] = acc2[r][n][e] = 0.0f;
+      for (int e = 0; e < 16; e++) acc[r][n][e] = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 16; e++) acc2[0][0][e] = 0.0f;
 
   f32x4 xr[GD][PPT][2];
   u32x4 wr[GD][RT][2 * WL];
@@ -1098,19 +1104,20 @@ __global__ __launch_bounds__(NW * 64) void mm_gemm32(MMParams p, uint32_t n_tblk
           for (int v = 0; v < 2 * WL; v++) cur[u][r][v] = wr[d + u][r][v];
         load_w(c + u + GD, wr[d + u]);
       }
-      // Every B operand of the iteration is requested before the first product (one LDS
-      // wait per iteration instead of one per k-step).
-      bf16x8 bx[CPI][4][NT][2];
+      auto read_b = [&](int u, int ks, bf16x8 (&bk)[NT][2]) {
+        const int slot = 64 * ks + 32 * h + (c32 ^ (4 * h + ks));
 #pragma unroll
-      for (int u = 0; u < CPI; u++)
+        for (int n = 0; n < NT; n++)
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-          const int slot = 64 * ks + 32 * h + (c32 ^ (4 * h + ks));
+          for (int hl = 0; hl < 2; hl++) bk[n][hl] = __builtin_bit_cast(bf16x8, xs[buf][u][n][hl][slot]);
+      };
+      bf16x8 bx[CPI][UPF ? 4 : 1][NT][2];
+      if constexpr (UPF) {
 #pragma unroll
-          for (int n = 0; n < NT; n++)
+        for (int u = 0; u < CPI; u++)
 #pragma unroll
-            for (int hl = 0; hl < 2; hl++) bx[u][ks][n][hl] = __builtin_bit_cast(bf16x8, xs[buf][u][n][hl][slot]);
-        }
+          for (int ks = 0; ks < 4; ks++) read_b(u, ks, bx[u][ks]);
+      }
       __builtin_amdgcn_sched_barrier(0);
       // The next iteration's X (requested GD - CPI chunks ago) to the other buffer while this
       // iteration's operands arrive, then the chunks GD further requested into its registers:
@@ -1136,22 +1143,28 @@ __global__ __launch_bounds__(NW * 64) void mm_gemm32(MMParams p, uint32_t n_tblk
               a[r] = __builtin_bit_cast(bf16x8, cur[u][r][ks]);
             }
           }
+          auto products = [&](const bf16x8 (&bk)[NT][2]) {
 #pragma unroll
-          for (int n = 0; n < NT; n++)
+            for (int n = 0; n < NT; n++)
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-              f32x16& g = (ks & 1) ? acc2[r][n] : acc[r][n];
-              g = mfma32(a[r], bx[u][ks][n][0], g);
-              g = mfma32(a[r], bx[u][ks][n][1], g);
-            }
+              for (int r = 0; r < RT; r++) {
+                f32x16& g = (DUAL && (ks & 1)) ? acc2[0][0] : acc[r][n];
+                g = mfma32(a[r], bk[n][0], g);
+                g = mfma32(a[r], bk[n][1], g);
+              }
+          };
+          if constexpr (UPF) {
+            products(bx[u][ks]);
+          } else {
+            bf16x8 bk[NT][2];
+            read_b(u, ks, bk);
+            products(bk);
+          }
         }
       lds_barrier();
     }
   }
-#pragma unroll
-  for (int r = 0; r < RT; r++)
-#pragma unroll
-    for (int n = 0; n < NT; n++) acc[r][n] += acc2[r][n];
+  if constexpr (DUAL) acc[0][0] += acc2[0][0];
   // Per-row int8 scales: lane (c, h) holds rows 8 j + 4 h + i of each tile.
   if (FMT == SV_FMT_I8) {
 #pragma unroll
@@ -1275,14 +1288,15 @@ static GemmCfg pick_gemm(uint32_t fmt, bool grouped, uint32_t n, uint32_t m, uin
                    g_gemm_tune.mf ? g_gemm_tune.mf : 16, g_gemm_tune.nw ? g_gemm_tune.nw : 4,
                    g_gemm_tune.cpi ? g_gemm_tune.cpi : 1};
   const uint32_t nch = k / GKC;
-  // int8 at 96 rows and more: 32 x 32 tiles, 8 waves of one 32-row tile (256-row blocks), 32
-  // tokens (64 for the widest matrices), the fewest k splits that give 160 workgroups, four
-  // chunks in flight at 32 tokens. Measured on MI355X against the 16-wide shapes below at 160
-  // and 512 rows: qkv 14.0 -> 13.4 and 23.6 -> 20.1 us, o 13.9 -> 13.1 and 20.5 -> 17.8, down
-  // 26.5 -> 23.9 and 51.6 -> 44.1, gate_up 34.2 -> 31.8 and 73.5 -> 73.0.
+  // int8 at 96 rows and more: 32 x 32 tiles, 8 waves, four chunks in flight; one 32-row tile
+  // per wave (256-row blocks) and 32 tokens, or for the widest matrices two tiles per wave
+  // (512-row blocks) and 64 tokens from 384 rows; the fewest k splits that give 160
+  // workgroups. Measured on MI355X against the 16-wide shapes below at 160 and 512 rows: qkv
+  // 14.0 -> 13.4 and 23.6 -> 20.1 us, o 13.9 -> 13.1 and 20.5 -> 17.8, down 26.5 -> 23.9 and
+  // 51.6 -> 44.1, gate_up 34.2 -> 31.6 and 73.5 -> 67.6.
+  const bool wide = m >= 8192 && m % 512 == 0;
   if (fmt == SV_FMT_I8 && !grouped && n >= 96 && m % 256 == 0) {
-    GemmCfg c{1, m >= 8192 ? 2 : 1, 1, 4, 32, 8, 1};
-    if (c.nt == 2) c.d = 2;
+    GemmCfg c{wide ? 2 : 1, wide && n >= 384 ? 2 : 1, 1, 4, 32, 8, 1};
     const uint32_t cells = m / c.bm() * ((n + c.bn() - 1) / c.bn());
     for (int s : {1, 2, 4, 8})
       if (nch % s == 0 && nch / s >= 4) {
