@@ -233,7 +233,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
                emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless,
                lossless_streams=None if tree else sum(same), divergences=divergences, prof=prof,
                per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
-               flops=flops, info=info, rows=rows)
+               flops=flops, info=info, rows=rows, mat_elems=mat_elems, n_rows=n_rows)
     return res
 
 
@@ -248,7 +248,31 @@ def extra_object(res, workload, rows, reps, key=None):
             "steps": res["steps"], "emitted_per_step": round(res["emitted"] / res["steps"], 3),
             "lossless_trace_check": res["lossless"], "config": {"workload": workload, "rows_per_step": rows},
             "roofline": roofline_of(res, reps, key), "step_roofline": step_roofline(res),
+            "gemm_roofline": gemm_roofline(res),
             "kernel_ms_per_step": {kk: round(v, 4) for kk, v in res["per_step_ms"].items()}}
+
+
+def gemm_roofline(res):
+    """The verify step's GEMMs against the dense bf16 matrix-core peak: algorithmic flops per
+    launch (2 n m k for n rows, the reference's product) / the kind's mean launch duration (the
+    same hipExtLaunchKernelGGL events as `roofline`). The kernels run every product twice (bf16
+    hi and lo halves of the fp32 activations), so `frac_hi_lo` counts the matrix-core work done.
+    Meaningful at many rows (the GEMM path); below 17 rows the matmuls are HBM-bound GEMVs."""
+    prof = res["prof"]
+    per = {}
+    for kk, elems in res["mat_elems"].items():
+        if kk in prof and prof[kk][1]:
+            us = prof[kk][0] / prof[kk][1] * 1e3
+            tf = 2.0 * res["n_rows"] * elems / (us * 1e-6) / 1e12
+            per[kk] = {"avg_launch_us": round(us, 3), "achieved": round(tf, 1)}
+    if not per:
+        return None
+    dom = max(per, key=lambda kk: res["mat_elems"][kk])
+    a = per[dom]["achieved"]
+    return {"bound": "mfma", "kernel": dom, "achieved": a, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(a / MFMA_BF16_PEAK_TFLOPS, 4), "frac_hi_lo": round(2 * a / MFMA_BF16_PEAK_TFLOPS, 4),
+            "flops_per_launch": int(2 * res["n_rows"] * res["mat_elems"][dom]), "avg_launch_us": per[dom]["avg_launch_us"],
+            "per_matrix": per}
 
 
 def roofline_of(res, profile_reps, workload=None):
@@ -543,7 +567,7 @@ def main() -> int:
                                       "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
                           "rows_per_step": 32 * r2["rows"]},
                "roofline": roofline_of(r2, 2, "configs[2]"), "step_roofline": step_roofline(r2),
-               "cpu_baseline": cpu2,
+               "gemm_roofline": gemm_roofline(r2), "cpu_baseline": cpu2,
                "kernel_ms_per_step": {kk: round(v, 4) for kk, v in r2["per_step_ms"].items()}}
         r2["eng"].close()
 
