@@ -548,6 +548,7 @@ GEMM_CASES = [
     # (m, k, fmt, group)  group None: one scale per row
     (16384, 2048, "i8", None),  # gate_up at 32 streams
     (2048, 8192, "i8", None),   # down
+    (3072, 2048, "i8", None),   # qkv (256-row blocks of the 32-wide kernel)
     (3072, 2048, "i8", 64),     # int8 groups of 64 (the reference's default)
     (1280, 1280, "i8", 128),    # 20 chunks of 64 in 4 k splits: groups straddle splits
     (2048, 2048, "bf16", None),
@@ -555,7 +556,7 @@ GEMM_CASES = [
 
 
 @pytest.mark.parametrize("m,k,fmt,group", GEMM_CASES)
-@pytest.mark.parametrize("n", [17, 40, 160, 512])
+@pytest.mark.parametrize("n", [17, 40, 100, 160, 512])
 @pytest.mark.parametrize("epi", [L.EPI_NORM, L.EPI_RESID, L.EPI_SWIGLU, L.EPI_HEAD])
 def test_matmul_many_rows(gpu, m, k, fmt, group, n, epi):
     banner(f"gemm m={m} k={k} {fmt} group={group} n={n} epi={epi}")
