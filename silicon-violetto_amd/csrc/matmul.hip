@@ -1171,9 +1171,9 @@ __global__ __launch_bounds__(NW * 64) void mm_gemm32(MMParams p, uint32_t n_tblk
     for (int r = 0; r < RT; r++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint2 sw = *(const uint2*)(p.scales + row0 + 32 * r + 8 * j + 4 * h);
-        const float s0 = __uint_as_float(sw.x << 16), s1 = __uint_as_float(sw.x & 0xffff0000u),
-                    s2 = __uint_as_float(sw.y << 16), s3 = __uint_as_float(sw.y & 0xffff0000u);
+        const uint16_t* sp4 = p.scales + row0 + 32 * r + 8 * j + 4 * h;  // any alignment
+        const float s0 = bf(ldg_u16(sp4)), s1 = bf(ldg_u16(sp4 + 1)), s2 = bf(ldg_u16(sp4 + 2)),
+                    s3 = bf(ldg_u16(sp4 + 3));
 #pragma unroll
         for (int n = 0; n < NT; n++) {
           acc[r][n][4 * j + 0] *= s0;
