@@ -172,7 +172,9 @@ sv_status draft_kv_launch(hipStream_t stream, const sv_shape* sh, const float* k
                           const uint32_t* on_path, const float* rope, uint16_t* kc, uint16_t* vc, const uint32_t* table,
                           const sv_kv_args* kv, uint32_t n, uint32_t n_layers) {
   if (!sh || !kvp || !meta || !on_path || !rope || !kc || !vc || !table || !kv) return fail(SV_ERR_ARG, "draft_kv: null pointer");
-  if (sh->head_dim % 4 || sh->head_dim > 128 || sh->n_kv_heads * sh->head_dim / 4 > 256)
+  // a head's D / 4 lanes sum its squares with xor shuffles (a power of two dividing 64) and
+  // rope pairs (j, j + D / 2) from the 32-pair table: head_dim 64 or 128 only
+  if ((sh->head_dim != 64 && sh->head_dim != 128) || sh->n_kv_heads * sh->head_dim / 4 > 256)
     return fail(SV_ERR_UNSUPPORTED, "draft_kv: %u kv heads x %u dims", sh->n_kv_heads, sh->head_dim);
   if (kv->page_shift < 4 || kv->page_shift > 16 || kv->n_pages == 0 || kv->max_pages == 0)
     return fail(SV_ERR_ARG, "draft_kv: pages of 2^%u, %u pages, %u per sequence", kv->page_shift, kv->n_pages, kv->max_pages);

@@ -1038,7 +1038,7 @@ extern "C" sv_status sv_engine_set_drafter(sv_engine* e, const sv_drafter* d) {
   if (!(d->inv_temperature > 0.0f) || !std::isfinite(d->inv_temperature))
     return fail(SV_ERR_ARG, "set_drafter: inverse temperature %g", d->inv_temperature);
   if (!e->embed) return fail(SV_ERR_STATE, "set_drafter: no embedding set (sv_engine_set_embed)");
-  if (NKV * D / 4 > 256 || D % 4) return fail(SV_ERR_UNSUPPORTED, "set_drafter: %u kv heads x %u dims", NKV, D);
+  if (NKV * D / 4 > 256 || (D != 64 && D != 128)) return fail(SV_ERR_UNSUPPORTED, "set_drafter: %u kv heads x %u dims", NKV, D);
   SV_HIP(hipStreamSynchronize(e->stream), "set_drafter");
   // a captured step and the plan were laid out without this drafter: both go
   if (e->graph) {

@@ -392,7 +392,10 @@ __global__ __launch_bounds__(64 * W) void mm_stream(MMParams p) {
   uint2 rsc = {0u, 0u};
   if (wv < RT) {
     const uint32_t row0 = (xg * RT + wv) * 16 + 4 * q;
-    if (I8 && p.per_row) rsc = *(const uint2*)(p.scales + row0);
+    // four 16-bit loads: the scale array needs no alignment beyond its element's
+    if (I8 && p.per_row)
+      rsc = uint2{ldg_u16(p.scales + row0) | ((uint32_t)ldg_u16(p.scales + row0 + 1) << 16),
+                  ldg_u16(p.scales + row0 + 2) | ((uint32_t)ldg_u16(p.scales + row0 + 3) << 16)};
     if (p.epi == SV_EPI_RESID && (uint32_t)t < n) base_pre[0] = *(const f32x4*)(p.base + (size_t)t * p.m + row0);
   }
   float gsc[RT][4];

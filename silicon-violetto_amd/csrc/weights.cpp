@@ -81,8 +81,14 @@ extern "C" sv_status sv_weights_open(const char* path, sv_weights** out) {
     sv_tensor_info t{};
     size_t len = 0;
     while (len < 64 && r[len]) len++;
+    // sv_tensor_info.name holds 63 bytes and a NUL; the reference writer's names are shorter
+    // (tools/convert.py:137), and a longer one could not be looked up under its real name.
+    if (len == 64) {
+      delete w;
+      return fail(SV_ERR_ARG, "%s: record %u has a 64-byte name with no NUL", path, i);
+    }
     memcpy(t.name, r, len);
-    t.name[len < 64 ? len : 63] = 0;
+    t.name[len] = 0;
     t.dtype = u32_at(r + 64);
     t.ndim = u32_at(r + 68);
     for (int d = 0; d < 4; d++) t.shape[d] = u32_at(r + 72 + 4 * d);
@@ -94,13 +100,24 @@ extern "C" sv_status sv_weights_open(const char* path, sv_weights** out) {
     };
     if (t.dtype > 2) return bad(fail(SV_ERR_ARG, "%s: unknown dtype %u", t.name, t.dtype));
     if (t.ndim > 4) return bad(fail(SV_ERR_ARG, "%s: %u dimensions", t.name, t.ndim));
+    // Overflow-safe: the element count is built against the file's data region, so neither
+    // the product of the dims nor offset + nbytes can wrap.
+    const uint64_t avail = (uint64_t)size - data_offset;
     uint64_t elems = 1;
-    for (uint32_t d = 0; d < t.ndim; d++) elems *= t.shape[d];
-    if (elems * dtype_size(t.dtype) != t.nbytes)
-      return bad(fail(SV_ERR_ARG, "%s: %llu bytes for %llu elements of %s", t.name, (unsigned long long)t.nbytes,
-                      (unsigned long long)elems, dtype_name(t.dtype)));
-    if (t.offset + t.nbytes > (uint64_t)size - data_offset)
+    bool too_big = false;
+    for (uint32_t d = 0; d < t.ndim; d++) {
+      if (t.shape[d] != 0 && elems > avail / t.shape[d]) too_big = true;
+      if (!too_big) elems *= t.shape[d];
+    }
+    if (too_big || elems * dtype_size(t.dtype) != t.nbytes)
+      return bad(fail(SV_ERR_ARG, "%s: %llu bytes for a [%u, %u, %u, %u] %s shape", t.name, (unsigned long long)t.nbytes,
+                      t.shape[0], t.shape[1], t.shape[2], t.shape[3], dtype_name(t.dtype)));
+    if (t.offset > avail || t.nbytes > avail - t.offset)
       return bad(fail(SV_ERR_ARG, "%s: bytes past the end of the file", t.name));
+    // The writer aligns every tensor to 256 bytes (tools/convert.py:17,133); the kernels read
+    // weights, scales and tables with 8- and 16-byte vector loads from the device copy.
+    if (t.offset % 256 != 0)
+      return bad(fail(SV_ERR_ARG, "%s: offset %llu is not a multiple of 256", t.name, (unsigned long long)t.offset));
     if (w->index.count(t.name)) return bad(fail(SV_ERR_ARG, "%s: two tensors of this name", t.name));
     w->index[t.name] = i;
     w->tensors.push_back(t);

@@ -79,6 +79,33 @@ def test_matmul(gpu, m, k, fmt, n, epi, tiled):
         close(aux.cpu().numpy(), aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")
 
 
+@pytest.mark.parametrize("n", [5, 160])
+@pytest.mark.parametrize("tiled", [False, True])
+def test_matmul_scales_unaligned(gpu, n, tiled):
+    """Per-row int8 scales placed 2 bytes past an aligned base (the weight file only promises
+    the element's alignment for a `.scale` tensor): every kernel reads them as 16-bit words."""
+    banner(f"matmul unaligned scales n={n} tiled={tiled}")
+    m, k = 2048, 2048
+    rng = np.random.default_rng(77 + n)
+    w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+    q, s = quantize_rows(w)
+    buf = torch.zeros(m + 8, dtype=s.dtype, device="cuda")
+    buf[1:m + 1] = s.cuda().view(-1)
+    sd = buf[1:m + 1]
+    assert sd.data_ptr() % 8 == 2
+    mat = K.matrix(q.cuda(), sd, 31)
+    if tiled:
+        mat = mat.tiled()
+    x = rng.normal(0, 1, (n, k)).astype(np.float32)
+    base = rng.normal(0, 1, (n, m)).astype(np.float32)
+    a = L.MatArgs(n, k, m, L.EPI_RESID, 0, m, 0.75, 0.9, 1.3, 1, k, 31)
+    ref = oracle.matmul(L, q.numpy(), s.view(torch.int16).numpy().view(np.uint16), 31, x, a, base=base)
+    y = torch.zeros(n, m, device="cuda")
+    K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_RESID, scale=0.75, ra=0.9, rb=1.3, base=to_dev(base))
+    torch.cuda.synchronize()
+    close(y.cpu().numpy(), ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4, what="unaligned scales")
+
+
 def test_matmul_rows_gather(gpu):
     """x_rows gathers input rows (the head's head_rows)."""
     banner("matmul gather")

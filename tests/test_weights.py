@@ -87,10 +87,16 @@ def _rec(name, dtype, shape, off, nbytes):
     ("magic", "not a version-1 violetto weight file"),
     ("version", "not a version-1 violetto weight file"),
     ("dtype", "x: unknown dtype 5"),
-    ("bytes", "x: 12 bytes for 4 elements of F32"),
+    ("bytes", "x: 12 bytes for a \\[4, 0, 0, 0\\] F32 shape"),
     ("past_end", "x: bytes past the end of the file"),
     ("twice", "x: two tensors of this name"),
     ("records", "records do not fit the file"),
+    # dims whose product wraps in 64 bits to nbytes / 4 = 4 elements
+    ("wrap_shape", "x: 16 bytes for a \\[4, 242243305, 49477, 384773\\] F32 shape"),
+    # offset + nbytes wraps past zero
+    ("wrap_offset", "x: bytes past the end of the file"),
+    ("misaligned", "x: offset 16 is not a multiple of 256"),
+    ("long_name", "record 0 has a 64-byte name with no NUL"),
 ])
 def test_malformed_files_refused(tmp_path, case, msg):
     p = tmp_path / "bad.vlt"
@@ -104,9 +110,18 @@ def test_malformed_files_refused(tmp_path, case, msg):
     elif case == "bytes":
         _write_raw(p, [_rec("x", 0, [4], 0, 12)], data)
     elif case == "past_end":
-        _write_raw(p, [_rec("x", 0, [4], 250, 16)], data)
+        _write_raw(p, [_rec("x", 0, [4], 256, 16)], data)
     elif case == "twice":
-        _write_raw(p, [_rec("x", 0, [4], 0, 16), _rec("x", 0, [4], 16, 16)], data)
+        _write_raw(p, [_rec("x", 0, [4], 0, 16), _rec("x", 0, [4], 256, 16)], data * 2)
+    elif case == "wrap_shape":
+        # 4 (2^62 + 1) = 2^64 + 4: the product wraps to 4 elements, 16 bytes
+        _write_raw(p, [_rec("x", 0, [4, 5 * 5581 * 8681, 49477, 384773], 0, 16)], data)
+    elif case == "wrap_offset":
+        _write_raw(p, [_rec("x", 0, [4], 2**64 - 256, 16)], data)
+    elif case == "misaligned":
+        _write_raw(p, [_rec("x", 0, [4], 16, 16)], data)
+    elif case == "long_name":
+        _write_raw(p, [_rec("y" * 64, 0, [4], 0, 16)], data)
     else:
         _write_raw(p, [_rec("x", 0, [4], 0, 16)], data, n=200)
     with pytest.raises(L.SvError, match=msg):
