@@ -372,6 +372,12 @@ sv_status sv_replay_draft(void* stream, const sv_run_in* d_runs, uint32_t nruns,
 typedef struct sv_engine sv_engine;
 
 /* EngineConfig (engine.rs:32-57) plus the model's shape and constants. */
+/* sv_engine_config.options. SV_OPT_LAYERS_KERNEL: steps of 1-8 rows whose layers the
+ * persistent layer kernel takes (global attention, no extras, no drafter, per-row int8 matrices
+ * at hidden 2048 / ffn 8192, splits of at most 384 keys that fit the grid) run all their layers
+ * in one launch instead of one launch per matmul and attention. */
+#define SV_OPT_LAYERS_KERNEL 1u
+
 typedef struct sv_engine_config {
   sv_shape shape;
   uint32_t max_seqs;        /* sequence slots                                   */
@@ -382,7 +388,7 @@ typedef struct sv_engine_config {
   uint32_t page_shift;      /* log2 tokens per page (reference: 7; configs: 4)  */
   float attn_scale;         /* softmax scale (reference ATTN_SCALE, model.rs:19) */
   uint32_t split_keys;      /* cached keys per attention split, multiple of 32; 0: auto */
-  uint32_t options;         /* reserved: 0                                      */
+  uint32_t options;         /* SV_OPT_* bits                                     */
   /* Sliding-window layers (model.rs:16-17,116; kv.rs:26-32): keys a local query sees
    * besides itself, and which layers are local ([n_layers], 1 local; NULL: all global).
    * Local layers keep a ring of ceil((window + max_step_tokens) / page) pages per slot. */
@@ -596,7 +602,8 @@ enum {
   SV_KIND_KV_WRITE = 12,   /* prompt chunks: the new K/V rows, before the attention */
   SV_KIND_MUDD = 13,
   SV_KIND_DRAFT = 14,      /* the drafter's pass (every launch of it) */
-  SV_KIND_COUNT = 15
+  SV_KIND_LAYERS = 15,     /* every layer of a 1-8 row step in one persistent launch */
+  SV_KIND_COUNT = 16
 };
 sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches);
 

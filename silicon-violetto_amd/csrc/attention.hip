@@ -665,6 +665,65 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   return check_launch("attn_merge");
 }
 
+// ------------------------------------------- the persistent layer kernel's attention
+size_t attn_params_bytes() { return sizeof(AttnParams); }
+
+// Floats of one layer's split partials (o, then l at *l_off), 64-float aligned.
+size_t attn_part_floats(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run, size_t* l_off) {
+  const size_t maxcols = cols_pad(sh, max_run);
+  const size_t o = ((size_t)n_runs * sh->n_kv_heads * max_splits * maxcols * sh->head_dim + 63) / 64 * 64;
+  *l_off = o;
+  return o + ((size_t)n_runs * sh->n_kv_heads * max_splits * maxcols + 63) / 64 * 64;
+}
+
+sv_status attn_params_fill(void* out, const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
+                           uint16_t* v_cache, const uint32_t* page_table, const float* rope_rows,
+                           const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* host_runs,
+                           uint32_t n_runs, uint32_t max_run, const uint32_t* vis, float* o, float* part_o,
+                           float* part_l) {
+  if (!out || !sh || !kv || !args || !host_runs) return fail(SV_ERR_ARG, "layers: attention arguments");
+  if (n_runs == 0 || n_runs > SV_INLINE_RUNS) return fail(SV_ERR_UNSUPPORTED, "layers: %u attention runs", n_runs);
+  if (sh->head_dim != 64 || !kv->is_global || args->split % 32 || args->split > 32u * 4 * 4)
+    return fail(SV_ERR_UNSUPPORTED, "layers: head_dim %u, global %u, split %u", sh->head_dim, kv->is_global, args->split);
+  if (args->rope && !rope_rows) return fail(SV_ERR_ARG, "layers: rope rows missing");
+  AttnParams p{};
+  p.qkv = qkv;
+  p.meta = meta;
+  p.kc = k_cache;
+  p.vc = v_cache;
+  p.page_table = page_table;
+  p.rope = nullptr;
+  p.rope_rows = rope_rows;
+  p.runs = nullptr;
+  p.vis = vis;
+  p.out = o;
+  p.part_o = part_o;
+  p.part_l = part_l;
+  p.counters = nullptr;
+  p.NQ = sh->n_heads;
+  p.NKV = sh->n_kv_heads;
+  p.G = sh->n_heads / sh->n_kv_heads;
+  p.W = (sh->n_heads + 2 * sh->n_kv_heads) * sh->head_dim;
+  p.KOFF = sh->n_heads * sh->head_dim;
+  p.VOFF = (sh->n_heads + sh->n_kv_heads) * sh->head_dim;
+  p.split = args->split;
+  p.max_splits = args->max_splits;
+  p.scale_log2 = args->scale_log2;
+  p.rope_on = args->rope;
+  p.page_shift = kv->page_shift;
+  p.n_pages = kv->n_pages;
+  p.max_pages = kv->max_pages;
+  p.layer = kv->kv_layer;
+  p.maxcols = cols_pad(sh, max_run);
+  p.n_inline = n_runs;
+  for (uint32_t i = 0; i < 3 * n_runs; i++) p.inl[i] = host_runs[i];
+  p.newest_own = 1;
+  p.local = 0;
+  p.window = 0;
+  memcpy(out, &p, sizeof p);
+  return SV_OK;
+}
+
 // ------------------------------------------------- the entry point that allocates nothing
 // Split partials of sv_attn_verify_noalloc live in this array: one copy per GPU, held until the
 // process ends. Its name is a host-side stand-in; host code uses the device address that

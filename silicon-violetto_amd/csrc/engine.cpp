@@ -241,6 +241,9 @@ struct Plan {
   // Steps this plan may run (encodes, graph replays, profiled steps): each advances a run by at
   // most its row count, and every position it can reach has a reserved page.
   uint64_t budget = 0, issued = 0;
+  // The persistent layer kernel runs the layers (layers.hip), with these parameters.
+  bool persist = false;
+  LayersParams lp{};
 };
 
 template <typename T>
@@ -354,6 +357,16 @@ struct sv_engine {
   std::vector<bool> used;
   std::vector<sv_sample_row> sampling;
 
+  // The persistent layer kernel's buffers: activation slices per layer (grown by plans that
+  // use it), its per-layer parameters and attention parameters, and its counters (256 bytes
+  // apart, never reset but after an abort), the epoch word embed increments and the abort word.
+  float* pl_buf = nullptr;
+  size_t pl_floats = 0;
+  LayerW* pl_layers = nullptr;
+  void* pl_attn = nullptr;
+  uint32_t* pl_sync = nullptr;
+  size_t pl_sync_words = 0;
+
   Plan plan;
   bool planned = false;
   // sv_profile_step: an event pair around every kernel while `prof` is set.
@@ -402,6 +415,8 @@ struct sv_engine {
     for (void* b : bufs)
       if (b) (void)hipFree(b);
     for (void* b : packed)
+      if (b) (void)hipFree(b);
+    for (void* b : {(void*)pl_buf, (void*)pl_layers, pl_attn, (void*)pl_sync})
       if (b) (void)hipFree(b);
     if (head_tiled) (void)hipFree(head_tiled);
     if (tap[0]) (void)hipFree(tap[0]);
@@ -525,6 +540,140 @@ struct sv_engine {
     return matmul_launch(stream, &w, x, x_rows, y, base, aux, &a, mm_ws, mm_ws_bytes);
   }
 
+  // Whether the persistent layer kernel takes this plan, and its parameters if so: 1-8 rows,
+  // no prompt chunk, global layers without extras or MUDD, no drafter, per-row int8 tiled
+  // matrices at hidden 2048 / ffn 8192, head_dim 64, splits of at most 384 keys, and every
+  // phase's workgroups within one set of the grid.
+  sv_status plan_layers(Plan& P) {
+    P.persist = false;
+    const sv_shape& s = sh;
+    if (!(cfg.options & SV_OPT_LAYERS_KERNEL) || P.n > 8 || P.chunk || n_local || has_drafter || extras.n_mudd)
+      return SV_OK;
+    if (s.hidden != 2048 || s.ffn != 8192 || s.head_dim != 64 || P.n_attn > 32 || P.split > 384)
+      return SV_OK;
+    for (uint32_t li = 0; li < s.n_layers; li++) {
+      const sv_layer& L = layers[li];
+      if (L.ve_gate || L.attn_gate || L.xsa) return SV_OK;
+      for (const sv_matrix* m : {&L.qkv, &L.o, &L.gate_up, &L.down}) {
+        const bool per_row = m->gshift >= 32 || (1ull << m->gshift) >= m->k;
+        if (m->format != (SV_FMT_I8 | SV_FMT_TILED) || !per_row || !m->d_scales) return SV_OK;
+      }
+    }
+    const int ns = layers_grid_per_set();
+    const uint32_t G = s.n_heads / s.n_kv_heads, D = 64, maxcols = (P.max_run * G + 15) / 16 * 16;
+    if (ns <= 0 || P.max_run * G > 32) return SV_OK;
+    uint32_t mP = 1;
+    while (mP < 64 && 8 * mP < P.max_splits) mP *= 2;
+    const uint32_t G4 = 256 / mP, mz = (maxcols * D / 4 + G4 - 1) / G4;
+    const uint32_t tq = qkv_w / 16, th = s.hidden / 16, tgu = (2 * s.ffn / 16 + 3) / 4;
+    const uint32_t attn_items = P.n_attn * s.n_kv_heads * P.max_splits, merge_items = P.n_attn * s.n_kv_heads * mz;
+    for (uint32_t c : {tq, th, tgu, attn_items, merge_items})
+      if (c > (uint32_t)ns) return SV_OK;
+    // buffers: h (L + 1 slices), qkv, attn, mixed, act and the split partials (L slices each)
+    const uint32_t L = s.n_layers, NR = 8;
+    LayersParams& lp = P.lp;
+    lp = LayersParams{};
+    lp.n_layers = L;
+    lp.n = P.n;
+    lp.H = s.hidden;
+    lp.F = s.ffn;
+    lp.qkv_m = qkv_w;
+    lp.G = G;
+    lp.h_stride = NR * s.hidden;
+    lp.qkv_stride = NR * qkv_w;
+    lp.attn_stride = NR * s.n_heads * D;
+    lp.mixed_stride = NR * s.hidden;
+    lp.act_stride = NR * s.ffn;
+    size_t l_off = 0;
+    const size_t part = attn_part_floats(&s, P.n_attn, P.max_splits, P.max_run, &l_off);
+    const size_t per_layer = (size_t)lp.qkv_stride + lp.attn_stride + lp.mixed_stride + lp.act_stride + part;
+    const size_t need = (size_t)(L + 1) * lp.h_stride + (size_t)L * per_layer;
+    if (need > pl_floats) {
+      if (graph) return fail(SV_ERR_STATE, "layer buffers must grow after a graph was captured");
+      SV_HIP(hipStreamSynchronize(stream), "layers: buffers");
+      if (pl_buf) SV_HIP(hipFree(pl_buf), "layers: buffers");
+      pl_buf = nullptr;
+      pl_floats = 0;
+      SV_HIP(hipMalloc(&pl_buf, need * 4), "layers: buffers");
+      SV_HIP(hipMemset(pl_buf, 0, need * 4), "layers: buffers");
+      pl_floats = need;
+    }
+    if (!pl_layers) {
+      SV_HIP(hipMalloc(&pl_layers, (size_t)L * sizeof(LayerW)), "layers: parameters");
+      SV_HIP(hipMalloc(&pl_attn, (size_t)L * attn_params_bytes()), "layers: parameters");
+      pl_sync_words = (size_t)L * 6 * 16 * 64 + 2;
+      SV_HIP(hipMalloc(&pl_sync, pl_sync_words * 4), "layers: counters");
+      SV_HIP(hipMemset(pl_sync, 0, pl_sync_words * 4), "layers: counters");
+    }
+    float* b = pl_buf;
+    lp.h = b;
+    b += (size_t)(L + 1) * lp.h_stride;
+    lp.qkv = b;
+    b += (size_t)L * lp.qkv_stride;
+    lp.attn_out = b;
+    b += (size_t)L * lp.attn_stride;
+    lp.mixed = b;
+    b += (size_t)L * lp.mixed_stride;
+    lp.act = b;
+    b += (size_t)L * lp.act_stride;
+    float* parts = b;
+    std::vector<LayerW> lw(L);
+    std::vector<uint8_t> ap((size_t)L * attn_params_bytes());
+    sv_attn_args aa{};
+    aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
+    aa.split = P.split;
+    aa.max_splits = P.max_splits;
+    for (uint32_t li = 0; li < L; li++) {
+      const sv_layer& Ly = layers[li];
+      const sv_matrix* mats[4] = {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down};
+      for (int k = 0; k < 4; k++) {
+        lw[li].w[k] = (const uint8_t*)mats[k]->d_w;
+        lw[li].s[k] = mats[k]->d_scales;
+      }
+      lw[li].qkv_scale = Ly.qkv_scale;
+      lw[li].o_scale = Ly.o_scale;
+      lw[li].ra_attn = Ly.resid_attn;
+      lw[li].rb_attn = Ly.post_attn;
+      lw[li].ra_mlp = Ly.resid_mlp;
+      lw[li].rb_mlp = Ly.post_mlp;
+      aa.rope = Ly.rope;
+      const sv_kv_args kv = kv_args(li);
+      float* po = parts + (size_t)li * part;
+      SV_TRY(attn_params_fill(ap.data() + (size_t)li * attn_params_bytes(), &s, lp.qkv + (size_t)li * lp.qkv_stride,
+                              meta, k_cache, v_cache, page_table, rope_rows, &kv, &aa, P.inl.data(), P.n_attn,
+                              P.max_run, vis, lp.attn_out + (size_t)li * lp.attn_stride, po, po + l_off));
+    }
+    SV_HIP(hipMemcpyAsync(pl_layers, lw.data(), lw.size() * sizeof(LayerW), hipMemcpyHostToDevice, stream),
+           "layers: parameters");
+    SV_HIP(hipMemcpyAsync(pl_attn, ap.data(), ap.size(), hipMemcpyHostToDevice, stream), "layers: parameters");
+    lp.layers = pl_layers;
+    lp.attn = (const AttnParams*)pl_attn;
+    lp.attn_items = attn_items;
+    lp.merge_items = merge_items;
+    lp.merge_P = mP;
+    lp.merge_z = mz;
+    const uint32_t cnt[6] = {tq, attn_items, merge_items, th, tgu, th};
+    for (int k = 0; k < 6; k++) lp.cnt[k] = cnt[k];
+    // counters and epoch from zero for this plan (its phases' producer counts are its own)
+    SV_HIP(hipMemsetAsync(pl_sync, 0, pl_sync_words * 4, stream), "layers: counters");
+    lp.sync = pl_sync;
+    lp.epoch = pl_sync + pl_sync_words - 2;
+    lp.abort = pl_sync + pl_sync_words - 1;
+    P.persist = true;
+    return SV_OK;
+  }
+
+  // After a step that ran the layer kernel: an aborted launch (a wait that ran out) is an error;
+  // its counters are cleared for the next one.
+  sv_status check_layers() {
+    if (!pl_sync) return SV_OK;
+    uint32_t ab = 0;
+    SV_HIP(hipMemcpy(&ab, pl_sync + pl_sync_words - 1, 4, hipMemcpyDeviceToHost), "layers: abort word");
+    if (!ab) return SV_OK;
+    SV_HIP(hipMemset(pl_sync, 0, pl_sync_words * 4), "layers: counters");
+    return fail(SV_ERR_HIP, "the persistent layer kernel gave up waiting (not every workgroup was resident)");
+  }
+
   // Counts `steps` more runs of the plan against its page reservation.
   sv_status issue(uint64_t steps) {
     if (!planned) return fail(SV_ERR_STATE, "no plan");
@@ -542,6 +691,15 @@ struct sv_engine {
     if (!planned) return fail(SV_ERR_STATE, "no plan");
     const Plan& P = plan;
     const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
+    if (P.persist) {
+      // embed into the first h slice (and the epoch the layer kernel's counters count in), every
+      // layer in one launch, then the head on the last slice
+      SV_TIMED(SV_KIND_EMBED, embed_launch(stream, &sh, embed, tokens, tok_res, P.lp.h, tin, meta, lens, feed, tree, vis,
+                                           n, rope, rope_rows, cfg.max_seq_len + SV_FEED_W,
+                                           pl_sync + pl_sync_words - 2));
+      SV_TIMED(SV_KIND_LAYERS, layers_launch(stream, P.lp, P.max_run));
+      return encode_tail(flags, P.lp.h + (size_t)sh.n_layers * P.lp.h_stride);
+    }
     SV_TIMED(SV_KIND_EMBED,
              embed_launch(stream, &sh, embed, tokens, tok_res, emb_out(), tin, meta, lens, feed, tree, vis, n, rope,
                           rope_rows, cfg.max_seq_len + SV_FEED_W));
@@ -592,9 +750,15 @@ struct sv_engine {
     }
     (void)F;
     (void)NQD;
+    return encode_tail(flags, out_of(sh.n_layers - 1));
+  }
+
+  // The head, sampler and step tail after the layers; `last` holds the last layer's rows.
+  sv_status encode_tail(uint32_t flags, const float* last) {
+    const Plan& P = plan;
     if (P.n_head > 0) {
       // rmsnorm_rows + the tied head (encode.rs:390-393), the norm folded into the matmul.
-      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, out_of(sh.n_layers - 1), head_rows, logits, SV_EPI_HEAD,
+      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, last, head_rows, logits, SV_EPI_HEAD,
                                     SV_FLAG_NORM_IN, 1.0f, 0, 0, nullptr, nullptr));
       SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
     }
@@ -721,7 +885,7 @@ extern "C" sv_status sv_engine_create(const sv_engine_config* cfg, const float* 
   if (cfg->max_seqs == 0 || cfg->max_step_tokens == 0 || cfg->max_seq_len == 0 || cfg->max_head_rows == 0 ||
       cfg->kv_tokens == 0)
     return fail(SV_ERR_ARG, "engine_create: zero capacity");
-  if (cfg->options != 0) return fail(SV_ERR_ARG, "engine_create: options %u (none are defined)", cfg->options);
+  if (cfg->options & ~SV_OPT_LAYERS_KERNEL) return fail(SV_ERR_ARG, "engine_create: options %u", cfg->options);
   if (cfg->local) {
     bool any = false;
     for (uint32_t li = 0; li < s.n_layers; li++) any = any || cfg->local[li];
@@ -1478,6 +1642,7 @@ extern "C" sv_status sv_plan(sv_engine* e, const sv_run* runs_in, uint32_t n_run
   SV_TRY(e->upload(e->sample_rows, samples.data(), samples.size() * sizeof(sv_sample_row)));
   SV_TRY(e->upload(e->runs, run_in.data(), run_in.size() * sizeof(sv_run_in)));
   SV_TRY(e->upload(e->attn_runs, attn_runs.data(), attn_runs.size() * 4));
+  SV_TRY(e->plan_layers(P));
   SV_HIP(hipStreamSynchronize(e->stream), "plan upload");
   e->plan = P;
   e->planned = true;
@@ -1533,7 +1698,7 @@ extern "C" sv_status sv_graph_replay(sv_engine* e, uint32_t count) {
 extern "C" sv_status sv_sync(sv_engine* e) {
   if (!e) return fail(SV_ERR_ARG, "sync: null engine");
   SV_HIP(hipStreamSynchronize(e->stream), "sync");
-  return SV_OK;
+  return e->check_layers();
 }
 
 // engine.rs:310-314 step, with generate.rs:446-463 collect: plan, encode, wait, read the
@@ -1547,6 +1712,7 @@ extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, 
   SV_TRY(e->issue(1));
   SV_TRY(e->encode(flags));
   SV_HIP(hipStreamSynchronize(e->stream), "step");
+  SV_TRY(e->check_layers());
   std::vector<uint32_t> em(n_runs);
   SV_HIP(hipMemcpy(em.data(), e->emitted, n_runs * 4, hipMemcpyDeviceToHost), "step emitted");
   if (ids && pi.n_head) SV_HIP(hipMemcpy(ids, e->out_ids, pi.n_head * 4, hipMemcpyDeviceToHost), "step ids");

@@ -25,11 +25,12 @@ __global__ __launch_bounds__(256) void embed_kernel(const uint16_t* table, const
                                                     const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
                                                     const uint32_t* feed, const uint32_t* tree, uint32_t* vis,
                                                     uint32_t H, uint32_t vocab, const float* rope, float* rope_rows,
-                                                    uint32_t rope_n) {
+                                                    uint32_t rope_n, uint32_t* epoch) {
   __shared__ float red[4];
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
   const uint32_t slot = tin[2 * t];
   uint32_t tok = tokens[t], depth = tin[2 * t + 1];
+  if (epoch && t == 0 && tid == 0) *epoch += 1;
   if (tok >= SV_FEED_ROW) {
     const uint32_t i = tok - SV_FEED_ROW, node = tree[slot * SV_FEED_W + i];
     tok = feed[slot * SV_FEED_W + i];
@@ -433,13 +434,13 @@ __global__ __launch_bounds__(256) void step_tail_kernel(TailParams p) {
 sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* table, const uint32_t* tokens,
                        uint32_t* tokens_out, float* out, const uint32_t* tin, uint32_t* meta, const uint32_t* lens,
                        const uint32_t* feed, const uint32_t* tree, uint32_t* vis, uint32_t n, const float* rope,
-                       float* rope_rows, uint32_t rope_n) {
+                       float* rope_rows, uint32_t rope_n, uint32_t* epoch) {
   if (!sh || !table || !tokens || !tokens_out || !out || !tin || !meta || !lens || !feed || !tree || !vis)
     return fail(SV_ERR_ARG, "embed: null pointer");
   if (rope_rows && (!rope || rope_n == 0)) return fail(SV_ERR_ARG, "embed: rope rows without the table");
   if (n == 0) return SV_OK;
   launch(embed_kernel, dim3(n), dim3(256), 0, stream, table, tokens, tokens_out, out, tin, meta, lens, feed,
-                     tree, vis, sh->hidden, sh->vocab, rope, rope_rows, rope_n);
+                     tree, vis, sh->hidden, sh->vocab, rope, rope_rows, rope_n, epoch);
   return check_launch("embed");
 }
 

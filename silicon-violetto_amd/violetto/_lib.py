@@ -39,7 +39,8 @@ FMT_BF16, FMT_I8 = 0, 1
 FMT_TILED = 0x10  # layout flag: 16-row tiles in matrix-core lane order (sv_pack_matrix)
 STEP_REPLAY, STEP_COMPACT, STEP_NO_COMPACT, STEP_DRAFT = 1, 2, 4, 8
 KINDS = ("embed", "qkv", "attn", "o", "gate_up", "down", "head", "sample", "accept", "compact", "replay", "attn_merge", "kv_write",
-         "mudd", "draft")
+         "mudd", "draft", "layers")
+OPT_LAYERS_KERNEL = 1
 
 STATUS = {0: "OK", 1: "ERR_ARG", 2: "ERR_HIP", 3: "ERR_CAPACITY", 4: "ERR_UNSUPPORTED", 5: "ERR_STATE"}
 

@@ -38,14 +38,15 @@ class Engine:
     def __init__(self, shape: ModelShape, *, max_seqs: int = 8, max_step_tokens: int = 64, max_seq_len: int = 8192,
                  max_head_rows: int = 16, kv_tokens: int | None = None, page_shift: int = 4, attn_scale: float = 0.125,
                  split_keys: int = 0, freq: np.ndarray | None = None, local: list[int] | None = None,
-                 window: int = 0):
-        """local: per layer 1 for a sliding-window layer of `window` keys (model.rs:16-17,116)."""
+                 window: int = 0, options: int = 0):
+        """local: per layer 1 for a sliding-window layer of `window` keys (model.rs:16-17,116);
+        options: SV_OPT_* bits (OPT_LAYERS_KERNEL: the persistent layer kernel where it applies)."""
         self.shape = shape
         self.lib = L.lib()
         self._local = None if local is None else (C.c_uint8 * shape.n_layers)(*[int(x) for x in local])
         cfg = L.EngineConfig(shape.c(), max_seqs, max_step_tokens, max_seq_len, max_head_rows,
                              kv_tokens if kv_tokens is not None else max_seqs * max_seq_len, page_shift, attn_scale,
-                             split_keys, 0, window, 0,
+                             split_keys, options, window, 0,
                              C.cast(self._local, C.c_void_p) if self._local is not None else None)
         self.cfg = cfg
         f = np.ascontiguousarray(freq if freq is not None else rope_freq(500000.0, shape.head_dim), dtype=np.float32)
