@@ -60,6 +60,8 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
 
     tree: each stream verifies the fixed 16-node draft tree TREE_PARENTS every step (node ids
     random, drawn once; no replay drafter, no trace): the configs[4] workload."""
+    import ctypes as C
+
     import numpy as np
     import torch
 
@@ -69,7 +71,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
 
     k = args.draft
     rows = 16 if tree else k + 1
-    n_steps = warmup + steps + profile_reps + 4
+    n_steps = warmup + 2 * steps + profile_reps + 4  # the timed steps run twice (the re-run classifies)
     trace_n = rows * n_steps + 32
     max_ctx = max(ctxs)
     max_seq_len = max_ctx + trace_n + 64
@@ -164,34 +166,48 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
         eng.graph_capture(L.STEP_REPLAY)
     lens = eng.view("d_lens", (streams,))
     divergences = []
+    outv = eng.view("d_out_ids", (streams * rows,))
+    seen = set()
+
+    def checked_step(w, leg):
+        """One replay, each stream's emitted tokens checked against its plain decode. Where they
+        first differ, the distance between the drawn and the recorded id in the sampler's fixed
+        order says what moved the draw: 1 is the neighbouring id (a CDF edge that the two
+        computations' fp32 rounding put on different sides of the uniform)."""
+        before = lens.cpu().numpy().astype(np.int64)
+        eng.graph_replay(1)
+        eng.sync()
+        after = lens.cpu().numpy().astype(np.int64)
+        out = outv.cpu().numpy().view(np.uint32)
+        for i, s in enumerate(slots):
+            if s in seen:
+                continue
+            got = [int(x) for x in out[rows * i: rows * i + after[s] - before[s]]]
+            off = int(before[s]) - ctxs[i] + 1
+            want = traces[i][off: off + len(got)]
+            if got != want:
+                m = next(j for j in range(len(got)) if j >= len(want) or got[j] != want[j])
+                seen.add(s)
+                divergences.append({"stream": s, "leg": leg, "step": w, "position": int(before[s]) + m,
+                                    "order_distance": None if m >= len(want) else
+                                    abs(sample_order(got[m], shape.vocab) - sample_order(want[m], shape.vocab))})
+        return int((after - before).sum())
+
     if tree:
         eng.graph_replay(warmup)
         eng.sync()
     else:
-        # Warm-up steps one at a time, each stream's emitted tokens checked against its plain
-        # decode. Where they first differ, the distance between the drawn and the recorded id in
-        # the sampler's fixed order says what moved the draw: 1 is the neighbouring id (a CDF edge
-        # that the two computations' fp32 rounding put on different sides of the uniform).
-        outv = eng.view("d_out_ids", (streams * rows,))
-        seen = set()
         for w in range(warmup):
-            before = lens.cpu().numpy().astype(np.int64)
-            eng.graph_replay(1)
-            eng.sync()
-            after = lens.cpu().numpy().astype(np.int64)
-            out = outv.cpu().numpy().view(np.uint32)
-            for i, s in enumerate(slots):
-                if s in seen:
-                    continue
-                got = [int(x) for x in out[rows * i: rows * i + after[s] - before[s]]]
-                off = int(before[s]) - ctxs[i] + 1
-                want = traces[i][off: off + len(got)]
-                if got != want:
-                    m = next(j for j in range(len(got)) if j >= len(want) or got[j] != want[j])
-                    seen.add(s)
-                    divergences.append({"stream": s, "step": w, "position": int(before[s]) + m,
-                                        "order_distance": None if m >= len(want) else
-                                        abs(sample_order(got[m], shape.vocab) - sample_order(want[m], shape.vocab))})
+            checked_step(w, "warmup")
+    # The state the timed steps start from (sequence state and K/V cache, on the device): after
+    # timing, the same steps are re-run from it one at a time to classify every stream that leaves
+    # its trace during them (graph replays are deterministic: the re-run emits the same tokens).
+    snap = None
+    if not tree:
+        snap = {nm: eng.view(nm, shp).clone() for nm, shp in
+                (("d_lens", (streams,)), ("d_feed", (streams * 16,)), ("d_tree", (streams * 16,)),
+                 ("d_gen", (streams * C.sizeof(L.GenState) // 4,)))}
+        snap["k"], snap["v"] = kd.clone(), vd.clone()
     len0 = lens.cpu().numpy().astype(np.int64)
     log(f"split {info.split} keys, grid {info.max_splits} splits; timing {steps} steps")
     torch.cuda.synchronize()
@@ -216,6 +232,19 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
 
     prof = eng.profile_step(L.STEP_REPLAY, reps=profile_reps)
     per_step_ms = {kk: v[0] / profile_reps for kk, v in prof.items() if v[1]}
+    rerun_emitted = None
+    if snap is not None:
+        for nm, shp in (("d_lens", (streams,)), ("d_feed", (streams * 16,)), ("d_tree", (streams * 16,)),
+                        ("d_gen", (streams * C.sizeof(L.GenState) // 4,))):
+            eng.view(nm, shp).copy_(snap[nm])
+        kd.copy_(snap["k"])
+        vd.copy_(snap["v"])
+        del snap
+        torch.cuda.synchronize()
+        rerun_emitted = sum(checked_step(w, "timed") for w in range(steps))
+        log(f"re-run of the timed steps: {rerun_emitted} tokens (timed: {emitted}); "
+            f"{len(divergences)} stream(s) left the trace, order distances "
+            f"{[d['order_distance'] for d in divergences]}")
     ctx_mid = float(((len0 + len1) / 2).sum())
     H, F, V = shape.hidden, shape.ffn, shape.vocab
     n_rows = streams * rows
@@ -235,6 +264,7 @@ def run_workload(args, model, shape, *, streams: int, ctxs: list[int], temperatu
                steps=steps, warmup=warmup,
                emitted=emitted, secs=secs, ms_step=ms_step, value=emitted / secs, lossless=lossless,
                lossless_streams=None if tree else sum(same), divergences=divergences, prof=prof,
+               rerun_emitted=rerun_emitted,
                per_step_ms=per_step_ms, attn_bytes=attn_bytes, mat_bytes=mat_bytes, step_bytes=step_bytes,
                layers_bytes=layers_bytes,
                flops=flops, info=info, rows=rows, mat_elems=mat_elems, n_rows=n_rows)
@@ -583,7 +613,7 @@ def main() -> int:
         s32 = {"value": round(r2["value"], 2), "unit": "verified tok/s", "ms_per_step": round(r2["ms_step"], 5),
                "steps": r2["steps"], "emitted_per_step": round(r2["emitted"] / r2["steps"], 3),
                "lossless_trace_check": r2["lossless"], "lossless_streams": r2["lossless_streams"],
-               "warmup_divergences": r2["divergences"],
+               "divergences": r2["divergences"], "emitted": r2["emitted"], "rerun_emitted": r2["rerun_emitted"],
                "config": {"workload": "configs[2]: 32 streams, ctx U[1024,8192] (mean %d), shuffled page tables, "
                                       "k=4, T=0.7 Philox-seeded sample-and-match" % int(np.mean(ctxs)),
                           "rows_per_step": 32 * r2["rows"]},

@@ -437,8 +437,9 @@ sv_status sv_engine_set_embed(sv_engine* e, const uint16_t* d_embed);
 sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_layer* l);
 sv_status sv_engine_set_extras(sv_engine* e, const sv_model_extras* x);
 /* A head of its own (model.rs:93-95: the weight file's quantized `head`), [vocab][hidden]: bf16,
- * or int8 with one scale per row or per group of 64 or more (the reference's int8 head default,
- * groups of 8, is not built); NULL: the tied embedding again. */
+ * or int8 with one scale per row or per group of 8 to 256 (groups under 64, such as the
+ * reference converter's default of 8, run as two exact bf16 matrices hi + lo and a softcap
+ * pass); NULL: the tied embedding again. */
 sv_status sv_engine_set_head(sv_engine* e, const sv_matrix* head);
 /* The HIP stream the engine runs on (a hipStream_t), created by the engine. */
 void* sv_engine_stream(sv_engine* e);

@@ -264,6 +264,10 @@ struct sv_engine {
   const uint16_t* embed = nullptr;
   sv_matrix head_mat{};  // the head: the tied embedding or its own (tiled when the shape allows)
   bool own_head = false;
+  // A head of its own in int8 groups under 64 (tools/convert.py's default, groups of 8): the
+  // exact sum of two bf16 matrices, head_mat (hi) and head_lo; softcapped after both.
+  sv_matrix head_lo{};
+  void* head_lo_tiled = nullptr;
   std::vector<sv_layer> layers;  // as used: matrices repacked into the tiled layout where they fit it
   std::vector<bool> layer_set;
   std::vector<void*> packed;     // engine-owned tiled copies [layer * 4 + matrix]
@@ -419,6 +423,7 @@ struct sv_engine {
     for (void* b : {(void*)pl_buf, (void*)pl_layers, pl_attn, (void*)pl_sync})
       if (b) (void)hipFree(b);
     if (head_tiled) (void)hipFree(head_tiled);
+    if (head_lo_tiled) (void)hipFree(head_lo_tiled);
     if (tap[0]) (void)hipFree(tap[0]);
     if (tap[1] && tap[1] != tap[0]) (void)hipFree(tap[1]);
     free_drafter();
@@ -758,8 +763,17 @@ struct sv_engine {
     const Plan& P = plan;
     if (P.n_head > 0) {
       // rmsnorm_rows + the tied head (encode.rs:390-393), the norm folded into the matmul.
-      SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, last, head_rows, logits, SV_EPI_HEAD,
-                                    SV_FLAG_NORM_IN, 1.0f, 0, 0, nullptr, nullptr));
+      if (head_lo.d_w) {
+        // hi + lo products (raw, the norm folded), then the softcap
+        SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, last, head_rows, logits, SV_EPI_RAW, SV_FLAG_NORM_IN, 1.0f,
+                                      0, 0, nullptr, nullptr));
+        SV_TIMED(SV_KIND_HEAD, matmul(head_lo, P.n_head, last, head_rows, logits, SV_EPI_RESID, SV_FLAG_NORM_IN, 1.0f,
+                                      1.0f, 1.0f, logits, nullptr));
+        SV_TIMED(SV_KIND_HEAD, head_cap_launch(stream, logits, P.n_head, sh.vocab, sh.vocab_real));
+      } else {
+        SV_TIMED(SV_KIND_HEAD, matmul(head_mat, P.n_head, last, head_rows, logits, SV_EPI_HEAD,
+                                      SV_FLAG_NORM_IN, 1.0f, 0, 0, nullptr, nullptr));
+      }
       SV_TIMED(SV_KIND_SAMPLE, sample_launch(stream, logits, sample_rows, out_ids, meta, P.n_head, sh.vocab));
     }
     // accept + kv_compact + replay drafter (encode.rs:394-435, 439-451) as one launch.
@@ -1106,6 +1120,7 @@ extern "C" sv_status sv_engine_set_layer(sv_engine* e, uint32_t layer, const sv_
 extern "C" sv_status sv_engine_set_head(sv_engine* e, const sv_matrix* head) {
   if (!e) return fail(SV_ERR_ARG, "set_head: null engine");
   if (e->graph) return fail(SV_ERR_STATE, "set_head: after a graph was captured");
+  e->head_lo = sv_matrix{};
   if (!head) {
     e->own_head = false;
     if (!e->embed) return SV_OK;
@@ -1115,9 +1130,29 @@ extern "C" sv_status sv_engine_set_head(sv_engine* e, const sv_matrix* head) {
   SV_TRY(check_matrix(*head, e->sh.vocab, e->sh.hidden, "head"));
   const uint32_t fmt = head->format & ~(uint32_t)SV_FMT_TILED;
   const bool per_row = head->gshift >= 32 || (1ull << head->gshift) >= head->k;
-  if (fmt == SV_FMT_I8 && !per_row && head->gshift < 6)
-    return fail(SV_ERR_UNSUPPORTED, "set_head: int8 groups of %u (64 or more, or one per row, are built)",
-                1u << head->gshift);
+  if (fmt == SV_FMT_I8 && !per_row && head->gshift < 6) {
+    // groups of 8-32 (model.rs:98 accepts 8-256; the converter's head default is 8): a matrix
+    // core step would mix several groups' scales, so the head runs as two bf16 matrices whose
+    // sum is exactly q s (8 + 8 significant bits hold the 15 of the product)
+    if (head->format & SV_FMT_TILED) return fail(SV_ERR_UNSUPPORTED, "set_head: a tiled head in groups under 64");
+    const size_t elems = (size_t)head->m * head->k;
+    uint16_t *hi = nullptr, *lo = nullptr;
+    SV_TRY(dalloc(&hi, elems, "head hi"));
+    sv_status st = dalloc(&lo, elems, "head lo");
+    if (st == SV_OK) st = split_i8_launch(e->stream, head, hi, lo);
+    if (st == SV_OK) st = check_hip(hipStreamSynchronize(e->stream), "head split");
+    const sv_matrix mh{hi, nullptr, head->m, head->k, SV_FMT_BF16, 0}, ml{lo, nullptr, head->m, head->k, SV_FMT_BF16, 0};
+    if (st == SV_OK) st = pack_into(e, mh, &e->head_tiled, &e->head_mat);
+    if (st == SV_OK) st = pack_into(e, ml, &e->head_lo_tiled, &e->head_lo);
+    (void)hipFree(hi);
+    if (lo) (void)hipFree(lo);
+    if (st != SV_OK) {
+      e->head_lo = sv_matrix{};
+      return st;
+    }
+    e->own_head = true;
+    return SV_OK;
+  }
   SV_TRY(pack_into(e, *head, &e->head_tiled, &e->head_mat));
   e->own_head = true;
   return SV_OK;

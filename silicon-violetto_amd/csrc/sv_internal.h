@@ -125,6 +125,7 @@ sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* t
                        const float* rope = nullptr,  // with rope_rows: the table's row at each token's position
                        float* rope_rows = nullptr, uint32_t rope_n = 0,  // rope_n: the table's rows
                        uint32_t* epoch = nullptr);  // incremented once (the persistent kernel's step count)
+sv_status head_cap_launch(hipStream_t stream, float* logits, uint32_t rows, uint32_t vocab, uint32_t vocab_real);
 sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
                               uint32_t hidden);
 sv_status sample_launch(hipStream_t stream, const float* logits, const sv_sample_row* rows, uint32_t* out,

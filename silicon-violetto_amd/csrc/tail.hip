@@ -444,6 +444,24 @@ sv_status embed_launch(hipStream_t stream, const sv_shape* sh, const uint16_t* t
   return check_launch("embed");
 }
 
+// The head's softcap (kernels.metal:196-199) over logits a matmul left raw (a head in int8 groups
+// under 64 runs as two bf16 products, hi + lo): y = 23 sigmoid((y + 5) / 7.5), -inf at ids >=
+// vocab_real; the same expression as the matmul's head epilogue.
+__global__ __launch_bounds__(256) void head_cap_kernel(float* logits, uint32_t vocab, uint32_t vocab_real, size_t total) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t col = (uint32_t)(i % vocab);
+  logits[i] = col < vocab_real ? 23.0f * (1.0f / (1.0f + __expf(-((logits[i] + 5.0f) / 7.5f)))) : -__builtin_inff();
+}
+
+sv_status head_cap_launch(hipStream_t stream, float* logits, uint32_t rows, uint32_t vocab, uint32_t vocab_real) {
+  if (!logits || vocab == 0 || vocab_real > vocab) return fail(SV_ERR_ARG, "head_cap: arguments");
+  const size_t total = (size_t)rows * vocab;
+  if (total == 0) return SV_OK;
+  launch(head_cap_kernel, dim3((uint32_t)((total + 255) / 256)), dim3(256), 0, stream, logits, vocab, vocab_real, total);
+  return check_launch("head_cap");
+}
+
 sv_status rmsnorm_rows_launch(hipStream_t stream, const float* in, const uint32_t* rows, float* out, uint32_t n,
                               uint32_t hidden) {
   if (!in || !rows || !out) return fail(SV_ERR_ARG, "rmsnorm_rows: null pointer");

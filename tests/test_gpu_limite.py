@@ -366,12 +366,44 @@ def test_limite_from_weight_file(gpu, tmp_path, head_group):
     wf.close()
 
 
-def test_head_of_small_groups_is_refused(gpu):
-    """An int8 head in groups of 8 (the reference converter's head default) is refused with a
-    clear error; groups of 64 and more, or one per row, are served."""
-    shape = ModelShape(hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=256, vocab=512, vocab_real=500, n_layers=1)
-    model = SyntheticModel.generate(shape, seed=1).with_head(8).to("cuda")
-    eng = Engine(shape, max_seqs=1, max_step_tokens=16, max_seq_len=64, freq=rope_freq(500000.0, 64))
-    with pytest.raises(L.SvError, match="groups of 8"):
-        eng.set_model(model)
+@pytest.mark.parametrize("group", [8, 32])
+def test_head_in_small_groups(gpu, group):
+    """The reference converter's default int8 head (groups of 8, tools/convert.py:20; model.rs:98
+    accepts 8-256) and groups of 32, with layers in groups of 64 as INT8_DEFAULT writes them:
+    the engine serves the head as two exact bf16 matrices hi + lo and a softcap pass. Two
+    streams of 5-row verify steps (the one-shot matmul) and of 12-row steps (24 rows: the
+    GEMM path) against the oracle engine with the same int8 head."""
+    banner(f"int8 head in groups of {group}")
+    shape = ModelShape(hidden=512, n_heads=8, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024, vocab_real=1000,
+                       n_layers=2)
+    model = SyntheticModel.generate(shape, seed=17, device="cpu", group=64).with_head(group)
+    freq = rope_freq(500000.0, 64)
+    eng = Engine(shape, max_seqs=2, max_step_tokens=32, max_seq_len=512, max_head_rows=32, kv_tokens=1024,
+                 attn_scale=0.125, freq=freq)
+    eng.set_model(model.to("cuda"))
+    emb, lay, sc = oracle.host_weights(model)
+    ref = oracle.OracleEngine(L, shape, emb, lay, sc, max_seqs=2, max_seq_len=512, kv_tokens=1024, attn_scale=0.125,
+                              freq=freq, head=oracle.host_head(model))
+    rng = np.random.default_rng(group)
+    slots = []
+    for c in (200, 90):
+        s = eng.new_seq()
+        assert s == ref.new_seq()
+        eng.bench_fill(s, c)
+        ref.bench_fill(s, c)
+        slots.append(s)
+    kd, vd = eng.kv_cache()
+    for dev_t, host in ((kd, ref.k), (vd, ref.v)):
+        bits = rand_bits(rng, host.shape)
+        host[...] = bits
+        dev_t.copy_(torch.from_numpy(bits.view(np.int16)).cuda().view(torch.bfloat16))
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, ref.seq_len[s], t)
+        ref.set_feed(s, ref.seq_len[s], t)
+    for step, rows in enumerate((5, 12, 5)):
+        runs = [(s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, rows - 1)], True) for s in slots]
+        same, _, _, _ = step_both(eng, ref, runs, slots, f"step {step} ({rows} rows per stream)")
+        if not same:
+            break
     eng.close()

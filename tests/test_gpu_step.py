@@ -700,3 +700,26 @@ def test_prompt_chunks_then_verify(gpu):
     ids_r, logits_r, em_r, extra_r = ref.step(runs)
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots, runs=runs)
     eng.close()
+
+
+@pytest.mark.parametrize("n_seqs", [1, 8])
+def test_config3_long_context_bf16(gpu, n_seqs):
+    """configs[3] end to end: unquantised bf16 weights (N(0, 0.02)) over two layers, 1 or 8
+    streams each with 65536 cached tokens (random bf16 K/V), two greedy verify steps of k = 4
+    linear drafts, the split-KV attention at the engine's own split choice, against the oracle
+    engine: logits, greedy ids, emitted counts, lengths and page tables at the step bar."""
+    banner(f"configs[3] end to end, {n_seqs} stream(s) x 65536")
+    shape = ModelShape(n_layers=2)
+    model, gm, eng, ref, slots, rng = build_pair(shape, ctx=65536, n_seqs=n_seqs, seed=31, int8=False,
+                                                 max_seq_len=65536 + 64, fast_kv=True, max_head_rows=16 * n_seqs)
+    for s in slots:
+        t = int(rng.integers(0, shape.vocab_real))
+        eng.set_feed(s, 65536, t)
+        ref.set_feed(s, 65536, t)
+    for step in range(2):
+        runs = [(s, [L.FEED_ROW] + [int(x) for x in rng.integers(0, shape.vocab_real, 4)], True) for s in slots]
+        ids_r, logits_r, em_r, extra_r = ref.step(runs)
+        res = eng.step(runs, logits=True)
+        print(f"  step {step}: split {res.info.split} keys, {res.info.max_splits} splits", flush=True)
+        compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots, runs=runs)
+    eng.close()
