@@ -666,8 +666,6 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
 }
 
 // ------------------------------------------- the persistent layer kernel's attention
-size_t attn_params_bytes() { return sizeof(AttnParams); }
-
 // Floats of one layer's split partials (o, then l at *l_off), 64-float aligned.
 size_t attn_part_floats(const sv_shape* sh, uint32_t n_runs, uint32_t max_splits, uint32_t max_run, size_t* l_off) {
   const size_t maxcols = cols_pad(sh, max_run);

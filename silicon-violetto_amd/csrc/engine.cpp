@@ -15,6 +15,7 @@
 #include <string>
 #include <vector>
 
+#include "layers.h"
 #include "sv_internal.h"
 
 namespace sv {
@@ -366,8 +367,6 @@ struct sv_engine {
   // apart, never reset but after an abort), the epoch word embed increments and the abort word.
   float* pl_buf = nullptr;
   size_t pl_floats = 0;
-  LayerW* pl_layers = nullptr;
-  void* pl_attn = nullptr;
   uint32_t* pl_sync = nullptr;
   size_t pl_sync_words = 0;
 
@@ -420,7 +419,7 @@ struct sv_engine {
       if (b) (void)hipFree(b);
     for (void* b : packed)
       if (b) (void)hipFree(b);
-    for (void* b : {(void*)pl_buf, (void*)pl_layers, pl_attn, (void*)pl_sync})
+    for (void* b : {(void*)pl_buf, (void*)pl_sync})
       if (b) (void)hipFree(b);
     if (head_tiled) (void)hipFree(head_tiled);
     if (head_lo_tiled) (void)hipFree(head_lo_tiled);
@@ -593,6 +592,7 @@ struct sv_engine {
     const size_t part = attn_part_floats(&s, P.n_attn, P.max_splits, P.max_run, &l_off);
     const size_t per_layer = (size_t)lp.qkv_stride + lp.attn_stride + lp.mixed_stride + lp.act_stride + part;
     const size_t need = (size_t)(L + 1) * lp.h_stride + (size_t)L * per_layer;
+    if (L > PL_MAX_LAYERS) return SV_OK;
     if (need > pl_floats) {
       if (graph) return fail(SV_ERR_STATE, "layer buffers must grow after a graph was captured");
       SV_HIP(hipStreamSynchronize(stream), "layers: buffers");
@@ -603,10 +603,8 @@ struct sv_engine {
       SV_HIP(hipMemset(pl_buf, 0, need * 4), "layers: buffers");
       pl_floats = need;
     }
-    if (!pl_layers) {
-      SV_HIP(hipMalloc(&pl_layers, (size_t)L * sizeof(LayerW)), "layers: parameters");
-      SV_HIP(hipMalloc(&pl_attn, (size_t)L * attn_params_bytes()), "layers: parameters");
-      pl_sync_words = (size_t)L * 6 * 16 * 64 + 2;
+    if (!pl_sync) {
+      pl_sync_words = (size_t)PL_MAX_LAYERS * 6 * 16 * 64 + 2;
       SV_HIP(hipMalloc(&pl_sync, pl_sync_words * 4), "layers: counters");
       SV_HIP(hipMemset(pl_sync, 0, pl_sync_words * 4), "layers: counters");
     }
@@ -621,38 +619,34 @@ struct sv_engine {
     b += (size_t)L * lp.mixed_stride;
     lp.act = b;
     b += (size_t)L * lp.act_stride;
-    float* parts = b;
-    std::vector<LayerW> lw(L);
-    std::vector<uint8_t> ap((size_t)L * attn_params_bytes());
+    lp.part = b;
+    lp.part_stride = (uint32_t)part;
+    lp.part_l_off = (uint32_t)l_off;
     sv_attn_args aa{};
     aa.scale_log2 = cfg.attn_scale * 1.44269504088896340736f;
     aa.split = P.split;
     aa.max_splits = P.max_splits;
+    aa.rope = 1;
+    lp.rope_mask = 0;
     for (uint32_t li = 0; li < L; li++) {
       const sv_layer& Ly = layers[li];
       const sv_matrix* mats[4] = {&Ly.qkv, &Ly.o, &Ly.gate_up, &Ly.down};
       for (int k = 0; k < 4; k++) {
-        lw[li].w[k] = (const uint8_t*)mats[k]->d_w;
-        lw[li].s[k] = mats[k]->d_scales;
+        lp.layers[li].w[k] = (const uint8_t*)mats[k]->d_w;
+        lp.layers[li].s[k] = mats[k]->d_scales;
       }
-      lw[li].qkv_scale = Ly.qkv_scale;
-      lw[li].o_scale = Ly.o_scale;
-      lw[li].ra_attn = Ly.resid_attn;
-      lw[li].rb_attn = Ly.post_attn;
-      lw[li].ra_mlp = Ly.resid_mlp;
-      lw[li].rb_mlp = Ly.post_mlp;
-      aa.rope = Ly.rope;
-      const sv_kv_args kv = kv_args(li);
-      float* po = parts + (size_t)li * part;
-      SV_TRY(attn_params_fill(ap.data() + (size_t)li * attn_params_bytes(), &s, lp.qkv + (size_t)li * lp.qkv_stride,
-                              meta, k_cache, v_cache, page_table, rope_rows, &kv, &aa, P.inl.data(), P.n_attn,
-                              P.max_run, vis, lp.attn_out + (size_t)li * lp.attn_stride, po, po + l_off));
+      lp.layers[li].qkv_scale = Ly.qkv_scale;
+      lp.layers[li].o_scale = Ly.o_scale;
+      lp.layers[li].ra_attn = Ly.resid_attn;
+      lp.layers[li].rb_attn = Ly.post_attn;
+      lp.layers[li].ra_mlp = Ly.resid_mlp;
+      lp.layers[li].rb_mlp = Ly.post_mlp;
+      if (Ly.rope) lp.rope_mask |= 1u << li;
     }
-    SV_HIP(hipMemcpyAsync(pl_layers, lw.data(), lw.size() * sizeof(LayerW), hipMemcpyHostToDevice, stream),
-           "layers: parameters");
-    SV_HIP(hipMemcpyAsync(pl_attn, ap.data(), ap.size(), hipMemcpyHostToDevice, stream), "layers: parameters");
-    lp.layers = pl_layers;
-    lp.attn = (const AttnParams*)pl_attn;
+    // the shared attention parameters (layer 0's slices; the kernel replaces them per layer)
+    const sv_kv_args kv0 = kv_args(0);
+    SV_TRY(attn_params_fill(&lp.ap, &s, lp.qkv, meta, k_cache, v_cache, page_table, rope_rows, &kv0, &aa,
+                            P.inl.data(), P.n_attn, P.max_run, vis, lp.attn_out, lp.part, lp.part + l_off));
     lp.attn_items = attn_items;
     lp.merge_items = merge_items;
     lp.merge_P = mP;

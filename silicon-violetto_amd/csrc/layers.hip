@@ -36,8 +36,7 @@
 // targets are epoch x producers. Every poll is bounded; a workgroup that waits too long sets
 // the abort word (every poll reads it) and the whole grid drains without hanging; the host
 // reports it and clears the counters.
-#include "attn_device.h"
-#include "sv_internal.h"
+#include "layers.h"
 
 namespace sv {
 
@@ -284,17 +283,17 @@ struct AttnItem {
 
 // Every batch slot is written (slots the item does not need read nothing: offsets past the
 // range), so no earlier batch stays live around the layer loop. item >= items: inactive.
-__device__ __forceinline__ void attn_prefetch(const AttnParams& p, uint32_t item, uint32_t items, AttnItem& a, int wv,
-                                              int lane) {
+__device__ __forceinline__ void attn_prefetch(const AttnParams& p, const uint32_t* inl, uint32_t item, uint32_t items,
+                                              AttnItem& a, int wv, int lane) {
   a.active = item < items;
   if (!a.active) item = 0;
   const uint32_t per_run = p.NKV * p.max_splits;
   a.r = item / per_run;
   a.g = (item / p.max_splits) % p.NKV;
   a.s = item % p.max_splits;
-  a.t0 = p.inl[3 * a.r];
-  a.T = p.inl[3 * a.r + 1];
-  a.seq = p.inl[3 * a.r + 2];
+  a.t0 = inl[3 * a.r];
+  a.T = inl[3 * a.r + 1];
+  a.seq = inl[3 * a.r + 2];
   const uint32_t kbeg = a.s * p.split;
   const uint32_t tpos = kbeg + 32 * (wv + 4 * (lane >> 1)) + 16 * (lane & 1);
   const uint32_t pword = p.page_table[(size_t)a.seq * p.max_pages + min(tpos >> p.page_shift, p.max_pages - 1)];
@@ -465,7 +464,8 @@ __device__ __forceinline__ void attn_compute(const AttnParams& p, AttnItem& a, c
 
 // The split merge (attn_dec_reduce, kernels.metal:1316-1362) as attn_merge_kernel: item
 // (run, kv head, z) with P parts of 256 / P float4 outputs each.
-__device__ __forceinline__ void attn_merge_item(const AttnParams& p, uint32_t item, uint32_t P, uint32_t mz, char* smem,
+__device__ __forceinline__ void attn_merge_item(const AttnParams& p, const uint32_t* inl, uint32_t item, uint32_t P,
+                                                uint32_t mz, char* smem,
                                                 int tid) {
   constexpr int D = 64;
   f32x4* so = (f32x4*)smem;
@@ -473,7 +473,7 @@ __device__ __forceinline__ void attn_merge_item(const AttnParams& p, uint32_t it
   const uint32_t G4 = 256 / P, part = tid / G4, gi = tid % G4;
   const uint32_t r = item / (p.NKV * mz), g = (item / mz) % p.NKV, z = item % mz;
   const uint32_t i4 = z * G4 + gi;
-  const uint32_t t0 = p.inl[3 * r], T = p.inl[3 * r + 1];
+  const uint32_t t0 = inl[3 * r], T = inl[3 * r + 1];
   const uint32_t ncols = T * p.G;
   const bool live = 4 * i4 < ncols * D;
   const uint32_t col = live ? (4 * i4) / D : 0u, d = (4 * i4) % D;
@@ -516,6 +516,18 @@ __device__ __forceinline__ void attn_merge_item(const AttnParams& p, uint32_t it
     store_wt4(coherent_rsrc(p.out), (((t * p.NQ) + h) * D + d) * 4, o / l);
   }
   __syncthreads();
+}
+
+// Layer l's attention: the shared parameters with its slices, its cache layer and its rope.
+__device__ __forceinline__ AttnParams layer_attn(const LayersParams& p, uint32_t l) {
+  AttnParams a = p.ap;
+  a.qkv = p.qkv + (size_t)l * p.qkv_stride;
+  a.out = p.attn_out + (size_t)l * p.attn_stride;
+  a.part_o = p.part + (size_t)l * p.part_stride;
+  a.part_l = a.part_o + p.part_l_off;
+  a.layer = l;
+  a.rope_on = (p.rope_mask >> l) & 1u;
+  return a;
 }
 
 // ------------------------------------------------------------------------------ kernel
@@ -568,10 +580,10 @@ __device__ __forceinline__ void run_set_b(const LayersParams& p, uint32_t j, uin
   const uint32_t H = p.H, F = p.F, n = p.n, L = p.n_layers;
   const uint32_t th = H / 16;
   AttnItem ai;
-  attn_prefetch(p.attn[0], j, p.attn_items, ai, wv, lane);
+  attn_prefetch(layer_attn(p, 0), p.ap.inl, j, p.attn_items, ai, wv, lane);
   for (uint32_t l = 0; l < L; l++) {
     const LayerW& lw = p.layers[l];
-    const AttnParams& ap = p.attn[l];
+    const AttnParams ap = layer_attn(p, l);
     if (!pl_wait(p, 6 * l + 0, epoch * p.cnt[0], sflag)) return;
     pl_stamp(p, 1, j, l, 1, 0);
     if (j < p.attn_items) {
@@ -585,7 +597,7 @@ __device__ __forceinline__ void run_set_b(const LayersParams& p, uint32_t j, uin
       if (!pl_wait(p, 6 * l + 1, epoch * p.cnt[1], sflag)) return;
       pl_stamp(p, 1, j, l, 2, 0);
       if (j < p.merge_items) {
-        attn_merge_item(ap, j, p.merge_P, p.merge_z, smem, tid);
+        attn_merge_item(ap, p.ap.inl, j, p.merge_P, p.merge_z, smem, tid);
         pl_arrive(p, 6 * l + 2, j);
         pl_stamp(p, 1, j, l, 2, 1);
       }
@@ -613,7 +625,7 @@ __device__ __forceinline__ void run_set_b(const LayersParams& p, uint32_t j, uin
       }
     }
     const uint32_t ln = l + 1 < L ? l + 1 : l;
-    attn_prefetch(p.attn[ln], l + 1 < L ? j : p.attn_items, p.attn_items, ai, wv, lane);
+    attn_prefetch(layer_attn(p, ln), p.ap.inl, l + 1 < L ? j : p.attn_items, p.attn_items, ai, wv, lane);
   }
 }
 

@@ -150,6 +150,24 @@ __device__ __forceinline__ u32x4 philox(u32x4 c, uint32_t k0, uint32_t k1) {
 // then counts its arrival with a relaxed agent-scope atomic; the last of `expected`
 // arrivals reads every partial with relaxed agent-scope atomic loads (sc1, pipelined) and resets
 // the counter for the next launch. All threads of the workgroup must call arrive_last.
+//
+// The ordering this relies on, instruction by instruction (not the HIP memory model's
+// release/acquire, which would emit the L2 write-back and invalidate):
+//   - An sc1 (device-scope) store is written through the XCD's L2 to memory, the level every
+//     XCD's loads reach; its vmcnt decrement comes when that write is acknowledged, so after
+//     s_waitcnt vmcnt(0) the data is visible to any device-scope load.
+//   - s_waitcnt vmcnt(0) in every thread, then s_barrier, then the counter atomic from one
+//     thread: the atomic issues after every thread's stores were acknowledged (the wait is an
+//     instruction the hardware executes in order; the compiler does not move memory operations
+//     across it or across the barrier).
+//   - The consumer's device-scope atomic returns the count from memory; its partial loads are
+//     sc1 loads issued after that return (their addresses do not depend on it, but the branch
+//     on the count does: a wave does not issue an instruction after a branch before the branch
+//     resolves, and the load is not hoisted above it: it sits behind the workgroup barrier that
+//     publishes the count). They miss in any L2 line that could be stale: sc1 loads are served
+//     at device scope.
+// The split-k matmul and the counted attention merge are tested against the oracle (their
+// partials cross XCDs in every launch), which is the regression check of this contract.
 __device__ __forceinline__ void store_wt(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

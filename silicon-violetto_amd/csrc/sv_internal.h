@@ -76,41 +76,8 @@ sv_status attn_launch_noalloc(hipStream_t stream, const sv_shape* sh, const floa
                               uint32_t max_run, const uint32_t* vis, float* out);
 size_t attn_scratch_bytes();
 
-// The persistent layer kernel (layers.hip): every decoder layer of a 1-8 row step in one
-// launch. Per layer: the tiled int8 matrices (qkv, o, gate_up, down) and their per-row scales.
-struct AttnParams;
-struct LayerW {
-  const uint8_t* w[4];
-  const uint16_t* s[4];
-  float qkv_scale, o_scale, ra_attn, rb_attn, ra_mlp, rb_mlp;
-};
-struct LayersParams {
-  const LayerW* layers;       // [n_layers] (device)
-  const AttnParams* attn;     // [n_layers] (device): each layer's attention, its slices filled in
-  uint32_t n_layers, n, H, F, qkv_m, G;
-  // activation slices, one per layer (h: n_layers + 1, slice 0 the embedding's rows)
-  float *h, *qkv, *attn_out, *mixed, *act;
-  uint32_t h_stride, qkv_stride, attn_stride, mixed_stride, act_stride;
-  uint32_t attn_items, merge_items, merge_P, merge_z;
-  uint32_t cnt[6];            // workgroups that arrive at each of a layer's six phases
-  uint32_t* sync;             // [n_layers * 6][16] counters, 256 bytes apart (never reset)
-  const uint32_t* epoch;      // incremented by embed before every launch
-  uint32_t* abort;            // set by a workgroup whose wait ran out
-  uint32_t spin;              // polls before a wait gives up
-  // Tests and probes: per (set, workgroup, layer, phase) the 100 MHz clock after the phase's
-  // wait and at its arrival ([2][256][n_layers][6][2]); null: none.
-  uint64_t* stamps;
-};
-// Tests: a smaller poll limit, and producers added to the attention phase's count (a barrier
-// that cannot complete, so the abort path runs and every workgroup still exits); 0: off.
-extern uint32_t g_layers_spin, g_layers_extra;
-extern uint64_t g_layers_stamps;  // device address of a stamp buffer (0: none)
-// Workgroups per set the device holds (0: the kernel does not fit two per compute unit).
-int layers_grid_per_set();
-sv_status layers_launch(hipStream_t stream, const LayersParams& p, uint32_t max_run);
-size_t attn_params_bytes();
-// Fills `out` (host memory, attn_params_bytes()) as attn_launch would for these arguments (the
-// inline runs given), for the persistent kernel's attention and merge phases.
+// Fills `out` (an AttnParams) as attn_launch would for these arguments (the inline runs given),
+// for the persistent layer kernel's attention and merge phases.
 sv_status attn_params_fill(void* out, const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
                            uint16_t* v_cache, const uint32_t* page_table, const float* rope_rows,
                            const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* host_runs,
