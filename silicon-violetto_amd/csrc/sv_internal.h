@@ -51,6 +51,7 @@ struct GemmTune {
   int rtw, nt, s, d, mf, nw, cpi;  // mf: MFMA tile (16 or 32); nw: waves (4); cpi: chunks per barrier (1)
 };
 extern GemmTune g_gemm_tune;
+extern int g_gemm_order;  // tests: the GEMMs' work order (-1: modelled choice; 0 legacy; g: groups of g row blocks)
 extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave, splits)
 sv_status pack_matrix(hipStream_t stream, const sv_matrix* src, void* dst, sv_matrix* out);
 sv_status matmul_launch(hipStream_t stream, const sv_matrix* w, const float* x, const uint32_t* x_rows, float* y,

@@ -828,3 +828,33 @@ def test_matmul_int8_groups_one_shot(gpu, m, k, group, n, epi, tiled):
     close(y.cpu().numpy(), ref, atol=5e-5 * max(mag, 1.0), rtol=1e-4, what=f"grouped epi {epi}")
     if epi in (L.EPI_NORM, L.EPI_RESID):
         close(aux.cpu().numpy(), aux_ref, atol=1e-5 * max(1.0, np.abs(aux_ref).max()), rtol=1e-4, what="aux")
+
+
+@pytest.mark.parametrize("m,k,n", [(2048, 8192, 512), (2048, 8192, 160), (2048, 2048, 512)])
+def test_matmul_gemm_work_orders(gpu, m, k, n):
+    """The GEMM's work order (which XCD takes which row blocks, splits and token blocks) changes
+    only where operands are cached: the legacy order, each grouping of row blocks and the
+    modelled choice give bit-identical outputs, within the bar of the oracle."""
+    banner(f"gemm work orders m={m} k={k} n={n}")
+    rng = np.random.default_rng(m + k + n)
+    w = torch.from_numpy(rng.normal(0, 0.02, (m, k)).astype(np.float32))
+    q, s = quantize_rows(w)
+    mat = K.matrix(q.cuda(), s.cuda(), 31).tiled()
+    x = rng.normal(0, 1, (n, k)).astype(np.float32)
+    base = rng.normal(0, 1, (n, m)).astype(np.float32)
+    a = L.MatArgs(n, k, m, L.EPI_RESID, 0, m, 0.75, 0.9, 1.3, 1, k, 31)
+    ref = oracle.matmul(L, q.numpy(), s.view(torch.int16).numpy().view(np.uint16), 31, x, a, base=base)
+    order = C.c_int.in_dll(L.lib(), "_ZN2sv12g_gemm_orderE")
+    outs = []
+    try:
+        for g in (-1, 0, 1, 2, 4, 8):
+            order.value = g
+            y = torch.zeros(n, m, device="cuda")
+            K.matmul(mat, to_dev(x), y, n=n, epi=L.EPI_RESID, scale=0.75, ra=0.9, rb=1.3, base=to_dev(base))
+            torch.cuda.synchronize()
+            outs.append(y.cpu().numpy())
+    finally:
+        order.value = -1
+    close(outs[0], ref, atol=5e-5 * max(float(np.abs(ref).max()), 1.0), rtol=1e-4, what="gemm")
+    for g, o in zip((0, 1, 2, 4, 8), outs[1:]):
+        assert np.array_equal(o, outs[0]), f"order {g} differs"
