@@ -24,6 +24,7 @@
 #include "sv_internal.h"
 
 #include <algorithm>
+#include <mutex>
 #include <vector>
 
 namespace sv {
@@ -1452,7 +1453,7 @@ static void gemm_dispatch32(hipStream_t stream, uint32_t fmt, const GemmCfg& c, 
 // split) its activations once per XCD. The activations are fp32, so at many rows and long k
 // (down at 512 rows: 16.8 MB of weights, 16.8 MB of activations) dealing whole row blocks to
 // an XCD re-reads the activations from every XCD.
-static uint32_t gemm_order(uint32_t nrb, uint32_t n_tblk, uint32_t S, double w_bytes, double x_bytes) {
+static uint32_t gemm_order_model(uint32_t nrb, uint32_t n_tblk, uint32_t S, double w_bytes, double x_bytes) {
   const uint32_t nwg = nrb * n_tblk * S;
   uint32_t best = 0;
   double best_t = 0;
@@ -1483,6 +1484,27 @@ static uint32_t gemm_order(uint32_t nrb, uint32_t n_tblk, uint32_t S, double w_b
     if (g == 0 || t < best_t * 0.97) best_t = t, best = g;  // another order only where it saves 3 %
   }
   return best;
+}
+
+// The model sorts every item of the launch for each order: memoised per launch shape, since
+// plans that are rebuilt per step (prompt chunks) launch the same few shapes many times.
+static uint32_t gemm_order(uint32_t nrb, uint32_t n_tblk, uint32_t S, double w_bytes, double x_bytes) {
+  struct Key {
+    uint32_t nrb, n_tblk, S;
+    double w, x;
+    bool operator==(const Key& o) const {
+      return nrb == o.nrb && n_tblk == o.n_tblk && S == o.S && w == o.w && x == o.x;
+    }
+  };
+  static std::mutex mu;
+  static std::vector<std::pair<Key, uint32_t>> memo;
+  const Key key{nrb, n_tblk, S, w_bytes, x_bytes};
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& e : memo)
+    if (e.first == key) return e.second;
+  const uint32_t g = gemm_order_model(nrb, n_tblk, S, w_bytes, x_bytes);
+  if (memo.size() < 4096) memo.push_back({key, g});
+  return g;
 }
 
 static sv_status gemm_launch(hipStream_t stream, uint32_t fmt, MMParams& p, void* ws, size_t ws_bytes) {
