@@ -72,7 +72,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   float* lred = lds + 4 * COLS * D;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c16 = lane & 15, q = lane >> 4;
-  const uint32_t s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  // Workgroups are dispatched in linear order (x fastest); they take their (split, kv head, run)
+  // split-major, so every run's first splits go out before any run's later ones, and the
+  // workgroups past a run's last split (the grid is sized for the longest context; they exit
+  // once their prologue has read the context length) come last, into the tail, instead of
+  // holding CU slots between live ones (configs[2]: about half the grid).
+  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), per = gridDim.y * gridDim.z;
+  const uint32_t s = lin / per, g = lin % per % gridDim.y, r = lin % per / gridDim.y;
   uint32_t t0, T, seq;
   run_header<INL>(p, r, t0, T, seq);
   // The run's visibility masks (the newest split's masks): requested with the first loads and
