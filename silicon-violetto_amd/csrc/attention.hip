@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   // Workgroups are dispatched in linear order (x fastest); they take their (split, kv head, run)
   // split-major, so every run's first splits go out before any run's later ones, and the
   // workgroups past a run's last split (the grid is sized for the longest context; they exit
-  // once their prologue has read the context length) come last, into the tail, instead of
-  // holding CU slots between live ones (configs[2]: about half the grid).
+  // once the context length is in) come last, into the tail, instead of holding CU slots
+  // between live ones (configs[2]: about half the grid).
   const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), per = gridDim.y * gridDim.z;
   const uint32_t s = lin / per, g = lin % per % gridDim.y, r = lin % per / gridDim.y;
   uint32_t t0, T, seq;
@@ -160,6 +160,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     // 2. (Without inline runs, the rope words: they need the positions.) Then every batch of
     //    the wave (they need the page words; slots past the split's batches read nothing).
     if constexpr (!INL) load_rope(p.rope, false);
+    // Streaming variant: a split past the run's context (the grid is sized for the longest
+    // one), or a grid with too few splits for it, is known once p0 is in, in the round trip of
+    // the page words: it leaves before requesting K/V or building queries. The all-in-flight
+    // variant (about one workgroup per CU, few past the context) does not wait for p0 before
+    // its K/V requests (measured 8 % slower at configs[1] when it did) and checks after.
+    if constexpr (NBW == 0) {
+      const uint32_t nsplit = attn_nsplit_t<LOCAL>(p, p0);
+      if (nsplit > p.max_splits) {
+        // Its output is NaN (never a partial sum) and the counter is left alone.
+        if (s == 0)
+          for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+            const uint32_t col = idx / D, i = col / p.G, h = g * p.G + col % p.G;
+            p.out[(size_t)(t0 + i) * p.NQ * D + h * D + idx % D] = __builtin_nanf("");
+          }
+        return;
+      }
+      if (s >= nsplit) return;
+    }
     if ((uint32_t)lane < 2 * nbw_full) {
       const uint32_t page = min(pword, p.n_pages - 1);
       tile_off = ((((size_t)p.layer * p.n_pages + page) * p.NKV + g) << p.page_shift) * D +
@@ -201,17 +219,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   }
 
   const uint32_t nsplit = attn_nsplit_t<LOCAL>(p, p0);
-  if (nsplit > p.max_splits) {
-    // The grid has too few splits for this run's context: its output is NaN (never a
-    // partial sum) and the counter is left alone.
-    if (s == 0)
-      for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
-        const uint32_t col = idx / D, i = col / p.G, h = g * p.G + col % p.G;
-        p.out[(size_t)(t0 + i) * p.NQ * D + h * D + idx % D] = __builtin_nanf("");
-      }
-    return;
+  if constexpr (NBW > 0) {
+    if (nsplit > p.max_splits) {
+      // The grid has too few splits for this run's context: its output is NaN (never a
+      // partial sum) and the counter is left alone.
+      if (s == 0)
+        for (uint32_t idx = tid; idx < ncols * D; idx += 256) {
+          const uint32_t col = idx / D, i = col / p.G, h = g * p.G + col % p.G;
+          p.out[(size_t)(t0 + i) * p.NQ * D + h * D + idx % D] = __builtin_nanf("");
+        }
+      return;
+    }
+    if (s >= nsplit) return;
   }
-  if (s >= nsplit) return;
   // Each lane column's first visible cached key, and the highest of any column of the run (its
   // positions are at most p0 + T - 1): batches at or above it need no window mask.
   uint32_t clo[NCT];
