@@ -582,6 +582,32 @@ sv_status sv_engine_draft_buffers(sv_engine* e, sv_draft_buffers* out);
 sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
                   float* logits, uint32_t* emitted, sv_plan_info* info);
 
+/* One layer's intermediates over a capture step (LayerCapture, engine.rs:176-188): host
+ * arrays of n rows each, valid for the duration of the callback. */
+typedef struct sv_layer_capture {
+  uint32_t layer, n;
+  uint32_t hidden;         /* row width of resid_in, attn_in, attn_out, mlp_in, mlp_out, resid_base */
+  uint32_t qkv_width;      /* (n_heads + 2 n_kv_heads) head_dim                                    */
+  uint32_t sdpa_width;     /* n_heads head_dim                                                      */
+  uint32_t pad;
+  const float* resid_in;   /* the layer's input residual                                            */
+  const float* attn_in;    /* rms_norm of the attention input (the MUDD mix on MUDD layers)         */
+  const float* qkv;        /* q | k | v after the norms, RoPE and value embeddings                  */
+  const float* sdpa_out;   /* the attention output before XSA and the gate                          */
+  const float* attn_out;   /* the o projection's product, before the residual                       */
+  const float* mlp_in;     /* rms_norm of the MLP input                                              */
+  const float* mlp_out;    /* the down projection's product, before the residual                    */
+  const float* resid_base; /* MUDD's residual base; null on other layers                            */
+} sv_layer_capture;
+typedef void (*sv_capture_fn)(const sv_layer_capture* cap, void* user);
+
+/* Engine::step_capture (engine.rs:318-355), the parity hook: sv_step's step run layer by
+ * layer, waiting after each layer and handing its intermediates to fn (layers in order), then
+ * the head and tail; outputs as sv_step's. It runs the launch-per-kernel path (also with
+ * SV_OPT_LAYERS_KERNEL) and is not captured into graphs. */
+sv_status sv_step_capture(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, sv_capture_fn fn,
+                          void* user, uint32_t* ids, float* logits, uint32_t* emitted, sv_plan_info* info);
+
 /* Per-kernel timing of one encoded step (the reference's profile/bench_matmul hooks,
  * hooks.rs:60-112, cli/src/profile.rs): encodes the planned step `reps` times on the engine's
  * stream with a hipEvent pair around every kernel, waits, and adds each kernel's elapsed

@@ -346,6 +346,15 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
                      uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
                      const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
                      float* out, const sv_attn_extras* ex) {
+  orc_attn_verify_cap(sh, qkv, meta, k_cache, v_cache, page_table, rope, kv, args, runs, n_runs, vis, out, ex, NULL,
+                      NULL, NULL, NULL);
+}
+
+void orc_attn_verify_cap(const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
+                         uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
+                         const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
+                         float* out, const sv_attn_extras* ex, float* cap_q, float* cap_k, float* cap_v,
+                         float* cap_sdpa) {
   const uint32_t D = sh->head_dim, NQ = sh->n_heads, NKV = sh->n_kv_heads, G = NQ / NKV;
   const uint32_t W = (NQ + 2 * NKV) * D, KOFF = NQ * D, VOFF = (NQ + NKV) * D;
   const uint32_t L = kv->kv_layer;
@@ -375,6 +384,8 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
           if (ve_gate) v += ve_g * orc_bf(ex->d_value_embed[((size_t)ex->d_tokens[t] * NKV + g) * D + d]);
           vdir[((size_t)i * NKV + g) * D + d] = v;
           vs += v * v;
+          if (cap_k) cap_k[((size_t)t * NKV + g) * D + d] = (float)tmp[d];
+          if (cap_v) cap_v[((size_t)t * NKV + g) * D + d] = (float)v;
           const uint16_t kb = orc_to_bf((float)tmp[d]);
           const uint16_t vb = orc_to_bf((float)v);
           nk[((size_t)i * NKV + g) * D + d] = kb;
@@ -394,6 +405,7 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
         double q[128], o[128];
         norm_rope_d(qkv + (size_t)t * W + h * D, q, D, (int)args->rope, rope + (size_t)pos * 64);
         for (uint32_t d = 0; d < D; d++) {
+          if (cap_q) cap_q[(size_t)t * NQ * D + h * D + d] = (float)q[d];
           q[d] *= args->scale_log2;
           o[d] = 0.0;
         }
@@ -415,6 +427,8 @@ void orc_attn_verify(const sv_shape* sh, const float* qkv, const uint32_t* meta,
           for (uint32_t d = 0; d < D; d++) o[d] += p * orc_bf(nv[((size_t)j * NKV + g) * D + d]);
         }
         for (uint32_t d = 0; d < D; d++) o[d] /= l;
+        if (cap_sdpa)
+          for (uint32_t d = 0; d < D; d++) cap_sdpa[(size_t)t * NQ * D + h * D + d] = (float)o[d];
         if (xsa) {
           const double* vd = vdir + ((size_t)i * NKV + g) * D;
           double dp = 0.0;
@@ -854,6 +868,20 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
   float* xattn = (float*)malloc(sizeof(float) * n * H);
   float* rbase = (float*)malloc(sizeof(float) * n * H);
   if (!h || !qkv || !attn || !mixed || !act || !inv || !hfin || !h0 || !taps || !xattn || !rbase) return -1;
+  /* step_capture: per-layer blocks (orc_step_io.cap) and the attention's q, k, v before they
+   * are interleaved into the block's qkv rows */
+  const uint32_t NQD = NQ * D, NKD = NKV * D;
+  const size_t cap_layer = (size_t)n * (6 * H + W + NQD);
+  uint32_t* iota = NULL;
+  float *cq = NULL, *ck = NULL, *cv = NULL;
+  if (io->cap) {
+    iota = (uint32_t*)malloc(sizeof(uint32_t) * n);
+    cq = (float*)malloc(sizeof(float) * n * NQD);
+    ck = (float*)malloc(sizeof(float) * n * NKD);
+    cv = (float*)malloc(sizeof(float) * n * NKD);
+    if (!iota || !cq || !ck || !cv) return -1;
+    for (uint32_t t = 0; t < n; t++) iota[t] = t;
+  }
 
   orc_embed(sh, embed, io->tokens, h, io->tin, io->meta, io->lens, io->feed, io->tree, io->vis, n);
   memcpy(h0, h, sizeof(float) * n * H);
@@ -864,13 +892,26 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     const uint32_t kv_index = local ? n_local++ : n_global++;
     const float* x = h;
     const float* resid = h;
+    float* cb = io->cap ? io->cap + li * cap_layer : NULL;
+    float *c_qkv = NULL, *c_sdpa = NULL, *c_attn_out = NULL, *c_mlp_in = NULL, *c_mlp_out = NULL;
+    if (cb) {
+      c_qkv = cb + 2 * (size_t)n * H;
+      c_sdpa = c_qkv + (size_t)n * W;
+      c_attn_out = c_sdpa + (size_t)n * NQD;
+      c_mlp_in = c_attn_out + (size_t)n * H;
+      c_mlp_out = c_mlp_in + (size_t)n * H;
+      memcpy(cb, h, sizeof(float) * n * H);
+      memset(c_mlp_out + (size_t)n * H, 0, sizeof(float) * n * H);
+    }
     for (uint32_t site = 0; site < n_mudd; site++)
       if (mx->mudd_layer[site] == li) {
         orc_mudd(h, h0, taps + (size_t)site * n * H, mx->mudd_dense1,
                  mx->mudd_mix + (size_t)site * 6 * (SV_MUDD_INNER + 1), xattn, rbase, n, H);
         x = xattn;
         resid = rbase;
+        if (cb) memcpy(c_mlp_out + (size_t)n * H, rbase, sizeof(float) * n * H);
       }
+    if (cb) orc_rmsnorm_rows(x, iota, cb + (size_t)n * H, n, H);
     sv_mat_args a;
     memset(&a, 0, sizeof a);
     a.n = n;
@@ -893,19 +934,27 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     sv_kv_args kv = local ? io->kv_local : io->kv;
     kv.kv_layer = kv_index;
     sv_attn_extras ex = {x, inv, io->tokens, mx ? mx->value_embed : NULL, l->ve_gate, l->attn_gate, l->xsa, NULL, H, 0};
-    orc_attn_verify(sh, qkv, io->meta, local ? io->k_local : io->k_cache, local ? io->v_local : io->v_cache,
-                    local ? io->local_table : io->page_table, io->rope, &kv, &aa, io->attn_runs,
-                    io->n_attn ? io->n_attn : io->n_runs, io->vis, attn, &ex);
+    orc_attn_verify_cap(sh, qkv, io->meta, local ? io->k_local : io->k_cache, local ? io->v_local : io->v_cache,
+                        local ? io->local_table : io->page_table, io->rope, &kv, &aa, io->attn_runs,
+                        io->n_attn ? io->n_attn : io->n_runs, io->vis, attn, &ex, cq, ck, cv, c_sdpa);
+    if (cb)
+      for (uint32_t t = 0; t < n; t++) {
+        memcpy(c_qkv + (size_t)t * W, cq + (size_t)t * NQD, sizeof(float) * NQD);
+        memcpy(c_qkv + (size_t)t * W + NQD, ck + (size_t)t * NKD, sizeof(float) * NKD);
+        memcpy(c_qkv + (size_t)t * W + NQD + NKD, cv + (size_t)t * NKD, sizeof(float) * NKD);
+      }
     /* o: Resid (encode.rs:172-175) */
     a.k = NQ * D;
     a.m = H;
     a.epi = SV_EPI_RESID;
-    a.flags = 0;
+    a.flags = cb ? SV_FLAG_WRITE_RAW : 0;
     a.scale = l->o_scale;
     a.ra = l->resid_attn;
     a.rb = l->post_attn;
     a.gshift = l->o.gshift;
-    orc_matmul(&l->o, attn, NULL, mixed, resid, NULL, &a);
+    orc_matmul(&l->o, attn, NULL, mixed, resid, c_attn_out, &a);
+    if (cb) orc_rmsnorm_rows(mixed, iota, c_mlp_in, n, H);
+    a.flags = 0;
     /* gate_up: SwiGlu (encode.rs:179-181) */
     a.k = H;
     a.m = 2 * F;
@@ -922,7 +971,9 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
     a.ra = l->resid_mlp;
     a.rb = l->post_mlp;
     a.gshift = l->down.gshift;
-    orc_matmul(&l->down, act, NULL, h, mixed, NULL, &a);
+    a.flags = cb ? SV_FLAG_WRITE_RAW : 0;
+    orc_matmul(&l->down, act, NULL, h, mixed, c_mlp_out, &a);
+    a.flags = 0;
     for (uint32_t site = 0; site < n_mudd; site++)
       if (mx->mudd_tap[site] == li) memcpy(taps + (size_t)site * n * H, h, sizeof(float) * n * H);
     for (uint32_t k = 0; k < io->n_taps; k++)
@@ -963,6 +1014,10 @@ int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, 
   free(taps);
   free(xattn);
   free(rbase);
+  free(iota);
+  free(cq);
+  free(ck);
+  free(cv);
   free(h);
   free(qkv);
   free(attn);

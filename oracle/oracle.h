@@ -127,10 +127,24 @@ typedef struct orc_step_io {
   uint32_t n_taps;
   const uint32_t* tap_layers;
   float* const* tap_out;
+  /* Engine::step_capture (engine.rs:318-355; NULL: off): per layer, [n] rows each of the input
+   * residual [H], rms_norm of the attention input [H], q | k | v after the norms, RoPE and value
+   * embeddings [W], the attention output before XSA and the gate [NQ D], o's and down's products
+   * before the residual with rms_norm of the MLP input between them [H] x 3, and MUDD's
+   * residual base [H] (zeros on other layers); layer blocks in order. */
+  float* cap;
 } orc_step_io;
 
 int orc_step(const sv_shape* sh, const uint16_t* embed, const sv_layer* layers, float attn_scale,
              orc_step_io* io);
+/* orc_attn_verify that also writes, where non-NULL, each token's queries after the norm and RoPE
+ * [n][NQ D], keys after the norm and RoPE and values after the value embedding [n][NKV D], and
+ * the attention output before XSA and the gate [n][NQ D] (fp32). */
+void orc_attn_verify_cap(const sv_shape* sh, const float* qkv, const uint32_t* meta, uint16_t* k_cache,
+                         uint16_t* v_cache, const uint32_t* page_table, const float* rope, const sv_kv_args* kv,
+                         const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs, const uint32_t* vis,
+                         float* out, const sv_attn_extras* ex, float* cap_q, float* cap_k, float* cap_v,
+                         float* cap_sdpa);
 
 /* The drafter (drafter.rs:278-447, kernels.metal:135-148, 1725-1934); host pointers. */
 void orc_tap_rows(const float* in, float* out, uint32_t n, uint32_t hidden);

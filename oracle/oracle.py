@@ -247,7 +247,8 @@ class StepIO(C.Structure):
                 ("page_table", vp), ("kv", C.c_uint32 * 8), ("rope", vp), ("meta", vp), ("logits", vp),
                 ("out", vp), ("emitted", vp), ("path", vp), ("path_len", vp), ("on_path", vp), ("hidden", vp),
                 ("n_attn", u32), ("extras", vp), ("local", vp), ("k_local", vp), ("v_local", vp), ("local_table", vp),
-                ("kv_local", C.c_uint32 * 8), ("head", vp), ("n_taps", u32), ("tap_layers", vp), ("tap_out", vp)]
+                ("kv_local", C.c_uint32 * 8), ("head", vp), ("n_taps", u32), ("tap_layers", vp), ("tap_out", vp),
+                ("cap", vp)]
 
 
 class DraftIO(C.Structure):
@@ -313,6 +314,7 @@ class OracleEngine:
         self.local_table = np.array([[slot * self.ring_pages + p % max(1, self.ring_pages) for p in range(self.max_pages)]
                                      for slot in range(max_seqs)], np.uint32)
         self._mx = None
+        self._mudd_layers = tuple(extras["mudd_layer"]) if extras else ()
         if extras:
             n = len(extras["mudd_layer"])
             self._mx = L.ModelExtras(ptr(extras["value_embed"]), ptr(extras["mudd_dense1"]), ptr(extras["mudd_mix"]), n,
@@ -446,10 +448,13 @@ class OracleEngine:
         assert self.pool.reserve(slot, self.seq_len[slot])
         self.lens[slot] = self.seq_len[slot]
 
-    def step(self, runs, compact=None, want_hidden=False, draft=False, taps=None):
+    def step(self, runs, compact=None, want_hidden=False, draft=False, taps=None, capture=False):
         """runs: (slot, tokens, verify[, head]). Returns (ids, logits, emitted, extra). With a
         drafter set: its context pass, and with draft=True its blocks; `taps` replaces the
-        oracle's own tapped rows as the drafter's input (to check the drafter alone)."""
+        oracle's own tapped rows as the drafter's input (to check the drafter alone). With
+        capture: extra["capture"], per layer a dict of its intermediates (Engine::step_capture,
+        engine.rs:318-355): resid_in, attn_in, qkv, sdpa_out, attn_out, mlp_in, mlp_out,
+        resid_base (None off the MUDD layers), [n][width] each."""
         L = self.L
         n_runs = len(runs)
         in_runs = np.zeros((n_runs, 4), np.uint32)
@@ -514,6 +519,12 @@ class OracleEngine:
             tl = np.array(dr.taps, np.uint32)
             tp = (vp * len(tap_out))(*[t.ctypes.data for t in tap_out])
             io.n_taps, io.tap_layers, io.tap_out = len(tap_out), ptr(tl), C.cast(tp, vp)
+        H, D = self.shape.hidden, self.shape.head_dim
+        NQD, W = self.shape.n_heads * D, (self.shape.n_heads + 2 * self.shape.n_kv_heads) * D
+        widths = [("resid_in", H), ("attn_in", H), ("qkv", W), ("sdpa_out", NQD), ("attn_out", H), ("mlp_in", H),
+                  ("mlp_out", H), ("resid_base", H)]
+        cap = np.zeros((self.shape.n_layers, n * sum(w for _, w in widths)), np.float32) if capture else None
+        io.cap = ptr(cap)
         sh = self.shape.c()
         rc = lib().orc_step(C.byref(sh), ptr(self.embed), self.layers, f32(self.attn_scale), C.byref(io))
         assert rc == 0
@@ -527,6 +538,18 @@ class OracleEngine:
                 self.seq_len[r[0]] -= len(r[1]) - min(int(emitted[i]), len(r[1]))
         extra = dict(tokens=tokens, meta=meta.reshape(n, 2), vis=vis, path=path.reshape(n_runs, 16),
                      path_len=path_len, on_path=on_path, hidden=hidden, head_rows=head_rows[:n_head], **dx)
+        if capture:
+            mudd_layers = set(self._mudd_layers)
+            layers = []
+            for li in range(self.shape.n_layers):
+                d, o = {}, 0
+                for name, w in widths:
+                    d[name] = cap[li, o:o + n * w].reshape(n, w).copy()
+                    o += n * w
+                if li not in mudd_layers:
+                    d["resid_base"] = None
+                layers.append(d)
+            extra["capture"] = layers
         return out[:n_head].copy(), logits[:n_head].copy(), emitted, extra
 
 

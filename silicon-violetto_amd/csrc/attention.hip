@@ -215,7 +215,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
         for (int ks = 0; ks < KST; ks++)
 #pragma unroll
           for (int e = 0; e < 8; e++) qr.v[ct][ks][e] = 0.0f;
-    qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane);
+    qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane, s == 0 ? p.cap_q : nullptr, t0, g);
   }
 
   const uint32_t nsplit = attn_nsplit_t<LOCAL>(p, p0);
@@ -371,6 +371,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     }
     const uint32_t i = col / p.G, h = g * p.G + col % p.G;
     *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
+    if (p.cap_sdpa) *(f32x4*)(p.cap_sdpa + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
   }
 }
 
@@ -433,6 +434,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p, uint32_t 
   if (!live || attn_nsplit(p, p0) > p.max_splits) return;  // NaN written by the attention
   const uint32_t i = col / p.G, h = g * p.G + col % p.G, t = t0 + i;
   f32x4 res = o / l;
+  if (p.cap_sdpa) *(f32x4*)(p.cap_sdpa + (size_t)t * p.NQ * D + h * D + d) = res;
   if (p.xsa) {
     const f32x4 vd = *(const f32x4*)(p.vdir + ((size_t)t * p.NKV + g) * D + d);
     float dp = ((res[0] * vd[0] + res[1] * vd[1]) + res[2] * vd[2]) + res[3] * vd[3];
@@ -511,6 +513,7 @@ static uint32_t attn_cus() {
   }
   return (uint32_t)cus;
 }
+thread_local AttnCapture g_attn_capture;
 bool g_attn_fused_merge = false;  // tests: the last split to arrive merges (measured slower)
 int g_attn_allin = -1;  // -1: by shape; 0 / 1: force the one-batch-ahead / all-batches variant where built
 
@@ -610,6 +613,10 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.xsa = ex ? ex->d_xsa : nullptr;
   p.vdir = ex && ex->d_xsa ? ex->d_vdir : nullptr;
   p.H = ex ? ex->hidden : 0u;
+  p.cap_q = g_attn_capture.q;
+  p.cap_k = g_attn_capture.k;
+  p.cap_v = g_attn_capture.v;
+  p.cap_sdpa = g_attn_capture.sdpa;
   p.rope_rows = rope_rows;
   // inline runs take the queries' rope words from the step's rows by token
   if (host_runs && rope_rows && n_runs <= SV_INLINE_RUNS) {

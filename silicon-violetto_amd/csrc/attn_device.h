@@ -51,6 +51,13 @@ struct AttnParams {
   const float* xsa;
   float* vdir;
   uint32_t H;
+  // Per-layer capture (sv_step_capture; null: off): each token's queries after the norm and
+  // RoPE [n][NQ D], its keys after the norm and RoPE and values after the value embedding
+  // [n][NKV D], and the attention output before XSA and the gate [n][NQ D], all fp32.
+  float* cap_q;
+  float* cap_k;
+  float* cap_v;
+  float* cap_sdpa;
 };
 
 // The first cached key the query at pos sees (kernels.metal:808-811 key_lo); LOCAL: the layer
@@ -482,7 +489,8 @@ __device__ __forceinline__ void qrope_load(const AttnParams& p, uint32_t ncols, 
 template <int D, int NCT>
 __device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r,
                                            const float2 (&cs)[NCT][D / 32][4], bf16x8 (&qh)[NCT][D / 32],
-                                           bf16x8 (&ql)[NCT][D / 32], int lane) {
+                                           bf16x8 (&ql)[NCT][D / 32], int lane, float* capq = nullptr,
+                                           uint32_t t0 = 0, uint32_t g = 0) {
   constexpr int KST = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -508,6 +516,13 @@ __device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, 
           v[2 * jj] = cs[ct][ks][jj].x * a0 + cs[ct][ks][jj].y * a1;
           v[2 * jj + 1] = cs[ct][ks][jj].x * a1 - cs[ct][ks][jj].y * a0;
         }
+      }
+      if (capq && ok) {
+        // the query after the norm and RoPE (column 16 ct + c16: token c / G, head g G + c % G)
+        const uint32_t c = 16 * ct + c16;
+        float* dst = capq + (size_t)(t0 + c / p.G) * p.NQ * D + (g * p.G + c % p.G) * D + 32 * ks + 8 * q;
+        *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
+        *(f32x4*)(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
       }
 #pragma unroll
       for (int e = 0; e < 8; e++) v[e] *= p.scale_log2;
@@ -607,6 +622,13 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
           const float r0 = cs.x * k0 + cs.y * k1, r1 = cs.x * k1 - cs.y * k0;
           k0 = r0;
           k1 = r1;
+        }
+        if (p.cap_k) {
+          const size_t co = (size_t)t * p.NKV * D + g * D + d;
+          p.cap_k[co] = k0;
+          p.cap_k[co + 1] = k1;
+          p.cap_v[co] = vv[e];
+          p.cap_v[co + 1] = vv[e + 1];
         }
         kb[e / 2] = (uint32_t)to_bf(k0) | ((uint32_t)to_bf(k1) << 16);
         vb[e / 2] = (uint32_t)to_bf(vv[e]) | ((uint32_t)to_bf(vv[e + 1]) << 16);

@@ -291,6 +291,16 @@ struct sv_engine {
   float* tap[SV_MUDD_SITES] = {};   // outputs of the tap layers
   float* xattn = nullptr;           // MUDD's attention input
   float* rbase = nullptr;           // MUDD's residual base
+  // sv_step_capture (engine.rs:318-355): the per-layer callback and the device buffers the
+  // layers write their intermediates to (null: an ordinary step).
+  struct Capture {
+    sv_capture_fn fn = nullptr;
+    void* user = nullptr;
+    uint32_t* iota = nullptr;  // rows 0..n-1 for rmsnorm_rows
+    float *resid_in = nullptr, *attn_in = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *sdpa = nullptr;
+    float *attn_out = nullptr, *mlp_in = nullptr, *mlp_out = nullptr, *base = nullptr;
+  };
+  Capture* capture = nullptr;
   float* vdir = nullptr;            // XSA directions [n][NKV][D]
   // The drafter (drafter.rs): its matrices, the target's tapped rows, its rings (as the local
   // layers': pages behind a cyclic table) and its block rows' buffers.
@@ -690,7 +700,7 @@ struct sv_engine {
     if (!planned) return fail(SV_ERR_STATE, "no plan");
     const Plan& P = plan;
     const uint32_t n = P.n, H = sh.hidden, F = sh.ffn, NQD = sh.n_heads * sh.head_dim;
-    if (P.persist) {
+    if (P.persist && !capture) {
       // embed into the first h slice (and the epoch the layer kernel's counters count in), every
       // layer in one launch, then the head on the last slice
       SV_TIMED(SV_KIND_EMBED, embed_launch(stream, &sh, embed, tokens, tok_res, P.lp.h, tin, meta, lens, feed, tree, vis,
@@ -718,6 +728,14 @@ struct sv_engine {
         x = xattn;
         resid = rbase;
       }
+      Capture* cp = capture;
+      if (cp) {
+        SV_HIP(hipMemcpyAsync(cp->resid_in, hin, (size_t)n * H * 4, hipMemcpyDeviceToDevice, stream), "capture");
+        SV_TRY(rmsnorm_rows_launch(stream, x, cp->iota, cp->attn_in, n, H));
+        if (site >= 0)
+          SV_HIP(hipMemcpyAsync(cp->base, rbase, (size_t)n * H * 4, hipMemcpyDeviceToDevice, stream), "capture");
+        g_attn_capture = AttnCapture{cp->q, cp->k, cp->v, cp->sdpa};
+      }
       SV_TIMED(SV_KIND_QKV,
                matmul(L.qkv, n, x, nullptr, qkv, SV_EPI_NORM, SV_FLAG_WRITE_INV, L.qkv_scale, 0, 0, nullptr, inv));
       aa.rope = L.rope;
@@ -738,18 +756,64 @@ struct sv_engine {
       SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
                                                P.max_run, vis, attn, ws, ws_bytes, 2, P.inl.data(), true, exp_,
                                                rope_rows));
-      SV_TIMED(SV_KIND_O, matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, 0, L.o_scale, L.resid_attn, L.post_attn,
-                                 resid, nullptr));
+      g_attn_capture = AttnCapture{};
+      const uint32_t raw = cp ? (uint32_t)SV_FLAG_WRITE_RAW : 0u;
+      SV_TIMED(SV_KIND_O, matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, raw, L.o_scale, L.resid_attn, L.post_attn,
+                                 resid, cp ? cp->attn_out : nullptr));
+      if (cp) SV_TRY(rmsnorm_rows_launch(stream, mixed, cp->iota, cp->mlp_in, n, H));
       SV_TIMED(SV_KIND_GATE_UP, matmul(L.gate_up, n, mixed, nullptr, act, SV_EPI_SWIGLU, 0, 1.0f, 0, 0, nullptr, nullptr));
-      SV_TIMED(SV_KIND_DOWN,
-               matmul(L.down, n, act, nullptr, hout, SV_EPI_RESID, 0, 1.0f, L.resid_mlp, L.post_mlp, mixed, nullptr));
+      SV_TIMED(SV_KIND_DOWN, matmul(L.down, n, act, nullptr, hout, SV_EPI_RESID, raw, 1.0f, L.resid_mlp, L.post_mlp,
+                                    mixed, cp ? cp->mlp_out : nullptr));
       // the drafter's taps (encode.rs:186-190): this layer's output, normed, rounded to bf16
       for (uint32_t k = 0; has_drafter && k < dr.n_taps; k++)
         if (dr.taps[k] == li) SV_TIMED(SV_KIND_DRAFT, tap_rows_launch(stream, hout, tapbuf[k], n, H));
+      if (cp) SV_TRY(capture_layer(li, site >= 0));
     }
     (void)F;
     (void)NQD;
     return encode_tail(flags, out_of(sh.n_layers - 1));
+  }
+
+  // sv_step_capture: wait for layer li, read its intermediates back and hand them to the
+  // callback (q | k | v assembled per row as the qkv matmul lays them out).
+  sv_status capture_layer(uint32_t li, bool mudd) {
+    const Capture& c = *capture;
+    const uint32_t n = plan.n, H = sh.hidden, D = sh.head_dim, NQD = sh.n_heads * D, NKD = sh.n_kv_heads * D;
+    const uint32_t W = NQD + 2 * NKD;
+    SV_HIP(hipStreamSynchronize(stream), "capture");
+    std::vector<float> resid_in((size_t)n * H), attn_in((size_t)n * H), q((size_t)n * NQD), k((size_t)n * NKD),
+        v((size_t)n * NKD), sdpa((size_t)n * NQD), attn_out((size_t)n * H), mlp_in((size_t)n * H),
+        mlp_out((size_t)n * H), base(mudd ? (size_t)n * H : 0), qkv_rows((size_t)n * W);
+    const std::pair<float*, const float*> reads[] = {{resid_in.data(), c.resid_in}, {attn_in.data(), c.attn_in},
+                                                     {attn_out.data(), c.attn_out}, {mlp_in.data(), c.mlp_in},
+                                                     {mlp_out.data(), c.mlp_out}};
+    for (const auto& rd : reads) SV_HIP(hipMemcpy(rd.first, rd.second, (size_t)n * H * 4, hipMemcpyDeviceToHost), "capture");
+    SV_HIP(hipMemcpy(sdpa.data(), c.sdpa, (size_t)n * NQD * 4, hipMemcpyDeviceToHost), "capture");
+    SV_HIP(hipMemcpy(q.data(), c.q, (size_t)n * NQD * 4, hipMemcpyDeviceToHost), "capture");
+    SV_HIP(hipMemcpy(k.data(), c.k, (size_t)n * NKD * 4, hipMemcpyDeviceToHost), "capture");
+    SV_HIP(hipMemcpy(v.data(), c.v, (size_t)n * NKD * 4, hipMemcpyDeviceToHost), "capture");
+    if (mudd) SV_HIP(hipMemcpy(base.data(), c.base, (size_t)n * H * 4, hipMemcpyDeviceToHost), "capture");
+    for (uint32_t t = 0; t < n; t++) {
+      memcpy(&qkv_rows[(size_t)t * W], &q[(size_t)t * NQD], NQD * 4);
+      memcpy(&qkv_rows[(size_t)t * W + NQD], &k[(size_t)t * NKD], NKD * 4);
+      memcpy(&qkv_rows[(size_t)t * W + NQD + NKD], &v[(size_t)t * NKD], NKD * 4);
+    }
+    sv_layer_capture lc{};
+    lc.layer = li;
+    lc.n = n;
+    lc.hidden = H;
+    lc.qkv_width = W;
+    lc.sdpa_width = NQD;
+    lc.resid_in = resid_in.data();
+    lc.attn_in = attn_in.data();
+    lc.qkv = qkv_rows.data();
+    lc.sdpa_out = sdpa.data();
+    lc.attn_out = attn_out.data();
+    lc.mlp_in = mlp_in.data();
+    lc.mlp_out = mlp_out.data();
+    lc.resid_base = mudd ? base.data() : nullptr;
+    c.fn(&lc, c.user);
+    return SV_OK;
   }
 
   // The head, sampler and step tail after the layers; `last` holds the last layer's rows.
@@ -1733,11 +1797,9 @@ extern "C" sv_status sv_sync(sv_engine* e) {
 // engine.rs:310-314 step, with generate.rs:446-463 collect: plan, encode, wait, read the
 // head rows' ids (and logits), the tokens each run emitted, and give back a verify run's
 // unused positions (settle).
-extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
-                             float* logits, uint32_t* emitted, sv_plan_info* info) {
-  sv_plan_info pi;
-  SV_TRY(sv_plan(e, runs, n_runs, 0, &pi));
-  if (info) *info = pi;
+// sv_step after its plan: encode, wait, read the outputs, roll back the rejected rows' lengths.
+static sv_status step_planned(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
+                              float* logits, uint32_t* emitted, const sv_plan_info& pi) {
   SV_TRY(e->issue(1));
   SV_TRY(e->encode(flags));
   SV_HIP(hipStreamSynchronize(e->stream), "step");
@@ -1754,6 +1816,56 @@ extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, 
       e->seq_len[slot] -= runs[ri].count - std::min(em[ri], runs[ri].count);
     }
   return SV_OK;
+}
+
+extern "C" sv_status sv_step(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags, uint32_t* ids,
+                             float* logits, uint32_t* emitted, sv_plan_info* info) {
+  sv_plan_info pi;
+  SV_TRY(sv_plan(e, runs, n_runs, 0, &pi));
+  if (info) *info = pi;
+  return step_planned(e, runs, n_runs, flags, ids, logits, emitted, pi);
+}
+
+// engine.rs:318-355 step_capture: the step's layers one at a time, each layer's intermediates
+// written to buffers of this call and handed to fn after the layer.
+extern "C" sv_status sv_step_capture(sv_engine* e, const sv_run* runs, uint32_t n_runs, uint32_t flags,
+                                     sv_capture_fn fn, void* user, uint32_t* ids, float* logits, uint32_t* emitted,
+                                     sv_plan_info* info) {
+  if (!e || !fn) return fail(SV_ERR_ARG, "step_capture: null engine or callback");
+  sv_plan_info pi;
+  SV_TRY(sv_plan(e, runs, n_runs, 0, &pi));
+  if (info) *info = pi;
+  const uint32_t n = e->plan.n, H = e->sh.hidden, NQD = e->sh.n_heads * e->sh.head_dim;
+  const uint32_t NKD = e->sh.n_kv_heads * e->sh.head_dim;
+  sv_engine::Capture c;
+  c.fn = fn;
+  c.user = user;
+  std::vector<void*> bufs;
+  sv_status st = SV_OK;
+  auto alloc = [&](float** p, size_t floats) {
+    if (st != SV_OK) return;
+    if (hipMalloc((void**)p, floats * 4) != hipSuccess) {
+      st = fail(SV_ERR_HIP, "step_capture: %zu bytes of capture buffers", floats * 4);
+      return;
+    }
+    bufs.push_back(*p);
+  };
+  alloc((float**)&c.iota, n);
+  for (float** p : {&c.resid_in, &c.attn_in, &c.attn_out, &c.mlp_in, &c.mlp_out, &c.base}) alloc(p, (size_t)n * H);
+  for (float** p : {&c.q, &c.sdpa}) alloc(p, (size_t)n * NQD);
+  for (float** p : {&c.k, &c.v}) alloc(p, (size_t)n * NKD);
+  std::vector<uint32_t> iota(n);  // outlives the asynchronous upload (the step waits for it)
+  for (uint32_t i = 0; i < n; i++) iota[i] = i;
+  if (st == SV_OK) st = e->upload(c.iota, iota.data(), n * 4);
+  if (st == SV_OK) {
+    e->capture = &c;
+    st = step_planned(e, runs, n_runs, flags, ids, logits, emitted, pi);
+    e->capture = nullptr;
+    g_attn_capture = AttnCapture{};
+  }
+  (void)hipStreamSynchronize(e->stream);
+  for (void* b : bufs) (void)hipFree(b);
+  return st;
 }
 
 extern "C" sv_status sv_profile_step(sv_engine* e, uint32_t flags, uint32_t reps, float* ms, uint32_t* launches) {

@@ -50,6 +50,15 @@ extern int g_mm_variant;
 struct GemmTune {
   int rtw, nt, s, d, mf, nw, cpi;  // mf: MFMA tile (16 or 32); nw: waves (4); cpi: chunks per barrier (1)
 };
+// The capture buffers attn_launch passes to the kernels (the engine's sv_step_capture sets
+// them around a layer's attention launches on its thread; null: no capture).
+struct AttnCapture {
+  float* q = nullptr;
+  float* k = nullptr;
+  float* v = nullptr;
+  float* sdpa = nullptr;
+};
+extern thread_local AttnCapture g_attn_capture;
 extern GemmTune g_gemm_tune;
 extern int g_gemm_order;  // tests: the GEMMs' work order (-1: modelled choice; 0 legacy; g: groups of g row blocks)
 extern SkinnyTune g_skinny_tune;  // path 3: the one-shot 1-16 row kernel with (rt, w, s = chunks per wave, splits)

@@ -148,6 +148,14 @@ class PlanInfo(C.Structure):
     _fields_ = [(n, u32) for n in ("n_tokens", "n_head", "n_runs", "branches", "max_run", "split", "max_splits")]
 
 
+class LayerCapture(C.Structure):
+    _fields_ = ([(n, u32) for n in ("layer", "n", "hidden", "qkv_width", "sdpa_width", "pad")] +
+                [(n, C.POINTER(C.c_float)) for n in ("resid_in", "attn_in", "qkv", "sdpa_out", "attn_out", "mlp_in",
+                                                     "mlp_out", "resid_base")])
+
+
+CAPTURE_FN = C.CFUNCTYPE(None, C.POINTER(LayerCapture), C.c_void_p)
+
 P = C.POINTER
 # name -> (restype, argtypes): every entry point include/sv_verify.h declares.
 PROTOS = {
@@ -211,6 +219,7 @@ PROTOS = {
     "sv_sync": (C.c_int, [vp]),
     "sv_set_replay": (C.c_int, [vp, u32, f32]),
     "sv_step": (C.c_int, [vp, P(Run), u32, u32, P(u32), P(f32), P(u32), P(PlanInfo)]),
+    "sv_step_capture": (C.c_int, [vp, P(Run), u32, u32, CAPTURE_FN, vp, P(u32), P(f32), P(u32), P(PlanInfo)]),
     "sv_profile_step": (C.c_int, [vp, u32, u32, P(f32), P(u32)]),
     "sv_sample_logits": (C.c_int, [vp, P(f32), u32, P(f32), P(f32), P(C.c_uint64), P(u32), P(u32)]),
 }

@@ -34,6 +34,25 @@ class StepResult:
     info: L.PlanInfo
 
 
+@dataclass
+class LayerCapture:
+    """One layer's intermediates over a capture step (LayerCapture, engine.rs:176-188), [n][width]
+    fp32 each: the layer's input residual, rms_norm of the attention input, q | k | v after the
+    norms, RoPE and value embeddings, the attention output before XSA and the gate, o's product
+    before the residual, rms_norm of the MLP input, down's product before the residual, and
+    MUDD's residual base (None on other layers)."""
+    layer: int
+    n: int
+    resid_in: np.ndarray
+    attn_in: np.ndarray
+    qkv: np.ndarray
+    sdpa_out: np.ndarray
+    attn_out: np.ndarray
+    mlp_in: np.ndarray
+    mlp_out: np.ndarray
+    resid_base: np.ndarray | None
+
+
 class Engine:
     def __init__(self, shape: ModelShape, *, max_seqs: int = 8, max_step_tokens: int = 64, max_seq_len: int = 8192,
                  max_head_rows: int = 16, kv_tokens: int | None = None, page_shift: int = 4, attn_scale: float = 0.125,
@@ -233,6 +252,39 @@ class Engine:
         info = L.PlanInfo()
         L.check(self.lib.sv_step(self.h, arr, len(runs), flags, ids,
                                  lg.ctypes.data_as(C.POINTER(C.c_float)) if lg is not None else None, em, C.byref(info)))
+        return StepResult(np.array(ids[:n_head], np.uint32), lg, np.array(em[:], np.uint32), info)
+
+    def step_capture(self, runs: list[tuple], f, flags: int = 0, logits: bool = False) -> StepResult:
+        """Engine::step_capture (engine.rs:318-355): the step run layer by layer; f(LayerCapture)
+        is called for each layer in order (its arrays are copies), then the head and tail run as
+        in step(), whose result this returns."""
+        torch.cuda.synchronize()
+        arr, keep = self._runs(runs)
+        n_head = sum(len(r[1]) if r[2] else (r[3] if len(r) > 3 else 1) for r in runs)
+        ids = (C.c_uint32 * max(1, n_head))()
+        em = (C.c_uint32 * len(runs))()
+        lg = np.zeros((n_head, self.shape.vocab), np.float32) if logits else None
+        info = L.PlanInfo()
+        errors = []
+
+        def cb(cp, _user):
+            if errors:
+                return
+            try:
+                c = cp.contents
+                rows = lambda p, w: np.ctypeslib.as_array(p, shape=(c.n, w)).copy() if p else None
+                f(LayerCapture(c.layer, c.n, rows(c.resid_in, c.hidden), rows(c.attn_in, c.hidden),
+                               rows(c.qkv, c.qkv_width), rows(c.sdpa_out, c.sdpa_width), rows(c.attn_out, c.hidden),
+                               rows(c.mlp_in, c.hidden), rows(c.mlp_out, c.hidden), rows(c.resid_base, c.hidden)))
+            except BaseException as e:  # raised again after the step (a callback cannot raise through C)
+                errors.append(e)
+
+        fn = L.CAPTURE_FN(cb)
+        L.check(self.lib.sv_step_capture(self.h, arr, len(runs), flags, fn, None, ids,
+                                         lg.ctypes.data_as(C.POINTER(C.c_float)) if lg is not None else None, em,
+                                         C.byref(info)))
+        if errors:
+            raise errors[0]
         return StepResult(np.array(ids[:n_head], np.uint32), lg, np.array(em[:], np.uint32), info)
 
     def profile_step(self, flags: int = 0, reps: int = 1) -> dict[str, tuple[float, int]]:

@@ -38,13 +38,14 @@ def test_library_exports_every_declared_symbol():
 STRUCTS = ["sv_shape", "sv_matrix", "sv_mat_args", "sv_kv_args", "sv_attn_args", "sv_sample_row", "sv_run_in",
            "sv_gen_state", "sv_replay_args", "sv_engine_config", "sv_layer", "sv_engine_buffers", "sv_run",
            "sv_plan_info", "sv_tensor_info", "sv_model_extras", "sv_attn_extras", "sv_draft_layer", "sv_drafter",
-           "sv_draft_buffers"]
+           "sv_draft_buffers", "sv_layer_capture"]
 PY = {"sv_shape": L.Shape, "sv_matrix": L.Matrix, "sv_mat_args": L.MatArgs, "sv_kv_args": L.KvArgs,
       "sv_attn_args": L.AttnArgs, "sv_sample_row": L.SampleRow, "sv_run_in": L.RunIn, "sv_gen_state": L.GenState,
       "sv_replay_args": L.ReplayArgs, "sv_engine_config": L.EngineConfig, "sv_layer": L.Layer,
       "sv_engine_buffers": L.EngineBuffers, "sv_run": L.Run, "sv_plan_info": L.PlanInfo,
       "sv_tensor_info": L.TensorInfo, "sv_model_extras": L.ModelExtras, "sv_attn_extras": L.AttnExtras,
-      "sv_draft_layer": L.DraftLayer, "sv_drafter": L.Drafter, "sv_draft_buffers": L.DraftBuffers}
+      "sv_draft_layer": L.DraftLayer, "sv_drafter": L.Drafter, "sv_draft_buffers": L.DraftBuffers,
+      "sv_layer_capture": L.LayerCapture}
 
 
 def test_struct_layouts_match_c(tmp_path):
