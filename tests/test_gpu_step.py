@@ -120,6 +120,10 @@ def test_config0_step(gpu):
     res = eng.step([run], logits=True)
     ids_r, logits_r, em_r, extra_r = ref.step([run])
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots, runs=[run])
+    # this seed's step has no near-tie row: every id, the accept/rollback state and the pages agree
+    assert np.array_equal(res.ids, ids_r), f"ids {res.ids} != {ids_r}"
+    assert np.array_equal(res.emitted, em_r) and eng.seq_len(s) == ref.seq_len[s]
+    assert eng.seq_pages(s) == ref.pool.pages(s)
 
 
 @pytest.mark.parametrize("scalars", [LayerScalars(), LayerScalars(0.8, 1.2, 0.9, 1.1, 0.95, 0.7, 1),
