@@ -72,13 +72,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
   float* lred = lds + 4 * COLS * D;
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, c16 = lane & 15, q = lane >> 4;
-  // Workgroups are dispatched in linear order (x fastest); they take their (split, kv head, run)
-  // split-major, so every run's first splits go out before any run's later ones, and the
-  // workgroups past a run's last split (the grid is sized for the longest context; they exit
-  // once the context length is in) come last, into the tail, instead of holding CU slots
-  // between live ones (configs[2]: about half the grid).
-  const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), per = gridDim.y * gridDim.z;
-  const uint32_t s = lin / per, g = lin % per % gridDim.y, r = lin % per / gridDim.y;
+  // Streaming variant: workgroups are dispatched in linear order (x fastest) and take their
+  // (split, kv head, run) split-major, so every run's first splits go out before any run's later
+  // ones, and the workgroups past a run's last split (the grid is sized for the longest context;
+  // they exit once the context length is in) come last, into the tail, instead of holding CU
+  // slots between live ones (configs[2]: about half the grid). Within a split the kv head is the
+  // fastest index (the run fastest measured 4 % slower per step at configs[2]). The all-in-flight
+  // variant (about one workgroup per CU, few past the context) keeps split fastest: an XCD
+  // (workgroup id mod 8) reads every kv head of its splits' pages (split-major measured 0.7 %
+  // slower per step at configs[1], each XCD then reading one kv head's slice of every page).
+  uint32_t s = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
+  if constexpr (NBW == 0) {
+    const uint32_t lin = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z), per = gridDim.y * gridDim.z;
+    s = lin / per;
+    g = lin % per % gridDim.y;
+    r = lin % per / gridDim.y;
+  }
   uint32_t t0, T, seq;
   run_header<INL>(p, r, t0, T, seq);
   // The run's visibility masks (the newest split's masks): requested with the first loads and
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
         for (int ks = 0; ks < KST; ks++)
 #pragma unroll
           for (int e = 0; e < 8; e++) qr.v[ct][ks][e] = 0.0f;
-    qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane, s == 0 ? p.cap_q : nullptr, t0, g);
+    qfinish_cs<D, NCT>(p, ncols, qr, cs, qh, ql, lane);
   }
 
   const uint32_t nsplit = attn_nsplit_t<LOCAL>(p, p0);
@@ -504,6 +513,67 @@ void attn_init() {
 }
 
 // Compute units of the current device (the all-batches-in-flight choice).
+// sv_step_capture (engine.rs:318-355; kernels.metal:932,1035): each token's queries after the
+// norm and RoPE, and its new keys after the norm and RoPE and values after the value embedding,
+// computed by the verify kernel's own loads and device code (qfinish_cs, new_keys), so they are
+// the bits the attention used; nothing else is written. Grid (kv heads, runs); launched only by
+// the capture step, after the layer's attention.
+template <int D, int NCT, bool INL>
+__global__ __launch_bounds__(256) void attn_capture_kernel(AttnParams p) {
+  constexpr int KST = D / 32;
+  __shared__ __attribute__((aligned(16))) uint16_t nk[SV_MAX_RUN * D], nv[SV_MAX_RUN * D];
+  const int tid = threadIdx.x, lane = tid & 63, c16 = lane & 15, q = lane >> 4;
+  const uint32_t g = blockIdx.x, r = blockIdx.y;
+  uint32_t t0, T, seq;
+  run_header<INL>(p, r, t0, T, seq);
+  const uint32_t ncols = T * p.G;
+  if (tid < 64) {
+    QRaw<D, NCT> qr;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++) {
+      const uint32_t c = min(16u * ct + c16, ncols - 1), i = c / p.G, h = g * p.G + c % p.G, t = t0 + i;
+      qr.pos[ct] = p.meta[2 * t + 1];
+      const size_t qo = (size_t)t * p.W + h * D + 8 * q;
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++) {
+        const f32x4 a = *(const f32x4*)(p.qkv + qo + 32 * ks), b = *(const f32x4*)(p.qkv + qo + 32 * ks + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          qr.v[ct][ks][e] = a[e];
+          qr.v[ct][ks][4 + e] = b[e];
+        }
+      }
+    }
+    float2 cs[NCT][KST][4];
+    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(INL ? p.rope_rows : p.rope), 0, p.rope_on ? 0x7fffffff : 0, 0x00020000);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++)
+#pragma unroll
+      for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          const uint32_t j = 16 * ks + 4 * q + jj;
+          const bool on = p.rope_on && 32 * ks + 8 * q < 64;
+          const uint32_t c = min(16u * ct + c16, ncols - 1);
+          const uint32_t row = INL ? t0 + c / p.G : qr.pos[ct];
+          const uint32_t off = (row * SV_ROPE_PAIRS + j) * 8 + (on ? 0u : 0x80000000u);
+          cs[ct][ks][jj] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(rrs, off, 0, 0));
+          if (!on) cs[ct][ks][jj] = float2{1.0f, 0.0f};
+        }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ct++)
+      if (16u * ct + c16 >= ncols)
+#pragma unroll
+        for (int ks = 0; ks < KST; ks++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) qr.v[ct][ks][e] = 0.0f;
+    bf16x8 qh[NCT][KST], ql[NCT][KST];
+    qfinish_cs<D, NCT, true>(p, ncols, qr, cs, qh, ql, lane, t0, g);
+  }
+  new_keys<D, false, true, false>(p, seq, g, t0, T, p.meta[2 * t0 + 1], nk, nv, tid, 256);
+}
+
 static uint32_t attn_cus() {
   static int cus = 0;
   if (!cus) {
@@ -679,6 +749,34 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
 #undef SV_ATTN
 #undef SV_ATTN3
     SV_TRY_LAUNCH("attn_verify");
+  }
+  if (parts & 8) {
+    // the capture step's queries, keys and values (attn_capture_kernel)
+    if (!p.cap_q || !p.cap_k || !p.cap_v) return fail(SV_ERR_ARG, "attn_verify: capture without its buffers");
+    const dim3 gc(NKV, n_runs);
+    const bool inl = p.n_inline != 0;
+#define SV_ATTN_CAP(DD, N)                                                              \
+  do {                                                                                  \
+    if (inl) launch((attn_capture_kernel<DD, N, true>), gc, dim3(256), 0, stream, p);   \
+    else launch((attn_capture_kernel<DD, N, false>), gc, dim3(256), 0, stream, p);      \
+  } while (0)
+    if (D == 64) {
+      switch (nct) {
+        case 1: SV_ATTN_CAP(64, 1); break;
+        case 2: SV_ATTN_CAP(64, 2); break;
+        case 3: SV_ATTN_CAP(64, 3); break;
+        default: SV_ATTN_CAP(64, 4); break;
+      }
+    } else {
+      switch (nct) {
+        case 1: SV_ATTN_CAP(128, 1); break;
+        case 2: SV_ATTN_CAP(128, 2); break;
+        case 3: SV_ATTN_CAP(128, 3); break;
+        default: SV_ATTN_CAP(128, 4); break;
+      }
+    }
+#undef SV_ATTN_CAP
+    SV_TRY_LAUNCH("attn_capture");
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
   // parts: enough that a thread adds at most eight splits (a power of two, up to 64)

@@ -53,7 +53,8 @@ struct AttnParams {
   uint32_t H;
   // Per-layer capture (sv_step_capture; null: off): each token's queries after the norm and
   // RoPE [n][NQ D], its keys after the norm and RoPE and values after the value embedding
-  // [n][NKV D], and the attention output before XSA and the gate [n][NQ D], all fp32.
+  // [n][NKV D] (written by attn_capture_kernel only), and the attention output before XSA and
+  // the gate [n][NQ D] (by the merge), all fp32.
   float* cap_q;
   float* cap_k;
   float* cap_v;
@@ -486,11 +487,11 @@ __device__ __forceinline__ void qrope_load(const AttnParams& p, uint32_t ncols, 
 }
 
 // Norm, RoPE (words from qrope_load), scale and hi/lo split of the raw queries.
-template <int D, int NCT>
+// CAP (the capture kernel only): the queries after the norm and RoPE also go to p.cap_q.
+template <int D, int NCT, bool CAP = false>
 __device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, QRaw<D, NCT>& r,
                                            const float2 (&cs)[NCT][D / 32][4], bf16x8 (&qh)[NCT][D / 32],
-                                           bf16x8 (&ql)[NCT][D / 32], int lane, float* capq = nullptr,
-                                           uint32_t t0 = 0, uint32_t g = 0) {
+                                           bf16x8 (&ql)[NCT][D / 32], int lane, uint32_t t0 = 0, uint32_t g = 0) {
   constexpr int KST = D / 32;
   const int c16 = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -517,10 +518,10 @@ __device__ __forceinline__ void qfinish_cs(const AttnParams& p, uint32_t ncols, 
           v[2 * jj + 1] = cs[ct][ks][jj].x * a1 - cs[ct][ks][jj].y * a0;
         }
       }
-      if (capq && ok) {
+      if (CAP && ok) {
         // the query after the norm and RoPE (column 16 ct + c16: token c / G, head g G + c % G)
         const uint32_t c = 16 * ct + c16;
-        float* dst = capq + (size_t)(t0 + c / p.G) * p.NQ * D + (g * p.G + c % p.G) * D + 32 * ks + 8 * q;
+        float* dst = p.cap_q + (size_t)(t0 + c / p.G) * p.NQ * D + (g * p.G + c % p.G) * D + 32 * ks + 8 * q;
         *(f32x4*)dst = f32x4{v[0], v[1], v[2], v[3]};
         *(f32x4*)(dst + 4) = f32x4{v[4], v[5], v[6], v[7]};
       }
@@ -556,7 +557,10 @@ __device__ __forceinline__ void build_queries(const AttnParams& p, uint32_t t0, 
 // within a thread); threads tid < nthreads of the caller take keys tid / 16, + nthreads / 16...
 // With the extras: the value embedding added to V first (add_ve, kernels.metal:738-747) and
 // V's direction V / max(|V|, 1e-4) to vdir for XSA (fp32, before rounding).
-template <int D, bool COH>
+// CAP (the capture kernel only): the keys after the norm and RoPE and the values after the value
+// embedding also go to p.cap_k / p.cap_v; with CACHE false nothing is written to the cache, LDS
+// or vdir (the step's attention already wrote the same bits).
+template <int D, bool COH, bool CAP = false, bool CACHE = true>
 __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint32_t g, uint32_t t0, uint32_t T,
                                          uint32_t p0, uint16_t* nk, uint16_t* nv, uint32_t tid, uint32_t nthreads) {
   constexpr int DL = D / 16;
@@ -593,7 +597,7 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
 #pragma unroll
         for (int e = 0; e < DL; e++) vv[e] = __builtin_fmaf(gate, bf(ve[e]), vv[e]);
       }
-      if (p.vdir) {
+      if (CACHE && p.vdir) {
         float vs = 0.0f;
 #pragma unroll
         for (int e = 0; e < DL; e++) vs = __builtin_fmaf(vv[e], vv[e], vs);
@@ -623,7 +627,7 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
           k0 = r0;
           k1 = r1;
         }
-        if (p.cap_k) {
+        if constexpr (CAP) {
           const size_t co = (size_t)t * p.NKV * D + g * D + d;
           p.cap_k[co] = k0;
           p.cap_k[co + 1] = k1;
@@ -634,7 +638,7 @@ __device__ __forceinline__ void new_keys(const AttnParams& p, uint32_t seq, uint
         vb[e / 2] = (uint32_t)to_bf(vv[e]) | ((uint32_t)to_bf(vv[e + 1]) << 16);
       }
 #pragma unroll
-      for (int e = 0; e < DL / 2; e += 2) {
+      for (int e = 0; e < DL / 2 && CACHE; e += 2) {
         const u32x2 kw = u32x2{kb[e], kb[e + 1]}, vw = u32x2{vb[e], vb[e + 1]};
         *(u32x2*)(p.kc + row + DL * l16 + 2 * e) = kw;
         *(u32x2*)(p.vc + row + DL * l16 + 2 * e) = vw;

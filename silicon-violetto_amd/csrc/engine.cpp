@@ -756,6 +756,9 @@ struct sv_engine {
       SV_TIMED(SV_KIND_ATTN_MERGE, attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn,
                                                P.max_run, vis, attn, ws, ws_bytes, 2, P.inl.data(), true, exp_,
                                                rope_rows));
+      if (cp)  // the layer's queries, keys and values as the attention computed them
+        SV_TRY(attn_launch(stream, &sh, qkv, meta, kc, vc, tab, rope, &kv, &aa, attn_runs, P.n_attn, P.max_run, vis,
+                           attn, ws, ws_bytes, 8, P.inl.data(), true, exp_, rope_rows));
       g_attn_capture = AttnCapture{};
       const uint32_t raw = cp ? (uint32_t)SV_FLAG_WRITE_RAW : 0u;
       SV_TIMED(SV_KIND_O, matmul(L.o, n, attn, nullptr, mixed, SV_EPI_RESID, raw, L.o_scale, L.resid_attn, L.post_attn,

@@ -73,7 +73,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
                       uint16_t* k_cache, uint16_t* v_cache, const uint32_t* page_table, const float* rope,
                       const sv_kv_args* kv, const sv_attn_args* args, const uint32_t* runs, uint32_t n_runs,
                       uint32_t max_run, const uint32_t* vis, float* out, void* ws, size_t ws_bytes,
-                      uint32_t parts = 3,  // bit 0: attention, bit 1: the split merge, bit 2: runs' new K/V first
+                      uint32_t parts = 3,  // bits: 1 attention, 2 split merge, 4 new K/V first, 8 capture q/k/v
                       const uint32_t* host_runs = nullptr,  // (first token, rows, slot) per run, if known
                       bool may_fuse = true,  // the counted last-split merge may be used (tests select it)
                       const sv_attn_extras* ex = nullptr,   // the layer's extras (null: none)
