@@ -347,36 +347,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(attn_waves(
     store_wt(pl + idx, ((lred[idx] + lred[COLS + idx]) + lred[2 * COLS + idx]) + lred[3 * COLS + idx]);
   if (!p.counters) return;  // attn_merge_kernel merges
 
-  // The last split of (run, kv head) to arrive merges (attn_dec_reduce, kernels.metal:1316-1362):
-  // plain sums in split order, 16-byte coherent loads, eight splits in flight per thread.
+  // The last split of (run, kv head) to arrive merges (attn_dec_reduce, kernels.metal:1316-1362)
+  // in attn_merge_kernel's order, so both give the same bits: P parts (p.merge_parts <= 4), part
+  // j adding splits j, j + P, ... (at most eight) from zero, the parts then added in part order.
+  // Thread (part, gi) takes items gi, gi + 256 / P, ... of four outputs (column, dims d .. d + 3),
+  // three items' loads in flight at once; each part's sums meet in the reduction buffer.
   __shared__ uint32_t flag;
   if (!arrive_last(&p.counters[r * p.NKV + g], nsplit, &flag)) return;
+  const uint32_t P = p.merge_parts, G4 = 256 / P, part = tid / G4, gi = tid % G4;
   const size_t rec0 = ((size_t)r * p.NKV + g) * p.max_splits;
   const uint32_t so = p.maxcols * D * 4;  // bytes per split partial
   const __amdgpu_buffer_rsrc_t po0 = coherent_rsrc(p.part_o + rec0 * p.maxcols * D);
   const float* pl0 = p.part_l + rec0 * p.maxcols;
+  f32x4* red = (f32x4*)ored;  // [P][n4] (P n4 16 <= 4 COLS D 4 bytes)
+  constexpr int IB = 3;
+  for (uint32_t b0 = gi; b0 < n4; b0 += IB * G4) {
+    f32x4 ov[IB][8];
+#pragma unroll
+    for (int b = 0; b < IB; b++)
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const uint32_t i4 = b0 + b * G4, x = part + u * P;
+        ov[b][u] = i4 < n4 && x < nsplit ? load_wt4(po0, x * so + i4 * 16) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int b = 0; b < IB; b++) {
+      f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        if (part + u * P < nsplit) o += ov[b][u];
+      if (b0 + b * G4 < n4) red[part * n4 + b0 + b * G4] = o;
+    }
+  }
+  // l per (part, column)
+  if (tid < P * ncols) {
+    const uint32_t lp = tid / ncols, col = tid % ncols;
+    float lv[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const uint32_t x = lp + u * P;
+      lv[u] = x < nsplit ? load_wt(pl0 + x * p.maxcols + col) : 0.0f;
+    }
+    float l = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 8; u++)
+      if (lp + u * P < nsplit) l += lv[u];
+    lred[lp * COLS + col] = l;
+  }
+  __syncthreads();
   for (uint32_t i4 = tid; i4 < n4; i4 += 256) {
     const uint32_t col = (4 * i4) / D, d = (4 * i4) % D;
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-    float l = 0.0f;
-    uint32_t sp = 0;
-    for (; sp + 8 <= nsplit; sp += 8) {
-      f32x4 ov[8];
-      float lv[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        ov[u] = load_wt4(po0, (sp + u) * so + i4 * 16);
-        lv[u] = load_wt(pl0 + (sp + u) * p.maxcols + col);
-      }
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        o += ov[u];
-        l += lv[u];
-      }
-    }
-    for (; sp < nsplit; sp++) {
-      o += load_wt4(po0, sp * so + i4 * 16);
-      l += load_wt(pl0 + sp * p.maxcols + col);
+    f32x4 o = red[i4];
+    float l = lred[col];
+    for (uint32_t j = 1; j < P; j++) {
+      o += red[j * n4 + i4];
+      l += lred[j * COLS + col];
     }
     const uint32_t i = col / p.G, h = g * p.G + col % p.G;
     *(f32x4*)(p.out + (size_t)(t0 + i) * p.NQ * D + h * D + d) = o / l;
@@ -584,7 +609,7 @@ static uint32_t attn_cus() {
   return (uint32_t)cus;
 }
 thread_local AttnCapture g_attn_capture;
-bool g_attn_fused_merge = false;  // tests: the last split to arrive merges (measured slower)
+bool g_attn_fused_merge = false;  // tests: the last split to arrive merges (bit-identical, measured slower)
 int g_attn_allin = -1;  // -1: by shape; 0 / 1: force the one-batch-ahead / all-batches variant where built
 
 static uint32_t cols_pad(const sv_shape* sh, uint32_t max_run) {
@@ -635,7 +660,13 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   // faster at 9-65 splits); with g_attn_fused_merge set the last split of each (run, kv head)
   // to arrive merges instead.
   const bool merge_extras = ex && (ex->d_xsa || ex->d_attn_gate);
-  const bool fused_merge = may_fuse && g_attn_fused_merge && !merge_extras;
+  // merge parts: enough that a thread adds at most eight splits (a power of two, up to 64)
+  // (with XSA or the gate, a column's D / 4 threads stay in part 0: P <= 1024 / D); the fused
+  // merge holds its parts' sums in the reduction buffer: P <= 4
+  const uint32_t P_max = merge_extras ? 1024u / D : 64u;
+  uint32_t P = 1;
+  while (P < P_max && 8 * P < args->max_splits) P *= 2;
+  const bool fused_merge = may_fuse && g_attn_fused_merge && !merge_extras && P <= 4;
   const size_t need = attn_ws_bytes(sh, n_runs, args->max_splits, max_run);
   if (!ws || ws_bytes < need) return fail(SV_ERR_ARG, "attn_verify: workspace %zu < %zu bytes", ws_bytes, need);
   AttnParams p;
@@ -650,6 +681,7 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
   p.out = out;
   // counters (zero at rest), then the partials
   p.counters = fused_merge ? (uint32_t*)ws : nullptr;
+  p.merge_parts = P;
   size_t off = ((size_t)n_runs * NKV * 4 + 255) / 256 * 256;
   p.part_o = (float*)((char*)ws + off);
   off += (size_t)n_runs * NKV * args->max_splits * maxcols * D * 4;
@@ -779,11 +811,6 @@ sv_status attn_launch(hipStream_t stream, const sv_shape* sh, const float* qkv, 
     SV_TRY_LAUNCH("attn_capture");
   }
   if (fused_merge || !(parts & 2)) return SV_OK;
-  // parts: enough that a thread adds at most eight splits (a power of two, up to 64)
-  // (with XSA or the gate, a column's D / 4 threads stay in part 0: P <= 1024 / D)
-  const uint32_t P_max = merge_extras ? 1024u / D : 64u;
-  uint32_t P = 1;
-  while (P < P_max && 8 * P < args->max_splits) P *= 2;
   const uint32_t G4 = 256 / P, mz = (maxcols * D / 4 + G4 - 1) / G4;
   const dim3 mg(n_runs, NKV, mz);
   if (D == 64) {
@@ -829,6 +856,7 @@ sv_status attn_params_fill(void* out, const sv_shape* sh, const float* qkv, cons
   p.part_o = part_o;
   p.part_l = part_l;
   p.counters = nullptr;
+  p.merge_parts = 1;
   p.NQ = sh->n_heads;
   p.NKV = sh->n_kv_heads;
   p.G = sh->n_heads / sh->n_kv_heads;

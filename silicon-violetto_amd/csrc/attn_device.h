@@ -24,6 +24,7 @@ struct AttnParams {
   float* part_o;
   float* part_l;
   uint32_t* counters;  // per (run, kv head): fused merge; null: attn_merge_kernel merges
+  uint32_t merge_parts;  // the merge's parts P (both merges: splits j, j + P, ... per part)
   uint32_t NQ, NKV, G, W, KOFF, VOFF;
   uint32_t split, max_splits;
   float scale_log2;

@@ -331,6 +331,50 @@ def test_attn_verify(gpu, runs_T, p0s, split, tree, rope, allin):
         sel.value = -1
 
 
+@pytest.mark.parametrize("runs_T,p0s,split,tree", [([5], [8192], 384, False), ([5], [8192], 256, False),
+                                                   ([5, 4], [1000, 2047], 512, False), ([16], [300], 64, True),
+                                                   ([3, 5, 2], [31, 100, 64], 32, False),
+                                                   ([4] * 40, [37 * i for i in range(40)], 128, False)])
+@pytest.mark.parametrize("allin", [1, 0])
+def test_attn_fused_merge_bit_identical(gpu, runs_T, p0s, split, tree, allin):
+    """The merge by the last split to arrive (attention launch only) adds the splits' partials
+    in attn_merge_kernel's order (P parts of every P-th split from zero, then the parts in
+    order), so both merges give the same bits: configs[1]'s run (23 splits: four parts; at 33
+    splits, eight parts, the separate merge runs), ragged runs, a draft tree, 40 runs read from
+    memory; both cached-key variants. The second fused call shares the workspace, so it also
+    finds the counters back at zero (graph replays rely on it)."""
+    banner(f"attn fused merge runs={runs_T} p0={p0s} split={split} tree={tree} allin={allin}")
+    sh = SH
+    c = make_attn_case(sh, runs_T, p0s, seed=len(runs_T) * 17 + split, tree=tree)
+    freq = oracle.np.asarray((500000.0 ** (-2.0 * np.arange(32) / 64)), np.float32)
+    rope_tab = to_dev(oracle.rope_table(freq, max(p0s) + 20))
+    kv = L.KvArgs(1, 0, 0, len(runs_T), c["page_shift"], c["n_pages"], c["max_pages"], 0)
+    max_splits = max(-(-p // split) + 1 for p in p0s)
+    args = L.AttnArgs(split, max_splits, sh.head_dim ** -0.5 * 1.4426950408889634, 1, 0, 0, 0, 0, 0)
+    runs = to_dev(c["runs"].reshape(-1).copy())
+    qkv, meta, vis, pt = to_dev(c["qkv"]), to_dev(c["meta"]), to_dev(c["vis"]), to_dev(c["page_table"])
+    kd, vd = to_dev(c["k"]), to_dev(c["v"])
+    sel = C.c_int.in_dll(L.lib(), "_ZN2sv12g_attn_allinE")
+    fused = C.c_bool.in_dll(L.lib(), "_ZN2sv18g_attn_fused_mergeE")
+    outs = []
+    ws = K.Workspace(64 << 20)
+    assert L.lib().sv_attn_workspace_bytes(C.byref(sh.c()), len(runs_T), max_splits, max(runs_T)) <= ws.nbytes
+    try:
+        sel.value = allin
+        for f in (False, True, True):
+            fused.value = f
+            out = torch.full((sum(runs_T), sh.n_heads * sh.head_dim), 7.0, device="cuda")
+            K.attn_verify(sh, qkv, meta, kd, vd, pt, rope_tab, kv, args, runs, len(runs_T), max(runs_T), vis, out, ws=ws)
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+    finally:
+        fused.value = False
+        sel.value = -1
+    assert np.isfinite(outs[0]).all()
+    for i in (1, 2):
+        assert np.array_equal(outs[0].view(np.uint32), outs[i].view(np.uint32)), f"fused merge call {i} differs"
+
+
 @pytest.mark.parametrize("runs_T,p0s,split", [([5], [65536], 1152), ([5] * 8, [65536] * 8, 3584)])
 def test_attn_verify_long_context(gpu, runs_T, p0s, split):
     """configs[3]'s attention: 65536 cached keys per stream (1 stream with 1152-key splits, 8
