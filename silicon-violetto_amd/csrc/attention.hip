@@ -22,9 +22,11 @@
 //   - The 4 waves' (l, o) meet in LDS and the split's partial goes to the workspace with
 //     coherent stores (sc1: write-through to the agent-coherent level). attn_merge_kernel,
 //     the next launch, sums the partials of each (run, kv head) output in split order and
-//     writes o / l. With g_attn_fused_merge set the last split of (run, kv head) to arrive (a
-//     relaxed agent-scope counter: no L2 write-back or invalidate) does the same with
-//     coherent 16-byte loads.
+//     writes o / l. With g_attn_fused_merge set (tests; measured slower) the last split of
+//     (run, kv head) to arrive (a relaxed agent-scope counter: no L2 write-back or invalidate)
+//     does the same, in the same order (the same bits), with coherent 16-byte loads.
+//   - The capture step (sv_step_capture) adds attn_capture_kernel after the merge: it repeats
+//     the query and new-key device code into float buffers; the kernels above are unchanged.
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
