@@ -8,6 +8,8 @@ from __future__ import annotations
 import ctypes as C
 import itertools
 
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -116,6 +118,25 @@ def test_quantize_ties_round_to_even():
     q, sc = O.quantize(row[None, :].repeat(1, 0), 8)
     assert O.bf16_to_f32(sc)[0, 0] == s
     assert q[0].tolist() == [127, 0, 2, 2, 0, -2, 3, -126]
+
+
+def test_quantize_matches_reference_converter_vectors():
+    """orc_quantize against the reference converter's own quantize (tools/convert.py:41-50),
+    vectors written by tests/golden/make_quantize_vectors.py: every q and bf16 scale bit for
+    bit at groups of 8, 64 and 512, on rows that include exact half steps (ties), groups whose
+    scale rounded down (the clamp) and a zero row."""
+    f = np.load(Path(__file__).parent / "golden" / "quantize_vectors.npz")
+    w = f["w"]
+    clamped = ties = 0
+    for group in (8, 64, 512):
+        q, s = O.quantize(w, group)
+        assert np.array_equal(q, f[f"q{group}"]), f"group {group}: q differs"
+        assert np.array_equal(s, f[f"s{group}"]), f"group {group}: scales differ"
+        sf = O.bf16_to_f32(s).astype(np.float64)
+        g = w.reshape(w.shape[0], -1, group).astype(np.float64)
+        clamped += int((np.abs(g).max(-1) > 127 * sf).sum())
+        ties += int((np.abs(g / np.where(sf > 0, sf, 1)[..., None] % 1 - 0.5) < 1e-12).sum())
+    assert clamped > 0 and ties > 0, "the vectors should hold clamped groups and exact half steps"
 
 
 # -------------------------------------------------------------------------------- matmul
