@@ -25,11 +25,16 @@ FIELDS = ("resid_in", "attn_in", "qkv", "sdpa_out", "attn_out", "mlp_in", "mlp_o
 # 8 Limite layers; the attention kernel alone, on identical cache bits, is within 2e-4).
 REL_TOL = {"sdpa_out": 3e-3, "attn_out": 3e-3}
 REL_TOL_OTHER = 5e-4
+# At the reference model's layer shape (1280 hidden, five query heads of 128 per kv head) those
+# one-ulp K/V differences move every field about ten times as much: observed up to 2.6e-3 in the
+# attention output and 5.0e-4 in later fields over 8 layers.
+REF_TOL_OTHER = 1e-3
 
 
-def compare_capture(got, want, what):
+def compare_capture(got, want, what, tol_other=REL_TOL_OTHER):
     assert [c.layer for c in got] == list(range(len(want))), f"{what}: layers out of order"
-    worst = 0.0
+    worst = {}
+    bad = []
     for c, w in zip(got, want):
         for name in FIELDS:
             a, b = getattr(c, name), w[name]
@@ -39,12 +44,14 @@ def compare_capture(got, want, what):
             assert a is not None and a.shape == b.shape, f"{what} layer {c.layer}: {name} shape"
             scale = max(float(np.abs(b).max()), 1e-6)
             err = float(np.abs(a.astype(np.float64) - b).max()) / scale
-            worst = max(worst, err)
-            assert err <= REL_TOL.get(name, REL_TOL_OTHER), f"{what} layer {c.layer}: {name} off by {err:.2e} of its scale"
-    print(f"  {what}: worst field error {worst:.2e} of scale", flush=True)
+            worst[name] = max(worst.get(name, 0.0), err)
+            if err > REL_TOL.get(name, tol_other):
+                bad.append(f"layer {c.layer}: {name} off by {err:.2e} of its scale")
+    print(f"  {what}: worst error of scale per field " + ", ".join(f"{k} {v:.1e}" for k, v in worst.items()), flush=True)
+    assert not bad, f"{what}: " + "; ".join(bad)
 
 
-def captured_step(eng, ref, runs, slots, what):
+def captured_step(eng, ref, runs, slots, what, tol_other=REL_TOL_OTHER):
     got = []
     res = eng.step_capture(runs, got.append, logits=True)
     ids_r, logits_r, em_r, extra_r = ref.step(runs, capture=True)
@@ -53,7 +60,7 @@ def captured_step(eng, ref, runs, slots, what):
         # the sequences no longer hold the same tokens
         print(f"  {what}: capture not compared (slots {sorted(eng._diverged)} diverged)", flush=True)
     else:
-        compare_capture(got, extra_r["capture"], what)
+        compare_capture(got, extra_r["capture"], what, tol_other)
     compare_step(res, ids_r, logits_r, em_r, extra_r, eng, ref, slots, runs=runs)
 
 
@@ -92,6 +99,23 @@ def test_capture_against_oracle_limite(gpu):
     captured_step(eng, ref, [(s, prompt, False, 1)], slots, "chunk")
     runs = [(s, [L.FEED_ROW] + [int(t) for t in rng.integers(0, shape.vocab_real, 4)], True)]
     captured_step(eng, ref, runs, slots, "verify step")
+    eng.close()
+
+
+def test_capture_against_oracle_reference_shape(gpu):
+    """The reference model's own layer shape (hidden 1280, 10 query heads of 128 over 2 kv heads,
+    ffn 3328) in the Limite layout over 8 layers: the capture's head_dim 128 kernels, five query
+    heads per kv head (a 20-row prompt chunk runs as attention runs of 12 rows), then a verify
+    step."""
+    banner("step_capture vs oracle: reference layer shape")
+    shape = ModelShape(hidden=1280, n_heads=10, n_kv_heads=2, head_dim=128, ffn=3328, vocab=1024, vocab_real=1000,
+                       n_layers=8)
+    model, gm, eng, ref, slots, rng = build_limite_pair(shape, window=48, ctx=[150], seed=29, max_seq_len=512)
+    s = slots[0]
+    prompt = [int(t) for t in rng.integers(0, shape.vocab_real, 20)]
+    captured_step(eng, ref, [(s, prompt, False, 1)], slots, "chunk", tol_other=REF_TOL_OTHER)
+    runs = [(s, [L.FEED_ROW] + [int(t) for t in rng.integers(0, shape.vocab_real, 4)], True)]
+    captured_step(eng, ref, runs, slots, "verify step", tol_other=REF_TOL_OTHER)
     eng.close()
 
 
